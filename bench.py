@@ -1,0 +1,215 @@
+#!/usr/bin/env python3
+"""MI355X decode-attention benchmark (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--all]
+
+One "step" is one decode-attention call of the named configuration over one
+batch of synthetic inputs already resident in HBM.  W untimed warm-up steps
+run first; then exactly K steps are captured into one hipGraph (each step on
+its own copy of the inputs, rotating through enough copies to exceed 2x the
+256 MB Infinity Cache, so every step streams from HBM) and the graph replay
+is timed with HIP events on the capture's stream, between two device
+synchronisations.  Rank 0 prints one JSON line.
+
+The cpu_baseline leg times the CPU oracle (test infrastructure, oracle/) on a
+bounded sample of the same workload, only on rank 0 at N=1.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+MALL_BYTES = 256 << 20     # Infinity Cache
+
+
+# ---------------------------------------------------------------------------
+# Cases
+# ---------------------------------------------------------------------------
+class Case:
+    name = ""
+    workload = ""
+    dtype = "bf16"
+    kernel = ""            # kernel symbol (substring) that dominates the step
+
+    def bytes_per_step(self) -> int:
+        raise NotImplementedError
+
+    def make(self, dev):
+        raise NotImplementedError
+
+    def step(self, inp):
+        raise NotImplementedError
+
+    def cpu_sample(self):
+        """-> (description, fn running the oracle on the sample, full/sample work ratio)."""
+        raise NotImplementedError
+
+
+class DenseCase(Case):
+    kernel = "dense_decode_kernel"
+
+    def __init__(self, name, B, Hq, Hk, D, L):
+        self.name, self.shape = name, (B, Hq, Hk, D, L)
+        self.workload = f"dense bf16 GQA decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L}"
+
+    def bytes_per_step(self):
+        B, Hq, Hk, D, L = self.shape
+        return 2 * B * Hk * L * D * 2 + 2 * B * Hq * D * 2
+
+    def make(self, dev):
+        from bytes_amd import workloads as W
+        x = W.dense(*self.shape, seed=0, device="cpu")
+        return {"q": x["q"].to(dev), "k": x["k"].to(dev), "v": x["v"].to(dev), "scale": x["scale"]}
+
+    def step(self, inp):
+        from bytes_amd.attention_kernels import decode_attn_bf16
+        return decode_attn_bf16(inp["q"], inp["k"], inp["v"], inp["scale"])
+
+    def cpu_sample(self):
+        from bytes_amd import workloads as W
+        from oracle import reference as R
+        B, Hq, Hk, D, L = self.shape
+        x = W.dense(1, Hq // Hk, 1, D, L, seed=0)          # one (b, kv-head) unit
+        units = B * Hk
+        return (f"one (b, kv-head) unit of {units}: q [1,{Hq // Hk},1,{D}], K/V [1,1,{L},{D}]",
+                lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), units)
+
+
+def cases():
+    from bytes_amd import workloads as W
+    return {
+        "c1_dense": DenseCase("c1_dense", *W.SHAPES["c1_dense"]),
+        "dense_16k": DenseCase("dense_16k", *W.SHAPES["dense_16k"]),
+        "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
+    }
+
+
+HEADLINE = "dense_16k"
+
+
+# ---------------------------------------------------------------------------
+# Timing
+# ---------------------------------------------------------------------------
+def clone_inputs(inp, copies):
+    out = [inp]
+    for _ in range(copies - 1):
+        out.append({k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()})
+    return out
+
+
+def time_gpu(case: Case, steps: int, warmup: int, dev) -> dict:
+    base = case.make(dev)
+    nbytes = case.bytes_per_step()
+    copies = max(2, math.ceil(2 * MALL_BYTES / max(nbytes, 1)) + 1)
+    inps = clone_inputs(base, copies)
+    for i in range(warmup):
+        case.step(inps[i % copies])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            case.step(inps[i % copies])
+    torch.cuda.synchronize()
+    g.replay()                       # untimed: uploads the graph
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    g.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del g
+    return {"ms_per_step": ms, "copies": copies, "bytes_per_step": nbytes}
+
+
+def time_cpu(case: Case, budget_s: float = 20.0) -> dict:
+    desc, fn, ratio = case.cpu_sample()
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    fn()                                            # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s / 4 and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    med = statistics.median(times)
+    return {"value": med * ratio * 1e6, "unit": "us/step", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{desc}; median of {len(times)} runs x {ratio} to a full step"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default=HEADLINE)
+    ap.add_argument("--all", action="store_true", help="also time every other config (per_config)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (every configuration is one GPU's "
+              "shard; see DESIGN.md for how the path would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    allc = cases()
+    if args.config not in allc:
+        print(f"unknown config {args.config}; known: {sorted(allc)}", file=sys.stderr)
+        sys.exit(2)
+    head = allc[args.config]
+    r = time_gpu(head, args.steps, args.warmup, dev)
+    us = r["ms_per_step"] * 1e3
+    achieved = r["bytes_per_step"] / (r["ms_per_step"] * 1e-3)
+    line = {
+        "metric": "decode-attn us/step & % of HBM peak BW (BF16/KIVI/PQ/top-k), 1 MI355X",
+        "value": round(us, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head.dtype,
+        "data": "synthetic (seeded N(0,1), BASELINE.json configs)",
+        "config": {"workload": head.workload, "name": head.name, "mall_rotation_copies": r["copies"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "kernel": head.kernel, "algorithmic_bytes": r["bytes_per_step"]},
+    }
+    if args.all:
+        per = {}
+        for name, c in allc.items():
+            if name == head.name:
+                continue
+            rr = time_gpu(c, min(args.steps, 100), args.warmup, dev)
+            a = rr["bytes_per_step"] / (rr["ms_per_step"] * 1e-3)
+            per[name] = {"us_per_step": round(rr["ms_per_step"] * 1e3, 3), "GBps": round(a / 1e9, 1),
+                         "hbm_frac": round(a / HBM_PEAK, 4), "bytes": rr["bytes_per_step"],
+                         "workload": c.workload}
+        line["per_config"] = per
+    if not args.no_cpu:
+        line["cpu_baseline"] = time_cpu(head)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,105 @@
+"""ctypes binding of libbytes_amd.so, the C ABI over the gfx950 kernels.
+
+Every exported function takes device pointers, shape ints, int64 element
+strides, a workspace pointer/size and a hipStream_t, and returns 0 or a
+hipError_t.  This module maps a non-zero return to RuntimeError.  There is no
+fallback: if the library is missing, every operator raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Dict, Tuple
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libbytes_amd.so")
+
+c_int, c_i64, c_f32, c_sz, c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+c_szp = ctypes.POINTER(ctypes.c_size_t)
+
+# name -> argtypes (restype is always c_int unless listed in _RESTYPES)
+SIGNATURES: Dict[str, Tuple] = {
+    "bytes_abi_version": (),
+    "bytes_error_string": (c_int,),
+    "bytes_decode_attn_bf16_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
+    "bytes_decode_attn_bf16": (
+        c_vp, c_vp, c_vp, c_vp,                       # q, k, v, out
+        c_int, c_int, c_int, c_int, c_int,            # B, Hq, Hk, S, D
+        c_i64, c_i64,                                 # q strides (b, h)
+        c_i64, c_i64, c_i64,                          # k strides (b, h, s)
+        c_i64, c_i64, c_i64,                          # v strides (b, h, s)
+        c_i64, c_i64,                                 # out strides (b, h)
+        c_f32, c_int, c_vp, c_sz, c_vp),              # scale, chunk, workspace, bytes, stream
+}
+_RESTYPES = {"bytes_error_string": ctypes.c_char_p}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib():
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"bytes_amd: {LIB_PATH} is missing; build it with "
+                    "`python -m bytes_amd.build` (there is no CPU fallback)")
+            h = ctypes.CDLL(LIB_PATH)
+            for name, argt in SIGNATURES.items():
+                fn = getattr(h, name)
+                fn.argtypes = list(argt)
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = h
+    return _lib
+
+
+def check(rc: int, name: str) -> None:
+    if rc != 0:
+        msg = lib().bytes_error_string(rc)
+        raise RuntimeError(f"bytes_amd.{name}: {msg.decode() if msg else 'error'} (hipError {rc})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+# ---------------------------------------------------------------------------
+# Workspaces: one zero-initialised byte buffer per device.  Kernels that use
+# split-K counters leave them at zero when they finish, so a buffer is cleared
+# only when it is (re)allocated.  It grows on demand; the usual warm-up call
+# before a graph capture sizes it.  Calls that share it must be ordered on one
+# stream (the reference harness runs everything on the current stream).
+# ---------------------------------------------------------------------------
+_ws: Dict[int, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _ws.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(int(nbytes), 1 << 20)
+        buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+        _ws[key] = buf
+    return buf
+
+
+def size_query(name: str, *args) -> int:
+    out = ctypes.c_size_t(0)
+    call(name, *args, ctypes.byref(out))
+    return int(out.value)

@@ -1,0 +1,51 @@
+"""Drop-in decode-attention operators (src/attention_kernels.py surface).
+
+Each function keeps the reference's name, argument meaning and output
+layout/dtype, launches a hand-written gfx950 HIP kernel through the C ABI on
+the current stream (no host sync), and allocates only its output (plus a
+cached, zero-initialised split-K workspace).  BLOCK_* arguments of the
+reference are tuning hints for Triton and are accepted and ignored.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _checks as C
+from ._lib import call, ptr, size_query, stream_of, workspace
+
+
+def decode_attn_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 1.0,
+                     *, chunk: int = 0) -> torch.Tensor:
+    """softmax(scale * q.K^T) V for one query per (b, h_q); GQA h_k = h_q // G.
+
+    Replaces src/attention_kernels.py:65-92.  q [B,H_q,1,D] bf16; k, v
+    [B,H_k,S,D] bf16 (any strides; a copy is made if rows are not 16-byte
+    aligned with unit stride in D).  Returns [B,H_q,1,D] in q's dtype.
+    The reference applies no scale (:42): `scale` defaults to 1.0; pass
+    1/sqrt(D) for standard attention.  `chunk` forces the split-K chunk
+    length in tokens (0 = automatic).
+    """
+    C.cuda_tensors(q, k, v)
+    C.ndim(q, 4, "q"), C.ndim(k, 4, "k"), C.ndim(v, 4, "v")
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        C.dtype_in(t, n, torch.bfloat16)
+    B, Hq, one, D = q.shape
+    _, Hk, S, Dk = k.shape
+    if one != 1 or Dk != D or tuple(v.shape) != tuple(k.shape) or k.shape[0] != B:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if Hq % Hk != 0:
+        raise ValueError(f"H_q={Hq} is not a multiple of H_k={Hk}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if S == 0:
+        raise ValueError("empty KV cache (S == 0)")
+    qs = C.rows16(q.squeeze(2))
+    k, v = C.rows16(k), C.rows16(v)
+    out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    nbytes = size_query("bytes_decode_attn_bf16_workspace_size", B, Hq, Hk, S, D, int(chunk))
+    ws = workspace(q.device, nbytes)
+    call("bytes_decode_attn_bf16", ptr(qs), ptr(k), ptr(v), ptr(out), B, Hq, Hk, S, D,
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2),
+         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1),
+         float(scale), int(chunk), ptr(ws), ws.numel(), stream_of(q))
+    return out.unsqueeze(2)

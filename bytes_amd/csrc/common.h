@@ -1,0 +1,64 @@
+// Shared device helpers for the bytes_amd gfx950 (CDNA4) kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * wave64; MFMA operand layouts are those of v_mfma_f32_16x16x32_{bf16,f16}:
+//      A[m][k]: lane l holds m = l%16, k = (l/16)*8 + j   (j = 0..7)
+//      B[k][n]: lane l holds n = l%16, k = (l/16)*8 + j
+//      C[m][n]: lane l holds n = l%16, m = (l/16)*4 + i   (i = 0..3)
+//  * softmax runs in the log2 domain: x = score * scale * log2(e), p = 2^(x - m).
+//  * every entry point returns 0 or a hipError_t and never throws.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bytes_amd {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte global load (caller guarantees 16-byte alignment).
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Wave-scope ordering point for wave-private LDS buffers: keeps the compiler
+// from moving LDS accesses across it and orders them at wavefront scope.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+}  // namespace bytes_amd

@@ -1,0 +1,120 @@
+// Split-K flash-decode epilogue shared by the dense, KIVI, PQ and gather kernels.
+//
+// A "unit" is one (b, kv-head, head-block) triple: up to 16 query heads of one
+// GQA group that read the same K/V rows.  The token axis of a unit is cut into
+// `nsplit` chunks, one workgroup each.  Every workgroup merges its waves'
+// online-softmax states in LDS and then either writes the final output
+// (nsplit == 1) or writes an fp32 partial (m, l, acc[D]) per head to the
+// workspace; a second, small kernel (splitk_combine) merges the partials of
+// each (unit, head) in a fixed order, so results are deterministic.
+//
+// The merge is a separate launch on purpose: a same-kernel "last workgroup
+// merges" scheme needs an agent-scope release/acquire per workgroup, which on
+// gfx950 writes back and invalidates the whole per-XCD L2 and stalls every
+// other wave on that XCD.
+#pragma once
+#include "common.h"
+
+namespace bytes_amd {
+
+enum OutDtype : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
+
+struct SplitKOut {
+  void* out;            // [B, Hq, D] with element strides o_sb, o_sh (d stride 1)
+  int out_dtype;        // OutDtype
+  int64_t o_sb, o_sh;
+  float* part_acc;      // [units][nsplit][16][D]
+  float* part_ml;       // [units][nsplit][16][2]
+  int nsplit;
+  int Hk, HB, G;        // unit u -> b = u / (Hk*HB), hk, hb; query head = hk*G + hb*16 + h
+};
+
+// Workspace layout: part_ml then part_acc (256-byte aligned).
+inline size_t splitk_workspace_bytes(long units, long nsplit, int D) {
+  if (nsplit <= 1) return 256;
+  size_t ml = ((size_t)units * nsplit * 16 * 2 * 4 + 255) / 256 * 256;
+  size_t acc = (size_t)units * nsplit * 16 * D * 4;
+  return ml + acc;
+}
+
+inline void splitk_carve(void* ws, long units, long nsplit, SplitKOut& o) {
+  char* p = static_cast<char*>(ws);
+  size_t ml = ((size_t)units * nsplit * 16 * 2 * 4 + 255) / 256 * 256;
+  o.part_ml = reinterpret_cast<float*>(p);
+  o.part_acc = reinterpret_cast<float*>(p + ml);
+  o.nsplit = (int)nsplit;
+}
+
+__device__ __forceinline__ void store_out(const SplitKOut& o, int b, int hq, int d, float v) {
+  int64_t off = (int64_t)b * o.o_sb + (int64_t)hq * o.o_sh + d;
+  if (o.out_dtype == kOutBF16) {
+    reinterpret_cast<uint16_t*>(o.out)[off] = f32_to_bf16_bits(v);
+  } else if (o.out_dtype == kOutF16) {
+    reinterpret_cast<_Float16*>(o.out)[off] = (_Float16)v;
+  } else {
+    reinterpret_cast<float*>(o.out)[off] = v;
+  }
+}
+
+// LDS floats needed by splitk_epilogue.
+template <int D, int NW>
+constexpr int splitk_smem_floats() {
+  return NW * 16 * 2 + NW * D * 16;
+}
+
+// m_run: running max (log2 domain) of this lane's head l%16, identical across
+// the four lanes l%16 + 16*j; l_run: this lane's partial denominator;
+// acc[db][i]: O^T[d = db*16 + (l/16)*4 + i][h = l%16].
+// All threads of the workgroup must call this (it contains barriers).
+template <int D, int NW>
+__device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], float* smem,
+                                const SplitKOut& o, int unit, int split, int b, int hq0, int nh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
+  constexpr int NT = NW * 64;
+  l_run += shfl_xor_f(l_run, 16);
+  l_run += shfl_xor_f(l_run, 32);
+  float* wm = smem;
+  float* wl = wm + NW * 16;
+  float* wacc = wl + NW * 16;
+  __syncthreads();
+  if (lg == 0) {
+    wm[w * 16 + l16] = m_run;
+    wl[w * 16 + l16] = l_run;
+  }
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wacc[(w * D + db * 16 + lg * 4 + i) * 16 + l16] = acc[db][i];
+  __syncthreads();
+
+  const bool direct = o.nsplit <= 1;
+  for (int e = threadIdx.x; e < nh * D; e += NT) {
+    const int h = e / D, d = e - h * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, wm[ww * 16 + h]);
+    const float Ms = (M == kNegInf) ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = exp2f(wm[ww * 16 + h] - Ms);
+      L += f * wl[ww * 16 + h];
+      A += f * wacc[(ww * D + d) * 16 + h];
+    }
+    if (direct) {
+      store_out(o, b, hq0 + h, d, A / L);
+    } else {
+      const size_t slot = ((size_t)unit * o.nsplit + split) * 16 + h;
+      o.part_acc[slot * D + d] = A;
+      if (d == 0) {
+        o.part_ml[slot * 2 + 0] = M;
+        o.part_ml[slot * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Launch the partial merge (no-op when nsplit <= 1).  units = B*Hk*HB.
+int splitk_combine(const SplitKOut& o, long units, int D, hipStream_t stream);
+
+}  // namespace bytes_amd

@@ -1,0 +1,53 @@
+"""Seeded synthetic inputs for the BASELINE.json decode-attention configs.
+
+All tensors are drawn on the CPU from a torch.Generator seeded per config
+(default seed 0), then moved to `device`.  Shapes and distributions follow
+BASELINE.json `configs`; choices the config leaves open are fixed here and
+recorded in the returned dict under "meta".
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict
+
+import torch
+
+# name -> (B, Hq, Hk, D, L)
+SHAPES = {
+    "c1_dense": (1, 14, 2, 64, 8192),
+    "dense_16k": (4, 28, 4, 128, 16384),     # the L>=16K dense bandwidth point
+    "c2_kivi": (4, 28, 4, 128, 16384),
+    "c3_pq": (1, 28, 4, 128, 32768),
+    "c4_quest": (1, 28, 4, 128, 32768),
+    "c5_topk": (8, 24, 8, 128, 131072),
+}
+
+
+def _gen(seed: int) -> torch.Generator:
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    return g
+
+
+def randn_bf16(shape, g: torch.Generator) -> torch.Tensor:
+    return torch.randn(*shape, generator=g, dtype=torch.float32).to(torch.bfloat16)
+
+
+def dense(B: int, Hq: int, Hk: int, D: int, L: int, seed: int = 0, device="cpu") -> Dict:
+    """q, K, V i.i.d. N(0,1) as bf16 (BASELINE C1 and the dense L>=16K point)."""
+    g = _gen(seed)
+    q = randn_bf16((B, Hq, 1, D), g)
+    k = randn_bf16((B, Hk, L, D), g)
+    v = randn_bf16((B, Hk, L, D), g)
+    return {"q": q.to(device), "k": k.to(device), "v": v.to(device),
+            "scale": 1.0 / math.sqrt(D),
+            "meta": {"seed": seed, "shape": (B, Hq, Hk, D, L)}}
+
+
+def c1_dense(seed: int = 0, device="cpu") -> Dict:
+    return dense(*SHAPES["c1_dense"], seed=seed, device=device)
+
+
+def dense_16k(seed: int = 0, device="cpu", L: int = 16384) -> Dict:
+    B, Hq, Hk, D, _ = SHAPES["dense_16k"]
+    return dense(B, Hq, Hk, D, L, seed=seed, device=device)

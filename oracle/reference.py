@@ -1,0 +1,580 @@
+"""CPU restatement of the saifmb0/bytes decode-attention hot path (the oracle).
+
+TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py as the checker; never by the product path.
+
+Every function cites the reference file:line it restates (paths relative to
+the saifmb0/bytes checkout).  All arithmetic is plain torch on the CPU in
+fp32 unless a function says otherwise; integer/bit work is exact.
+
+Pinning (how each function is checked independently of its own formula) is
+listed in each docstring as "Pinned by:"; the tests in tests/test_oracle*.py
+carry those checks.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+NEG_INF = float("-inf")
+
+
+# ---------------------------------------------------------------------------
+# GQA helpers
+# ---------------------------------------------------------------------------
+def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """[B,Hk,S,D] -> [B,Hk*n_rep,S,D]; query head h reads KV head h // n_rep.
+
+    Restates benchmarks/sparse_attention.py:85-90 (same as
+    benchmarks/kivi_latency.py:20-24).
+    Pinned by: test_repeat_kv_matches_index_rule (h -> h // G by brute force).
+    """
+    if n_rep == 1:
+        return x
+    B, H, S, D = x.shape
+    return x[:, :, None, :, :].expand(B, H, n_rep, S, D).reshape(B, H * n_rep, S, D)
+
+
+def _softmax_attend(scores: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """fp32 softmax over the last dim of scores, then weights @ v (fp32)."""
+    p = torch.softmax(scores.float(), dim=-1)
+    return torch.matmul(p, v.float())
+
+
+# ---------------------------------------------------------------------------
+# a1: dense decode attention
+# ---------------------------------------------------------------------------
+def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                scale: float = 1.0, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Single-query GQA attention: softmax(scale * q.K^T) V per (b, h_q).
+
+    Restates src/attention_kernels.py:8-92 (`_decode_attn_bf16_kernel`,
+    `decode_attn_bf16`): fp32 scores and online softmax, fp32 accumulation,
+    output cast to q's dtype (:77).  The reference applies no softmax scale
+    (:42); ``scale`` (default 1.0) multiplies the fp32 scores.  The fp8 form
+    (:97-182) is the same with K/V upcast from float8_e4m3fn.
+    Loop reference: benchmarks/test_correctness.py:64-75.
+
+    q [B,Hq,1,D]; k, v [B,Hk,S,D] -> [B,Hq,1,D].
+    Pinned by: per-head brute-force loop, uniform-V invariant, G=1 == MHA,
+    softmax rows summing to one (tests/test_oracle.py).
+    """
+    B, Hq, _, D = q.shape
+    Hk = k.shape[1]
+    G = Hq // Hk
+    qf = q.float().reshape(B, Hk, G, D)
+    s = torch.matmul(qf, k.float().transpose(-1, -2)) * scale       # [B,Hk,G,S]
+    o = _softmax_attend(s, v)                                         # [B,Hk,G,D]
+    od = out_dtype if out_dtype is not None else q.dtype
+    return o.reshape(B, Hq, 1, D).to(od)
+
+
+# ---------------------------------------------------------------------------
+# a2/a3: KIVI pack / unpack / dequant (int32 words, codes along the last dim)
+# ---------------------------------------------------------------------------
+def kivi_unpack_last_dim(code: torch.Tensor, bits: int) -> torch.Tensor:
+    """int32 words -> integer codes along the last dim (int64 result).
+
+    Restates benchmarks/kivi_latency.py:26-35 (`unpack_tensor_last_dim`):
+    logical position w*(32/bits)+i is held in word w at bits [i*bits,(i+1)*bits).
+    (The reference returns the codes as fp16; the values are identical.)
+    Pinned by: exhaustive round trip with kivi_pack_last_dim over every code
+    value in every slot, and a hand-built word (tests/test_oracle.py).
+    """
+    fpi = 32 // bits
+    mask = (1 << bits) - 1
+    c = code.to(torch.int64) & 0xFFFFFFFF
+    shifts = torch.arange(fpi, dtype=torch.int64) * bits
+    vals = (c.unsqueeze(-1) >> shifts) & mask                         # [..., W, fpi]
+    return vals.reshape(*code.shape[:-1], code.shape[-1] * fpi)
+
+
+def kivi_pack_last_dim(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """Integer codes [..., N] -> int32 words [..., N*bits/32]; inverse of
+    kivi_unpack_last_dim (the bit layout read by kivi_latency.py:26-35)."""
+    fpi = 32 // bits
+    N = codes.shape[-1]
+    assert N % fpi == 0
+    c = codes.to(torch.int64).reshape(*codes.shape[:-1], N // fpi, fpi)
+    shifts = torch.arange(fpi, dtype=torch.int64) * bits
+    w = (c << shifts).sum(-1)                                         # < 2^32, exact
+    w = torch.where(w >= 2 ** 31, w - 2 ** 32, w)
+    return w.to(torch.int32)
+
+
+def asym_quant_codes(x: torch.Tensor, levels: int, dim: int):
+    """Asymmetric min/max uniform quantization: returns (codes, scale, xmin) in fp32.
+
+    Restates src/quantization.py:432-442 (`_asym_uniform_fakequant`) without
+    the final dequant: scale = max(max-min, 1e-8)/(levels-1),
+    code = clamp(round_half_even((x-min)/scale), 0, levels-1).
+    Pinned by: codes reproduce the fake-quant values of the closed form,
+    endpoints map to 0 and levels-1, constant groups give code 0.
+    """
+    xf = x.float()
+    xmin = xf.amin(dim=dim, keepdim=True)
+    xmax = xf.amax(dim=dim, keepdim=True)
+    scale = (xmax - xmin).clamp(min=1e-8) / (levels - 1)
+    q = torch.clamp(torch.round((xf - xmin) / scale), 0, levels - 1)
+    return q.to(torch.int64), scale, xmin
+
+
+def kivi_quantize_and_pack_last_dim(x: torch.Tensor, group_size: int, bits: int):
+    """Group-wise asym quantize along the last dim and pack (KIVI layout).
+
+    Restates the call contract of KIVI's `triton_quantize_and_pack_along_last_dim`
+    (called at benchmarks/kivi_latency.py:123,127): groups of `group_size`
+    consecutive elements of the last dim share fp16 (scale, mn); codes are
+    packed 32/bits per int32 in the layout of kivi_latency.py:26-35.  The
+    arithmetic is src/quantization.py:432-442 in fp32; scale and mn are
+    rounded to fp16 after the codes are chosen.  KIVI's own kernel is not in
+    the reference checkout, so its exact rounding is parity unpinned; this
+    function is the build's definition (bit-exact target for the GPU pack).
+
+    x [..., T] (T % group_size == 0, group_size % (32/bits) == 0)
+    -> (code int32 [..., T*bits/32], scale fp16 [..., T/group_size], mn fp16 same)
+    """
+    T = x.shape[-1]
+    assert T % group_size == 0
+    xg = x.reshape(*x.shape[:-1], T // group_size, group_size)
+    codes, scale, xmin = asym_quant_codes(xg, 2 ** bits, dim=-1)
+    code = kivi_pack_last_dim(codes.reshape(*x.shape[:-1], T), bits)
+    return code, scale.squeeze(-1).to(torch.float16), xmin.squeeze(-1).to(torch.float16)
+
+
+def kivi_dequant_k(Kq, K_scale, K_mn, group_size: int, bits: int, fp16_math: bool = False):
+    """Packed per-channel keys [B,H,D,Sq*bits/32] -> dequantized [B,H,Sq,D].
+
+    Restates benchmarks/kivi_latency.py:37-46 (`dequant_k`).  With
+    fp16_math=True the arithmetic is the reference's fp16 (c*scale rounded,
+    then +mn rounded); otherwise c*scale+mn in fp32 (the build's kernels).
+    """
+    B, H, D, _ = Kq.shape
+    c = kivi_unpack_last_dim(Kq, bits)                                # [B,H,D,Sq]
+    Sq = c.shape[-1]
+    ng = Sq // group_size
+    c = c.reshape(B, H, D, ng, group_size)
+    if fp16_math:
+        kd = c.to(torch.float16) * K_scale.unsqueeze(-1) + K_mn.unsqueeze(-1)
+    else:
+        kd = c.float() * K_scale.float().unsqueeze(-1) + K_mn.float().unsqueeze(-1)
+    return kd.reshape(B, H, D, Sq).transpose(2, 3).contiguous()
+
+
+def kivi_dequant_v(Vq, V_scale, V_mn, group_size: int, bits: int, fp16_math: bool = False):
+    """Packed per-token values [B,H,Sq,D*bits/32] -> dequantized [B,H,Sq,D].
+
+    Restates benchmarks/kivi_latency.py:48-57 (`dequant_v`); fp16_math as in
+    kivi_dequant_k.
+    """
+    B, H, Sq, _ = Vq.shape
+    c = kivi_unpack_last_dim(Vq, bits)                                # [B,H,Sq,D]
+    D = c.shape[-1]
+    ng = D // group_size
+    c = c.reshape(B, H, Sq, ng, group_size)
+    if fp16_math:
+        vd = c.to(torch.float16) * V_scale.unsqueeze(-1) + V_mn.unsqueeze(-1)
+    else:
+        vd = c.float() * V_scale.float().unsqueeze(-1) + V_mn.float().unsqueeze(-1)
+    return vd.reshape(B, H, Sq, D)
+
+
+def kivi_decode_attn(Q, Kq, K_scale, K_mn, K_residual, Vq, V_scale, V_mn, V_residual,
+                     bits: int, group_size: int = 32, scale: Optional[float] = None):
+    """softmax([Q.K_dq^T, Q.K_res^T] * scale) . [V_dq; V_res] per query head.
+
+    Restates the semantics of benchmarks/kivi_latency.py:59-100
+    (`kivi_decode_attn` == `kivi_decode_attn_ref` over `dequant_k`/`dequant_v`);
+    scale defaults to 1/sqrt(D) (:76).  The dequantized cache is c*scale+mn in
+    fp32, the softmax and accumulation are fp32 (the reference rounds
+    intermediate scores/weights to Q's dtype); output is Q's dtype.
+    Pinned by: equals decode_attn() on the explicitly dequantized and
+    concatenated cache; with bits-only codes at scale 1 / mn 0 it reduces to
+    attention on integer keys (tests/test_oracle.py).
+    """
+    D = Q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    Kd = kivi_dequant_k(Kq, K_scale, K_mn, group_size, bits)
+    Vd = kivi_dequant_v(Vq, V_scale, V_mn, group_size, bits)
+    K = torch.cat([Kd, K_residual.float()], dim=2)
+    V = torch.cat([Vd, V_residual.float()], dim=2)
+    return decode_attn(Q, K, V, scale=scale, out_dtype=Q.dtype)
+
+
+# ---------------------------------------------------------------------------
+# a5/a6: product quantization
+# ---------------------------------------------------------------------------
+def _per_head_codebook(cb: torch.Tensor, Hk: int) -> torch.Tensor:
+    """Shared [M,K,dsub] (reference layout, src/quantization.py:145) or per-head
+    [Hk,M,K,dsub] codebooks -> [Hk,M,K,dsub]."""
+    if cb.dim() == 3:
+        return cb.unsqueeze(0).expand(Hk, *cb.shape)
+    assert cb.dim() == 4 and cb.shape[0] == Hk
+    return cb
+
+
+def pq_encode(x: torch.Tensor, centroids: torch.Tensor) -> torch.Tensor:
+    """Nearest-codeword indices: argmin_c sum_e (x_e - c_e)^2, first index on ties.
+
+    Restates src/quantization.py:203-211 (CPU path of ProductQuantizer.quantize:
+    cdist + argmin).  The squared distance is accumulated in fp32 in element
+    order e = 0..dsub-1 with separate multiply and add (no fused multiply-add),
+    the order the GPU encode kernel uses, so indices are bit-exact.
+    x [..., M*dsub]; centroids [M,K,dsub] -> uint8/int64 [..., M].
+    Pinned by: brute force against torch.cdist argmin on tie-free inputs;
+    exact codewords encode to their own index (tests/test_oracle.py).
+    """
+    M, K, dsub = centroids.shape
+    xs = x.float().reshape(-1, M, dsub)
+    c = centroids.float()
+    dist = torch.zeros(xs.shape[0], M, K)
+    for e in range(dsub):
+        d = xs[:, :, e].unsqueeze(-1) - c[:, :, e].unsqueeze(0)      # [N,M,K]
+        dist = dist + d * d
+    idx = torch.argmin(dist, dim=-1)                                   # first min
+    return idx.reshape(*x.shape[:-1], M)
+
+
+def pq_decode(idx: torch.Tensor, centroids: torch.Tensor) -> torch.Tensor:
+    """Codes [..., M] -> vectors [..., M*dsub] (src/quantization.py:213-226)."""
+    M, K, dsub = centroids.shape
+    flat = idx.reshape(-1, M).long()
+    out = torch.stack([centroids[j][flat[:, j]] for j in range(M)], dim=1)
+    return out.reshape(*idx.shape[:-1], M * dsub)
+
+
+def kmeans(X: torch.Tensor, k: int, num_iters: int, generator: torch.Generator) -> torch.Tensor:
+    """Codebook fitting (setup only, not on the timed path).
+
+    Restates src/quantization.py:102-132 (`kmeans_pytorch`): random-point
+    init, assign by nearest centroid, mean update, empty clusters re-seeded
+    from a random point.  Values depend on the RNG stream, so codebooks are
+    treated as inputs: parity is measured given identical codebooks.
+    """
+    N, d = X.shape
+    X = X.float()
+    if N <= k:
+        return torch.cat([X.clone(), torch.zeros(k - N, d)], 0)
+    perm = torch.randperm(N, generator=generator)
+    cent = X[perm[:k]].clone()
+    for _ in range(num_iters):
+        dists = torch.cdist(X, cent)
+        labels = torch.argmin(dists, dim=1)
+        sums = torch.zeros(k, d).index_add_(0, labels, X)
+        counts = torch.bincount(labels, minlength=k).float()
+        empty = counts == 0
+        cent = torch.where(empty[:, None], cent, sums / counts.clamp(min=1)[:, None])
+        if empty.any():
+            ridx = torch.randint(0, N, (int(empty.sum()),), generator=generator)
+            cent[empty] = X[ridx]
+    return cent
+
+
+def pq_build_lut(q: torch.Tensor, centroids: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """LUT[b,h,j,c] = scale * sum_e q[b,h,j*dsub+e] * cb[h//G, j, c, e]  (fp32).
+
+    Restates the LUT precompute of benchmarks/test_correctness.py:181-182 and
+    :272-273 (`einsum("bhmd,mkd->bhmk")`), with optional per-KV-head codebooks
+    [Hk,M,K,dsub] (BASELINE C3) and the softmax scale folded in.
+    q [B,Hq,1,D] or [B,Hq,D] -> [B,Hq,M,K].
+    """
+    if q.dim() == 4:
+        q = q.squeeze(2)
+    B, Hq, D = q.shape
+    if centroids.dim() == 3:
+        M, K, dsub = centroids.shape
+        qs = q.float().reshape(B, Hq, M, dsub)
+        lut = torch.einsum("bhmd,mkd->bhmk", qs, centroids.float())
+    else:
+        Hk, M, K, dsub = centroids.shape
+        G = Hq // Hk
+        qs = q.float().reshape(B, Hk, G, M, dsub)
+        lut = torch.einsum("bhgmd,hmkd->bhgmk", qs, centroids.float()).reshape(B, Hq, M, K)
+    return lut * scale
+
+
+def pq_lut_scores(lut: torch.Tensor, k_idx: torch.Tensor) -> torch.Tensor:
+    """scores[b,h,t] = sum_j lut[b,h,j,k_idx[b,h//G,t,j]] (fp32, j ascending).
+
+    Restates the score loop of src/attention_kernels.py:330-341 / :425-435.
+    Pinned by: per-token Python loop (benchmarks/test_correctness.py:282-291
+    form) at small shapes.
+    """
+    B, Hq, M, K = lut.shape
+    Hk = k_idx.shape[1]
+    G = Hq // Hk
+    idx = repeat_kv(k_idx.long(), G)                                   # [B,Hq,S,M]
+    s = torch.zeros(B, Hq, idx.shape[2])
+    for j in range(M):
+        s = s + torch.gather(lut[:, :, j, :].float(), 2, idx[..., j])
+    return s
+
+
+def decode_attn_pq_lut_kv(lut, k_idx, v_idx, v_centroids, d_sub_v: int = 8):
+    """LUT-scored keys + codebook-reconstructed values.
+
+    Restates src/attention_kernels.py:397-500 (`decode_attn_pq_lut_kv`): no
+    scale inside (fold it into the LUT); output dtype = v_centroids.dtype (:484).
+    v_centroids [M_v,K_v,dsub] (reference) or [Hk,M_v,K_v,dsub] (per head).
+    """
+    B, Hq, M, K = lut.shape
+    Hk = k_idx.shape[1]
+    G = Hq // Hk
+    s = pq_lut_scores(lut, k_idx)                                      # [B,Hq,S]
+    cb = _per_head_codebook(v_centroids, Hk).float()                   # [Hk,Mv,Kv,dsub]
+    Mv = cb.shape[1]
+    vh = torch.stack([cb[h][torch.arange(Mv)[None, :], v_idx[:, h].long()]
+                      for h in range(Hk)], dim=1)                      # [B,Hk,S,Mv,dsub]
+    vh = vh.reshape(B, Hk, v_idx.shape[2], -1)
+    o = _softmax_attend(s.reshape(B, Hk, G, -1), vh)                  # [B,Hk,G,D]
+    return o.reshape(B, Hq, 1, -1).to(v_centroids.dtype)
+
+
+def decode_attn_pq_lut(lut, k_idx, v):
+    """LUT-scored keys, dense V.  Restates src/attention_kernels.py:301-392;
+    output dtype = v.dtype (:375)."""
+    B, Hq, M, K = lut.shape
+    Hk = k_idx.shape[1]
+    G = Hq // Hk
+    s = pq_lut_scores(lut, k_idx)
+    o = _softmax_attend(s.reshape(B, Hk, G, -1), v)
+    return o.reshape(B, Hq, 1, -1).to(v.dtype)
+
+
+def decode_attn_dequant(q, k_idx, centroids, v, d_sub: int = 8):
+    """Codebook-reconstructed keys, dense V, no scale.
+
+    Restates src/attention_kernels.py:187-296 (`decode_attn_dequant`); output
+    dtype = q.dtype (:278).  Loop reference benchmarks/test_correctness.py:142-150.
+    """
+    Hk = k_idx.shape[1]
+    cb = _per_head_codebook(centroids, Hk).float()
+    kh = torch.stack([pq_decode(k_idx[:, h], cb[h]) for h in range(Hk)], dim=1)
+    return decode_attn(q, kh, v, scale=1.0, out_dtype=q.dtype)
+
+
+# ---------------------------------------------------------------------------
+# a10: deterministic top-k (total order: score desc, index asc)
+# ---------------------------------------------------------------------------
+def canonical_scores(s: torch.Tensor) -> torch.Tensor:
+    """Canonicalise fp32 scores for ranking: -0 -> +0, every NaN -> +NaN.
+
+    The build's total order ranks NaN above +inf (as torch.topk does) and
+    treats +0/-0 as equal so the lowest index wins their tie."""
+    s = s.float()
+    s = torch.where(s == 0, torch.zeros_like(s), s)
+    return s
+
+
+def order_key(s: torch.Tensor) -> torch.Tensor:
+    """Monotone int64 key of canonical fp32 scores (larger score -> larger key;
+    NaN -> largest).  Used to make ranking a pure integer sort."""
+    s = canonical_scores(s)
+    nan = torch.isnan(s)
+    bits = s.view(torch.int32).to(torch.int64)
+    key = torch.where(bits < 0, -(bits & 0x7FFFFFFF) - 1, bits)        # order-preserving
+    return torch.where(nan, torch.full_like(key, 2 ** 40), key)
+
+
+def topk_indices(scores: torch.Tensor, k: int, sorted_by_score: bool = True) -> torch.Tensor:
+    """Indices of the k largest entries per row under the total order
+    (score descending, index ascending on ties).
+
+    Replaces `scores.topk(kb, dim=-1).indices` (src/attention_kernels.py:1262,
+    benchmarks/sparse_attention.py:307,358) whose tie order is unspecified;
+    the lowest-index tie rule is the BASELINE contract.  With
+    sorted_by_score=True the result is ordered like torch.topk(sorted=True);
+    otherwise by ascending index.  Returns int64 [..., k].
+    Pinned by: brute force with Python's sorted() on tiny rows, equality with
+    torch.topk on tie-free rows, chunked streaming merge == global selection.
+    """
+    key = order_key(scores)
+    n = key.shape[-1]
+    idx = torch.arange(n, dtype=torch.int64).expand_as(key)
+    # composite key: primary -key (desc), secondary index (asc).  Stable sort on
+    # -key keeps ascending index among equal keys.
+    order = torch.sort(-key, dim=-1, stable=True).indices
+    sel = order[..., :k]
+    if not sorted_by_score:
+        sel = torch.sort(sel, dim=-1).values
+    del idx
+    return sel
+
+
+def streaming_topk(scores: torch.Tensor, k: int, chunk: int) -> torch.Tensor:
+    """Chunked streaming top-k with running candidate merge, as in
+    benchmarks/sparse_attention.py:287-309 (`select_topk`, sentinel idx = S for
+    unfilled slots, :292-293), under the build's total order.  Returns indices
+    ordered like topk_indices(sorted_by_score=True)."""
+    S = scores.shape[-1]
+    lead = scores.shape[:-1]
+    run_s = torch.full((*lead, k), NEG_INF)
+    run_i = torch.full((*lead, k), S, dtype=torch.int64)
+    for c0 in range(0, S, chunk):
+        c1 = min(c0 + chunk, S)
+        cs = torch.cat([run_s, scores[..., c0:c1].float()], -1)
+        ci = torch.cat([run_i, torch.arange(c0, c1).expand(*lead, c1 - c0)], -1)
+        # rank candidates by (score desc, index asc); sentinels (index S) lose ties
+        key = order_key(cs)
+        o = torch.sort(ci, dim=-1, stable=True).indices                 # index asc
+        o2 = torch.sort(-torch.gather(key, -1, o), dim=-1, stable=True).indices
+        perm = torch.gather(o, -1, o2)[..., :k]
+        run_s = torch.gather(cs, -1, perm)
+        run_i = torch.gather(ci, -1, perm)
+    return run_i
+
+
+# ---------------------------------------------------------------------------
+# a8/a9: scoring and gather attention
+# ---------------------------------------------------------------------------
+def sparse_score_scalar(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tensor:
+    """fp32 scores[b,h,t] = (q[b,h] . k[b,h//G,t]) * scaling.
+
+    Restates src/attention_kernels.py:1077-1133 (`sparse_score_scalar`; bf16
+    or float8_e4m3fn keys upcast to fp32).  Loop reference
+    benchmarks/test_correctness.py:694-700.
+    """
+    B, Hq, _, D = q.shape
+    Hk = k.shape[1]
+    G = Hq // Hk
+    qf = q.float().reshape(B, Hk, G, D)
+    s = torch.matmul(qf, k.float().transpose(-1, -2)) * scaling
+    return s.reshape(B, Hq, -1)
+
+
+def group_scores(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tensor:
+    """Per-KV-head scores summed over the query group:
+    s[b,h,t] = sum_{g<G} score(q[b,h*G+g], k[b,h,t]) (g ascending, fp32).
+
+    BASELINE C5's group-summed selection score, built on the per-head score of
+    src/attention_kernels.py:1077-1110 and the chunked scoring of
+    benchmarks/sparse_attention.py:208-223.
+    """
+    B, Hq, _, D = q.shape
+    Hk = k.shape[1]
+    G = Hq // Hk
+    s = sparse_score_scalar(q, k, scaling).reshape(B, Hk, G, -1)
+    acc = s[:, :, 0]
+    for g in range(1, G):
+        acc = acc + s[:, :, g]
+    return acc
+
+
+def sparse_gather_attn(q, k, v, idx, scaling: float):
+    """Exact fp32 attention over the gathered rows idx (per query head).
+
+    Restates src/attention_kernels.py:987-1059 (`sparse_gather_attn`) and the
+    torch semantics of benchmarks/sparse_attention.py:367-387 (`attend_topk`):
+    index entries outside [0, S) are masked (sentinel rule, :376).  idx is
+    [B,Hq,kb] or per-KV-head [B,Hk,kb] (shared by the query group).  Output
+    dtype bf16 if v is float8_e4m3fn else v.dtype (:1044).
+    """
+    B, Hq, _, D = q.shape
+    Hk, S = k.shape[1], k.shape[2]
+    G = Hq // Hk
+    if idx.shape[1] == Hk and Hk != Hq:
+        idx = idx.repeat_interleave(G, dim=1)
+    idx = idx.long()
+    valid = (idx >= 0) & (idx < S)
+    gi = idx.clamp(0, S - 1)
+    kr = repeat_kv(k.float(), G)
+    vr = repeat_kv(v.float(), G)
+    kb = idx.shape[-1]
+    ks = torch.gather(kr, 2, gi.unsqueeze(-1).expand(B, Hq, kb, D))
+    vs = torch.gather(vr, 2, gi.unsqueeze(-1).expand(B, Hq, kb, D))
+    sc = (q.float().reshape(B, Hq, 1, D) * ks).sum(-1) * scaling        # [B,Hq,kb]
+    sc = torch.where(valid, sc, torch.full_like(sc, NEG_INF))
+    p = torch.softmax(sc, dim=-1)
+    o = (p.unsqueeze(-1) * vs).sum(2)
+    od = torch.bfloat16 if v.dtype == torch.float8_e4m3fn else v.dtype
+    return o.reshape(B, Hq, 1, D).to(od)
+
+
+def budget(frac: float, S: int) -> int:
+    """kb = max(1, round(frac*S)) with Python's round (src/attention_kernels.py:1261)."""
+    return max(1, int(round(frac * S)))
+
+
+def sparse_decode_scalar(q, k_score, k_val, v_val, frac: float, scaling: float):
+    """Two-pass sparse decode, per query head: score -> top-kb -> gather attend.
+
+    Restates src/attention_kernels.py:1252-1263 for score_bits 16/8 with the
+    build's deterministic top-k (ties to the lowest index)."""
+    s = sparse_score_scalar(q, k_score, scaling)
+    kb = budget(frac, s.shape[-1])
+    idx = topk_indices(s, kb)
+    return sparse_gather_attn(q, k_val, v_val, idx, scaling)
+
+
+def token_topk_decode(q, k, v, kb: int, scaling: float):
+    """BASELINE C5 pipeline: group-summed fp32 scores per KV head, top-kb per
+    (b, kv head), gathered attention for every query head of the group.
+    Returns (out [B,Hq,1,D], idx [B,Hk,kb] ordered by score desc, index asc)."""
+    s = group_scores(q, k, scaling)
+    idx = topk_indices(s, kb)
+    return sparse_gather_attn(q, k, v, idx, scaling), idx
+
+
+# ---------------------------------------------------------------------------
+# a7: Quest page selection
+# ---------------------------------------------------------------------------
+def quest_page_minmax(k: torch.Tensor, page: int):
+    """Per-page elementwise min/max of the keys; the last partial page is padded
+    with the last key.  Restates benchmarks/sparse_attention.py:336-344
+    (`_quest_select`) / benchmarks/eval_ppl.py:56-63 (`_quest_mask`).
+    k [B,H,S,D] -> (kmin, kmax) [B,H,ceil(S/page),D] in k's dtype (exact)."""
+    B, H, S, D = k.shape
+    np_ = (S + page - 1) // page
+    pad = np_ * page - S
+    kp = k
+    if pad:
+        kp = torch.cat([k, k[:, :, -1:, :].expand(B, H, pad, D)], dim=2)
+    kp = kp.reshape(B, H, np_, page, D)
+    return kp.amin(dim=3), kp.amax(dim=3)
+
+
+def quest_page_scores(q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor,
+                      scale: float = 1.0) -> torch.Tensor:
+    """bound[b,h,p] = scale * sum_d max(q_d*kmin_d, q_d*kmax_d)  (fp32).
+
+    Restates benchmarks/sparse_attention.py:342-345 (fp32 via `_scast`).  The
+    products are exact in fp32 (bf16 x bf16); the sum over d is accumulated
+    in ascending d so the GPU kernel can match it bit for bit.  At decode
+    (query at position S-1) every page is causally valid (:347-349).
+    q [B,Hq,1,D]; kmin/kmax [B,Hk,np,D] -> [B,Hq,np].
+    Pinned by: the bound is >= max_t q.k_t over each page (Quest upper bound)
+    and equals it for single-token pages (tests/test_oracle.py).
+    """
+    B, Hq, _, D = q.shape
+    Hk = kmin.shape[1]
+    G = Hq // Hk
+    qf = q.float().reshape(B, Hk, G, 1, D)
+    a = qf * kmin.float().unsqueeze(2)
+    b = qf * kmax.float().unsqueeze(2)
+    m = torch.maximum(a, b)                                             # [B,Hk,G,np,D]
+    acc = m[..., 0]
+    for d in range(1, D):
+        acc = acc + m[..., d]
+    out = acc.reshape(B, Hq, -1)
+    return out * scale if scale != 1.0 else out
+
+
+def quest_select(q, k, budget_tokens: int, page: int = 16, scale: float = 1.0):
+    """Quest decode selection: page bounds -> top ceil(kb/page) pages (score
+    desc, index asc) -> token ids clamped to S-1.
+
+    Restates benchmarks/sparse_attention.py:328-364 (`_quest_select`) for one
+    decode query.  Returns (page_ids [B,Hq,npick] int64, token_ids
+    [B,Hq,npick*page] int64, bounds [B,Hq,np] fp32).
+    """
+    S = k.shape[2]
+    kmin, kmax = quest_page_minmax(k, page)
+    bound = quest_page_scores(q, kmin, kmax, scale)
+    np_ = bound.shape[-1]
+    npick = min(max(1, (budget_tokens + page - 1) // page), np_)
+    pidx = topk_indices(bound, npick)
+    tok = (pidx.unsqueeze(-1) * page + torch.arange(page)).reshape(*pidx.shape[:-1], -1)
+    return pidx, tok.clamp(max=S - 1), bound

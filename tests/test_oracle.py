@@ -1,0 +1,289 @@
+"""Pins the CPU oracle against brute force, closed forms and invariants.
+
+Each check is chosen so that a plausible slip in the oracle (dropped term,
+wrong index or sign, transposed operand, wrong tie rule) fails it.  CPU only.
+"""
+import itertools
+import math
+
+import pytest
+import torch
+
+from oracle import reference as R
+
+
+def _bf16(*shape, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------- GQA / dense
+def test_repeat_kv_matches_index_rule():
+    x = torch.arange(2 * 3 * 4 * 5, dtype=torch.float32).reshape(2, 3, 4, 5)
+    y = R.repeat_kv(x, 4)
+    assert y.shape == (2, 12, 4, 5)
+    for h in range(12):
+        assert torch.equal(y[:, h], x[:, h // 4])
+
+
+def _attn_bruteforce(q, k, v, scale):
+    """float64 per-(b, h_q) loop with explicit exp/sum (test_correctness.py:64-75 form)."""
+    B, Hq, _, D = q.shape
+    Hk, S = k.shape[1], k.shape[2]
+    G = Hq // Hk
+    out = torch.zeros(B, Hq, 1, D, dtype=torch.float64)
+    for b in range(B):
+        for h in range(Hq):
+            qq = q[b, h, 0].double()
+            kk = k[b, h // G].double()
+            vv = v[b, h // G].double()
+            s = [float((qq * kk[t]).sum()) * scale for t in range(S)]
+            m = max(s)
+            e = [math.exp(x - m) for x in s]
+            z = sum(e)
+            out[b, h, 0] = sum(e[t] / z * vv[t] for t in range(S))
+    return out
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D", [(2, 8, 2, 37, 16), (1, 3, 3, 20, 8), (1, 6, 1, 9, 4)])
+def test_decode_attn_bruteforce(B, Hq, Hk, S, D):
+    q, k, v = _bf16(B, Hq, 1, D, seed=1), _bf16(B, Hk, S, D, seed=2), _bf16(B, Hk, S, D, seed=3)
+    ref = _attn_bruteforce(q, k, v, 0.37)
+    out = R.decode_attn(q, k, v, scale=0.37, out_dtype=torch.float32)
+    assert (out.double() - ref).abs().max() < 1e-5
+
+
+def test_decode_attn_invariants():
+    q, k = _bf16(1, 4, 1, 8, seed=4), _bf16(1, 2, 50, 8, seed=5)
+    row = _bf16(8, seed=6)
+    v = row.expand(1, 2, 50, 8).contiguous()
+    out = R.decode_attn(q, k, v, out_dtype=torch.float32)        # uniform V -> V row
+    assert torch.allclose(out[0, :, 0], row.float().expand(4, 8), atol=1e-6)
+    ones = torch.ones(1, 2, 50, 8)
+    assert torch.allclose(R.decode_attn(q, k, ones, out_dtype=torch.float32), torch.ones(1, 4, 1, 8), atol=1e-6)
+    # head h_q reads kv head h_q // G: swapping kv heads swaps query-head groups
+    v2 = _bf16(1, 2, 50, 8, seed=7)
+    a = R.decode_attn(q, k, v2, out_dtype=torch.float32)
+    b = R.decode_attn(q[:, [2, 3, 0, 1]], k.flip(1), v2.flip(1), out_dtype=torch.float32)
+    assert torch.allclose(a[:, [2, 3, 0, 1]], b, atol=1e-6)
+
+
+# ---------------------------------------------------------------- KIVI layout
+@pytest.mark.parametrize("bits", [2, 4])
+def test_kivi_pack_unpack_exhaustive(bits):
+    fpi = 32 // bits
+    vals = list(range(2 ** bits))
+    # every code value in every slot of a word
+    codes = torch.tensor([[c if i == s else 0 for i in range(fpi)]
+                          for s in range(fpi) for c in vals], dtype=torch.int64)
+    words = R.kivi_pack_last_dim(codes, bits)
+    assert words.dtype == torch.int32 and words.shape == (len(codes), 1)
+    for row, w in zip(codes.tolist(), words[:, 0].tolist()):
+        expect = sum(c << (i * bits) for i, c in enumerate(row))
+        assert (w & 0xFFFFFFFF) == expect
+    assert torch.equal(R.kivi_unpack_last_dim(words, bits), codes)
+
+
+def test_kivi_unpack_hand_word():
+    # bits=2: logical positions 0..15 of word 0 at bits 2i; 0xE4 = codes 0,1,2,3
+    w = torch.tensor([[0xE4, -1]], dtype=torch.int32)
+    c = R.kivi_unpack_last_dim(w, 2)
+    assert c[0, :4].tolist() == [0, 1, 2, 3] and c[0, 4:16].tolist() == [0] * 12
+    assert c[0, 16:].tolist() == [3] * 16
+    c4 = R.kivi_unpack_last_dim(torch.tensor([[0x76543210]], dtype=torch.int32), 4)
+    assert c4[0].tolist() == list(range(8))
+
+
+def test_asym_quant_closed_form():
+    x = torch.tensor([[-1.0, 0.0, 0.5, 2.0], [3.0, 3.0, 3.0, 3.0]])
+    codes, scale, xmin = R.asym_quant_codes(x, 4, dim=-1)
+    assert codes[0].tolist() == [0, 1, 2, 3]          # (x+1)/1: 0, 1, 1.5 -> 2, 3
+    # round half to even: (1.5+1)/1 = 2.5 -> 2 (not 3); (0.5+1)/1 = 1.5 -> 2
+    codes2, _, _ = R.asym_quant_codes(torch.tensor([[-1.0, 1.5, 0.5, 2.0]]), 4, dim=-1)
+    assert codes2[0].tolist() == [0, 2, 2, 3]
+    assert codes[1].tolist() == [0, 0, 0, 0]           # constant group
+    assert float(scale[1, 0]) == float(torch.tensor(1e-8) / 3)   # clamp(min=1e-8) in fp32
+    assert float(scale[0, 0]) == 1.0 and float(xmin[0, 0]) == -1.0
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_kivi_quantize_pack_roundtrip(bits):
+    x = _bf16(2, 3, 64, seed=8).to(torch.float16)
+    code, scale, mn = R.kivi_quantize_and_pack_last_dim(x, 32, bits)
+    assert code.shape == (2, 3, 64 * bits // 32) and scale.shape == (2, 3, 2) and mn.dtype == torch.float16
+    c = R.kivi_unpack_last_dim(code, bits)
+    # the codes are those of the fp32 fake-quant closed form
+    g = x.float().reshape(2, 3, 2, 32)
+    lo, hi = g.amin(-1, keepdim=True), g.amax(-1, keepdim=True)
+    s = (hi - lo).clamp(min=1e-8) / (2 ** bits - 1)
+    expect = torch.clamp(torch.round((g - lo) / s), 0, 2 ** bits - 1).reshape(2, 3, 64)
+    assert torch.equal(c, expect.long())
+    # min element -> code 0, max element -> top code, in every group
+    cg = c.reshape(2, 3, 2, 32)
+    assert torch.equal(torch.gather(cg, -1, g.argmin(-1, keepdim=True)), torch.zeros(2, 3, 2, 1, dtype=torch.long))
+    assert torch.equal(torch.gather(cg, -1, g.argmax(-1, keepdim=True)),
+                       torch.full((2, 3, 2, 1), 2 ** bits - 1, dtype=torch.long))
+
+
+def test_kivi_dequant_layouts():
+    bits, gs = 2, 32
+    B, H, D, Sq = 1, 2, 4, 64
+    codes = torch.randint(0, 4, (B, H, D, Sq), generator=torch.Generator().manual_seed(0))
+    Kq = R.kivi_pack_last_dim(codes, bits)
+    sc = torch.rand(B, H, D, Sq // gs, generator=torch.Generator().manual_seed(1)).half() + 0.5
+    mn = torch.rand(B, H, D, Sq // gs, generator=torch.Generator().manual_seed(2)).half() - 0.5
+    kd = R.kivi_dequant_k(Kq, sc, mn, gs, bits)
+    assert kd.shape == (B, H, Sq, D)
+    for d, t in itertools.product(range(D), [0, 31, 32, 63]):
+        e = codes[0, 1, d, t] * sc[0, 1, d, t // gs].float() + mn[0, 1, d, t // gs].float()
+        assert float(kd[0, 1, t, d]) == pytest.approx(float(e), abs=1e-6)
+    # values: per-token groups of 32 channels along the last dim
+    vc = torch.randint(0, 4, (B, H, 3, 64), generator=torch.Generator().manual_seed(3))
+    vs = torch.rand(B, H, 3, 2, generator=torch.Generator().manual_seed(4)).half() + 0.5
+    vm = torch.rand(B, H, 3, 2, generator=torch.Generator().manual_seed(5)).half() - 0.5
+    vd = R.kivi_dequant_v(R.kivi_pack_last_dim(vc, bits), vs, vm, gs, bits)
+    assert vd.shape == (B, H, 3, 64)
+    for t, d in itertools.product(range(3), [0, 31, 32, 63]):
+        e = vc[0, 1, t, d] * vs[0, 1, t, d // gs].float() + vm[0, 1, t, d // gs].float()
+        assert float(vd[0, 1, t, d]) == pytest.approx(float(e), abs=1e-6)
+
+
+def test_kivi_decode_matches_dense_on_dequantized_cache():
+    bits, gs, R_ = 4, 32, 16
+    B, Hq, Hk, D, Sq = 1, 4, 2, 64, 64
+    k, v, q = _bf16(B, Hk, Sq + R_, D, seed=9), _bf16(B, Hk, Sq + R_, D, seed=10), _bf16(B, Hq, 1, D, seed=11)
+    Kq, Ks, Km = R.kivi_quantize_and_pack_last_dim(k[:, :, :Sq].transpose(2, 3).half(), gs, bits)
+    Vq, Vs, Vm = R.kivi_quantize_and_pack_last_dim(v[:, :, :Sq].half(), gs, bits)
+    out = R.kivi_decode_attn(q, Kq, Ks, Km, k[:, :, Sq:], Vq, Vs, Vm, v[:, :, Sq:], bits, gs)
+    kd = torch.cat([R.kivi_dequant_k(Kq, Ks, Km, gs, bits), k[:, :, Sq:].float()], 2)
+    vd = torch.cat([R.kivi_dequant_v(Vq, Vs, Vm, gs, bits), v[:, :, Sq:].float()], 2)
+    ref = _attn_bruteforce(q, kd, vd, 1 / math.sqrt(D))
+    assert (out.double() - ref).abs().max() < 1e-2   # bf16 output rounding
+    # 4-bit dequant error is bounded by half a step of each group
+    err = (R.kivi_dequant_k(Kq, Ks, Km, gs, bits) - k[:, :, :Sq].float()).abs()
+    assert float(err.max()) <= float(Ks.float().max()) * 0.5 + 1e-2
+
+
+# ---------------------------------------------------------------- PQ
+def test_pq_encode_bruteforce():
+    g = torch.Generator().manual_seed(3)
+    cb = torch.randn(4, 16, 8, generator=g)
+    x = torch.randn(50, 32, generator=g)
+    idx = R.pq_encode(x, cb)
+    for j in range(4):
+        d = torch.cdist(x[:, j * 8:(j + 1) * 8].double(), cb[j].double())
+        assert torch.equal(idx[:, j], d.argmin(1))
+    exact = torch.stack([cb[j, 5] for j in range(4)]).reshape(1, 32)
+    assert R.pq_encode(exact, cb).tolist() == [[5, 5, 5, 5]]
+    dup = cb.clone()
+    dup[:, 9] = dup[:, 2]                                 # tie -> first index
+    assert R.pq_encode(torch.stack([dup[j, 2] for j in range(4)]).reshape(1, 32), dup).tolist() == [[2] * 4]
+
+
+def test_pq_lut_scores_loop_and_dequant_equivalence():
+    g = torch.Generator().manual_seed(4)
+    B, Hq, Hk, S, M, K, ds = 1, 4, 2, 12, 4, 8, 8
+    cb = torch.randn(M, K, ds, generator=g)
+    q = torch.randn(B, Hq, 1, M * ds, generator=g).to(torch.bfloat16)
+    k_idx = torch.randint(0, K, (B, Hk, S, M), generator=g)
+    v = torch.randn(B, Hk, S, M * ds, generator=g)
+    lut = R.pq_build_lut(q, cb)
+    sc = R.pq_lut_scores(lut, k_idx)
+    for h, t in itertools.product(range(Hq), range(S)):
+        e = sum(float(lut[0, h, j, k_idx[0, h // 2, t, j]]) for j in range(M))
+        assert float(sc[0, h, t]) == pytest.approx(e, abs=1e-5)
+    a = R.decode_attn_pq_lut(lut, k_idx, v)
+    b = R.decode_attn_dequant(q.float(), k_idx, cb, v)          # fp32 out (out dtype = q dtype)
+    assert (a - b).abs().max() < 1e-4                      # LUT path == dequant path
+    # per-head codebooks that are all equal == shared codebook
+    cbh = cb.unsqueeze(0).expand(Hk, M, K, ds).contiguous()
+    assert torch.allclose(R.pq_build_lut(q, cbh), lut)
+    vi = torch.randint(0, K, (B, Hk, S, M), generator=g)
+    o1 = R.decode_attn_pq_lut_kv(lut, k_idx, vi, cb)
+    o2 = R.decode_attn_pq_lut(lut, k_idx, torch.stack([R.pq_decode(vi[:, h], cb) for h in range(Hk)], 1))
+    assert (o1 - o2).abs().max() < 1e-5
+
+
+# ---------------------------------------------------------------- top-k
+def _topk_brute(row, k):
+    def key(i):
+        x = row[i]
+        if math.isnan(x):
+            return (0, 0.0, i)
+        return (1, -x if x != 0 else 0.0, i)
+    return sorted(range(len(row)), key=key)[:k]
+
+
+def test_topk_bruteforce_with_ties():
+    g = torch.Generator().manual_seed(5)
+    pool = torch.tensor([0.0, -0.0, 1.0, -1.0, 2.5, float("inf"), float("-inf"), float("nan")])
+    for trial in range(40):
+        n = int(torch.randint(1, 40, (1,), generator=g))
+        row = pool[torch.randint(0, len(pool), (n,), generator=g)]
+        for k in {1, n // 2 or 1, n}:
+            got = R.topk_indices(row, k).tolist()
+            assert got == _topk_brute(row.tolist(), k)
+
+
+def test_topk_matches_torch_without_ties():
+    x = torch.randperm(1000, generator=torch.Generator().manual_seed(6)).float().reshape(4, 250) * 0.37
+    for k in (1, 17, 250):
+        assert torch.equal(R.topk_indices(x, k), x.topk(k, dim=-1).indices)
+        assert torch.equal(R.topk_indices(x, k, sorted_by_score=False),
+                           torch.sort(x.topk(k, dim=-1).indices, -1).values)
+
+
+def test_streaming_topk_equals_global():
+    g = torch.Generator().manual_seed(7)
+    x = torch.randint(-5, 5, (3, 300), generator=g).float()      # heavy ties
+    for k, chunk in [(10, 64), (64, 64), (100, 17), (300, 1000)]:
+        assert torch.equal(R.streaming_topk(x, k, chunk), R.topk_indices(x, k))
+
+
+# ---------------------------------------------------------------- Quest
+def test_quest_bound_is_upper_bound():
+    B, Hq, Hk, S, D, page = 1, 4, 2, 50, 16, 16
+    q, k = _bf16(B, Hq, 1, D, seed=12), _bf16(B, Hk, S, D, seed=13)
+    kmin, kmax = R.quest_page_minmax(k, page)
+    assert kmin.shape == (B, Hk, 4, D)
+    bound = R.quest_page_scores(q, kmin, kmax)
+    s = R.sparse_score_scalar(q, k, 1.0)
+    for p in range(4):
+        hi = min(S, (p + 1) * page)
+        assert torch.all(bound[..., p] >= s[..., p * page:hi].amax(-1) - 1e-4)
+    # single-token pages: the bound is the exact score
+    k1min, k1max = R.quest_page_minmax(k, 1)
+    assert torch.allclose(R.quest_page_scores(q, k1min, k1max), s, atol=1e-4)
+    # last partial page is padded with the last key
+    assert torch.equal(kmin[:, :, 3], k[:, :, 48:50].amin(2))
+
+
+def test_quest_select_expansion():
+    B, Hq, Hk, S, D = 1, 2, 1, 40, 8
+    q, k = _bf16(B, Hq, 1, D, seed=14), _bf16(B, Hk, S, D, seed=15)
+    pidx, tok, bound = R.quest_select(q, k, budget_tokens=20, page=16)
+    assert pidx.shape == (1, 2, 2) and tok.shape == (1, 2, 32)
+    assert tok.max() <= S - 1
+    for h in range(2):
+        assert pidx[0, h].tolist() == _topk_brute(bound[0, h].tolist(), 2)
+
+
+# ---------------------------------------------------------------- scores / gather
+def test_group_scores_and_gather():
+    B, Hq, Hk, S, D = 1, 6, 2, 30, 16
+    q, k, v = _bf16(B, Hq, 1, D, seed=16), _bf16(B, Hk, S, D, seed=17), _bf16(B, Hk, S, D, seed=18)
+    s = R.sparse_score_scalar(q, k, 0.25)
+    gs = R.group_scores(q, k, 0.25)
+    for h in range(Hk):
+        assert torch.allclose(gs[0, h], s[0, 3 * h] + s[0, 3 * h + 1] + s[0, 3 * h + 2], atol=1e-5)
+    full = torch.arange(S).expand(B, Hq, S)
+    a = R.sparse_gather_attn(q, k, v, full, 0.25)
+    d = R.decode_attn(q, k, v, scale=0.25)
+    assert (a.float() - d.float()).abs().max() < 1e-2
+    # sentinel / out-of-range entries are masked
+    padded = torch.cat([full, torch.full((B, Hq, 3), S), torch.full((B, Hq, 1), -1)], -1)
+    assert torch.equal(R.sparse_gather_attn(q, k, v, padded, 0.25), a)
+    # per-KV-head idx shared by the group == repeated per-q-head idx
+    idx_kv = torch.randint(0, S, (B, Hk, 7), generator=torch.Generator().manual_seed(1))
+    assert torch.equal(R.sparse_gather_attn(q, k, v, idx_kv, 0.25),
+                       R.sparse_gather_attn(q, k, v, idx_kv.repeat_interleave(3, 1), 0.25))
