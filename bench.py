@@ -83,16 +83,67 @@ class DenseCase(Case):
                 lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), units)
 
 
+class KiviCase(Case):
+    kernel = "kivi_decode_kernel"
+
+    def __init__(self, name, bits, B=4, Hq=28, Hk=4, D=128, L=16384, R=128):
+        self.name, self.bits, self.shape = name, bits, (B, Hq, Hk, D, L, R)
+        self.dtype = f"u{bits}+fp16 meta+bf16"
+        self.workload = (f"KIVI-{bits} decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} "
+                         f"(Sq={L - R} packed, residual {R} bf16, group 32)")
+
+    def bytes_per_step(self):
+        B, Hq, Hk, D, L, R = self.shape
+        Sq = L - R
+        codes = 2 * B * Hk * D * Sq * self.bits // 8
+        kmeta = B * Hk * D * (Sq // 32) * 4
+        vmeta = B * Hk * Sq * (D // 32) * 4
+        resid = 2 * B * Hk * R * D * 2
+        return codes + kmeta + vmeta + resid + 2 * B * Hq * D * 2
+
+    def make(self, dev):
+        from bytes_amd import workloads as W
+        from bytes_amd.kivi import quantize_and_pack_along_last_dim
+        B, Hq, Hk, D, L, R = self.shape
+        raw = W.kivi_raw(B, Hq, Hk, D, L, R, seed=0)
+        raw = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in raw.items()}
+        x = W.kivi_pack_inputs(raw, quantize_and_pack_along_last_dim, self.bits)
+        x["K_residual"] = x["K_residual"].contiguous()
+        x["V_residual"] = x["V_residual"].contiguous()
+        return x
+
+    def step(self, x):
+        from bytes_amd.kivi import kivi_decode_attn
+        return kivi_decode_attn(x["Q"], x["Kq"], x["K_scale"], x["K_mn"], x["K_residual"], x["Vq"],
+                                x["V_scale"], x["V_mn"], x["V_residual"], self.bits, 32)
+
+    def cpu_sample(self):
+        from bytes_amd import workloads as W
+        from oracle import reference as R
+        B, Hq, Hk, D, L, Rw = self.shape
+        raw = W.kivi_raw(1, Hq // Hk, 1, D, L, Rw, seed=0)
+        x = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, self.bits)
+        units = B * Hk
+        args = [x[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn", "V_residual")]
+        return (f"one (b, kv-head) unit of {units}: oracle kivi_decode_attn on Q [1,{Hq // Hk},1,{D}], "
+                f"Sq={L - Rw} packed + {Rw} residual",
+                lambda: R.kivi_decode_attn(*args, self.bits, 32), units)
+
+
 def cases():
     from bytes_amd import workloads as W
     return {
+        "c2_kivi2": KiviCase("c2_kivi2", 2),
+        "c2_kivi4": KiviCase("c2_kivi4", 4),
         "c1_dense": DenseCase("c1_dense", *W.SHAPES["c1_dense"]),
         "dense_16k": DenseCase("dense_16k", *W.SHAPES["dense_16k"]),
         "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
+        "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536),
+        "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536),
     }
 
 
-HEADLINE = "dense_16k"
+HEADLINE = "c2_kivi2"
 
 
 # ---------------------------------------------------------------------------

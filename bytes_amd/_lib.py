@@ -33,6 +33,17 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64,                          # v strides (b, h, s)
         c_i64, c_i64,                                 # out strides (b, h)
         c_f32, c_int, c_vp, c_sz, c_vp),              # scale, chunk, workspace, bytes, stream
+    "bytes_kivi_quantize_pack": (c_vp, c_int, c_i64, c_int, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp),
+    "bytes_kivi_dequant": (c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_int, c_vp, c_int, c_vp),
+    "bytes_kivi_decode_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
+    "bytes_kivi_decode_attn": (
+        c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, kq, k_scale, k_mn, k_res
+        c_vp, c_vp, c_vp, c_vp, c_vp,                 # vq, v_scale, v_mn, v_res, out
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int,   # B, Hq, Hk, Sq, R, D, bits
+        c_i64, c_i64,                                 # q strides
+        c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,     # k_res / v_res strides
+        c_i64, c_i64,                                 # out strides
+        c_f32, c_int, c_vp, c_sz, c_vp),
 }
 _RESTYPES = {"bytes_error_string": ctypes.c_char_p}
 
@@ -97,6 +108,17 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         buf = torch.zeros(size, dtype=torch.uint8, device=dev)
         _ws[key] = buf
     return buf
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    """0 bf16, 1 fp16, 2 fp32 (the OutDtype / input-dtype codes of the C ABI)."""
+    codes = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+    if t.dtype not in codes:
+        raise ValueError(f"dtype {t.dtype} not supported (bf16, fp16, fp32)")
+    return codes[t.dtype]
+
+
+HIP_ERROR_NOT_SUPPORTED = 801
 
 
 def size_query(name: str, *args) -> int:

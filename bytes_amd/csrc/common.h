@@ -50,6 +50,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// 2^x on the hardware exp unit (v_exp_f32).  Used for softmax weights, whose
+// arguments are <= 0: results below the normal range flush towards zero,
+// which does not change a softmax numerator or denominator at fp32 precision.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Wave-scope ordering point for wave-private LDS buffers: keeps the compiler
 // from moving LDS accesses across it and orders them at wavefront scope.
 __device__ __forceinline__ void wave_lds_sync() {

@@ -1,0 +1,636 @@
+// KIVI-style quantized-KV decode attention, plus the KIVI pack / dequant helpers.
+//
+// Replaces benchmarks/kivi_latency.py:59-90 (`kivi_decode_attn`, whose device
+// work is KIVI's external `cuda_bmm_fA_qB_outer` GEMV twice plus a residual
+// matmul, softmax and cat) with one split-K flash-decode kernel, and the
+// external `triton_quantize_and_pack_along_last_dim` (kivi_latency.py:123,127)
+// plus the in-repo inverse `unpack_tensor_last_dim`/`dequant_k`/`dequant_v`
+// (kivi_latency.py:26-57) with pack/dequant kernels.
+//
+// Cache layout (the reference's): codes packed 32/bits per int32 along the
+// last dim, element i of word w at bits [i*bits, (i+1)*bits).
+//   keys   Kq [B,Hk,D,Sq*bits/32], K_scale/K_mn fp16 [B,Hk,D,Sq/32]  (per channel,
+//          groups of 32 tokens)
+//   values Vq [B,Hk,Sq,D*bits/32], V_scale/V_mn fp16 [B,Hk,Sq,D/32]  (per token,
+//          groups of 32 channels)
+//   residual K_res/V_res bf16 [B,Hk,R,D]
+//
+// Decode data path, per wave and 64-token tile (waves take interleaved tiles):
+//  * packed key and value words go HBM -> LDS untouched (global_load_lds_dwordx4);
+//  * ds_read_b64_tr_b4 transposes them at 4-bit granularity, which turns
+//    "16 tokens of one channel" (keys) / "16 channels of one token" (values)
+//    into the per-lane K-contiguous layout MFMA operands need;
+//  * two masks split each nibble into fp4 (2-bit codes, value c/2) or fp8
+//    (4-bit codes, value c*2^-9) operands that v_cvt_scalef32_pk_f16_{fp4,fp8}
+//    turn into exact fp16 codes; one v_pk_fma_f16 applies scale and zero;
+//  * S^T = K_dq Q^T and O^T += V_dq^T P^T run on v_mfma_f32_16x16x32_f16 with
+//    fp32 accumulation and an fp32 online softmax.
+// The bf16 residual window is one extra split handled by the dense tile loop.
+#include "dense_tile.h"
+
+namespace bytes_amd {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef int v2i_vs __attribute__((__vector_size__(2 * sizeof(int))));
+typedef __attribute__((address_space(3))) v2i_vs* tr_ptr_t;
+
+// ============================================================================
+// pack / dequant along the last dim
+// ============================================================================
+__device__ __forceinline__ float load_elem(const void* p, int dt, int64_t i) {
+  if (dt == 0) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  if (dt == 1) return (float)static_cast<const _Float16*>(p)[i];
+  return static_cast<const float*>(p)[i];
+}
+
+// One thread per (row, group).  Arithmetic follows src/quantization.py:432-442
+// in fp32: scale = max(max-min, 1e-8)/(2^bits-1), code = clamp(rint((x-min)/scale)).
+__global__ void kivi_pack_kernel(const void* x, int dt, int64_t rows, int T, int64_t x_rs, int gs, int bits,
+                                 uint32_t* code, _Float16* scale, _Float16* mn) {
+  const int ngr = T / gs;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= rows * ngr) return;
+  const int64_t row = gid / ngr;
+  const int grp = (int)(gid - row * ngr);
+  const int64_t base = row * x_rs + (int64_t)grp * gs;
+  float lo = __builtin_inff(), hi = -__builtin_inff();
+  for (int i = 0; i < gs; ++i) {
+    const float v = load_elem(x, dt, base + i);
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+  const int levels = 1 << bits;
+  const float s = fmaxf(hi - lo, 1e-8f) / (float)(levels - 1);
+  const int fpi = 32 / bits;
+  uint32_t* cw = code + row * (int64_t)(T / fpi) + (int64_t)grp * (gs / fpi);
+  for (int w = 0; w < gs / fpi; ++w) {
+    uint32_t word = 0;
+    for (int i = 0; i < fpi; ++i) {
+      const float v = load_elem(x, dt, base + w * fpi + i);
+      float c = rintf((v - lo) / s);
+      c = fminf(fmaxf(c, 0.f), (float)(levels - 1));
+      word |= (uint32_t)c << (i * bits);
+    }
+    cw[w] = word;
+  }
+  scale[row * ngr + grp] = (_Float16)s;
+  mn[row * ngr + grp] = (_Float16)lo;
+}
+
+// out[row, t] = code * scale + mn, in fp32 (fp16_math=0) or in the reference's
+// fp16 arithmetic (fp16_math=1: product rounded to fp16, then sum rounded).
+__global__ void kivi_dequant_kernel(const uint32_t* code, const _Float16* scale, const _Float16* mn, int64_t rows,
+                                    int T, int gs, int bits, int fp16_math, void* out, int out_dt) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= rows * T) return;
+  const int64_t row = gid / T;
+  const int t = (int)(gid - row * T);
+  const int fpi = 32 / bits, ngr = T / gs;
+  const uint32_t w = code[row * (T / fpi) + t / fpi];
+  const uint32_t c = (w >> ((t % fpi) * bits)) & ((1u << bits) - 1u);
+  const _Float16 s = scale[row * ngr + t / gs], m = mn[row * ngr + t / gs];
+  float v;
+  if (fp16_math) {
+#pragma clang fp contract(off)
+    const _Float16 p = (_Float16)c * s;   // rounded to fp16, then the sum rounded again
+    v = (float)(_Float16)(p + m);
+  } else {
+    v = (float)c * (float)s + (float)m;
+  }
+  if (out_dt == kOutBF16)
+    static_cast<uint16_t*>(out)[gid] = f32_to_bf16_bits(v);
+  else if (out_dt == kOutF16)
+    static_cast<_Float16*>(out)[gid] = (_Float16)v;
+  else
+    static_cast<float*>(out)[gid] = v;
+}
+
+// ============================================================================
+// decode
+// ============================================================================
+struct KiviArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint32_t* kq;       // contiguous [B,Hk,D,Sq*BITS/32]
+  const _Float16* ks;       // contiguous [B,Hk,D,Sq/32]
+  const _Float16* km;
+  const uint32_t* vq;       // contiguous [B,Hk,Sq,D*BITS/32]
+  const _Float16* vs;       // contiguous [B,Hk,Sq,D/32]
+  const _Float16* vm;
+  const uint16_t* kr;       // residual [B,Hk,R,D] bf16
+  const uint16_t* vr;
+  int64_t kr_sb, kr_sh, kr_ss, vr_sb, vr_sh, vr_ss;
+  int Hk, G, HB, Sq, R, chunk, nsq;
+  float scale_log2;
+  SplitKOut o;
+};
+
+constexpr int kKiviWaves = 4;
+constexpr int kKiviTile = 64;
+constexpr int kKiviChunkMax = 512;   // tokens per workgroup (multiple of 256)
+
+template <int D, int BITS>
+struct KiviCfg {
+  static constexpr int KK = D / 32;                        // MFMA k-steps over channels
+  static constexpr int KPIECES = kKiviChunkMax * BITS / 128;  // 16-byte key pieces per channel per chunk
+  static constexpr int KCROW = KPIECES * 16 + 16;          // LDS bytes per channel row (+16: bank spread)
+  static constexpr int KCBYTES = D * KCROW;                // staged key codes of one chunk
+  static constexpr int KMG = kKiviChunkMax / 32;           // key groups per chunk
+  static constexpr int KMETA = 2 * KMG * D * 2;            // staged key scales + zeros
+  static constexpr int VROW = D * BITS / 8;                // LDS bytes of one token's value codes
+  static constexpr int VBYTES = kKiviTile * VROW;
+  static constexpr int VDMA = VBYTES / 1024;               // 16-byte value chunks per lane per tile
+  static constexpr int NGV = D / 32;                        // value groups per token
+  static constexpr int VMBYTES = 2 * kKiviTile * NGV * 2;   // value scale + zero of one tile
+  static constexpr int WAVE_BYTES = VBYTES + VMBYTES;
+  static constexpr int kQuant = KCBYTES + KMETA + kKiviWaves * WAVE_BYTES;
+  static constexpr int kDense = DenseCfg<D>::kSmem;
+  static constexpr int kSmem = kQuant > kDense ? kQuant : kDense;
+};
+
+// Position of the k-slot order inside an 8-channel block (4-bit keys interleave
+// even/odd channels: slots hold channels 0,2,4,6,1,3,5,7).
+template <int BITS>
+__device__ __forceinline__ int kslot_pos(int ch) {
+  if (BITS == 2) return ch;
+  const int r = ch & 7;
+  return (ch & ~7) | ((r & 1) ? 4 + (r >> 1) : (r >> 1));
+}
+template <int BITS>
+__device__ __forceinline__ int kslot_ch(int jj) {  // channel offset held by k-slot jj
+  return BITS == 2 ? jj : (jj < 4 ? 2 * jj : 2 * (jj - 4) + 1);
+}
+
+// Value-meta slot of tile token tau for (sm, g): [sm][g][sg][lg][jj] (fp16 index).
+template <int D, int BITS>
+__device__ __forceinline__ int vmeta_slot(int sm, int g, int tau) {
+  constexpr int NGV = D / 32;
+  const int sg = tau >> 5, r = tau & 31;
+  int lg, jj;
+  if (BITS == 2) {
+    lg = r >> 3;
+    jj = r & 7;
+  } else {
+    const int hf = r >> 4, r2 = r & 15;
+    lg = r2 >> 2;
+    jj = hf * 4 + (r2 & 3);
+  }
+  return (((sm * NGV + g) * 2 + sg) * 4 + lg) * 8 + jj;
+}
+
+__device__ __forceinline__ u32x2 tr4(const char* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr4_b64_v2i32((tr_ptr_t)p));
+}
+
+__device__ __forceinline__ h2 u2h(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t h2u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// 8 fp4 nibbles (2-bit codes c -> value c/2) -> 8 fp16 c*scale + zero.
+__device__ __forceinline__ f16x8 deq_fp4(uint32_t dw, u32x4 s, u32x4 z) {
+  u32x4 r;
+  r[0] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 0)), u2h(s[0]), u2h(z[0])));
+  r[1] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 1)), u2h(s[1]), u2h(z[1])));
+  r[2] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 2)), u2h(s[2]), u2h(z[2])));
+  r[3] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 3)), u2h(s[3]), u2h(z[3])));
+  return __builtin_bit_cast(f16x8, r);
+}
+
+// lo/hi: 4 bytes each holding a 4-bit code (fp8 e4m3 value c*2^-9).  Output
+// k-slots: lo bytes 0,1 | lo bytes 2,3 | hi bytes 0,1 | hi bytes 2,3.
+__device__ __forceinline__ f16x8 deq_fp8(uint32_t lo, uint32_t hi, u32x4 s, u32x4 z) {
+  u32x4 r;
+  r[0] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false)), u2h(s[0]), u2h(z[0])));
+  r[1] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true)), u2h(s[1]), u2h(z[1])));
+  r[2] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false)), u2h(s[2]), u2h(z[2])));
+  r[3] = h2u(__builtin_elementwise_fma(__builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true)), u2h(s[3]), u2h(z[3])));
+  return __builtin_bit_cast(f16x8, r);
+}
+
+template <int D>
+using VMetaReg = typename std::conditional<(D >= 128), u32x4, u32x2>::type;
+
+// One tile's prefetched value codes and value scales/zeros (written to the
+// wave's LDS buffers when the tile runs).
+template <int D, int BITS>
+struct KiviRegs {
+  u32x4 v[KiviCfg<D, BITS>::VDMA];
+  VMetaReg<D> vm;
+};
+
+// Issue the value loads of the tile at o into registers (a dummy when !live:
+// same instructions, every lane reading the first bytes), so control flow
+// stays uniform and the compiler waits for exactly the registers it uses.
+// Value codes and value scales/zeros of a tile are contiguous in HBM.
+template <int D, int BITS>
+__device__ __forceinline__ void kivi_issue(const uint32_t* vqb, const _Float16* vsb, const _Float16* vmb, int o,
+                                           bool live, int lane, KiviRegs<D, BITS>& r) {
+  using C = KiviCfg<D, BITS>;
+  const char* vsrc = reinterpret_cast<const char*>(vqb) + (int64_t)o * C::VROW;
+#pragma unroll
+  for (int i = 0; i < C::VDMA; ++i) {
+    const char* src = live ? vsrc + (lane + 64 * i) * 16 : reinterpret_cast<const char*>(vqb);
+    r.v[i] = ld16(src);
+  }
+  const _Float16* mp = (lane < 32 ? vsb : vmb) + (int64_t)(o + 2 * (lane & 31)) * C::NGV;
+  r.vm = *reinterpret_cast<const VMetaReg<D>*>(live ? mp : vsb);
+}
+
+// Write one tile's prefetched value codes and scales/zeros to the wave's LDS buffers.
+template <int D, int BITS>
+__device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg, char* vst, char* vmeta_lds) {
+  using C = KiviCfg<D, BITS>;
+#pragma unroll
+  for (int i = 0; i < C::VDMA; ++i) *reinterpret_cast<u32x4*>(vst + (lane + 64 * i) * 16) = rg.v[i];
+  const _Float16* hv = reinterpret_cast<const _Float16*>(&rg.vm);
+  const int sm = lane >> 5, tau0 = 2 * (lane & 31);
+  _Float16* dst = reinterpret_cast<_Float16*>(vmeta_lds);
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int g = 0; g < C::NGV; ++g) dst[vmeta_slot<D, BITS>(sm, g, tau0 + u)] = hv[u * C::NGV + g];
+}
+
+// One 64-token tile: scores from the workgroup's staged key chunk (kc points at
+// this tile's first byte of channel row 0), online softmax, value accumulation
+// from the wave's staged value tile.
+template <int D, int BITS>
+__device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[D / 32], const char* kc,
+                                          const char* vst, const char* vmeta_lds, const char* kmeta, float& m_run,
+                                          float& l_run, f32x4 (&acc)[D / 16]) {
+  using C = KiviCfg<D, BITS>;
+  const int l16 = lane & 15, lg = lane >> 4;
+  constexpr int KMG = C::KMG;
+  const _Float16* kms = reinterpret_cast<const _Float16*>(kmeta);
+  const _Float16* kmz = kms + KMG * D;
+
+  // ---------------- scores ----------------
+  // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
+  // 4-bit: sc[tb][i]       is tile token 16tb + 4lg + i
+  f32x4 sc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) sc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    // 2-bit: blk = sub-tile sg (blk < 2); 4-bit: blk = 16-token block tb
+    if (BITS == 2 && blk >= 2) break;
+    const int grp = grp0 + (BITS == 2 ? blk : (blk >> 1));
+    u32x4 ksp[C::KK], kzp[C::KK];
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) {
+      const int off = (grp * D + lg * (D / 4) + kk * 8) * 2;
+      ksp[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kms) + off);
+      kzp[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kmz) + off);
+    }
+#pragma unroll
+    for (int rd = 0; rd < C::KK / 2; ++rd) {
+      const int ch = lg * (D / 4) + rd * 16 + l16;
+      const u32x2 x = tr4(kc + ch * C::KCROW + blk * 8);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int kk = rd * 2 + half;
+        if (BITS == 2) {
+          const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
+          sc[blk * 2 + 0] = mfma_f16(deq_fp4(e, ksp[kk], kzp[kk]), qh[kk], sc[blk * 2 + 0]);
+          sc[blk * 2 + 1] = mfma_f16(deq_fp4(od, ksp[kk], kzp[kk]), qh[kk], sc[blk * 2 + 1]);
+        } else {
+          const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
+          sc[blk] = mfma_f16(deq_fp8(lo, hi, ksp[kk], kzp[kk]), qh[kk], sc[blk]);
+        }
+      }
+    }
+  }
+
+  // ---------------- online softmax (Q carries scale*log2(e); tiles are full) ----------------
+  float mx = kNegInf;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[u][i]);
+  mx = fmaxf(mx, shfl_xor_f(mx, 16));
+  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = fast_exp2(m_run - m_new);
+  float p[16];
+  float psum = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[u * 4 + i] = fast_exp2(sc[u][i] - m_new);
+      psum += p[u * 4 + i];
+    }
+  l_run = l_run * alpha + psum;
+  m_run = m_new;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
+
+  // P^T as the B operand, k-slot jj of sub-tile sg:
+  //   2-bit: token 32sg + 8lg + jj  -> p[(sg*2 + jj%2)*4 + jj/2]
+  //   4-bit: tokens [tb=2sg: i0..3, tb=2sg+1: i0..3] -> p[(2sg + jj/4)*4 + jj%4]
+  f16x8 pb[2];
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg)
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int idx = BITS == 2 ? (sg * 2 + (jj & 1)) * 4 + (jj >> 1) : (2 * sg + (jj >> 2)) * 4 + (jj & 3);
+      pb[sg][jj] = (_Float16)p[idx];
+    }
+
+  // ---------------- values ----------------
+  const char* vml = vmeta_lds;
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    u32x4 vsp[C::NGV], vzp[C::NGV];
+#pragma unroll
+    for (int g = 0; g < C::NGV; ++g) {
+      vsp[g] = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16);
+      vzp[g] = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, g, sg * 32) * 2 + lg * 16);
+    }
+    if (BITS == 2) {
+      // cb = 32-channel block; one tr read covers cb pair (2rd, 2rd+1)
+#pragma unroll
+      for (int rd = 0; rd < D / 64; ++rd) {
+        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+        const int tok = 32 * sg + 8 * lg + r;
+        const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
+        const int ca = 2 * rd, cbb = 2 * rd + 1;
+        const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
+        const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
+        acc[ca * 2 + 0] = mfma_f16(deq_fp4(e0, vsp[ca], vzp[ca]), pb[sg], acc[ca * 2 + 0]);
+        acc[cbb * 2 + 0] = mfma_f16(deq_fp4(e1, vsp[cbb], vzp[cbb]), pb[sg], acc[cbb * 2 + 0]);
+        acc[ca * 2 + 1] = mfma_f16(deq_fp4(o0, vsp[ca], vzp[ca]), pb[sg], acc[ca * 2 + 1]);
+        acc[cbb * 2 + 1] = mfma_f16(deq_fp4(o1, vsp[cbb], vzp[cbb]), pb[sg], acc[cbb * 2 + 1]);
+      }
+    } else {
+      // cb = 16-channel block; one tr read covers cb pair (2rd, 2rd+1), both in group rd
+#pragma unroll
+      for (int rd = 0; rd < D / 32; ++rd) {
+        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+        const int tok = (r & 1) ? 32 * sg + 16 + 4 * lg + (r >> 1) : 32 * sg + 4 * lg + (r >> 1);
+        const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
+        const uint32_t lo0 = x[0] & 0x0F0F0F0Fu, hi0 = (x[0] >> 4) & 0x0F0F0F0Fu;
+        const uint32_t lo1 = x[1] & 0x0F0F0F0Fu, hi1 = (x[1] >> 4) & 0x0F0F0F0Fu;
+        acc[2 * rd] = mfma_f16(deq_fp8(lo0, hi0, vsp[rd], vzp[rd]), pb[sg], acc[2 * rd]);
+        acc[2 * rd + 1] = mfma_f16(deq_fp8(lo1, hi1, vsp[rd], vzp[rd]), pb[sg], acc[2 * rd + 1]);
+      }
+    }
+  }
+}
+
+template <int D, int BITS>
+__global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArgs a) {
+  using C = KiviCfg<D, BITS>;
+  __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int split = blockIdx.x, unit = blockIdx.y;
+  const int b = unit / (a.Hk * a.HB);
+  const int rem = unit - b * a.Hk * a.HB;
+  const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
+  const int hq0 = hk * a.G + hb * 16;
+  const int nh = min(16, a.G - hb * 16);
+  const uint16_t* qrow0 = a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh;
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (split == a.nsq) {
+    // bf16 residual window: dense tiles over [0, R)
+    bf16x8 qb[D / 32];
+    load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
+    const uint16_t* kbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
+    const uint16_t* vbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
+    dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, 0, a.R, w, lane, a.scale_log2, qb,
+                       smem_raw + w * DenseCfg<D>::WAVE, m_run, l_run, acc);
+    splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b,
+                                   hq0, nh, kDmapDense);
+    return;
+  }
+
+  const int Sq = a.Sq;
+  const int t_begin = split * a.chunk;
+  const int t_end = min(t_begin + a.chunk, Sq);
+  const int g_lo = t_begin >> 5;
+  const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
+  const int64_t bh = (int64_t)b * a.Hk + hk;
+  const int ngk = Sq >> 5;
+
+  char* kchunk = smem_raw;
+  char* kmeta = smem_raw + C::KCBYTES;
+  char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;
+  char* vml = vst + C::VBYTES;
+
+  const uint32_t* vqb = a.vq + bh * (int64_t)Sq * (D * BITS / 32);
+  const _Float16* vsb = a.vs + bh * (int64_t)Sq * C::NGV;
+  const _Float16* vmb = a.vm + bh * (int64_t)Sq * C::NGV;
+
+  // First value tile of this wave: in flight while the key chunk is staged.
+  constexpr int STEP = kKiviWaves * kKiviTile;
+  int t = t_begin + w * kKiviTile;
+  KiviRegs<D, BITS> rg;
+  kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg);
+
+  // Q as the fp16 B operand (scaled by scale*log2e):
+  //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
+  f16x8 qh[D / 32];
+  {
+    const bool live = l16 < nh;
+    const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * a.q_sh + lg * (D / 4);
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      u32x4 raw = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, raw);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
+    }
+  }
+
+  // Stage the chunk's key codes: channel rows of (t_end - t_begin)*BITS/8 bytes,
+  // consecutive threads covering consecutive 16-byte pieces of a row, so every
+  // request is a whole cache line.
+  {
+    constexpr int NT = kKiviWaves * 64;
+    constexpr int PER = D * C::KPIECES / NT;
+    const int pieces = (t_end - t_begin) * BITS / 128;
+    const uint32_t* kqb = a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32;
+    const int64_t wk = Sq * BITS / 32;
+    u32x4 kv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int pc = threadIdx.x + NT * i;
+      const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
+      kv[i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
+    }
+    // key scales/zeros: rows (sm, ch) of ngs fp16, two groups per 4-byte load
+    constexpr int WR = C::KMG / 2;
+    constexpr int PERM = 2 * D * WR / NT;
+    const int nwr = ngs >> 1;
+    uint32_t mv[PERM];
+#pragma unroll
+    for (int i = 0; i < PERM; ++i) {
+      const int pc = threadIdx.x + NT * i;
+      const int row = pc / WR, wi = pc - row * WR;
+      const int sm = row / D, ch = row - sm * D;
+      const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? a.km : a.ks) + (bh * D + ch) * ngk + g_lo);
+      mv[i] = src[min(wi, nwr - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int pc = threadIdx.x + NT * i;
+      const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
+      if (q < pieces) *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[i];
+    }
+    _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
+#pragma unroll
+    for (int i = 0; i < PERM; ++i) {
+      const int pc = threadIdx.x + NT * i;
+      const int row = pc / WR, wi = pc - row * WR;
+      const int sm = row / D, ch = row - sm * D;
+      if (wi < nwr) {
+        _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
+        dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] & 0xFFFFu));
+        dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] >> 16));
+      }
+    }
+  }
+  __syncthreads();
+
+  // One register set per wave: staged into LDS at the top of each tile, then
+  // refilled with the next tile, so one tile's values are always in flight.
+  for (; t < t_end; t += STEP) {
+    wave_lds_sync();
+    kivi_stage<D, BITS>(lane, rg, vst, vml);
+    kivi_issue<D, BITS>(vqb, vsb, vmb, t + STEP < t_end ? t + STEP : 0, t + STEP < t_end, lane, rg);
+    wave_lds_sync();
+    const int off = t - t_begin;
+    kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
+  }
+  splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
+                                 nh, BITS == 2 ? kDmapKivi2 : kDmapDense);
+}
+
+static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq) {
+  const int step = kKiviWaves * kKiviTile;
+  int c;
+  if (chunk_req > 0) {
+    c = (chunk_req + step - 1) / step * step;
+  } else {
+    const long target = 2L * device_cu_count();
+    const long per = ((long)Sq * units + target - 1) / target;
+    c = (int)((per + step - 1) / step * step);
+  }
+  if (c < step) c = step;
+  if (c > kKiviChunkMax) c = kKiviChunkMax;
+  *chunk = c;
+  *nsq = Sq > 0 ? (Sq + c - 1) / c : 0;
+  (void)R;
+}
+
+}  // namespace bytes_amd
+
+using namespace bytes_amd;
+
+extern "C" {
+
+int bytes_kivi_quantize_pack(const void* x, int x_dtype, int64_t rows, int T, int64_t x_row_stride, int group_size,
+                             int bits, void* code, void* scale, void* mn, void* stream) {
+  if (!x || !code || !scale || !mn || rows < 0 || T <= 0) return (int)hipErrorInvalidValue;
+  if ((bits != 2 && bits != 4) || group_size <= 0 || T % group_size != 0 || group_size % (32 / bits) != 0)
+    return (int)hipErrorInvalidValue;
+  if (x_dtype < 0 || x_dtype > 2) return (int)hipErrorInvalidValue;
+  const int64_t n = rows * (T / group_size);
+  if (n == 0) return 0;
+  const int th = 256;
+  hipLaunchKernelGGL(kivi_pack_kernel, dim3((unsigned)((n + th - 1) / th)), dim3(th), 0,
+                     static_cast<hipStream_t>(stream), x, x_dtype, rows, T, x_row_stride, group_size, bits,
+                     static_cast<uint32_t*>(code), static_cast<_Float16*>(scale), static_cast<_Float16*>(mn));
+  return (int)hipGetLastError();
+}
+
+int bytes_kivi_dequant(const void* code, const void* scale, const void* mn, int64_t rows, int T, int group_size,
+                       int bits, int fp16_math, void* out, int out_dtype, void* stream) {
+  if (!code || !scale || !mn || !out || rows < 0 || T <= 0) return (int)hipErrorInvalidValue;
+  if ((bits != 2 && bits != 4) || group_size <= 0 || T % group_size != 0 || T % (32 / bits) != 0)
+    return (int)hipErrorInvalidValue;
+  if (out_dtype < 0 || out_dtype > 2) return (int)hipErrorInvalidValue;
+  const int64_t n = rows * T;
+  if (n == 0) return 0;
+  const int th = 256;
+  hipLaunchKernelGGL(kivi_dequant_kernel, dim3((unsigned)((n + th - 1) / th)), dim3(th), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(code),
+                     static_cast<const _Float16*>(scale), static_cast<const _Float16*>(mn), rows, T, group_size,
+                     bits, fp16_math, out, out_dtype);
+  return (int)hipGetLastError();
+}
+
+int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D, int bits, int chunk_req,
+                                     size_t* bytes) {
+  if (!bytes || B <= 0 || Hk <= 0 || Hq % Hk != 0 || Sq < 0 || R < 0 || Sq + R <= 0) return (int)hipErrorInvalidValue;
+  if ((D != 64 && D != 128) || (bits != 2 && bits != 4)) return (int)hipErrorInvalidValue;
+  const int G = Hq / Hk, HB = (G + 15) / 16;
+  const long units = (long)B * Hk * HB;
+  int chunk, nsq;
+  kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq);
+  *bytes = splitk_workspace_bytes(units, nsq + (R > 0 ? 1 : 0), D);
+  return 0;
+}
+
+// Kq/K_scale/K_mn/Vq/V_scale/V_mn contiguous in the layouts above; Sq % 64 == 0
+// (Sq == 0 allowed); group size 32.  hipErrorNotSupported for other shapes.
+int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, const void* k_mn, const void* k_res,
+                           const void* vq, const void* v_scale, const void* v_mn, const void* v_res, void* out,
+                           int B, int Hq, int Hk, int Sq, int R, int D, int bits, int64_t q_sb, int64_t q_sh,
+                           int64_t kr_sb, int64_t kr_sh, int64_t kr_ss, int64_t vr_sb, int64_t vr_sh,
+                           int64_t vr_ss, int64_t o_sb, int64_t o_sh, float scale, int chunk_req, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!q || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || Sq < 0 || R < 0 || Sq + R <= 0)
+    return (int)hipErrorInvalidValue;
+  if ((D != 64 && D != 128) || (bits != 2 && bits != 4)) return (int)hipErrorInvalidValue;
+  if (Sq > 0 && (!kq || !k_scale || !k_mn || !vq || !v_scale || !v_mn)) return (int)hipErrorInvalidValue;
+  if (R > 0 && (!k_res || !v_res)) return (int)hipErrorInvalidValue;
+  if (Sq % kKiviTile != 0) return (int)hipErrorNotSupported;
+  const int G = Hq / Hk, HB = (G + 15) / 16;
+  const long units = (long)B * Hk * HB;
+  if (units > 65535) return (int)hipErrorInvalidConfiguration;
+  KiviArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_sb; a.q_sh = q_sh;
+  a.kq = static_cast<const uint32_t*>(kq);
+  a.ks = static_cast<const _Float16*>(k_scale);
+  a.km = static_cast<const _Float16*>(k_mn);
+  a.vq = static_cast<const uint32_t*>(vq);
+  a.vs = static_cast<const _Float16*>(v_scale);
+  a.vm = static_cast<const _Float16*>(v_mn);
+  a.kr = static_cast<const uint16_t*>(k_res);
+  a.vr = static_cast<const uint16_t*>(v_res);
+  a.kr_sb = kr_sb; a.kr_sh = kr_sh; a.kr_ss = kr_ss;
+  a.vr_sb = vr_sb; a.vr_sh = vr_sh; a.vr_ss = vr_ss;
+  a.Hk = Hk; a.G = G; a.HB = HB; a.Sq = Sq; a.R = R;
+  a.scale_log2 = scale * kLog2e;
+  kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq);
+  const int ns = a.nsq + (R > 0 ? 1 : 0);
+  if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
+  if (ns > 1024) return (int)hipErrorInvalidConfiguration;
+  a.o.out = out;
+  a.o.out_dtype = kOutBF16;
+  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
+  a.o.Hk = Hk; a.o.HB = HB; a.o.G = G;
+  splitk_carve(workspace, units, ns, a.o);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(ns, (unsigned)units), block(kKiviWaves * 64);
+  if (D == 128 && bits == 2)
+    hipLaunchKernelGGL((kivi_decode_kernel<128, 2>), grid, block, 0, st, a);
+  else if (D == 128 && bits == 4)
+    hipLaunchKernelGGL((kivi_decode_kernel<128, 4>), grid, block, 0, st, a);
+  else if (D == 64 && bits == 2)
+    hipLaunchKernelGGL((kivi_decode_kernel<64, 2>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((kivi_decode_kernel<64, 4>), grid, block, 0, st, a);
+  int rc = (int)hipGetLastError();
+  if (rc) return rc;
+  return splitk_combine(a.o, units, D, st);
+}
+
+}  // extern "C"

@@ -59,16 +59,25 @@ __device__ __forceinline__ void store_out(const SplitKOut& o, int b, int hq, int
 // LDS floats needed by splitk_epilogue.
 template <int D, int NW>
 constexpr int splitk_smem_floats() {
-  return NW * 16 * 2 + NW * D * 16;
+  return NW * 16 * 2 + NW * D * 16 + NW * 16 + 16;
+}
+
+// Head-dim position of accumulator element acc[db][i] held by lane group lg.
+//   kDmapDense: d = db*16 + lg*4 + i           (dense, KIVI 4-bit, PQ, gather)
+//   kDmapKivi2: d = 32*(db/2) + 8*lg + 2*i + db%2  (KIVI 2-bit value layout)
+enum : int { kDmapDense = 0, kDmapKivi2 = 1 };
+__device__ __forceinline__ int acc_d(int dmap, int db, int lg, int i) {
+  return dmap == kDmapKivi2 ? 32 * (db >> 1) + 8 * lg + 2 * i + (db & 1) : db * 16 + lg * 4 + i;
 }
 
 // m_run: running max (log2 domain) of this lane's head l%16, identical across
 // the four lanes l%16 + 16*j; l_run: this lane's partial denominator;
-// acc[db][i]: O^T[d = db*16 + (l/16)*4 + i][h = l%16].
+// acc[db][i]: O^T[d = acc_d(dmap, db, l/16, i)][h = l%16].
 // All threads of the workgroup must call this (it contains barriers).
 template <int D, int NW>
 __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], float* smem,
-                                const SplitKOut& o, int unit, int split, int b, int hq0, int nh) {
+                                const SplitKOut& o, int unit, int split, int b, int hq0, int nh,
+                                int dmap = kDmapDense) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
   constexpr int NT = NW * 64;
   l_run += shfl_xor_f(l_run, 16);
@@ -84,30 +93,42 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
 #pragma unroll
   for (int db = 0; db < D / 16; ++db)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wacc[(w * D + db * 16 + lg * 4 + i) * 16 + l16] = acc[db][i];
+    for (int i = 0; i < 4; ++i) wacc[(w * D + acc_d(dmap, db, lg, i)) * 16 + l16] = acc[db][i];
   __syncthreads();
 
-  const bool direct = o.nsplit <= 1;
-  for (int e = threadIdx.x; e < nh * D; e += NT) {
-    const int h = e / D, d = e - h * D;
+  // per-head merge factors of the waves, computed once
+  float* wf = wacc + NW * D * 16;   // [NW][16] factors, then [16] L
+  if (threadIdx.x < 16) {
+    const int h = threadIdx.x;
     float M = kNegInf;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, wm[ww * 16 + h]);
     const float Ms = (M == kNegInf) ? 0.f : M;
-    float L = 0.f, A = 0.f;
+    float L = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
-      const float f = exp2f(wm[ww * 16 + h] - Ms);
+      const float f = fast_exp2(wm[ww * 16 + h] - Ms);
+      wf[ww * 16 + h] = f;
       L += f * wl[ww * 16 + h];
-      A += f * wacc[(ww * D + d) * 16 + h];
     }
+    wf[NW * 16 + h] = L;
+    wm[h] = M;   // wave 0's slot is free now: holds the merged max
+  }
+  __syncthreads();
+  const bool direct = o.nsplit <= 1;
+  for (int e = threadIdx.x; e < nh * D; e += NT) {
+    const int h = e / D, d = e - h * D;
+    float A = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * 16 + h];
+    const float L = wf[NW * 16 + h];
     if (direct) {
       store_out(o, b, hq0 + h, d, A / L);
     } else {
       const size_t slot = ((size_t)unit * o.nsplit + split) * 16 + h;
       o.part_acc[slot * D + d] = A;
       if (d == 0) {
-        o.part_ml[slot * 2 + 0] = M;
+        o.part_ml[slot * 2 + 0] = wm[h];
         o.part_ml[slot * 2 + 1] = L;
       }
     }

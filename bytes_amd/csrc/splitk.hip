@@ -9,12 +9,15 @@
 namespace bytes_amd {
 
 constexpr int kCombineThreads = 256;
+constexpr int kSplitMax = 1024;
+constexpr int kSplitPerLane = kSplitMax / 64;
 
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKOut o) {
   constexpr int ITEMS = D / 4;                      // float4 items per head row
   constexpr int GROUPS = kCombineThreads / ITEMS;   // split groups
-  __shared__ float fw[256];
+  constexpr int PF = 8;                             // acc loads per thread issued up front
+  __shared__ float fw[kSplitMax];
   __shared__ float red[2][64];
   __shared__ float4 gacc[GROUPS][ITEMS];
   const int unit = blockIdx.x, h = blockIdx.y;
@@ -26,11 +29,21 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
   const int ns = o.nsplit, tid = threadIdx.x, lane = tid & 63;
   const size_t base = (size_t)unit * ns * 16 + h;
 
-  // max over splits (wave 0 of the block, lanes stride the splits)
-  float m_loc = kNegInf;
-  float mv[4], lv[4];
+  // Issue the first PF acc rows of this thread's splits and (wave 0) every
+  // split's (m, l) before consuming any of them: one memory round trip.
+  const int item = tid % ITEMS, g = tid / ITEMS;
+  const float4* src = reinterpret_cast<const float4*>(o.part_acc + base * D) + item;
+  const size_t stride4 = (size_t)16 * D / 4;
+  float4 pv[PF];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int u = 0; u < PF; ++u) {
+    const int s = g + u * GROUPS;
+    pv[u] = s < ns ? src[(size_t)s * stride4] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float m_loc = kNegInf;
+  float mv[kSplitPerLane], lv[kSplitPerLane];
+#pragma unroll
+  for (int k = 0; k < kSplitPerLane; ++k) {
     const int s = lane + 64 * k;
     if (tid < 64 && s < ns) {
       const float2 ml = *reinterpret_cast<const float2*>(o.part_ml + (base + (size_t)s * 16) * 2);
@@ -48,10 +61,10 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
     const float Ms = (m_loc == kNegInf) ? 0.f : m_loc;
     float l_loc = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kSplitPerLane; ++k) {
       const int s = lane + 64 * k;
       if (s < ns) {
-        const float f = exp2f(mv[k] - Ms);
+        const float f = fast_exp2(mv[k] - Ms);
         fw[s] = f;
         l_loc += f * lv[k];
       }
@@ -65,23 +78,17 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
     red[1][0] = 1.f / L;
   }
 
-  // weighted sum of the acc rows: thread (group g, item i) takes splits s = g, g+GROUPS, ...
-  const int item = tid % ITEMS, g = tid / ITEMS;
-  const float4* src = reinterpret_cast<const float4*>(o.part_acc + base * D) + item;
-  const size_t stride4 = (size_t)16 * D / 4;
+  // weighted sum: thread (group g, item) takes splits s = g, g+GROUPS, ... in order
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  int s = g;
-  for (; s + 3 * GROUPS < ns; s += 4 * GROUPS) {
-    float4 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = src[(size_t)(s + u * GROUPS) * stride4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float f = fw[s + u * GROUPS];
-      A.x += f * v[u].x; A.y += f * v[u].y; A.z += f * v[u].z; A.w += f * v[u].w;
+  for (int u = 0; u < PF; ++u) {
+    const int s = g + u * GROUPS;
+    if (s < ns) {
+      const float f = fw[s];
+      A.x += f * pv[u].x; A.y += f * pv[u].y; A.z += f * pv[u].z; A.w += f * pv[u].w;
     }
   }
-  for (; s < ns; s += GROUPS) {
+  for (int s = g + PF * GROUPS; s < ns; s += GROUPS) {
     const float4 v = src[(size_t)s * stride4];
     const float f = fw[s];
     A.x += f * v.x; A.y += f * v.y; A.z += f * v.z; A.w += f * v.w;
@@ -105,7 +112,7 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
 
 int splitk_combine(const SplitKOut& o, long units, int D, hipStream_t stream) {
   if (o.nsplit <= 1) return 0;
-  if (o.nsplit > 256) return (int)hipErrorInvalidValue;
+  if (o.nsplit > kSplitMax) return (int)hipErrorInvalidValue;
   dim3 grid((unsigned)units, 16);
   if (D == 64)
     hipLaunchKernelGGL(splitk_combine_kernel<64>, grid, dim3(kCombineThreads), 0, stream, o);

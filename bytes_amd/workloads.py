@@ -51,3 +51,35 @@ def c1_dense(seed: int = 0, device="cpu") -> Dict:
 def dense_16k(seed: int = 0, device="cpu", L: int = 16384) -> Dict:
     B, Hq, Hk, D, _ = SHAPES["dense_16k"]
     return dense(B, Hq, Hk, D, L, seed=seed, device=device)
+
+
+def kivi_raw(B: int = 4, Hq: int = 28, Hk: int = 4, D: int = 128, L: int = 16384, R: int = 128,
+             seed: int = 0, device="cpu", n_outlier: int = 4, outlier_scale: float = 8.0) -> Dict:
+    """BASELINE C2 raw tensors: bf16 K, V ~ N(0,1); `n_outlier` key channels chosen
+    by a seeded randperm(D) (the same for every b, h) are multiplied by
+    `outlier_scale`; q ~ N(0,1) bf16.  The last R tokens form the bf16 residual
+    window; the first L - R are to be packed (keys transposed per channel)."""
+    g = _gen(seed)
+    q = randn_bf16((B, Hq, 1, D), g)
+    k = torch.randn(B, Hk, L, D, generator=g)
+    v = torch.randn(B, Hk, L, D, generator=g)
+    ch = torch.randperm(D, generator=g)[:n_outlier]
+    k[..., ch] *= outlier_scale
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    Sq = L - R
+    return {"q": q.to(device), "k": k.to(device), "v": v.to(device), "Sq": Sq, "R": R,
+            "scale": 1.0 / math.sqrt(D),
+            "meta": {"seed": seed, "outlier_channels": ch.tolist(), "shape": (B, Hq, Hk, D, L, R)}}
+
+
+def kivi_pack_inputs(raw: Dict, pack_fn, bits: int, group_size: int = 32) -> Dict:
+    """Pack a kivi_raw() cache with `pack_fn(x, group_size, bits)` the way the
+    reference harness does (benchmarks/kivi_latency.py:121-128): keys transposed
+    to [B,Hk,D,Sq] and cast to fp16, values cast to fp16."""
+    Sq = raw["Sq"]
+    k, v = raw["k"], raw["v"]
+    kq, ks, km = pack_fn(k[:, :, :Sq].transpose(2, 3).contiguous().to(torch.float16), group_size, bits)
+    vq, vs, vm = pack_fn(v[:, :, :Sq].contiguous().to(torch.float16), group_size, bits)
+    return {"Q": raw["q"], "Kq": kq, "K_scale": ks, "K_mn": km, "K_residual": k[:, :, Sq:],
+            "Vq": vq, "V_scale": vs, "V_mn": vm, "V_residual": v[:, :, Sq:], "bits": bits,
+            "group_size": group_size}

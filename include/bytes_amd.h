@@ -53,6 +53,57 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
                            float scale, int chunk, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* ---------------------------------------------------------------------------
+ * KIVI asymmetric min/max quantize + pack along the last axis.
+ * Replaces the external KIVI `triton_quantize_and_pack_along_last_dim(x, 32, bits)`
+ * called at benchmarks/kivi_latency.py:123,127 (arithmetic of
+ * src/quantization.py:432-442; bit layout = inverse of kivi_latency.py:26-35).
+ *   x     [rows, T], dtype x_dtype (0 bf16, 1 f16, 2 f32), row stride x_row_stride
+ *   code  [rows, T*bits/32] int32: element i of word w = logical index w*(32/bits)+i,
+ *         at bits [i*bits, (i+1)*bits)
+ *   scale, mn [rows, T/group_size] f16:
+ *         scale = max(hi-lo, 1e-8)/(2^bits-1), code = clamp(rint((x-lo)/scale)),
+ *         both computed in fp32, scale/mn rounded to f16 afterwards.
+ * bits in {2, 4}; T % group_size == 0; group_size % (32/bits) == 0.
+ * ------------------------------------------------------------------------- */
+int bytes_kivi_quantize_pack(const void* x, int x_dtype, int64_t rows, int T, int64_t x_row_stride,
+                             int group_size, int bits, void* code, void* scale, void* mn, void* stream);
+
+/* KIVI unpack + dequant along the last axis (kivi_latency.py:26-57):
+ * out[r, t] = code * scale + mn, in f16 arithmetic when fp16_math != 0 (the
+ * reference's unpacked-fp16 * fp16-scale + fp16-mn), else in fp32.
+ * out [rows, T] contiguous, dtype out_dtype (0 bf16, 1 f16, 2 f32). */
+int bytes_kivi_dequant(const void* code, const void* scale, const void* mn, int64_t rows, int T,
+                       int group_size, int bits, int fp16_math, void* out, int out_dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused KIVI 2/4-bit decode attention.
+ * Replaces benchmarks/kivi_latency.py:59-90 (`kivi_decode_attn`; semantics
+ * `kivi_decode_attn_ref` :92-100): softmax([q.Kdq^T, q.Kres^T] * scale) [Vdq; Vres]
+ * with GQA head map h -> h / (Hq/Hk).
+ *   q        [B, Hq, D] bf16 (strides q_sb, q_sh)
+ *   kq       [B, Hk, D, Sq*bits/32] int32  (keys packed per channel along tokens)
+ *   k_scale, k_mn [B, Hk, D, Sq/32] f16
+ *   k_res    [B, Hk, R, D] bf16 (strides kr_*)
+ *   vq       [B, Hk, Sq, D*bits/32] int32  (values packed per token along channels)
+ *   v_scale, v_mn [B, Hk, Sq, D/32] f16
+ *   v_res    [B, Hk, R, D] bf16 (strides vr_*)
+ *   out      [B, Hq, D] bf16 (strides o_sb, o_sh)
+ * Packed tensors and their metadata are contiguous.  Sq % 64 == 0 (0 allowed),
+ * group size 32, D in {64, 128}; other Sq return hipErrorNotSupported (the
+ * Python layer then dequantizes and calls bytes_decode_attn_bf16).
+ * scale: the reference uses 1/sqrt(D).
+ * ------------------------------------------------------------------------- */
+int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D, int bits, int chunk,
+                                     size_t* bytes);
+int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, const void* k_mn,
+                           const void* k_res, const void* vq, const void* v_scale, const void* v_mn,
+                           const void* v_res, void* out, int B, int Hq, int Hk, int Sq, int R, int D,
+                           int bits, int64_t q_sb, int64_t q_sh, int64_t kr_sb, int64_t kr_sh,
+                           int64_t kr_ss, int64_t vr_sb, int64_t vr_sh, int64_t vr_ss, int64_t o_sb,
+                           int64_t o_sh, float scale, int chunk, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -1,0 +1,109 @@
+"""KIVI pack (bit-exact) and fused decode (north_star tolerance) vs the CPU oracle."""
+import pytest
+import torch
+
+from bytes_amd import kivi as K
+from bytes_amd import workloads as W
+from oracle import reference as R
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+pytestmark = pytest.mark.gpu
+
+
+def _to(d, dev):
+    return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+def _check(out, ref, tag):
+    d = (out.float().cpu() - ref.float()).abs()
+    print(f"{tag}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}", flush=True)
+    assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, tag
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_pack_bit_exact(dev, bits, dtype):
+    g = torch.Generator().manual_seed(bits)
+    x = (torch.randn(3, 5, 256, generator=g) * 3).to(dtype)
+    x[0, 0, :32] = 1.25                                  # constant group -> scale = 1e-8/levels
+    x[0, 1, 32:64] = torch.arange(32) * 0.5              # exact grid -> half-way rounding cases
+    code, scale, mn = K.quantize_and_pack_along_last_dim(x.to(dev), 32, bits)
+    rc, rs, rm = R.kivi_quantize_and_pack_last_dim(x, 32, bits)
+    assert torch.equal(code.cpu(), rc)
+    assert torch.equal(scale.cpu().view(torch.int16), rs.view(torch.int16))
+    assert torch.equal(mn.cpu().view(torch.int16), rm.view(torch.int16))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_unpack_and_dequant(dev, bits):
+    g = torch.Generator().manual_seed(10 + bits)
+    codes = torch.randint(0, 2 ** bits, (2, 3, 4, 128), generator=g)
+    words = R.kivi_pack_last_dim(codes, bits)
+    un = K.unpack_tensor_last_dim(words.to(dev), bits)
+    assert un.dtype == torch.float16 and torch.equal(un.cpu().long(), codes)
+    sc = (torch.rand(2, 3, 4, 4, generator=g) + 0.1).half()
+    mn = (torch.rand(2, 3, 4, 4, generator=g) - 0.5).half()
+    dk = K.dequant_k(words.to(dev), sc.to(dev), mn.to(dev), 32, bits)
+    ref = R.kivi_dequant_k(words, sc, mn, 32, bits, fp16_math=True)
+    assert torch.equal(dk.cpu(), ref.half())
+    dv = K.dequant_v(words.to(dev), sc.to(dev), mn.to(dev), 32, bits)
+    assert torch.equal(dv.cpu(), R.kivi_dequant_v(words, sc, mn, 32, bits, fp16_math=True).half())
+
+
+def _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=0, chunk=0):
+    raw = W.kivi_raw(B, Hq, Hk, D, L, Rw, seed=seed)
+    cpu = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, bits)
+    gpu = _to(cpu, dev)
+    args = [gpu[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn", "V_residual")]
+    out = K.kivi_decode_attn(*args, bits, 32, chunk=chunk)
+    ref = R.kivi_decode_attn(*[cpu[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale",
+                                                 "V_mn", "V_residual")], bits, 32)
+    assert out.shape == (B, Hq, 1, D) and out.dtype == torch.bfloat16
+    _check(out, ref, f"kivi{bits} B{B} Hq{Hq} Hk{Hk} D{D} L{L} R{Rw} chunk{chunk}")
+    return out
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("B,Hq,Hk,D,L,Rw", [
+    (2, 8, 2, 128, 256 + 128, 128),     # kivi_latency.py integrity-gate shape (:104-110)
+    (1, 7, 1, 128, 2048 + 64, 64),
+    (2, 4, 4, 64, 1024 + 32, 32),       # D = 64, G = 1
+    (1, 20, 1, 128, 640, 0),            # no residual, two head blocks
+    (1, 4, 2, 128, 128, 128),           # residual only (Sq = 0)
+])
+def test_decode_small(dev, bits, B, Hq, Hk, D, L, Rw):
+    _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_fallback_shape(dev, bits):
+    # Sq = 96 is not a multiple of the 64-token tile: GPU dequant + dense kernel path
+    _decode_case(dev, bits, 1, 4, 2, 128, 96 + 16, 16, seed=3)
+
+
+@pytest.mark.parametrize("chunk", [256, 512])
+def test_decode_split_counts(dev, chunk):
+    _decode_case(dev, 2, 1, 7, 1, 128, 4096 + 128, 128, seed=4, chunk=chunk)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_c2_full(dev, bits):
+    """BASELINE C2: B=4, Hq=28, Hkv=4, D=128, L=16384, residual 128, outlier key channels x8."""
+    raw = W.kivi_raw(seed=0)
+    g = _to(W.kivi_pack_inputs(_to(raw, dev), K.quantize_and_pack_along_last_dim, bits), dev)
+    out = K.kivi_decode_attn(*[g[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale",
+                                              "V_mn", "V_residual")], bits)
+    cpu = _to(g, "cpu")
+    ref = R.kivi_decode_attn(*[cpu[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale",
+                                                 "V_mn", "V_residual")], bits)
+    _check(out, ref, f"C2 kivi{bits}")
+    # the GPU pack of the full cache is bit-identical to the oracle's
+    ref_pack = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, bits)
+    for n in ("Kq", "Vq"):
+        assert torch.equal(cpu[n], ref_pack[n]), n
+    for n in ("K_scale", "K_mn", "V_scale", "V_mn"):
+        assert torch.equal(cpu[n].view(torch.int16), ref_pack[n].view(torch.int16)), n
+    # deterministic
+    out2 = K.kivi_decode_attn(*[g[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale",
+                                               "V_mn", "V_residual")], bits)
+    assert torch.equal(out, out2)
