@@ -130,9 +130,36 @@ class KiviCase(Case):
                 lambda: R.kivi_decode_attn(*args, self.bits, 32), units)
 
 
+class CopyCase(Case):
+    """Plain device copy of known size: the calibration point for HBM byte counters
+    (FETCH_SIZE / WRITE_SIZE of this kernel vs its exact 2 x nbytes traffic)."""
+    kernel = "elementwise_kernel"
+    dtype = "u8"
+
+    def __init__(self, name, nbytes):
+        self.name, self.nbytes = name, nbytes
+        self.workload = f"device copy {nbytes >> 20} MiB (counter calibration)"
+
+    def bytes_per_step(self):
+        return 2 * self.nbytes
+
+    def make(self, dev):
+        return {"src": torch.randint(0, 255, (self.nbytes,), dtype=torch.uint8, device=dev),
+                "dst": torch.empty(self.nbytes, dtype=torch.uint8, device=dev)}
+
+    def step(self, inp):
+        return inp["dst"].copy_(inp["src"])
+
+    def cpu_sample(self):
+        src = torch.randint(0, 255, (self.nbytes // 16,), dtype=torch.uint8)
+        dst = torch.empty_like(src)
+        return f"copy of {self.nbytes // 16} bytes", lambda: dst.copy_(src), 16
+
+
 def cases():
     from bytes_amd import workloads as W
     return {
+        "copy_calib": CopyCase("copy_calib", 256 << 20),
         "c2_kivi2": KiviCase("c2_kivi2", 2),
         "c2_kivi4": KiviCase("c2_kivi4", 4),
         "c1_dense": DenseCase("c1_dense", *W.SHAPES["c1_dense"]),
@@ -249,7 +276,7 @@ def main():
     if args.all:
         per = {}
         for name, c in allc.items():
-            if name == head.name:
+            if name in (head.name, "copy_calib"):
                 continue
             rr = time_gpu(c, min(args.steps, 100), args.warmup, dev)
             a = rr["bytes_per_step"] / (rr["ms_per_step"] * 1e-3)

@@ -38,7 +38,8 @@ __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(Dense
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int split = blockIdx.x, unit = blockIdx.y;
+  int unit, split;
+  xcd_unit_split(a.o.nsplit, unit, split);
   const int b = unit / (a.Hk * a.HB);
   const int rem = unit - b * a.Hk * a.HB;
   const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
@@ -129,8 +130,8 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
   a.o.out_dtype = kOutBF16;
   a.o.o_sb = o_sb; a.o.o_sh = o_sh;
   a.o.Hk = Hk; a.o.HB = HB; a.o.G = G;
-  splitk_carve(workspace, units, ns, a.o);
-  dim3 grid(ns, (unsigned)units);
+  splitk_carve(workspace, units, ns, a.o, /*allow_fused=*/false);
+  dim3 grid((unsigned)(ns * units));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64)
     hipLaunchKernelGGL(dense_decode_kernel<64>, grid, dim3(kDenseWaves * 64), 0, st, a);

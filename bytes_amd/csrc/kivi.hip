@@ -25,7 +25,8 @@
 //    turn into exact fp16 codes; one v_pk_fma_f16 applies scale and zero;
 //  * S^T = K_dq Q^T and O^T += V_dq^T P^T run on v_mfma_f32_16x16x32_f16 with
 //    fp32 accumulation and an fp32 online softmax.
-// The bf16 residual window is one extra split handled by the dense tile loop.
+// The bf16 residual window is handled by the last split's waves with the dense
+// tile loop, ahead of that split's quantized chunk.
 #include "dense_tile.h"
 
 namespace bytes_amd {
@@ -383,7 +384,8 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int split = blockIdx.x, unit = blockIdx.y;
+  int unit, split;
+  xcd_unit_split(a.o.nsplit, unit, split);
   const int b = unit / (a.Hk * a.HB);
   const int rem = unit - b * a.Hk * a.HB;
   const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
@@ -396,116 +398,139 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (split == a.nsq) {
-    // bf16 residual window: dense tiles over [0, R)
+  // The bf16 residual window [0, R) rides on the last split, ahead of its
+  // quantized chunk: dense tiles first, then (2-bit) the accumulator is moved
+  // to the 2-bit value layout so the quantized tiles continue the same state.
+  if (split == a.o.nsplit - 1 && a.R > 0) {
     bf16x8 qb[D / 32];
     load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
     const uint16_t* kbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
     const uint16_t* vbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
-    dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, 0, a.R, w, lane, a.scale_log2, qb,
-                       smem_raw + w * DenseCfg<D>::WAVE, m_run, l_run, acc);
-    splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b,
-                                   hq0, nh, kDmapDense);
-    return;
+    char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
+    dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, 0, a.R, w, lane, a.scale_log2, qb, wbuf, m_run, l_run,
+                       acc);
+    if (BITS == 2) {
+      static_assert(D * 16 * 4 <= DenseCfg<D>::WAVE, "relayout buffer fits the wave's tile buffers");
+      float* buf = reinterpret_cast<float*>(wbuf);
+      wave_lds_sync();
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) buf[(db * 16 + lg * 4 + i) * 16 + l16] = acc[db][i];
+      wave_lds_sync();
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[db][i] = buf[acc_d(kDmapKivi2, db, lg, i) * 16 + l16];
+    }
+    __syncthreads();   // the key chunk below reuses this LDS
   }
 
   const int Sq = a.Sq;
   const int t_begin = split * a.chunk;
   const int t_end = min(t_begin + a.chunk, Sq);
-  const int g_lo = t_begin >> 5;
-  const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
-  const int64_t bh = (int64_t)b * a.Hk + hk;
-  const int ngk = Sq >> 5;
+  if (t_begin < t_end) {
+    const int g_lo = t_begin >> 5;
+    const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
+    const int64_t bh = (int64_t)b * a.Hk + hk;
+    const int ngk = Sq >> 5;
 
-  char* kchunk = smem_raw;
-  char* kmeta = smem_raw + C::KCBYTES;
-  char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;
-  char* vml = vst + C::VBYTES;
+    char* kchunk = smem_raw;
+    char* kmeta = smem_raw + C::KCBYTES;
+    char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;
+    char* vml = vst + C::VBYTES;
 
-  const uint32_t* vqb = a.vq + bh * (int64_t)Sq * (D * BITS / 32);
-  const _Float16* vsb = a.vs + bh * (int64_t)Sq * C::NGV;
-  const _Float16* vmb = a.vm + bh * (int64_t)Sq * C::NGV;
+    const uint32_t* vqb = a.vq + bh * (int64_t)Sq * (D * BITS / 32);
+    const _Float16* vsb = a.vs + bh * (int64_t)Sq * C::NGV;
+    const _Float16* vmb = a.vm + bh * (int64_t)Sq * C::NGV;
 
-  // First value tile of this wave: in flight while the key chunk is staged.
-  constexpr int STEP = kKiviWaves * kKiviTile;
-  int t = t_begin + w * kKiviTile;
-  KiviRegs<D, BITS> rg;
-  kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg);
-
-  // Q as the fp16 B operand (scaled by scale*log2e):
-  //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
-  f16x8 qh[D / 32];
-  {
-    const bool live = l16 < nh;
-    const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * a.q_sh + lg * (D / 4);
+    // Every value tile of this wave (a chunk holds at most two per wave) is
+    // requested up front, so it is in flight while the key chunk is staged.
+    constexpr int STEP = kKiviWaves * kKiviTile;
+    constexpr int NTW = kKiviChunkMax / STEP;
+    const int tw = t_begin + w * kKiviTile;
+    KiviRegs<D, BITS> rg[NTW];
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) {
-      u32x4 raw = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
-      const bf16x8 qv = __builtin_bit_cast(bf16x8, raw);
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
+    for (int it = 0; it < NTW; ++it) {
+      const int t = tw + it * STEP;
+      kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[it]);
     }
-  }
 
-  // Stage the chunk's key codes: channel rows of (t_end - t_begin)*BITS/8 bytes,
-  // consecutive threads covering consecutive 16-byte pieces of a row, so every
-  // request is a whole cache line.
-  {
-    constexpr int NT = kKiviWaves * 64;
-    constexpr int PER = D * C::KPIECES / NT;
-    const int pieces = (t_end - t_begin) * BITS / 128;
-    const uint32_t* kqb = a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32;
-    const int64_t wk = Sq * BITS / 32;
-    u32x4 kv[PER];
+    // Q as the fp16 B operand (scaled by scale*log2e):
+    //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
+    f16x8 qh[D / 32];
+    {
+      const bool live = l16 < nh;
+      const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * a.q_sh + lg * (D / 4);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int pc = threadIdx.x + NT * i;
-      const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
-      kv[i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
-    }
-    // key scales/zeros: rows (sm, ch) of ngs fp16, two groups per 4-byte load
-    constexpr int WR = C::KMG / 2;
-    constexpr int PERM = 2 * D * WR / NT;
-    const int nwr = ngs >> 1;
-    uint32_t mv[PERM];
+      for (int kk = 0; kk < D / 32; ++kk) {
+        u32x4 raw = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
+        const bf16x8 qv = __builtin_bit_cast(bf16x8, raw);
 #pragma unroll
-    for (int i = 0; i < PERM; ++i) {
-      const int pc = threadIdx.x + NT * i;
-      const int row = pc / WR, wi = pc - row * WR;
-      const int sm = row / D, ch = row - sm * D;
-      const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? a.km : a.ks) + (bh * D + ch) * ngk + g_lo);
-      mv[i] = src[min(wi, nwr - 1)];
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int pc = threadIdx.x + NT * i;
-      const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
-      if (q < pieces) *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[i];
-    }
-    _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
-#pragma unroll
-    for (int i = 0; i < PERM; ++i) {
-      const int pc = threadIdx.x + NT * i;
-      const int row = pc / WR, wi = pc - row * WR;
-      const int sm = row / D, ch = row - sm * D;
-      if (wi < nwr) {
-        _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
-        dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] & 0xFFFFu));
-        dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] >> 16));
+        for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
       }
     }
-  }
-  __syncthreads();
 
-  // One register set per wave: staged into LDS at the top of each tile, then
-  // refilled with the next tile, so one tile's values are always in flight.
-  for (; t < t_end; t += STEP) {
-    wave_lds_sync();
-    kivi_stage<D, BITS>(lane, rg, vst, vml);
-    kivi_issue<D, BITS>(vqb, vsb, vmb, t + STEP < t_end ? t + STEP : 0, t + STEP < t_end, lane, rg);
-    wave_lds_sync();
-    const int off = t - t_begin;
-    kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
+    // Stage the chunk's key codes: channel rows of (t_end - t_begin)*BITS/8 bytes,
+    // consecutive threads covering consecutive 16-byte pieces of a row, so every
+    // request is a whole cache line.
+    {
+      constexpr int NT = kKiviWaves * 64;
+      constexpr int PER = D * C::KPIECES / NT;
+      const int pieces = (t_end - t_begin) * BITS / 128;
+      const uint32_t* kqb = a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32;
+      const int64_t wk = Sq * BITS / 32;
+      u32x4 kv[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int pc = threadIdx.x + NT * i;
+        const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
+        kv[i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
+      }
+      // key scales/zeros: rows (sm, ch) of ngs fp16, two groups per 4-byte load
+      constexpr int WR = C::KMG / 2;
+      constexpr int PERM = 2 * D * WR / NT;
+      const int nwr = ngs >> 1;
+      uint32_t mv[PERM];
+#pragma unroll
+      for (int i = 0; i < PERM; ++i) {
+        const int pc = threadIdx.x + NT * i;
+        const int row = pc / WR, wi = pc - row * WR;
+        const int sm = row / D, ch = row - sm * D;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? a.km : a.ks) + (bh * D + ch) * ngk + g_lo);
+        mv[i] = src[min(wi, nwr - 1)];
+      }
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int pc = threadIdx.x + NT * i;
+        const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
+        if (q < pieces) *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[i];
+      }
+      _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
+#pragma unroll
+      for (int i = 0; i < PERM; ++i) {
+        const int pc = threadIdx.x + NT * i;
+        const int row = pc / WR, wi = pc - row * WR;
+        const int sm = row / D, ch = row - sm * D;
+        if (wi < nwr) {
+          _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
+          dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] & 0xFFFFu));
+          dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] >> 16));
+        }
+      }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int it = 0; it < NTW; ++it) {
+      const int t = tw + it * STEP;
+      if (t >= t_end) break;
+      wave_lds_sync();
+      kivi_stage<D, BITS>(lane, rg[it], vst, vml);
+      wave_lds_sync();
+      const int off = t - t_begin;
+      kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
+    }
   }
   splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
                                  nh, BITS == 2 ? kDmapKivi2 : kDmapDense);
@@ -573,7 +598,7 @@ int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D
   const long units = (long)B * Hk * HB;
   int chunk, nsq;
   kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq);
-  *bytes = splitk_workspace_bytes(units, nsq + (R > 0 ? 1 : 0), D);
+  *bytes = splitk_workspace_bytes(units, nsq > 0 ? nsq : 1, D);
   return 0;
 }
 
@@ -610,7 +635,7 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.Hk = Hk; a.G = G; a.HB = HB; a.Sq = Sq; a.R = R;
   a.scale_log2 = scale * kLog2e;
   kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq);
-  const int ns = a.nsq + (R > 0 ? 1 : 0);
+  const int ns = a.nsq > 0 ? a.nsq : 1;
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
   a.o.out = out;
@@ -619,7 +644,7 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.o.Hk = Hk; a.o.HB = HB; a.o.G = G;
   splitk_carve(workspace, units, ns, a.o);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid(ns, (unsigned)units), block(kKiviWaves * 64);
+  dim3 grid((unsigned)(ns * units)), block(kKiviWaves * 64);
   if (D == 128 && bits == 2)
     hipLaunchKernelGGL((kivi_decode_kernel<128, 2>), grid, block, 0, st, a);
   else if (D == 128 && bits == 4)

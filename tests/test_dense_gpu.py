@@ -77,3 +77,42 @@ def test_dense_rejects_bad_input(dev):
         AK.decode_attn_bf16(q.float(), k[:, :2], k[:, :2])          # dtype
     with pytest.raises(ValueError):
         AK.decode_attn_bf16(q, k[:, :2, :0], k[:, :2, :0])          # empty cache
+
+
+def test_dense_back_to_back_calls_share_the_workspace(dev):
+    """Consecutive calls (same plan, then a different plan) on the shared
+    workspace each match the oracle."""
+    for seed, (B, Hq, Hk, S) in enumerate([(2, 28, 4, 5000), (2, 28, 4, 5000), (3, 16, 2, 2900),
+                                           (2, 28, 4, 5000)]):
+        x = W.dense(B, Hq, Hk, 128, S, seed=100 + seed)
+        out = AK.decode_attn_bf16(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), 0.09)
+        _check(out, R.decode_attn(x["q"], x["k"], x["v"], scale=0.09), f"call {seed} B{B} S{S}")
+
+
+def test_dense_many_splits_use_the_merge_kernel(dev):
+    # chunk 128 over 40000 tokens: 313 splits, above the in-kernel merge limit
+    x = W.dense(1, 8, 1, 128, 40000, seed=9)
+    out = AK.decode_attn_bf16(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), 0.09, chunk=128)
+    _check(out, R.decode_attn(x["q"], x["k"], x["v"], scale=0.09), "313 splits")
+
+
+def test_dense_graph_replays(dev):
+    """Captured once, replayed with new input contents (eager copies and syncs in
+    between): every replay equals the eager call on the same inputs."""
+    x = W.dense(2, 14, 2, 64, 3000, seed=21)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    AK.decode_attn_bf16(q, k, v, 0.125)                      # sizes the workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = AK.decode_attn_bf16(q, k, v, 0.125)
+    torch.cuda.synchronize()
+    for it in range(3):
+        y = W.dense(2, 14, 2, 64, 3000, seed=30 + it)
+        q.copy_(y["q"].to(dev)); k.copy_(y["k"].to(dev)); v.copy_(y["v"].to(dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager = AK.decode_attn_bf16(q, k, v, 0.125)
+        assert torch.equal(out, eager), f"replay {it}"
+        _check(out, R.decode_attn(y["q"], y["k"], y["v"], scale=0.125), f"replay {it}")

@@ -107,3 +107,17 @@ def test_decode_c2_full(dev, bits):
     out2 = K.kivi_decode_attn(*[g[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale",
                                                "V_mn", "V_residual")], bits)
     assert torch.equal(out, out2)
+
+
+def test_decode_back_to_back_calls(dev):
+    """The in-kernel split merge leaves its arrival counters at zero: consecutive
+    calls with new data (and a different plan in between) on the shared
+    workspace each match the oracle."""
+    for i, (B, Hq, Hk, L, Rw) in enumerate([(2, 8, 2, 4096 + 128, 128), (2, 8, 2, 4096 + 128, 128),
+                                            (1, 7, 1, 8192 + 64, 64), (2, 8, 2, 4096 + 128, 128)]):
+        _decode_case(dev, 2 + 2 * (i % 2), B, Hq, Hk, 128, L, Rw, seed=50 + i)
+
+
+def test_decode_many_splits_use_the_merge_kernel(dev):
+    # chunk 256 over 69120 packed tokens: 270 splits, above the in-kernel merge limit
+    _decode_case(dev, 2, 1, 7, 1, 128, 69120 + 32, 32, seed=6, chunk=256)
