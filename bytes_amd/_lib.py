@@ -44,6 +44,22 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,     # k_res / v_res strides
         c_i64, c_i64,                                 # out strides
         c_f32, c_int, c_vp, c_sz, c_vp),
+    "bytes_sparse_score": (
+        c_vp, c_vp, c_vp,                             # q, k, out
+        c_int, c_int, c_int, c_int, c_int, c_int,     # B, Hq, Hk, S, D, group_sum
+        c_i64, c_i64, c_i64, c_i64, c_i64,            # q (b, h), k (b, h, s) strides
+        c_i64, c_i64,                                 # out strides (b, h)
+        c_f32, c_vp),                                 # scaling, stream
+    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_vp, c_i64, c_vp),
+    "bytes_gather_attn_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
+    "bytes_gather_attn": (
+        c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, k, v, idx, out
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int,   # B, Hq, Hk, S, D, kb, per_head
+        c_i64, c_i64,                                 # q strides
+        c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,     # k, v strides (b, h, s)
+        c_i64, c_i64,                                 # idx strides (b, h)
+        c_i64, c_i64,                                 # out strides
+        c_f32, c_int, c_vp, c_sz, c_vp),              # scaling, chunk, workspace, bytes, stream
 }
 _RESTYPES = {"bytes_error_string": ctypes.c_char_p}
 

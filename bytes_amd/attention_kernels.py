@@ -49,3 +49,8 @@ def decode_attn_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
          v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1),
          float(scale), int(chunk), ptr(ws), ws.numel(), stream_of(q))
     return out.unsqueeze(2)
+
+
+# Sparse decode operators of the same module (src/attention_kernels.py:1037-1263).
+from .sparse import (sparse_decode_scalar, sparse_gather_attn, sparse_score_scalar,  # noqa: E402,F401
+                     topk_indices)

@@ -91,9 +91,16 @@ __device__ __forceinline__ void dense_stage(int lane, const DenseRegs<D>& r, cha
   }
 }
 
-// Scores, online softmax and PV for the tile staged in kst/vst.
+// Bit j of the tile mask = tile row j (0..31) takes part in the softmax.
+__device__ __forceinline__ uint32_t range_mask(int t0, int t_end) {
+  const int n = t_end - t0;
+  return n >= 32 ? 0xFFFFFFFFu : (n <= 0 ? 0u : ((1u << n) - 1u));
+}
+
+// Scores, online softmax and PV for the tile staged in kst/vst; rows whose
+// vmask bit is clear get probability zero.
 template <int D>
-__device__ __forceinline__ void dense_compute(int t0, int t_end, float scale_log2, int lane,
+__device__ __forceinline__ void dense_compute(uint32_t vmask, float scale_log2, int lane,
                                               const bf16x8 (&qb)[D / 32], const char* kst, const char* vst,
                                               float& m_run, float& l_run, f32x4 (&acc)[D / 16]) {
   using C = DenseCfg<D>;
@@ -116,8 +123,8 @@ __device__ __forceinline__ void dense_compute(int t0, int t_end, float scale_log
   for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = t0 + blk * 16 + lg * 4 + i;
-      const float xv = t < t_end ? s[blk][i] * scale_log2 : kNegInf;
+      const int j = blk * 16 + lg * 4 + i;
+      const float xv = ((vmask >> j) & 1u) ? s[blk][i] * scale_log2 : kNegInf;
       x[blk * 4 + i] = xv;
       mx = fmaxf(mx, xv);
     }
@@ -176,7 +183,7 @@ __device__ __forceinline__ void dense_wave_loop(const uint16_t* kbase, const uin
     dense_stage<D>(lane, r, kst, vst);
     dense_issue<D>(kbase, vbase, k_ss, v_ss, S, t + STEP, t_end, lane, r);
     wave_lds_sync();
-    dense_compute<D>(t, t_end, scale_log2, lane, qb, kst, vst, m_run, l_run, acc);
+    dense_compute<D>(range_mask(t, t_end), scale_log2, lane, qb, kst, vst, m_run, l_run, acc);
   }
 }
 

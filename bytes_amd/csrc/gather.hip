@@ -1,0 +1,217 @@
+// Gather attention over selected key/value rows.
+//
+// Replaces src/attention_kernels.py:987-1059 (`sparse_gather_attn`): exact
+// fp32 online-softmax attention of each query head over the K/V rows named by
+// an index list, with the masking rule of benchmarks/sparse_attention.py:376
+// (`attend_topk`: entries outside [0, S) take no part).  Two index layouts:
+//  * per query head  idx [B, Hq, kb]  (the reference's layout): a unit is one
+//    query head;
+//  * per KV head     idx [B, Hk, kb]  (one selection shared by the GQA group,
+//    the token top-k pipeline): a unit is up to 16 query heads of one group,
+//    which share every gathered row, so one MFMA tile serves all of them.
+// The index list of a unit is cut into split-K chunks; each workgroup stages
+// its chunk's row numbers in LDS, then its waves run the dense bf16 tile loop
+// with rows fetched through that list (prefetching the next tile's rows while
+// the current tile is computed).
+#include "dense_tile.h"
+
+namespace bytes_amd {
+
+struct GatherArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint16_t* k;
+  int64_t k_sb, k_sh, k_ss;
+  const uint16_t* v;
+  int64_t v_sb, v_sh, v_ss;
+  const int32_t* idx;        // [B, Hq or Hk, kb], unit stride along kb
+  int64_t i_sb, i_sh;
+  int Hk, G, HB, S, kb, chunk, per_head;
+  float scale_log2;
+  SplitKOut o;
+};
+
+constexpr int kGatherWaves = 4;
+constexpr int kGatherChunkMax = 1024;   // index-list entries per workgroup
+
+template <int D>
+struct GatherCfg {
+  static constexpr int kRows = kGatherChunkMax * 4;
+  static constexpr int kSmem = DenseCfg<D>::kSmem + kRows;
+};
+
+// Loads of one 32-row tile whose rows are rows[j0 .. j0+31] (entries past n or
+// negative read row 0: same instructions every tile, no divergence).
+template <int D>
+__device__ __forceinline__ void gather_issue(const uint16_t* kbase, const uint16_t* vbase, int64_t k_ss,
+                                             int64_t v_ss, const int32_t* rows, int j0, int n, int lane,
+                                             DenseRegs<D>& r) {
+  using C = DenseCfg<D>;
+#pragma unroll
+  for (int i = 0; i < C::CPL; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / C::CPR, pos = p - rr * C::CPR;
+    const int j = j0 + rr;
+    int row = j < n ? rows[j] : 0;
+    row = row < 0 ? 0 : row;
+    r.k[i] = ld16(kbase + (int64_t)row * k_ss + pos * 8);
+    r.v[i] = ld16(vbase + (int64_t)row * v_ss + pos * 8);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(GatherArgs a) {
+  using C = DenseCfg<D>;
+  __shared__ __attribute__((aligned(16))) char smem_raw[GatherCfg<D>::kSmem];
+  int32_t* rows = reinterpret_cast<int32_t*>(smem_raw + C::kSmem);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int unit, split;
+  xcd_unit_split(a.o.nsplit, unit, split);
+
+  int b, hk, hq0, nh;
+  const int32_t* irow;
+  if (a.per_head) {
+    const int Hq = a.Hk * a.G;
+    b = unit / Hq;
+    const int hq = unit - b * Hq;
+    hk = hq / a.G;
+    hq0 = hq;
+    nh = 1;
+    irow = a.idx + (int64_t)b * a.i_sb + (int64_t)hq * a.i_sh;
+  } else {
+    b = unit / (a.Hk * a.HB);
+    const int rem = unit - b * a.Hk * a.HB;
+    hk = rem / a.HB;
+    const int hb = rem - hk * a.HB;
+    hq0 = hk * a.G + hb * 16;
+    nh = min(16, a.G - hb * 16);
+    irow = a.idx + (int64_t)b * a.i_sb + (int64_t)hk * a.i_sh;
+  }
+
+  const int p_begin = split * a.chunk;
+  const int n = min(a.chunk, a.kb - p_begin);
+  for (int i = threadIdx.x; i < n; i += kGatherWaves * 64) {
+    const int r = irow[p_begin + i];
+    rows[i] = (r >= 0 && r < a.S) ? r : -1;
+  }
+
+  bf16x8 qb[C::KK];
+  load_q_bf16<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, nh, lane, qb);
+  __syncthreads();
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[C::DB];
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const uint16_t* kbase = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+  const uint16_t* vbase = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  char* kst = smem_raw + w * C::WAVE;
+  char* vst = kst + C::VT;
+  constexpr int STEP = kGatherWaves * kTile;
+  int j = w * kTile;
+  if (j < n) {
+    DenseRegs<D> r;
+    gather_issue<D>(kbase, vbase, a.k_ss, a.v_ss, rows, j, n, lane, r);
+    for (; j < n; j += STEP) {
+      // rows of this tile that take part: inside the chunk and a valid index
+      const int jj = j + (lane & 31);
+      const bool ok = jj < n && rows[jj < n ? jj : 0] >= 0;
+      const uint32_t vmask = (uint32_t)__ballot(ok);
+      wave_lds_sync();
+      dense_stage<D>(lane, r, kst, vst);
+      gather_issue<D>(kbase, vbase, a.k_ss, a.v_ss, rows, j + STEP, n, lane, r);
+      wave_lds_sync();
+      dense_compute<D>(vmask, a.scale_log2, lane, qb, kst, vst, m_run, l_run, acc);
+    }
+  }
+  splitk_epilogue<D, kGatherWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
+                                   nh, kDmapDense);
+}
+
+static void gather_plan(int kb, long units, int chunk_req, int* chunk, int* ns) {
+  const int step = kGatherWaves * kTile;
+  int c;
+  if (chunk_req > 0) {
+    c = chunk_req;
+  } else {
+    const long target = 2L * device_cu_count();
+    c = (int)(((long)kb * units + target - 1) / target);
+  }
+  c = (c + step - 1) / step * step;
+  if (c < step) c = step;
+  if (c > kGatherChunkMax) c = kGatherChunkMax;
+  *chunk = c;
+  *ns = (kb + c - 1) / c;
+}
+
+static long gather_units(int B, int Hq, int Hk, int per_head) {
+  const int G = Hq / Hk, HB = (G + 15) / 16;
+  return per_head ? (long)B * Hq : (long)B * Hk * HB;
+}
+
+}  // namespace bytes_amd
+
+using namespace bytes_amd;
+
+extern "C" {
+
+int bytes_gather_attn_workspace_size(int B, int Hq, int Hk, int kb, int D, int per_head, int chunk_req,
+                                     size_t* bytes) {
+  if (!bytes || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || kb <= 0) return (int)hipErrorInvalidValue;
+  if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  const long units = gather_units(B, Hq, Hk, per_head);
+  int chunk, ns;
+  gather_plan(kb, units, chunk_req, &chunk, &ns);
+  *bytes = splitk_workspace_bytes(units, ns, D);
+  return 0;
+}
+
+int bytes_gather_attn(const void* q, const void* k, const void* v, const void* idx, void* out, int B, int Hq, int Hk,
+                      int S, int D, int kb, int per_head, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh,
+                      int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb, int64_t i_sh,
+                      int64_t o_sb, int64_t o_sh, float scaling, int chunk_req, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  if (!q || !k || !v || !idx || !out || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || S <= 0 || kb <= 0)
+    return (int)hipErrorInvalidValue;
+  if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  const long units = gather_units(B, Hq, Hk, per_head);
+  if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
+  GatherArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_sb; a.q_sh = q_sh;
+  a.k = static_cast<const uint16_t*>(k);
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
+  a.v = static_cast<const uint16_t*>(v);
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.idx = static_cast<const int32_t*>(idx);
+  a.i_sb = i_sb; a.i_sh = i_sh;
+  a.Hk = Hk; a.G = Hq / Hk; a.HB = (a.G + 15) / 16; a.S = S; a.kb = kb;
+  a.per_head = per_head ? 1 : 0;
+  a.scale_log2 = scaling * kLog2e;
+  int ns;
+  gather_plan(kb, units, chunk_req, &a.chunk, &ns);
+  if (ns > 1024) return (int)hipErrorInvalidConfiguration;
+  if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
+  a.o.out = out;
+  a.o.out_dtype = kOutBF16;
+  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
+  // the merge kernel maps unit -> (b, first query head) through (Hk, HB, G)
+  if (per_head) {
+    a.o.Hk = Hq; a.o.HB = 1; a.o.G = 1;
+  } else {
+    a.o.Hk = Hk; a.o.HB = a.HB; a.o.G = a.G;
+  }
+  splitk_carve(workspace, units, ns, a.o);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)(ns * units)), block(kGatherWaves * 64);
+  if (D == 128)
+    hipLaunchKernelGGL(gather_decode_kernel<128>, grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL(gather_decode_kernel<64>, grid, block, 0, st, a);
+  int rc = (int)hipGetLastError();
+  if (rc) return rc;
+  return splitk_combine(a.o, units, D, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,154 @@
+"""Token-level sparse decode: scoring, deterministic top-k, gather attention.
+
+Drop-in replacements for the reference's two-pass sparse decode
+(src/attention_kernels.py:987-1263) plus the group-shared token top-k
+pipeline: every score, selection and attention step is a gfx950 HIP kernel
+launched through the C ABI on the current stream.  The top-k is
+deterministic: score descending, lowest index first among equal scores.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _checks as C
+from ._lib import HIP_ERROR_NOT_SUPPORTED, call, lib, ptr, size_query, stream_of, workspace
+
+TOPK_MAX = 8192
+
+
+def _qk_shapes(q: torch.Tensor, k: torch.Tensor):
+    C.cuda_tensors(q, k)
+    C.ndim(q, 4, "q"), C.ndim(k, 4, "k")
+    C.dtype_in(q, "q", torch.bfloat16)
+    B, Hq, one, D = q.shape
+    Bk, Hk, S, Dk = k.shape
+    if one != 1 or Dk != D or Bk != B:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}")
+    if Hq % Hk != 0:
+        raise ValueError(f"H_q={Hq} is not a multiple of H_k={Hk}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if S == 0:
+        raise ValueError("empty KV cache (S == 0)")
+    return B, Hq, Hk, S, D
+
+
+def _score(q, k_score, scaling, group_sum: bool) -> torch.Tensor:
+    B, Hq, Hk, S, D = _qk_shapes(q, k_score)
+    if k_score.dtype != torch.bfloat16:
+        raise ValueError(f"k_score: dtype {k_score.dtype} not supported (bf16)")
+    if group_sum and Hq // Hk > 16:
+        raise ValueError("group-summed scores support query groups of at most 16 heads")
+    qs = C.rows16(q.squeeze(2))
+    k = C.rows16(k_score)
+    H = Hk if group_sum else Hq
+    out = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    call("bytes_sparse_score", ptr(qs), ptr(k), ptr(out), B, Hq, Hk, S, D, int(group_sum),
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), out.stride(0), out.stride(1),
+         float(scaling), stream_of(q))
+    return out
+
+
+def sparse_score_scalar(q: torch.Tensor, k_score: torch.Tensor, scaling: float, *, score_bits: int = 16,
+                        BLOCK_N: int = 128) -> torch.Tensor:
+    """Pass 1: fp32 scores[b, h, t] = (q[b, h] . k[b, h // G, t]) * scaling.
+
+    Replaces src/attention_kernels.py:1113-1133.  q [B,H_q,1,D] bf16;
+    k_score [B,H_k,S,D] bf16.  Returns [B,H_q,S] fp32.
+    """
+    if score_bits != 16:
+        raise ValueError(f"score_bits={score_bits}: bf16 score keys (16) only")
+    return _score(q, k_score, scaling, group_sum=False)
+
+
+def group_scores(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tensor:
+    """Selection score of each KV head, summed over its query group:
+    s[b, hk, t] = sum_{g < G} (q[b, hk*G + g] . k[b, hk, t]) * scaling.
+    Returns [B,H_k,S] fp32."""
+    return _score(q, k, scaling, group_sum=True)
+
+
+def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Indices of the k largest scores per row of [..., n] fp32, ordered by score
+    descending, lowest index first among equal scores (+0 == -0; NaN ranks
+    above +inf).  Returns int32 [..., k].  Replaces `scores.topk(k).indices`
+    (src/attention_kernels.py:1262) with a deterministic tie rule."""
+    C.cuda_tensors(scores)
+    C.dtype_in(scores, "scores", torch.float32)
+    n = scores.shape[-1]
+    if not 1 <= k <= n:
+        raise ValueError(f"k={k} outside [1, {n}]")
+    if k > TOPK_MAX:
+        raise ValueError(f"k={k} above the supported maximum {TOPK_MAX}")
+    s = scores.reshape(-1, n)
+    if s.stride(-1) != 1:
+        s = s.contiguous()
+    rows = s.shape[0]
+    out = torch.empty((rows, k), dtype=torch.int32, device=scores.device)
+    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), ptr(out), out.stride(0), stream_of(scores))
+    return out.reshape(*scores.shape[:-1], k)
+
+
+def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor, scaling: float,
+                       BLOCK_K: int = 64, *, chunk: int = 0) -> torch.Tensor:
+    """Pass 2: exact attention over the gathered rows.
+
+    Replaces src/attention_kernels.py:1037-1059.  q [B,H_q,1,D] bf16; k, v
+    [B,H_k,S,D] bf16; idx [B,H_q,kb] (per query head, the reference layout) or
+    [B,H_k,kb] (one selection per KV head, shared by its query group), any
+    integer dtype.  Entries outside [0, S) are masked (sentinel rule of
+    benchmarks/sparse_attention.py:376).  Returns [B,H_q,1,D] bf16.
+    """
+    B, Hq, Hk, S, D = _qk_shapes(q, k)
+    C.cuda_tensors(q, v, idx)
+    C.dtype_in(k, "k", torch.bfloat16)
+    C.dtype_in(v, "v", torch.bfloat16)
+    if tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"shape mismatch: k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if idx.dim() != 3 or idx.shape[0] != B or idx.shape[1] not in (Hq, Hk):
+        raise ValueError(f"idx must be [B, H_q or H_k, kb]; got {tuple(idx.shape)}")
+    kb = idx.shape[-1]
+    if kb == 0:
+        raise ValueError("empty index list")
+    per_head = 1 if idx.shape[1] == Hq else 0
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if idx.stride(-1) != 1:
+        idx = idx.contiguous()
+    qs = C.rows16(q.squeeze(2))
+    k, v = C.rows16(k), C.rows16(v)
+    out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=q.device)
+    nbytes = size_query("bytes_gather_attn_workspace_size", B, Hq, Hk, kb, D, per_head, int(chunk))
+    ws = workspace(q.device, nbytes)
+    call("bytes_gather_attn", ptr(qs), ptr(k), ptr(v), ptr(idx), ptr(out), B, Hq, Hk, S, D, kb, per_head,
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
+         idx.stride(0), idx.stride(1), out.stride(0), out.stride(1), float(scaling), int(chunk), ptr(ws),
+         ws.numel(), stream_of(q))
+    return out.unsqueeze(2)
+
+
+def budget(frac: float, S: int) -> int:
+    """kb = max(1, round(frac * S)), as src/attention_kernels.py:1261."""
+    return max(1, int(round(frac * S)))
+
+
+def sparse_decode_scalar(q, k_score_or_packed, scale, zero, k_val, v_val, frac, scaling, *, score_bits,
+                         group_size=32, BLOCK_N=128, BLOCK_K=64):
+    """Two-pass sparse decode: score every key, keep the top kb = max(1, round(frac*S))
+    per query head, attend exactly over them.  Replaces
+    src/attention_kernels.py:1252-1263 for bf16 score keys (score_bits=16);
+    `scale`/`zero`/`group_size` belong to the packed-score variant.
+    Returns [B,H_q,1,D] bf16."""
+    scores = sparse_score_scalar(q, k_score_or_packed, scaling, score_bits=score_bits)
+    kb = budget(frac, scores.shape[-1])
+    idx = topk_indices(scores, kb)
+    return sparse_gather_attn(q, k_val, v_val, idx, scaling)
+
+
+def token_topk_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float):
+    """Group-shared token top-k decode: group-summed fp32 scores per KV head,
+    the kb best tokens per (b, KV head), attention of every query head of the
+    group over them.  Returns (out [B,H_q,1,D] bf16, idx [B,H_k,kb] int32)."""
+    s = group_scores(q, k, scaling)
+    idx = topk_indices(s, kb)
+    return sparse_gather_attn(q, k, v, idx, scaling), idx

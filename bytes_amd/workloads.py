@@ -83,3 +83,17 @@ def kivi_pack_inputs(raw: Dict, pack_fn, bits: int, group_size: int = 32) -> Dic
     return {"Q": raw["q"], "Kq": kq, "K_scale": ks, "K_mn": km, "K_residual": k[:, :, Sq:],
             "Vq": vq, "V_scale": vs, "V_mn": vm, "V_residual": v[:, :, Sq:], "bits": bits,
             "group_size": group_size}
+
+
+def c5_topk(seed: int = 0, device="cpu", B: int = 8, Hq: int = 24, Hk: int = 8, D: int = 128,
+            L: int = 131072) -> Dict:
+    """BASELINE C5 inputs: q, K, V ~ N(0,1) bf16.  Drawn on `device` from a
+    generator seeded there (the full-size cache is 2 GiB per tensor, so it is
+    generated where it is used)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    q = torch.randn(B, Hq, 1, D, generator=g, device=device, dtype=torch.bfloat16)
+    k = torch.randn(B, Hk, L, D, generator=g, device=device, dtype=torch.bfloat16)
+    v = torch.randn(B, Hk, L, D, generator=g, device=device, dtype=torch.bfloat16)
+    return {"q": q, "k": k, "v": v, "scale": 1.0 / math.sqrt(D),
+            "meta": {"seed": seed, "shape": (B, Hq, Hk, D, L), "generator": str(torch.device(device))}}

@@ -104,6 +104,52 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
                            int64_t o_sh, float scale, int chunk, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Token scoring.
+ * Replaces src/attention_kernels.py:1113-1133 (`sparse_score_scalar`, kernel
+ * :1077-1110) for bf16 keys:
+ *   group_sum = 0: out [B, Hq, S] fp32, out[b,h,t] = (q[b,h] . k[b,h/G,t]) * scaling
+ *   group_sum = 1: out [B, Hk, S] fp32, out[b,hk,t] = sum_{g<G} (q[b,hk*G+g] . k[b,hk,t]) * scaling
+ *                  (the per-KV-head selection score of the token top-k path; G <= 16)
+ *   q [B, Hq, D] bf16 (strides q_sb, q_sh); k [B, Hk, S, D] bf16 (strides k_*);
+ *   out strides o_sb, o_sh (unit stride along S).  D in {64, 128}.
+ * ------------------------------------------------------------------------- */
+int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, int Hk, int S, int D,
+                       int group_sum, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                       int64_t o_sb, int64_t o_sh, float scaling, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Deterministic top-k per row.
+ * Replaces `scores.topk(kb, dim=-1).indices` (src/attention_kernels.py:1262,
+ * benchmarks/sparse_attention.py:307,358; selection semantics of
+ * `select_topk` :226-325) with one total order: score descending, lowest index
+ * first among equal scores, +0 == -0, NaN above +inf.
+ *   scores [rows, n] fp32 (row stride row_stride, unit stride along n)
+ *   out    [rows, k] int32 (row stride out_stride), ordered by that order.
+ * 1 <= k <= min(n, 8192); larger k returns hipErrorNotSupported.
+ * ------------------------------------------------------------------------- */
+int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, void* out,
+               int64_t out_stride, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Gather attention over selected rows.
+ * Replaces src/attention_kernels.py:1037-1059 (`sparse_gather_attn`, kernel
+ * :987-1034) with the masking of benchmarks/sparse_attention.py:367-387:
+ *   out[b,h] = softmax_j(scaling * q[b,h] . k[b,h/G,idx_j]) v[b,h/G,idx_j]
+ * over the kb entries idx_j in [0, S); other entries are ignored.
+ *   per_head = 1: idx [B, Hq, kb] int32 (one list per query head, the reference layout)
+ *   per_head = 0: idx [B, Hk, kb] int32 (one list per KV head, shared by its G query heads)
+ *   idx strides i_sb, i_sh (unit stride along kb); k, v [B, Hk, S, D] bf16;
+ *   out [B, Hq, D] bf16.  D in {64, 128}.
+ * ------------------------------------------------------------------------- */
+int bytes_gather_attn_workspace_size(int B, int Hq, int Hk, int kb, int D, int per_head, int chunk,
+                                     size_t* bytes);
+int bytes_gather_attn(const void* q, const void* k, const void* v, const void* idx, void* out, int B, int Hq,
+                      int Hk, int S, int D, int kb, int per_head, int64_t q_sb, int64_t q_sh, int64_t k_sb,
+                      int64_t k_sh, int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb,
+                      int64_t i_sh, int64_t o_sb, int64_t o_sh, float scaling, int chunk, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -1,0 +1,155 @@
+"""Token scoring, deterministic top-k and gather attention vs the CPU oracle.
+
+Scores and attention outputs: north_star tolerance (fp32 scores compared to
+1e-3 absolute); top-k indices: bit-exact against the oracle run on the same
+fp32 scores.
+"""
+import math
+
+import pytest
+import torch
+
+from bytes_amd import sparse as SP
+from bytes_amd import workloads as W
+from oracle import reference as R
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+SCORE_TOL = 1e-3
+pytestmark = pytest.mark.gpu
+
+
+def _check(out, ref, tag):
+    d = (out.float().cpu() - ref.float()).abs()
+    print(f"{tag}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}", flush=True)
+    assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, tag
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D", [(2, 8, 2, 1000, 128), (1, 24, 8, 4099, 128), (2, 4, 4, 300, 64),
+                                          (1, 40, 2, 777, 128)])
+def test_score_per_head(dev, B, Hq, Hk, S, D):
+    x = W.dense(B, Hq, Hk, D, S, seed=S)
+    s = SP.sparse_score_scalar(x["q"].to(dev), x["k"].to(dev), 0.088)
+    ref = R.sparse_score_scalar(x["q"], x["k"], 0.088)
+    assert s.shape == (B, Hq, S) and s.dtype == torch.float32
+    assert (s.cpu() - ref).abs().max() <= SCORE_TOL
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S", [(2, 24, 8, 5000), (1, 4, 1, 129), (1, 32, 2, 1024)])
+def test_group_scores(dev, B, Hq, Hk, S):
+    x = W.dense(B, Hq, Hk, 128, S, seed=S + 1)
+    s = SP.group_scores(x["q"].to(dev), x["k"].to(dev), 0.088)
+    ref = R.group_scores(x["q"], x["k"], 0.088)
+    assert s.shape == (B, Hk, S)
+    assert (s.cpu() - ref).abs().max() <= SCORE_TOL
+
+
+def _tie_heavy(rows, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randint(-8, 8, (rows, n), generator=g).float() * 0.25      # many exact ties
+    s[0, ::7] = 0.0
+    s[0, 1::7] = -0.0
+    if rows > 1:
+        s[1, 5] = float("nan")
+        s[1, 9] = float("-nan")
+        s[1, 11] = float("inf")
+        s[1, 12] = float("-inf")
+    return s
+
+
+@pytest.mark.parametrize("rows,n,k", [(3, 1000, 1), (3, 1000, 17), (4, 4096, 256), (2, 1001, 1001),
+                                      (5, 333, 100), (28, 2048, 128), (2, 20000, 8192)])
+def test_topk_bit_exact_with_ties(dev, rows, n, k):
+    s = _tie_heavy(rows, n, seed=n + k)
+    got = SP.topk_indices(s.to(dev), k).cpu()
+    ref = R.topk_indices(s, k)
+    assert got.dtype == torch.int32
+    assert torch.equal(got.long(), ref)
+
+
+def test_topk_unaligned_rows(dev):
+    s = _tie_heavy(6, 2051, seed=3)
+    big = torch.zeros(6 * 2051 + 1)
+    big[1:] = s.reshape(-1)
+    view = big.to(dev)[1:].reshape(6, 2051)                # rows not 16-byte aligned
+    assert torch.equal(SP.topk_indices(view, 300).cpu().long(), R.topk_indices(s, 300))
+
+
+@pytest.mark.parametrize("k", [256, 1024, 4096])
+def test_topk_c5_rows(dev, k):
+    """64 rows x 131072 fp32 (BASELINE C5 selection shape)."""
+    g = torch.Generator().manual_seed(k)
+    s = torch.randn(64, 131072, generator=g)
+    s[3, 1000:1100] = 5.0                                   # a tied block straddling the boundary
+    got = SP.topk_indices(s.to(dev), k).cpu().long()
+    assert torch.equal(got, R.topk_indices(s, k))
+
+
+def _gather_case(dev, B, Hq, Hk, S, D, kb, per_head, seed, chunk=0):
+    x = W.dense(B, Hq, Hk, D, S, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    H = Hq if per_head else Hk
+    idx = torch.randint(0, S, (B, H, kb), generator=g)
+    idx[..., ::13] = -1                                     # masked entries
+    idx[..., 1::29] = S                                     # sentinel (unfilled slot)
+    if kb > 4:
+        idx[..., 2] = idx[..., 4]                           # a repeated row counts twice
+    out = SP.sparse_gather_attn(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), idx.to(dev), 0.09, chunk=chunk)
+    ref = R.sparse_gather_attn(x["q"], x["k"], x["v"], idx, 0.09)
+    assert out.shape == (B, Hq, 1, D) and out.dtype == torch.bfloat16
+    _check(out, ref, f"gather B{B} Hq{Hq} Hk{Hk} S{S} D{D} kb{kb} per_head{per_head} chunk{chunk}")
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D,kb", [(2, 8, 2, 2000, 128, 100), (1, 24, 8, 5000, 128, 1000),
+                                             (1, 7, 1, 300, 64, 31), (2, 28, 4, 4096, 128, 2048)])
+@pytest.mark.parametrize("per_head", [1, 0])
+def test_gather_matches_oracle(dev, B, Hq, Hk, S, D, kb, per_head):
+    _gather_case(dev, B, Hq, Hk, S, D, kb, per_head, seed=kb + per_head)
+
+
+@pytest.mark.parametrize("chunk", [128, 1024])
+def test_gather_split_counts(dev, chunk):
+    _gather_case(dev, 1, 8, 2, 40000, 128, 37000, 0, seed=7, chunk=chunk)     # 290 / 37 splits
+
+
+def test_gather_single_valid_row(dev):
+    x = W.dense(1, 4, 1, 128, 64, seed=1)
+    idx = torch.full((1, 1, 40), -1)
+    idx[0, 0, 17] = 5
+    out = SP.sparse_gather_attn(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), idx.to(dev), 0.1)
+    # one row survives the mask: the output is that value row for every head
+    assert torch.allclose(out.cpu().float()[0, :, 0], x["v"][0, 0, 5].float().expand(4, -1), atol=1e-2)
+
+
+@pytest.mark.parametrize("frac", [0.05, 0.25])
+def test_sparse_decode_scalar_pipeline(dev, frac):
+    x = W.dense(2, 8, 2, 128, 3000, seed=11)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    sc = 1 / math.sqrt(128)
+    out = SP.sparse_decode_scalar(q, k, None, None, k, v, frac, sc, score_bits=16)
+    ref = R.sparse_decode_scalar(x["q"], x["k"], x["k"], x["v"], frac, sc)
+    _check(out, ref, f"sparse_decode_scalar frac {frac}")
+    # selection is bit-exact given the same fp32 scores
+    s = SP.sparse_score_scalar(q, k, sc)
+    kb = SP.budget(frac, 3000)
+    assert torch.equal(SP.topk_indices(s, kb).cpu().long(), R.topk_indices(s.cpu(), kb))
+
+
+@pytest.mark.parametrize("kb", [256, 1024, 4096])
+def test_token_topk_c5_full(dev, kb):
+    """BASELINE C5 at full size: B8 Hq24 Hkv8 D128 L131072."""
+    x = W.c5_topk(seed=0, device=dev)
+    q, k, v = x["q"], x["k"], x["v"]
+    sc = x["scale"]
+    out, idx = SP.token_topk_decode(q, k, v, kb, sc)
+    # scores of batch 0 against the oracle
+    s = SP.group_scores(q, k, sc)
+    ref_s0 = R.group_scores(q[:1].cpu(), k[:1].cpu(), sc)
+    assert (s[:1].cpu() - ref_s0).abs().max() <= SCORE_TOL
+    # selection bit-exact on the same scores
+    ref_idx = R.topk_indices(s.cpu(), kb)
+    assert torch.equal(idx.cpu().long(), ref_idx)
+    # attention over the selected rows: dense oracle on the gathered rows
+    B, Hk = k.shape[:2]
+    gi = idx.long().unsqueeze(-1).expand(B, Hk, kb, k.shape[-1])
+    ks, vs = torch.gather(k, 2, gi).cpu(), torch.gather(v, 2, gi).cpu()
+    _check(out, R.decode_attn(q.cpu(), ks, vs, scale=sc), f"C5 kb{kb}")
