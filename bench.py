@@ -66,6 +66,10 @@ class DenseCase(Case):
 
     def make(self, dev):
         from bytes_amd import workloads as W
+        B, Hq, Hk, D, L = self.shape
+        if B * Hk * L * D > (1 << 28):       # multi-GiB caches are drawn on the device
+            x = W.c5_topk(seed=0, device=dev, B=B, Hq=Hq, Hk=Hk, D=D, L=L)
+            return {"q": x["q"], "k": x["k"], "v": x["v"], "scale": x["scale"]}
         x = W.dense(*self.shape, seed=0, device="cpu")
         return {"q": x["q"].to(dev), "k": x["k"].to(dev), "v": x["v"].to(dev), "scale": x["scale"]}
 
@@ -130,6 +134,48 @@ class KiviCase(Case):
                 lambda: R.kivi_decode_attn(*args, self.bits, 32), units)
 
 
+class TopkCase(Case):
+    """BASELINE C5: group-summed fp32 scores per KV head over the whole cache,
+    deterministic top-k per (b, KV head), gathered bf16 attention for every
+    query head of the group.  One step = score + top-k + gather."""
+    kernel = "score_kernel"
+
+    def __init__(self, name, kb, B=8, Hq=24, Hk=8, D=128, L=131072):
+        self.name, self.kb, self.shape = name, kb, (B, Hq, Hk, D, L)
+        self.workload = f"token top-k decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} k={kb} (group-summed scores)"
+
+    def bytes_per_step(self):
+        B, Hq, Hk, D, L = self.shape
+        keys = B * Hk * L * D * 2                 # score pass reads every key once
+        scores = B * Hk * L * 4 * 2               # fp32 scores written, read by the top-k
+        gather = 2 * B * Hk * self.kb * D * 2     # selected K and V rows
+        return keys + scores + gather + 2 * B * Hq * D * 2
+
+    def kernel_bytes(self):
+        B, Hq, Hk, D, L = self.shape
+        return B * Hk * L * D * 2 + B * Hk * L * 4 + B * Hq * D * 2
+
+    def make(self, dev):
+        from bytes_amd import workloads as W
+        B, Hq, Hk, D, L = self.shape
+        x = W.c5_topk(seed=0, device=dev, B=B, Hq=Hq, Hk=Hk, D=D, L=L)
+        return {"q": x["q"], "k": x["k"], "v": x["v"], "scale": x["scale"]}
+
+    def step(self, inp):
+        from bytes_amd.sparse import token_topk_decode
+        return token_topk_decode(inp["q"], inp["k"], inp["v"], self.kb, inp["scale"])
+
+    def cpu_sample(self):
+        from bytes_amd import workloads as W
+        from oracle import reference as R
+        B, Hq, Hk, D, L = self.shape
+        x = W.dense(1, Hq // Hk, 1, D, L, seed=0)
+        units = B * Hk
+        return (f"one (b, kv-head) unit of {units}: oracle group scores + top-{self.kb} + gather, "
+                f"q [1,{Hq // Hk},1,{D}], K/V [1,1,{L},{D}]",
+                lambda: R.token_topk_decode(x["q"], x["k"], x["v"], self.kb, x["scale"]), units)
+
+
 class CopyCase(Case):
     """Plain device copy of known size: the calibration point for HBM byte counters
     (FETCH_SIZE / WRITE_SIZE of this kernel vs its exact 2 x nbytes traffic)."""
@@ -167,6 +213,10 @@ def cases():
         "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
         "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536),
         "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536),
+        "c5_topk256": TopkCase("c5_topk256", 256),
+        "c5_topk1024": TopkCase("c5_topk1024", 1024),
+        "c5_topk4096": TopkCase("c5_topk4096", 4096),
+        "c5_dense": DenseCase("c5_dense", *W.SHAPES["c5_topk"]),
     }
 
 

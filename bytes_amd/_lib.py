@@ -50,7 +50,8 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64, c_i64, c_i64,            # q (b, h), k (b, h, s) strides
         c_i64, c_i64,                                 # out strides (b, h)
         c_f32, c_vp),                                 # scaling, stream
-    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_vp, c_i64, c_vp),
+    "bytes_topk_workspace_size": (c_i64, c_int, c_int, c_szp),
+    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
     "bytes_gather_attn_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
     "bytes_gather_attn": (
         c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, k, v, idx, out
@@ -106,18 +107,21 @@ def stream_of(t: torch.Tensor) -> int:
 
 
 # ---------------------------------------------------------------------------
-# Workspaces: one zero-initialised byte buffer per device.  Kernels that use
-# split-K counters leave them at zero when they finish, so a buffer is cleared
-# only when it is (re)allocated.  It grows on demand; the usual warm-up call
-# before a graph capture sizes it.  Calls that share it must be ordered on one
-# stream (the reference harness runs everything on the current stream).
+# Workspaces: zero-initialised byte buffers, one per (device, family).  The
+# split-K decode kernels (dense, KIVI, gather) share the "splitk" family: they
+# leave their arrival counters at zero when they finish.  The top-k kernels
+# keep a histogram and list counters that they also leave at zero, in a
+# buffer of their own ("topk").  A buffer is cleared only when it is
+# (re)allocated; it grows on demand, and the usual warm-up call before a graph
+# capture sizes it.  Calls that share a buffer must be ordered on one stream
+# (the reference harness runs everything on the current stream).
 # ---------------------------------------------------------------------------
-_ws: Dict[int, torch.Tensor] = {}
+_ws: Dict[Tuple[int, str], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int, family: str = "splitk") -> torch.Tensor:
     dev = torch.device(device)
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), family)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(int(nbytes), 1 << 20)

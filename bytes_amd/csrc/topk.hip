@@ -7,22 +7,32 @@
 // above +inf, as in torch.topk).  Output: int32 indices [rows, k] ordered by
 // that order, identical run to run.
 //
-// One 1024-thread workgroup per row:
-//  1. radix select on 32-bit order keys, 11/11/10-bit digits from the top:
-//     each pass builds an LDS histogram of the digit among the keys that
-//     still match the selected prefix and picks the digit holding the k-th
-//     largest key, so after three passes the k-th key T is known exactly,
-//     along with how many keys equal to T are needed;
-//  2. collection in index order: every key > T, plus the first `need` keys
-//     equal to T (a workgroup scan gives each thread its rank among them);
-//  3. bitonic sort of the k selected (key, ~index) pairs in LDS.
+// Three launches:
+//  1. histogram: many workgroups per row count the top 11 bits (digit) of the
+//     32-bit order keys into a per-row 2048-bin histogram (LDS, then one
+//     global atomic per non-empty bin);
+//  2. filter: many workgroups per row find the digit d0 holding the k-th
+//     largest key and copy every key with a larger digit to the row's
+//     "above" list and every key with digit d0 to its candidate list (list
+//     order is irrelevant: step 3 sorts);
+//  3. select: one workgroup per row sorts the above list plus the candidates
+//     by (key desc, index asc) with a bitonic sort in LDS and writes the first
+//     k indices.  If the candidates overflow their list (heavily tied rows),
+//     the workgroup instead runs an exact radix select over the whole row
+//     (11/11/10-bit digits), collects in index order and sorts the k results.
+// Step 3 also clears the histogram and list counters, which are zero between
+// calls.
 #include "common.h"
 
 namespace bytes_amd {
 
-constexpr int kTopkThreads = 1024;
+constexpr int kTopkThreads = 1024;     // select kernel
+constexpr int kPassThreads = 256;      // histogram and filter kernels
+constexpr int kSlice = 8192;           // row elements per histogram / filter workgroup
 constexpr int kTopkMaxK = 8192;
-constexpr int kBins = 2048;
+constexpr int kBins = 2048;            // digit = top 11 bits of the order key
+constexpr int kCandCap = 8192;         // candidate list capacity per row
+constexpr int kSortMax = 16384;        // LDS sort capacity (above list + candidates)
 
 // Monotone key: larger score -> larger key.  NaN -> 0xFFFFFFFF, -0 -> +0.
 __device__ __forceinline__ uint32_t order_key(float x) {
@@ -32,8 +42,15 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Inclusive prefix sum over the 1024 threads of the workgroup (thread order).
+// Sort value: descending order of (key, ~index) = key desc, index asc.
+__device__ __forceinline__ uint64_t sort_val(uint32_t key, int idx) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// Inclusive prefix sum over the NT threads of the workgroup (thread order).
+template <int NT>
 __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t x = v;
 #pragma unroll
@@ -44,16 +61,16 @@ __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum, 
   if (lane == 63) wsum[w] = x;
   __syncthreads();
   if (w == 0) {
-    uint32_t s = lane < kTopkThreads / 64 ? wsum[lane] : 0u;
+    uint32_t s = lane < NW ? wsum[lane] : 0u;
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
+    for (int off = 1; off < NW; off <<= 1) {
       const uint32_t y = __shfl_up(s, off, 64);
       if (lane >= off) s += y;
     }
-    if (lane < kTopkThreads / 64) wsum[lane] = s;
+    if (lane < NW) wsum[lane] = s;
   }
   __syncthreads();
-  total = wsum[kTopkThreads / 64 - 1];
+  total = wsum[NW - 1];
   const uint32_t r = x + (w > 0 ? wsum[w - 1] : 0u);
   __syncthreads();   // wsum is reused by the next scan
   return r;
@@ -74,17 +91,173 @@ __device__ __forceinline__ void load4(const float* x, int i, int n, uint32_t (&k
   }
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores, int64_t row_stride, int n, int k,
-                                                            int P, int32_t* out, int64_t out_stride) {
-  extern __shared__ uint64_t sortbuf[];          // [P] (key << 32) | ~index
-  __shared__ uint32_t hist[kBins];
-  __shared__ uint32_t wsum[kTopkThreads / 64];
-  __shared__ uint32_t sel[4];                    // digit, count above, slot counter, eq base
-  const int tid = threadIdx.x;
-  const float* x = scores + (int64_t)blockIdx.x * row_stride;
+// In-LDS bitonic sort of buf[0, P) into descending order (P a power of two).
+template <int NT>
+__device__ void bitonic_desc(uint64_t* buf, int P) {
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < P / 2; i += NT) {
+        const int lo = (i / stride) * stride * 2 + (i % stride);
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t va = buf[lo], vb = buf[hi];
+        if ((va < vb) == desc) {
+          buf[lo] = vb;
+          buf[hi] = va;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
 
-  // ---- 1. radix select ----
+constexpr int kRowBatch = 128;         // rows per launch group (fixed histogram region)
+
+// Workspace: a fixed-size region of per-row histograms and list counters for
+// kRowBatch rows, zero between calls (the select kernel clears what it used),
+// then the lists, whose size depends on (rows, k).  Because the zero region
+// never moves, list data of an earlier call can never land in it.
+struct TopkWs {
+  uint32_t* hist;    // [kRowBatch][kBins]
+  uint32_t* cnt;     // [kRowBatch][2]: above-list length, candidate count
+  uint64_t* above;   // [kRowBatch][k]
+  uint64_t* cand;    // [kRowBatch][kCandCap]
+};
+
+constexpr size_t kTopkZeroBytes = (size_t)kRowBatch * kBins * 4 + (size_t)kRowBatch * 2 * 4;
+
+inline size_t topk_ws_bytes(int k) {
+  return kTopkZeroBytes + (size_t)kRowBatch * k * 8 + (size_t)kRowBatch * kCandCap * 8;
+}
+
+inline TopkWs topk_ws_carve(void* ws, int k) {
+  char* p = static_cast<char*>(ws);
+  TopkWs t;
+  t.hist = reinterpret_cast<uint32_t*>(p);
+  t.cnt = reinterpret_cast<uint32_t*>(p + (size_t)kRowBatch * kBins * 4);
+  t.above = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes);
+  t.cand = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes + (size_t)kRowBatch * k * 8);
+  return t;
+}
+
+// ---- 1. per-row digit histogram ----
+template <bool VEC>
+__global__ __launch_bounds__(kPassThreads) void topk_hist_kernel(const float* scores, int64_t row_stride, int n,
+                                                                 int parts, uint32_t* hist) {
+  __shared__ uint32_t h[kBins];
+  // scores points at the batch's first row; row indexes the batch's workspace rows
+  const int row = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const float* x = scores + (int64_t)row * row_stride;
+  constexpr int R = kSlice / (kPassThreads * 4);
+  uint32_t key[R][4];
+  bool ok[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = part * kSlice + (r * kPassThreads + threadIdx.x) * 4;
+    load4<VEC>(x, i < n ? i : n, n, key[r], ok[r]);
+  }
+  for (int b = threadIdx.x; b < kBins; b += kPassThreads) h[b] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (ok[r][j]) atomicAdd(&h[key[r][j] >> 21], 1u);
+  __syncthreads();
+  uint32_t* hr = hist + (int64_t)row * kBins;
+  for (int b = threadIdx.x; b < kBins; b += kPassThreads)
+    if (h[b]) atomicAdd(hr + b, h[b]);
+}
+
+// The digit holding the k-th largest key of a row and the count of keys in
+// larger digits, from its histogram (thread t owns digits 8t .. 8t+7).
+template <int NT>
+__device__ __forceinline__ void find_digit(const uint32_t* hr, uint32_t k, uint32_t* wsum, uint32_t* sel) {
+  constexpr int PER = kBins / NT;
+  if (threadIdx.x == 0) sel[0] = 0xFFFFFFFFu;
+  uint32_t hb[PER], sum = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    hb[j] = hr[threadIdx.x * PER + j];
+    sum += hb[j];
+  }
+  uint32_t total;
+  const uint32_t incl = block_incl_scan<NT>(sum, wsum, total);
+  uint32_t above = total - incl;              // keys in digits > PER*t + PER-1
+#pragma unroll
+  for (int j = PER - 1; j >= 0; --j) {
+    if (above < k && above + hb[j] >= k) {
+      sel[0] = threadIdx.x * PER + j;
+      sel[1] = above;
+    }
+    above += hb[j];
+  }
+  __syncthreads();
+}
+
+// ---- 2. filter into the above list and the candidate list ----
+template <bool VEC>
+__global__ __launch_bounds__(kPassThreads) void topk_filter_kernel(const float* scores, int64_t row_stride, int n,
+                                                                   int k, int parts, TopkWs ws) {
+  __shared__ uint32_t wsum[kPassThreads / 64];
+  __shared__ uint32_t sel[4];
+  const int row = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const float* x = scores + (int64_t)row * row_stride;
+  constexpr int R = kSlice / (kPassThreads * 4);
+  uint32_t key[R][4];
+  bool ok[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = part * kSlice + (r * kPassThreads + threadIdx.x) * 4;
+    load4<VEC>(x, i < n ? i : n, n, key[r], ok[r]);
+  }
+  find_digit<kPassThreads>(ws.hist + (int64_t)row * kBins, (uint32_t)k, wsum, sel);
+  const uint32_t d0 = sel[0];                   // digits are < kBins: a missing pick keeps every key out
+  uint32_t na = 0, nc = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!ok[r][j]) continue;
+      const uint32_t d = key[r][j] >> 21;
+      na += d > d0 ? 1u : 0u;
+      nc += d == d0 ? 1u : 0u;
+    }
+  uint32_t ta, tc;
+  uint32_t oa = block_incl_scan<kPassThreads>(na, wsum, ta) - na;
+  uint32_t oc = block_incl_scan<kPassThreads>(nc, wsum, tc) - nc;
+  if (threadIdx.x == 0) {
+    sel[2] = ta ? atomicAdd(ws.cnt + row * 2 + 0, ta) : 0u;
+    sel[3] = tc ? atomicAdd(ws.cnt + row * 2 + 1, tc) : 0u;
+  }
+  __syncthreads();
+  oa += sel[2];
+  oc += sel[3];
+  uint64_t* al = ws.above + (int64_t)row * k;
+  uint64_t* cl = ws.cand + (int64_t)row * kCandCap;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!ok[r][j]) continue;
+      const uint32_t d = key[r][j] >> 21;
+      const int idx = part * kSlice + (r * kPassThreads + threadIdx.x) * 4 + j;
+      if (d > d0) {
+        if (oa < (uint32_t)k) al[oa] = sort_val(key[r][j], idx);
+        ++oa;
+      } else if (d == d0) {
+        if (oc < (uint32_t)kCandCap) cl[oc] = sort_val(key[r][j], idx);
+        ++oc;
+      }
+    }
+}
+
+// Exact selection over a whole row in one workgroup (used when the candidate
+// list overflowed): radix select, collection in index order, sort.
+template <bool VEC>
+__device__ void topk_row_exact(const float* x, int n, int k, uint64_t* sortbuf, uint32_t* hist, uint32_t* wsum,
+                               uint32_t* sel, int32_t* o) {
+  const int tid = threadIdx.x;
   uint32_t prefix = 0u, pmask = 0u;
   uint32_t kr = (uint32_t)k;
 #pragma unroll 1
@@ -102,11 +275,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
         if (ok[j] && (key[j] & pmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & dmask], 1u);
     }
     __syncthreads();
-    // thread t owns digits 2t, 2t+1; count of keys in digits above 2t+1
+    // digit d with count(digits > d) < kr <= count(digits >= d); shift-relative digits
     const uint32_t c0 = hist[2 * tid], c1 = hist[2 * tid + 1];
     uint32_t total;
-    const uint32_t incl = block_incl_scan(c0 + c1, wsum, total);
-    const uint32_t above = total - incl;     // digits > 2*tid + 1
+    const uint32_t incl = block_incl_scan<kTopkThreads>(c0 + c1, wsum, total);
+    const uint32_t above = total - incl;
     if (above < kr && above + c1 >= kr) {
       sel[0] = 2 * tid + 1;
       sel[1] = above;
@@ -115,16 +288,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
       sel[1] = above + c1;
     }
     __syncthreads();
-    const uint32_t d = sel[0];
     kr -= sel[1];
-    prefix |= d << shift;
+    prefix |= sel[0] << shift;
     pmask |= dmask << shift;
     __syncthreads();
   }
   const uint32_t T = prefix;
   const uint32_t need = kr;                      // keys equal to T to take, >= 1
-
-  // ---- 2. collection (index order decides among keys equal to T) ----
+  int P = 2;
+  while (P < k) P <<= 1;
   for (int i = tid; i < P; i += kTopkThreads) sortbuf[i] = 0ull;
   if (tid == 0) {
     sel[2] = 0u;
@@ -140,10 +312,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
 #pragma unroll
     for (int j = 0; j < 4; ++j) ne += (ok[j] && key[j] == T) ? 1u : 0u;
     uint32_t rank = 0, tot = 0;
-    if (__syncthreads_or(ne != 0)) {
-      const uint32_t incl = block_incl_scan(ne, wsum, tot);
-      rank = incl - ne;
-    }
+    if (__syncthreads_or(ne != 0)) rank = block_incl_scan<kTopkThreads>(ne, wsum, tot) - ne;
     const uint32_t eq0 = sel[3];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -153,34 +322,79 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
         take = eq0 + rank < need;
         ++rank;
       }
-      if (take) {
-        const uint32_t slot = atomicAdd(&sel[2], 1u);
-        sortbuf[slot] = ((uint64_t)key[j] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)(i + j));
-      }
+      if (take) sortbuf[atomicAdd(&sel[2], 1u)] = sort_val(key[j], i + j);
     }
     __syncthreads();
     if (tid == 0) sel[3] = eq0 + tot;
     __syncthreads();
   }
-
-  // ---- 3. bitonic sort, descending ----
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < P / 2; i += kTopkThreads) {
-        const int lo = (i / stride) * stride * 2 + (i % stride);
-        const int hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const uint64_t va = sortbuf[lo], vb = sortbuf[hi];
-        if ((va < vb) == desc) {
-          sortbuf[lo] = vb;
-          sortbuf[hi] = va;
-        }
-      }
-      __syncthreads();
-    }
-  }
-  int32_t* o = out + (int64_t)blockIdx.x * out_stride;
+  bitonic_desc<kTopkThreads>(sortbuf, P);
   for (int i = tid; i < k; i += kTopkThreads) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sortbuf[i]);
+}
+
+// ---- 3. per-row selection and sort ----
+template <bool VEC>
+__global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* scores, int64_t row_stride, int n,
+                                                                   int k, TopkWs ws, int32_t* out,
+                                                                   int64_t out_stride) {
+  extern __shared__ uint64_t sortbuf[];          // [kSortMax]
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t wsum[kTopkThreads / 64];
+  __shared__ uint32_t sel[4];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint32_t A = ws.cnt[row * 2 + 0], Cn = ws.cnt[row * 2 + 1];
+  int32_t* o = out + (int64_t)row * out_stride;
+  // lists are complete and consistent: fewer than k keys above the digit, the
+  // candidates fill the rest and fit their list
+  if (A < (uint32_t)k && A + Cn >= (uint32_t)k && Cn <= (uint32_t)kCandCap) {
+    const int m = (int)(A + Cn);
+    int P = 2;
+    while (P < m) P <<= 1;
+    const uint64_t* al = ws.above + (int64_t)row * k;
+    const uint64_t* cl = ws.cand + (int64_t)row * kCandCap;
+    for (int i = tid; i < P; i += kTopkThreads)
+      sortbuf[i] = i < (int)A ? al[i] : (i < m ? cl[i - A] : 0ull);
+    __syncthreads();
+    bitonic_desc<kTopkThreads>(sortbuf, P);
+    for (int i = tid; i < k; i += kTopkThreads) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sortbuf[i]);
+  } else {
+    topk_row_exact<VEC>(scores + (int64_t)row * row_stride, n, k, sortbuf, hist, wsum, sel, o);
+  }
+  // leave the row's histogram and list counters at zero for the next call
+  uint32_t* hr = ws.hist + (int64_t)row * kBins;
+  for (int b = tid; b < kBins; b += kTopkThreads) hr[b] = 0u;
+  if (tid == 0) {
+    ws.cnt[row * 2 + 0] = 0u;
+    ws.cnt[row * 2 + 1] = 0u;
+  }
+}
+
+template <bool VEC>
+static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_stride, int k, int32_t* out,
+                       int64_t out_stride, const TopkWs& ws, hipStream_t st) {
+  static bool lds_set = false;   // the select kernel's dynamic LDS exceeds the 64 KB default
+  if (!lds_set) {
+    int rc = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_select_kernel<VEC>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kSortMax * 8);
+    if (rc) return rc;
+    lds_set = true;
+  }
+  const int parts = (n + kSlice - 1) / kSlice;
+  for (int64_t r0 = 0; r0 < rows; r0 += kRowBatch) {
+    const int nr = (int)(rows - r0 < kRowBatch ? rows - r0 : kRowBatch);
+    const float* s = scores + r0 * row_stride;
+    int32_t* o = out + r0 * out_stride;
+    const unsigned grid = (unsigned)(nr * parts);
+    hipLaunchKernelGGL(topk_hist_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, parts,
+                       ws.hist);
+    hipLaunchKernelGGL(topk_filter_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, k, parts,
+                       ws);
+    hipLaunchKernelGGL(topk_select_kernel<VEC>, dim3((unsigned)nr), dim3(kTopkThreads), kSortMax * 8, st, s,
+                       row_stride, n, k, ws, o, out_stride);
+    const int rc = (int)hipGetLastError();
+    if (rc) return rc;
+  }
+  return 0;
 }
 
 }  // namespace bytes_amd
@@ -189,32 +403,28 @@ using namespace bytes_amd;
 
 extern "C" {
 
+int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes) {
+  if (!bytes || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
+  if (k > kTopkMaxK) return (int)hipErrorNotSupported;
+  *bytes = topk_ws_bytes(k);
+  return 0;
+}
+
 int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, void* out, int64_t out_stride,
-               void* stream) {
+               void* workspace, size_t workspace_bytes, void* stream) {
   if (!scores || !out || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
   if (k > kTopkMaxK) return (int)hipErrorNotSupported;
   if (rows == 0) return 0;
-  if (rows > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
-  int P = 1;
-  while (P < k) P <<= 1;
-  if (P < 2) P = 2;
-  const size_t lds = (size_t)P * 8;
+  const long parts = (n + kSlice - 1) / kSlice;
+  if (kRowBatch * parts > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  if (!workspace || workspace_bytes < topk_ws_bytes(k)) return (int)hipErrorInvalidValue;
+  const TopkWs ws = topk_ws_carve(workspace, k);
   const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0) && (row_stride % 4 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (vec) {
-    int rc = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (rc) return rc;
-    hipLaunchKernelGGL(topk_kernel<true>, dim3((unsigned)rows), dim3(kTopkThreads), lds, st,
-                       static_cast<const float*>(scores), row_stride, n, k, P, static_cast<int32_t*>(out), out_stride);
-  } else {
-    int rc = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<false>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (rc) return rc;
-    hipLaunchKernelGGL(topk_kernel<false>, dim3((unsigned)rows), dim3(kTopkThreads), lds, st,
-                       static_cast<const float*>(scores), row_stride, n, k, P, static_cast<int32_t*>(out), out_stride);
-  }
-  return (int)hipGetLastError();
+  const float* s = static_cast<const float*>(scores);
+  int32_t* o = static_cast<int32_t*>(out);
+  return vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, ws, st)
+             : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, ws, st);
 }
 
 }  // extern "C"

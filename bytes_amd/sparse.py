@@ -85,7 +85,10 @@ def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
         s = s.contiguous()
     rows = s.shape[0]
     out = torch.empty((rows, k), dtype=torch.int32, device=scores.device)
-    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), ptr(out), out.stride(0), stream_of(scores))
+    nbytes = size_query("bytes_topk_workspace_size", rows, n, int(k))
+    ws = workspace(scores.device, nbytes, "topk")
+    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), ptr(out), out.stride(0), ptr(ws), ws.numel(),
+         stream_of(scores))
     return out.reshape(*scores.shape[:-1], k)
 
 

@@ -12,7 +12,9 @@
  *  - `workspace` is caller-owned device memory of at least the size returned
  *    by the matching *_workspace_size query.  It must be zero-filled once
  *    before first use; the kernels leave their counters at zero on exit.
- *    Calls that share a workspace must be ordered on one stream.
+ *    One workspace may serve the split-K decode entry points together
+ *    (dense, KIVI, gather); bytes_topk needs a workspace of its own.  Calls
+ *    that share a workspace must be ordered on one stream.
  *  - Return value: 0 on success, otherwise a hipError_t value
  *    (bytes_error_string() gives its text).  No C++ exception crosses the ABI.
  */
@@ -128,8 +130,9 @@ int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, i
  *   out    [rows, k] int32 (row stride out_stride), ordered by that order.
  * 1 <= k <= min(n, 8192); larger k returns hipErrorNotSupported.
  * ------------------------------------------------------------------------- */
+int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes);
 int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, void* out,
-               int64_t out_stride, void* stream);
+               int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Gather attention over selected rows.

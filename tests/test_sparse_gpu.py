@@ -74,6 +74,22 @@ def test_topk_unaligned_rows(dev):
     assert torch.equal(SP.topk_indices(view, 300).cpu().long(), R.topk_indices(s, 300))
 
 
+@pytest.mark.parametrize("case", ["narrow", "all_equal"])
+def test_topk_crowded_digit_rows(dev, case):
+    """Every key of a row shares its top 11 bits: the candidate list overflows and
+    the whole-row exact selection runs."""
+    g = torch.Generator().manual_seed(5)
+    if case == "narrow":
+        s = 1.0 + torch.rand(3, 20000, generator=g) * 0.2
+        s[1, 7777] = 1.1                                      # plus exact ties
+        s[1, 7778] = 1.1
+    else:
+        s = torch.full((3, 20000), 0.5)
+    for k in (1, 100, 8192):
+        got = SP.topk_indices(s.to(dev), k).cpu().long()
+        assert torch.equal(got, R.topk_indices(s, k)), (case, k)
+
+
 @pytest.mark.parametrize("k", [256, 1024, 4096])
 def test_topk_c5_rows(dev, k):
     """64 rows x 131072 fp32 (BASELINE C5 selection shape)."""
