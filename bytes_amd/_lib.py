@@ -56,11 +56,19 @@ SIGNATURES: Dict[str, Tuple] = {
     "bytes_gather_attn": (
         c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, k, v, idx, out
         c_int, c_int, c_int, c_int, c_int, c_int, c_int,   # B, Hq, Hk, S, D, kb, per_head
+        c_int, c_int,                                 # page, limit
         c_i64, c_i64,                                 # q strides
         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,     # k, v strides (b, h, s)
         c_i64, c_i64,                                 # idx strides (b, h)
         c_i64, c_i64,                                 # out strides
         c_f32, c_int, c_vp, c_sz, c_vp),              # scaling, chunk, workspace, bytes, stream
+    "bytes_quest_page_minmax": (c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp),
+    "bytes_quest_page_scores": (
+        c_vp, c_vp, c_vp, c_vp,                       # q, kmin, kmax, bound
+        c_int, c_int, c_int, c_int, c_int, c_int,     # B, Hq, Hk, np, D, page
+        c_int, c_int,                                 # pos, local_w
+        c_i64, c_i64, c_i64, c_i64,                   # q strides, bound strides
+        c_f32, c_vp),                                 # scale, stream
 }
 _RESTYPES = {"bytes_error_string": ctypes.c_char_p}
 

@@ -9,6 +9,10 @@
 //  * per KV head     idx [B, Hk, kb]  (one selection shared by the GQA group,
 //    the token top-k pipeline): a unit is up to 16 query heads of one group,
 //    which share every gathered row, so one MFMA tile serves all of them.
+// In page mode the list holds page ids, each standing for `page` consecutive
+// rows p*page + o clamped to S-1 (benchmarks/sparse_attention.py:358-363, the
+// Quest expansion), expanded while the list is staged.  Rows at or past
+// `limit` (the causal bound, S at decode) are masked.
 // The index list of a unit is cut into split-K chunks; each workgroup stages
 // its chunk's row numbers in LDS, then its waves run the dense bf16 tile loop
 // with rows fetched through that list (prefetching the next tile's rows while
@@ -27,6 +31,8 @@ struct GatherArgs {
   const int32_t* idx;        // [B, Hq or Hk, kb], unit stride along kb
   int64_t i_sb, i_sh;
   int Hk, G, HB, S, kb, chunk, per_head;
+  int page;                  // 0: idx holds rows; > 0: idx holds page ids of `page` rows each
+  int limit;                 // rows >= limit take no part
   float scale_log2;
   SplitKOut o;
 };
@@ -91,8 +97,19 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
   const int p_begin = split * a.chunk;
   const int n = min(a.chunk, a.kb - p_begin);
   for (int i = threadIdx.x; i < n; i += kGatherWaves * 64) {
-    const int r = irow[p_begin + i];
-    rows[i] = (r >= 0 && r < a.S) ? r : -1;
+    const int j = p_begin + i;
+    int64_t r;
+    bool ok;
+    if (a.page > 0) {
+      const int pid = irow[j / a.page];
+      r = (int64_t)pid * a.page + j % a.page;
+      r = r < a.S - 1 ? r : a.S - 1;
+      ok = pid >= 0;
+    } else {
+      r = irow[j];
+      ok = r >= 0;
+    }
+    rows[i] = (ok && r < a.limit) ? (int)r : -1;
   }
 
   bf16x8 qb[C::KK];
@@ -168,16 +185,19 @@ int bytes_gather_attn_workspace_size(int B, int Hq, int Hk, int kb, int D, int p
 }
 
 int bytes_gather_attn(const void* q, const void* k, const void* v, const void* idx, void* out, int B, int Hq, int Hk,
-                      int S, int D, int kb, int per_head, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh,
-                      int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb, int64_t i_sh,
+                      int S, int D, int kb, int per_head, int page, int limit, int64_t q_sb, int64_t q_sh,
+                      int64_t k_sb, int64_t k_sh, int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb, int64_t i_sh,
                       int64_t o_sb, int64_t o_sh, float scaling, int chunk_req, void* workspace,
                       size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !idx || !out || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || S <= 0 || kb <= 0)
     return (int)hipErrorInvalidValue;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  if (page < 0 || (page > 0 && kb % page != 0) || limit < 0 || limit > S) return (int)hipErrorInvalidValue;
   const long units = gather_units(B, Hq, Hk, per_head);
   if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
   GatherArgs a;
+  a.page = page;
+  a.limit = limit;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
   a.k = static_cast<const uint16_t*>(k);

@@ -1,0 +1,166 @@
+// Quest page metadata and page bounds.
+//
+// Replaces the page part of benchmarks/sparse_attention.py:328-364
+// (`_quest_select`; dense form benchmarks/eval_ppl.py:54-79):
+//  * per-page elementwise min/max of the keys over pages of `page` tokens,
+//    the last partial page padded with the last key (:336-341);
+//  * bound[b, h, p] = scaling * sum_d max(q_d * kmin_d, q_d * kmax_d) in fp32
+//    (:342-345), -inf for pages that start after the query position
+//    (:346-348) and +inf for pages overlapping the recent window of
+//    `local_w` tokens (:349-355).
+// The products of bf16 values are exact in fp32 and every thread sums its
+// page's terms in ascending d, so the bounds are bit-identical to a
+// sequential fp32 evaluation; the page top-k that follows is then bit-exact.
+#include "common.h"
+
+namespace bytes_amd {
+
+// NaN-propagating min / max (torch.amin / amax semantics).
+__device__ __forceinline__ float nmin(float a, float b) { return (a < b || a != a) ? a : b; }
+__device__ __forceinline__ float nmax(float a, float b) { return (a > b || a != a) ? a : b; }
+
+// One thread per (b, hk, page, 8-dim chunk).
+__global__ void quest_minmax_kernel(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, int Hk, int S,
+                                    int D, int page, int np, uint16_t* kmin, uint16_t* kmax) {
+  const int chunks = D / 8;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (gid >= (int64_t)Hk * np * chunks) return;
+  const int c = (int)(gid % chunks);
+  const int64_t r = gid / chunks;
+  const int p = (int)(r % np);
+  const int hk = (int)(r / np);
+  const uint16_t* base = k + (int64_t)b * k_sb + (int64_t)hk * k_sh + c * 8;
+  float mn[8], mx[8];
+  for (int o = 0; o < page; ++o) {
+    const int t = min(p * page + o, S - 1);
+    const u32x4 raw = ld16(base + (int64_t)t * k_ss);
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = bf16_bits_to_f32(h[j]);
+      mn[j] = o == 0 ? v : nmin(mn[j], v);
+      mx[j] = o == 0 ? v : nmax(mx[j], v);
+    }
+  }
+  u32x4 omn, omx;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // min/max of bf16 values are bf16 values: truncation is exact
+    omn[j] = (__float_as_uint(mn[2 * j]) >> 16) | (__float_as_uint(mn[2 * j + 1]) & 0xFFFF0000u);
+    omx[j] = (__float_as_uint(mx[2 * j]) >> 16) | (__float_as_uint(mx[2 * j + 1]) & 0xFFFF0000u);
+  }
+  const int64_t o = (((int64_t)b * Hk + hk) * np + p) * D + c * 8;
+  *reinterpret_cast<u32x4*>(kmin + o) = omn;
+  *reinterpret_cast<u32x4*>(kmax + o) = omx;
+}
+
+constexpr int kQuestThreads = 256;
+
+// One thread per (b, hk, page), all G query heads of the group: the page's
+// min/max rows are read once and every head's bound is summed over d in order.
+template <int D>
+__global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                                                    const uint16_t* kmin, const uint16_t* kmax,
+                                                                    int Hk, int G, int np, int page, int pos,
+                                                                    int local_w, float scale, float* bound,
+                                                                    int64_t o_sb, int64_t o_sh) {
+  __shared__ float qs[16][D];
+  const int parts = (np + kQuestThreads - 1) / kQuestThreads;
+  const int bh = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const int b = bh / Hk, hk = bh - (bh / Hk) * Hk;
+  for (int i = threadIdx.x; i < G * D; i += kQuestThreads) {
+    const int g = i / D, d = i - (i / D) * D;
+    qs[g][d] = bf16_bits_to_f32(q[(int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d]);
+  }
+  __syncthreads();
+  const int p = part * kQuestThreads + threadIdx.x;
+  if (p >= np) return;
+  const int64_t row = ((int64_t)b * Hk + hk) * np + p;
+  const uint16_t* mnr = kmin + row * D;
+  const uint16_t* mxr = kmax + row * D;
+  float acc[16];
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    const u32x4 a = ld16(mnr + c * 8), z = ld16(mxr + c * 8);
+    const uint16_t* ha = reinterpret_cast<const uint16_t*>(&a);
+    const uint16_t* hz = reinterpret_cast<const uint16_t*>(&z);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = c * 8 + j;
+      const float lo = bf16_bits_to_f32(ha[j]), hi = bf16_bits_to_f32(hz[j]);
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        if (g < G) {
+          const float qd = qs[g][d];
+          const float t = nmax(qd * lo, qd * hi);
+          acc[g] = d == 0 ? t : acc[g] + t;
+        }
+      }
+    }
+  }
+  // causal validity and the forced recent window, at page granularity
+  const bool valid = (int64_t)p * page <= pos;
+  bool recent = false;
+  if (local_w > 0) {
+    const int lo = max(pos - local_w + 1, 0) / page, hi = pos / page;
+    recent = p >= lo && p <= hi;
+  }
+#pragma unroll
+  for (int g = 0; g < 16; ++g) {
+    if (g < G) {
+      float v = acc[g] * scale;
+      if (!valid) v = kNegInf;
+      if (recent) v = __builtin_inff();
+      bound[(int64_t)b * o_sb + (int64_t)(hk * G + g) * o_sh + p] = v;
+    }
+  }
+}
+
+}  // namespace bytes_amd
+
+using namespace bytes_amd;
+
+extern "C" {
+
+int bytes_quest_page_minmax(const void* k, void* kmin, void* kmax, int B, int Hk, int S, int D, int page,
+                            int64_t k_sb, int64_t k_sh, int64_t k_ss, void* stream) {
+  if (!k || !kmin || !kmax || B <= 0 || Hk <= 0 || S <= 0 || page <= 0 || D <= 0 || D % 8 != 0)
+    return (int)hipErrorInvalidValue;
+  if (B > 65535) return (int)hipErrorInvalidConfiguration;
+  const int np = (S + page - 1) / page;
+  const int64_t per_b = (int64_t)Hk * np * (D / 8);
+  const int th = 256;
+  dim3 grid((unsigned)((per_b + th - 1) / th), (unsigned)B);
+  hipLaunchKernelGGL(quest_minmax_kernel, grid, dim3(th), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(k), k_sb, k_sh, k_ss, Hk, S, D, page, np,
+                     static_cast<uint16_t*>(kmin), static_cast<uint16_t*>(kmax));
+  return (int)hipGetLastError();
+}
+
+int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, void* bound, int B, int Hq, int Hk,
+                            int np, int D, int page, int pos, int local_w, int64_t q_sb, int64_t q_sh,
+                            int64_t o_sb, int64_t o_sh, float scale, void* stream) {
+  if (!q || !kmin || !kmax || !bound || B <= 0 || Hk <= 0 || Hq % Hk != 0 || np <= 0 || page <= 0)
+    return (int)hipErrorInvalidValue;
+  const int G = Hq / Hk;
+  if (G > 16) return (int)hipErrorNotSupported;
+  if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  const int parts = (np + kQuestThreads - 1) / kQuestThreads;
+  const long grid = (long)B * Hk * parts;
+  if (grid > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* qq = static_cast<const uint16_t*>(q);
+  const uint16_t* mn = static_cast<const uint16_t*>(kmin);
+  const uint16_t* mx = static_cast<const uint16_t*>(kmax);
+  float* o = static_cast<float*>(bound);
+  if (D == 128)
+    hipLaunchKernelGGL(quest_score_kernel<128>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
+                       mn, mx, Hk, G, np, page, pos, local_w, scale, o, o_sb, o_sh);
+  else
+    hipLaunchKernelGGL(quest_score_kernel<64>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
+                       mn, mx, Hk, G, np, page, pos, local_w, scale, o, o_sb, o_sh);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

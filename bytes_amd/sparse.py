@@ -93,7 +93,7 @@ def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
 
 
 def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor, scaling: float,
-                       BLOCK_K: int = 64, *, chunk: int = 0) -> torch.Tensor:
+                       BLOCK_K: int = 64, *, chunk: int = 0, page: int = 1, limit=None) -> torch.Tensor:
     """Pass 2: exact attention over the gathered rows.
 
     Replaces src/attention_kernels.py:1037-1059.  q [B,H_q,1,D] bf16; k, v
@@ -101,7 +101,16 @@ def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: t
     [B,H_k,kb] (one selection per KV head, shared by its query group), any
     integer dtype.  Entries outside [0, S) are masked (sentinel rule of
     benchmarks/sparse_attention.py:376).  Returns [B,H_q,1,D] bf16.
+
+    page > 1: idx holds page ids, each standing for rows p*page .. p*page+page-1
+    clamped to S-1 (the Quest expansion, benchmarks/sparse_attention.py:360-363).
+    limit: rows at or past it are masked (the causal bound pos+1; default S).
     """
+    page = int(page)
+    if page < 1:
+        raise ValueError(f"page={page} must be >= 1")
+    if limit is not None and not 0 <= int(limit) <= k.shape[2]:
+        raise ValueError(f"limit={limit} outside [0, S]")
     B, Hq, Hk, S, D = _qk_shapes(q, k)
     C.cuda_tensors(q, v, idx)
     C.dtype_in(k, "k", torch.bfloat16)
@@ -121,10 +130,13 @@ def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: t
     qs = C.rows16(q.squeeze(2))
     k, v = C.rows16(k), C.rows16(v)
     out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=q.device)
-    nbytes = size_query("bytes_gather_attn_workspace_size", B, Hq, Hk, kb, D, per_head, int(chunk))
+    if page == 1:
+        page = 0                                    # plain row indices
+    nbytes = size_query("bytes_gather_attn_workspace_size", B, Hq, Hk, kb * max(page, 1), D, per_head, int(chunk))
     ws = workspace(q.device, nbytes)
-    call("bytes_gather_attn", ptr(qs), ptr(k), ptr(v), ptr(idx), ptr(out), B, Hq, Hk, S, D, kb, per_head,
-         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
+    call("bytes_gather_attn", ptr(qs), ptr(k), ptr(v), ptr(idx), ptr(out), B, Hq, Hk, S, D, kb * max(page, 1),
+         per_head, page, S if limit is None else int(limit), qs.stride(0), qs.stride(1),
+         k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
          idx.stride(0), idx.stride(1), out.stride(0), out.stride(1), float(scaling), int(chunk), ptr(ws),
          ws.numel(), stream_of(q))
     return out.unsqueeze(2)

@@ -97,3 +97,25 @@ def c5_topk(seed: int = 0, device="cpu", B: int = 8, Hq: int = 24, Hk: int = 8, 
     v = torch.randn(B, Hk, L, D, generator=g, device=device, dtype=torch.bfloat16)
     return {"q": q, "k": k, "v": v, "scale": 1.0 / math.sqrt(D),
             "meta": {"seed": seed, "shape": (B, Hq, Hk, D, L), "generator": str(torch.device(device))}}
+
+
+def c4_quest(seed: int = 0, device="cpu", B: int = 1, Hq: int = 28, Hk: int = 4, D: int = 128, L: int = 32768,
+             n_needle: int = 64, needle_scale: float = 4.0, noise: float = 0.1) -> Dict:
+    """BASELINE C4 inputs: q, K, V ~ N(0,1) bf16, plus `n_needle` needle tokens
+    per (b, KV head) at seeded random positions whose keys are set to
+    needle_scale * q_dir + noise * N(0,1), q_dir being the unit vector of the sum
+    of the group's query vectors (so every head of the group sees them)."""
+    g = _gen(seed)
+    q = torch.randn(B, Hq, 1, D, generator=g)
+    k = torch.randn(B, Hk, L, D, generator=g)
+    v = torch.randn(B, Hk, L, D, generator=g)
+    G = Hq // Hk
+    qdir = q.reshape(B, Hk, G, D).sum(2)
+    qdir = qdir / qdir.norm(dim=-1, keepdim=True)
+    pos = torch.stack([torch.randperm(L, generator=g)[:n_needle] for _ in range(B * Hk)]).reshape(B, Hk, n_needle)
+    for b in range(B):
+        for h in range(Hk):
+            k[b, h, pos[b, h]] = needle_scale * qdir[b, h] + noise * torch.randn(n_needle, D, generator=g)
+    return {"q": q.to(torch.bfloat16).to(device), "k": k.to(torch.bfloat16).to(device),
+            "v": v.to(torch.bfloat16).to(device), "scale": 1.0 / math.sqrt(D), "needles": pos,
+            "meta": {"seed": seed, "shape": (B, Hq, Hk, D, L), "n_needle": n_needle}}

@@ -144,14 +144,37 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
  *   per_head = 0: idx [B, Hk, kb] int32 (one list per KV head, shared by its G query heads)
  *   idx strides i_sb, i_sh (unit stride along kb); k, v [B, Hk, S, D] bf16;
  *   out [B, Hq, D] bf16.  D in {64, 128}.
+ * page = 0: idx entries are rows.  page > 0: idx holds kb/page page ids per list,
+ *   page id p standing for rows min(p*page + o, S-1), o < page (the Quest
+ *   expansion, benchmarks/sparse_attention.py:358-363).
+ * limit: rows >= limit are masked (the causal bound pos+1; S at decode).
  * ------------------------------------------------------------------------- */
 int bytes_gather_attn_workspace_size(int B, int Hq, int Hk, int kb, int D, int per_head, int chunk,
                                      size_t* bytes);
 int bytes_gather_attn(const void* q, const void* k, const void* v, const void* idx, void* out, int B, int Hq,
-                      int Hk, int S, int D, int kb, int per_head, int64_t q_sb, int64_t q_sh, int64_t k_sb,
+                      int Hk, int S, int D, int kb, int per_head, int page, int limit, int64_t q_sb, int64_t q_sh, int64_t k_sb,
                       int64_t k_sh, int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb,
                       int64_t i_sh, int64_t o_sb, int64_t o_sh, float scaling, int chunk, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Quest page metadata and bounds.
+ * Replaces the page part of benchmarks/sparse_attention.py:328-364 (`_quest_select`;
+ * dense form benchmarks/eval_ppl.py:54-79).
+ * bytes_quest_page_minmax: kmin/kmax [B, Hk, np, D] bf16 contiguous, np = ceil(S/page):
+ *   elementwise min/max of the keys of each page, the last partial page padded
+ *   with the last key (:336-341).  k [B, Hk, S, D] bf16 (strides k_*).
+ * bytes_quest_page_scores: bound [B, Hq, np] fp32 (strides o_sb, o_sh):
+ *   scale * sum_d max(q_d*kmin_d, q_d*kmax_d), d summed in ascending order in fp32
+ *   (bit-identical to a sequential evaluation); -inf for pages starting after
+ *   `pos`; +inf for pages overlapping (pos - local_w, pos] when local_w > 0.
+ *   q [B, Hq, D] bf16; G = Hq/Hk <= 16; D in {64, 128}.
+ * ------------------------------------------------------------------------- */
+int bytes_quest_page_minmax(const void* k, void* kmin, void* kmax, int B, int Hk, int S, int D, int page,
+                            int64_t k_sb, int64_t k_sh, int64_t k_ss, void* stream);
+int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, void* bound, int B, int Hq,
+                            int Hk, int np, int D, int page, int pos, int local_w, int64_t q_sb, int64_t q_sh,
+                            int64_t o_sb, int64_t o_sh, float scale, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */
