@@ -176,6 +176,51 @@ class TopkCase(Case):
                 lambda: R.token_topk_decode(x["q"], x["k"], x["v"], self.kb, x["scale"]), units)
 
 
+class QuestCase(Case):
+    """BASELINE C4: Quest page bounds from the per-page min/max metadata, top
+    ceil(2048/16) = 128 pages per query head, attention over their rows.  The
+    metadata is a property of the cache (built once, outside the step)."""
+    kernel = "gather_decode_kernel"
+
+    def __init__(self, name, budget=2048, page=16, B=1, Hq=28, Hk=4, D=128, L=32768):
+        self.name, self.budget, self.page, self.shape = name, budget, page, (B, Hq, Hk, D, L)
+        self.workload = (f"Quest page-sparse decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} page {page} "
+                         f"budget {budget} tokens (64 needles)")
+
+    def bytes_per_step(self):
+        B, Hq, Hk, D, L = self.shape
+        np_ = L // self.page
+        meta = 2 * B * Hk * np_ * D * 2                    # kmin + kmax read by the bound kernel
+        bounds = B * Hq * np_ * 4 * 2                      # written, then read by the top-k
+        rows = 2 * B * Hq * self.budget * D * 2            # gathered K and V rows (per query head)
+        return meta + bounds + rows + 2 * B * Hq * D * 2
+
+    def make(self, dev):
+        from bytes_amd import quest as Q
+        from bytes_amd import workloads as W
+        x = W.c4_quest(seed=0)
+        k = x["k"].to(dev)
+        return {"q": x["q"].to(dev), "k": k, "v": x["v"].to(dev), "meta": Q.quest_page_minmax(k, self.page),
+                "scale": x["scale"]}
+
+    def step(self, inp):
+        from bytes_amd.quest import quest_decode
+        return quest_decode(inp["q"], inp["k"], inp["v"], self.budget, inp["scale"], page=self.page,
+                            meta=inp["meta"])
+
+    def cpu_sample(self):
+        from bytes_amd import workloads as W
+        from oracle import reference as R
+        x = W.c4_quest(seed=0)
+        B, Hq, Hk, D, L = self.shape
+
+        def run():
+            _, tok, _ = R.quest_select(x["q"], x["k"], self.budget, self.page, x["scale"])
+            return R.sparse_gather_attn(x["q"], x["k"], x["v"], tok, x["scale"])
+        return (f"the whole step: oracle page metadata + bounds + page top-k + gather "
+                f"(B{B} Hq{Hq} L{L})", run, 1)
+
+
 class CopyCase(Case):
     """Plain device copy of known size: the calibration point for HBM byte counters
     (FETCH_SIZE / WRITE_SIZE of this kernel vs its exact 2 x nbytes traffic)."""
@@ -213,6 +258,7 @@ def cases():
         "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
         "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536),
         "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536),
+        "c4_quest": QuestCase("c4_quest"),
         "c5_topk256": TopkCase("c5_topk256", 256),
         "c5_topk1024": TopkCase("c5_topk1024", 1024),
         "c5_topk4096": TopkCase("c5_topk4096", 4096),

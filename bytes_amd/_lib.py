@@ -69,6 +69,18 @@ SIGNATURES: Dict[str, Tuple] = {
         c_int, c_int,                                 # pos, local_w
         c_i64, c_i64, c_i64, c_i64,                   # q strides, bound strides
         c_f32, c_vp),                                 # scale, stream
+    "bytes_pq_decode_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
+    "bytes_pq_decode_attn": (
+        c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,   # mode, lut, q, kcb, kidx, vidx, vcb, v, out
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int,         # out_dtype, B, Hq, Hk, S, D, K
+        c_i64, c_i64, c_i64, c_i64, c_i64,                       # lut (b, h), q (b, h), kcb head stride
+        c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,         # kidx (b, h, s), vidx (b, h, s), vcb head stride
+        c_i64, c_i64, c_i64, c_i64, c_i64,                       # v (b, h, s), out (b, h)
+        c_f32, c_int, c_vp, c_sz, c_vp),                         # scale, chunk, workspace, bytes, stream
+    "bytes_pq_build_lut": (c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_f32, c_vp),
+    "bytes_pq_encode": (c_vp, c_int, c_int, c_i64, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
+    "bytes_pq_decode_vectors": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
+    "bytes_pq_kmeans_update": (c_vp, c_int, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp),
 }
 _RESTYPES = {"bytes_error_string": ctypes.c_char_p}
 

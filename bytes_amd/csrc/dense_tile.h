@@ -97,26 +97,16 @@ __device__ __forceinline__ uint32_t range_mask(int t0, int t_end) {
   return n >= 32 ? 0xFFFFFFFFu : (n <= 0 ? 0u : ((1u << n) - 1u));
 }
 
-// Scores, online softmax and PV for the tile staged in kst/vst; rows whose
-// vmask bit is clear get probability zero.
-template <int D>
-__device__ __forceinline__ void dense_compute(uint32_t vmask, float scale_log2, int lane,
-                                              const bf16x8 (&qb)[D / 32], const char* kst, const char* vst,
-                                              float& m_run, float& l_run, f32x4 (&acc)[D / 16]) {
+// Online softmax and PV for one 32-row tile whose raw scores are s[blk][i]
+// (row blk*16 + lg*4 + i, head l%16; the layout of the score MFMA output) and
+// whose V rows are staged in vst (vswz layout); rows whose vmask bit is clear
+// get probability zero.  F16: V and P in fp16 (f16 MFMA), else bf16.
+template <int D, bool F16 = false>
+__device__ __forceinline__ void tile_softmax_pv(const f32x4 (&s)[2], uint32_t vmask, float scale_log2, int lane,
+                                                const char* vst, float& m_run, float& l_run,
+                                                f32x4 (&acc)[D / 16]) {
   using C = DenseCfg<D>;
   const int l16 = lane & 15, lg = lane >> 4;
-  f32x4 s[2];
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    s[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int row = blk * 16 + l16;
-#pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk) {
-      const bf16x8 ka = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(kst + row * (D * 2) + kswz<D>(row, kk * 4 + lg) * 16));
-      s[blk] = mfma_bf16(ka, qb[kk], s[blk]);
-    }
-  }
   float x[8];
   float mx = kNegInf;
 #pragma unroll
@@ -135,11 +125,15 @@ __device__ __forceinline__ void dense_compute(uint32_t vmask, float scale_log2, 
   const float alpha = fast_exp2(m_run - m_use);
   float psum = 0.f;
   bf16x8 pb;
+  f16x8 ph;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float p = fast_exp2(x[j] - m_use);
     psum += p;
-    pb[j] = (__bf16)p;
+    if (F16)
+      ph[j] = (_Float16)p;
+    else
+      pb[j] = (__bf16)p;
   }
   l_run = l_run * alpha + psum;
   m_run = m_new;
@@ -158,8 +152,34 @@ __device__ __forceinline__ void dense_compute(uint32_t vmask, float scale_log2, 
       h[hf] = tr16(vst + row * (D * 2) + vswz<D>(row, chunk) * 16 + (col & 7) * 2);
     }
     const u32x4 raw = {h[0][0], h[0][1], h[1][0], h[1][1]};
-    acc[db] = mfma_bf16(__builtin_bit_cast(bf16x8, raw), pb, acc[db]);
+    if (F16)
+      acc[db] = mfma_f16(__builtin_bit_cast(f16x8, raw), ph, acc[db]);
+    else
+      acc[db] = mfma_bf16(__builtin_bit_cast(bf16x8, raw), pb, acc[db]);
   }
+}
+
+// Scores (K rows staged in kst, Q in VGPRs), online softmax and PV for the
+// tile staged in kst/vst; rows whose vmask bit is clear get probability zero.
+template <int D>
+__device__ __forceinline__ void dense_compute(uint32_t vmask, float scale_log2, int lane,
+                                              const bf16x8 (&qb)[D / 32], const char* kst, const char* vst,
+                                              float& m_run, float& l_run, f32x4 (&acc)[D / 16]) {
+  using C = DenseCfg<D>;
+  const int l16 = lane & 15, lg = lane >> 4;
+  f32x4 s[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    s[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int row = blk * 16 + l16;
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) {
+      const bf16x8 ka = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const u32x4*>(kst + row * (D * 2) + kswz<D>(row, kk * 4 + lg) * 16));
+      s[blk] = mfma_bf16(ka, qb[kk], s[blk]);
+    }
+  }
+  tile_softmax_pv<D, false>(s, vmask, scale_log2, lane, vst, m_run, l_run, acc);
 }
 
 // Runs the pipelined dense tile loop of one wave over tokens

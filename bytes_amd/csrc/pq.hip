@@ -1,0 +1,523 @@
+// Product-quantized KV decode attention, LUT build, PQ encode and k-means update.
+//
+// Replaces src/attention_kernels.py:
+//   decode_attn_pq_lut_kv  :397-500  LUT-scored keys, codebook-reconstructed values
+//   decode_attn_pq_lut     :301-392  LUT-scored keys, dense V
+//   decode_attn_dequant    :187-296  codebook-reconstructed keys, dense V
+// and, on the setup side, the LUT precompute of benchmarks/test_correctness.py
+// :272-273, ProductQuantizer.quantize/.dequantize (src/quantization.py:160-226)
+// and the k-means of src/quantization.py:102-132.
+//
+// Layouts (d_sub = 8, M = D/8 subspaces, K <= 256 codewords):
+//   lut   [B, Hq, M, K] fp32, one head contiguous
+//   codes [B, Hk, S, M] uint8 (unit stride along M)
+//   codebooks fp16 [Hk or 1, M, K, 8] contiguous (per-KV-head or shared)
+//
+// Decode: a unit is (b, kv head, group of up to 4 query heads); its token axis
+// is cut into split-K chunks.  A workgroup stages the group's LUTs in LDS (for
+// dequant mode it builds them there from q and the key codebook: one 8-term
+// dot per entry, so q.k_hat is evaluated subspace by subspace) and, for
+// quantized values, the head's value codebook.  Per 32-token tile a wave sums
+// 16 LUT entries per (token, head) into the score-MFMA layout, runs the fp32
+// online softmax, rebuilds the V tile in LDS (16-byte codebook rows selected by
+// the value codes, or the bf16 V rows themselves), and accumulates O^T += V^T P^T
+// on MFMA, as the dense kernel does.
+#include "dense_tile.h"
+
+namespace bytes_amd {
+
+constexpr int kPqWaves = 4;
+constexpr int kPqHeads = 4;     // query heads per unit
+constexpr int kPqKMax = 256;    // codewords per subspace
+
+struct PqArgs {
+  const float* lut;          // mode LUT: [B, Hq, M, K]
+  int64_t l_sb, l_sh;
+  const uint16_t* q;         // mode dequant: q [B, Hq, D] bf16
+  int64_t q_sb, q_sh;
+  const _Float16* kcb;       // mode dequant: key codebook
+  int64_t kcb_sh;            // elements between heads (0: shared)
+  const uint8_t* kidx;
+  int64_t ki_sb, ki_sh, ki_ss;
+  const uint8_t* vidx;       // quantized V
+  int64_t vi_sb, vi_sh, vi_ss;
+  const _Float16* vcb;
+  int64_t vcb_sh;
+  const uint16_t* v;         // dense V [B, Hk, S, D] bf16
+  int64_t v_sb, v_sh, v_ss;
+  int Hk, G, HG, S, K, chunk;
+  float scale_log2;
+  SplitKOut o;
+};
+
+template <int D, bool QV>
+struct PqCfg {
+  static constexpr int M = D / 8;
+  static constexpr int LUT = kPqHeads * M * kPqKMax * 4;          // fp32 LUTs of the unit's heads
+  static constexpr int VCB = QV ? M * kPqKMax * 8 * 2 : 0;         // fp16 value codebook
+  static constexpr int TILE = kTile * D * 2;                        // one wave's V tile
+  static constexpr int kSmem = LUT + VCB + kPqWaves * TILE;
+};
+
+// Raw 16-bit V tile loads (dense V) for rows t0 .. t0+31 (clamped to S-1).
+template <int D>
+__device__ __forceinline__ void pq_issue_dense_v(const uint16_t* vbase, int64_t v_ss, int S, int t0, int lane,
+                                                 u32x4 (&r)[DenseCfg<D>::CPL]) {
+  using C = DenseCfg<D>;
+#pragma unroll
+  for (int i = 0; i < C::CPL; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / C::CPR, pos = p - rr * C::CPR;
+    r[i] = ld16(vbase + (int64_t)min(t0 + rr, S - 1) * v_ss + pos * 8);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void pq_stage_dense_v(int lane, const u32x4 (&r)[DenseCfg<D>::CPL], char* vst) {
+  using C = DenseCfg<D>;
+#pragma unroll
+  for (int i = 0; i < C::CPL; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / C::CPR, pos = p - rr * C::CPR;
+    *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, pos) * 16) = r[i];
+  }
+}
+
+// Codes of one tile, in registers:
+//  kc[blk*4+i]: the M key codes of tile row blk*16 + lg*4 + i (the score layout)
+//  vc[i]:       value code of row lane/16 + 4i, subspace lane%16 (the staging layout)
+template <int D, bool QV>
+struct PqRegs {
+  u32x4 kc[8];
+  uint32_t vc[QV ? 8 : 1];
+  u32x4 vd[QV ? 1 : DenseCfg<D>::CPL];
+};
+
+template <int D, bool QV>
+__device__ __forceinline__ void pq_issue(const PqArgs& a, const uint8_t* kib, const uint8_t* vib, const uint16_t* vbase,
+                                         int t0, int lane, PqRegs<D, QV>& r) {
+  constexpr int M = D / 8;
+  const int lg = lane >> 4;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = min(t0 + blk * 16 + lg * 4 + i, a.S - 1);
+      const uint8_t* p = kib + (int64_t)t * a.ki_ss;
+      if (M == 16) {
+        r.kc[blk * 4 + i] = ld16(p);
+      } else {
+        const u32x2 h = *reinterpret_cast<const u32x2*>(p);
+        r.kc[blk * 4 + i] = u32x4{h[0], h[1], 0u, 0u};
+      }
+    }
+  if constexpr (QV) {
+    // staging chunk p = lane + 64*i covers row p / M, subspace p % M
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int p = lane + 64 * i;
+      const int rr = p / M, j = p - (p / M) * M;
+      const int t = min(t0 + rr, a.S - 1);
+      r.vc[i] = (rr < kTile) ? vib[(int64_t)t * a.vi_ss + j] : 0u;
+    }
+  } else {
+    pq_issue_dense_v<D>(vbase, a.v_ss, a.S, t0, lane, r.vd);
+  }
+}
+
+template <int D, bool QV>
+__device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV>& r, uint32_t vmask, int lane, int nh,
+                                        const float* lut, const char* vcb, char* vst, float& m_run, float& l_run,
+                                        f32x4 (&acc)[D / 16]) {
+  constexpr int M = D / 8;
+  const int l16 = lane & 15;
+  // V tile into LDS
+  if constexpr (QV) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int p = lane + 64 * i;
+      const int rr = p / M, j = p - (p / M) * M;
+      if (rr < kTile) {
+        const u32x4 row = *reinterpret_cast<const u32x4*>(vcb + ((j * kPqKMax + r.vc[i]) * 8) * 2);
+        *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, j) * 16) = row;
+      }
+    }
+  } else {
+    pq_stage_dense_v<D>(lane, r.vd, vst);
+  }
+  // scores: lane (head l16, row group lg) sums its 8 rows' LUT entries in subspace order
+  f32x4 s[2];
+  const float* lh = lut + (l16 < nh ? l16 : 0) * (M * kPqKMax);
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 c = r.kc[blk * 4 + i];
+      float sc = 0.f;
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        const uint32_t code = (c[j >> 2] >> ((j & 3) * 8)) & 0xFFu;
+        sc += lh[j * kPqKMax + code];
+      }
+      s[blk][i] = sc;
+    }
+  wave_lds_sync();
+  tile_softmax_pv<D, QV>(s, l16 < nh ? vmask : 0u, a.scale_log2, lane, vst, m_run, l_run, acc);
+}
+
+template <int D, bool BUILD_LUT, bool QV>
+__global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
+  using C = PqCfg<D, QV>;
+  constexpr int M = D / 8;
+  __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
+  float* lut = reinterpret_cast<float*>(smem_raw);
+  char* vcb = smem_raw + C::LUT;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int unit, split;
+  xcd_unit_split(a.o.nsplit, unit, split);
+  const int b = unit / (a.Hk * a.HG);
+  const int rem = unit - b * a.Hk * a.HG;
+  const int hk = rem / a.HG, hg = rem - (rem / a.HG) * a.HG;
+  const int hq0 = hk * a.G + hg * kPqHeads;
+  const int nh = min(kPqHeads, a.G - hg * kPqHeads);
+
+  // ---- stage the group's LUTs (and the value codebook) ----
+  const int K = a.K;
+  if (BUILD_LUT) {
+    // LUT[h][j][c] = sum_e q[h][8j+e] * kcb[j][c][e], e ascending, fp32
+    const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
+    for (int e = threadIdx.x; e < nh * M * K; e += kPqWaves * 64) {
+      const int h = e / (M * K), r2 = e - h * (M * K);
+      const int j = r2 / K, c = r2 - j * K;
+      const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + h) * a.q_sh + j * 8;
+      const u32x4 qraw = ld16(qp);
+      const u32x4 craw = ld16(cb + ((int64_t)j * K + c) * 8);
+      const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
+      const _Float16* ch = reinterpret_cast<const _Float16*>(&craw);
+      float sum = 0.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) sum += bf16_bits_to_f32(qh[x]) * (float)ch[x];
+      lut[(h * M + j) * kPqKMax + c] = sum;
+    }
+  } else {
+    for (int e = threadIdx.x; e < nh * M * (K / 4); e += kPqWaves * 64) {
+      const int h = e / (M * (K / 4)), r2 = e - h * (M * (K / 4));
+      const int j = r2 / (K / 4), c4 = r2 - j * (K / 4);
+      const float* src = a.lut + (int64_t)b * a.l_sb + (int64_t)(hq0 + h) * a.l_sh + j * K + c4 * 4;
+      *reinterpret_cast<u32x4*>(lut + (h * M + j) * kPqKMax + c4 * 4) = ld16(src);
+    }
+  }
+  if (QV) {
+    const _Float16* cb = a.vcb + (int64_t)hk * a.vcb_sh;
+    for (int e = threadIdx.x; e < M * K; e += kPqWaves * 64) {
+      const int j = e / K, c = e - j * K;
+      *reinterpret_cast<u32x4*>(vcb + ((j * kPqKMax + c) * 8) * 2) = ld16(cb + (int64_t)e * 8);
+    }
+  }
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int t_begin = split * a.chunk;
+  const int t_end = min(t_begin + a.chunk, a.S);
+  const uint8_t* kib = a.kidx + (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh;
+  const uint8_t* vib = QV ? a.vidx + (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh : nullptr;
+  const uint16_t* vbase = QV ? nullptr : a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  char* vst = smem_raw + C::LUT + C::VCB + w * C::TILE;
+  constexpr int STEP = kPqWaves * kTile;
+  int t = t_begin + w * kTile;
+  PqRegs<D, QV> r;
+  if (t < t_end) pq_issue<D, QV>(a, kib, vib, vbase, t, lane, r);
+  __syncthreads();
+  for (; t < t_end; t += STEP) {
+    PqRegs<D, QV> cur = r;
+    if (t + STEP < t_end) pq_issue<D, QV>(a, kib, vib, vbase, t + STEP, lane, r);
+    wave_lds_sync();
+    pq_tile<D, QV>(a, cur, range_mask(t, t_end), lane, nh, lut, vcb, vst, m_run, l_run, acc);
+  }
+  splitk_epilogue<D, kPqWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0, nh,
+                               kDmapDense);
+}
+
+static void pq_plan(int S, long units, int chunk_req, int* chunk, int* ns) {
+  const int step = kPqWaves * kTile;
+  int c;
+  if (chunk_req > 0) {
+    c = chunk_req;
+  } else {
+    const long target = device_cu_count();   // one workgroup per CU (LDS-bound)
+    c = (int)(((long)S * units + target - 1) / target);
+  }
+  c = (c + step - 1) / step * step;
+  if (c < step) c = step;
+  *chunk = c;
+  *ns = (S + c - 1) / c;
+}
+
+// ============================================================================
+// LUT build: lut[b, h, j, c] = scale * sum_e q[b, h, 8j+e] * cb[h/G][j][c][e]
+// ============================================================================
+__global__ void pq_lut_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh, const _Float16* cb, int64_t cb_sh,
+                              int Hq, int G, int M, int K, float scale, float* lut) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_b = (int64_t)Hq * M * K;
+  const int b = blockIdx.y;
+  if (gid >= per_b) return;
+  const int h = (int)(gid / (M * K));
+  const int r = (int)(gid - (int64_t)h * M * K);
+  const int j = r / K, c = r - (r / K) * K;
+  const u32x4 qraw = ld16(q + (int64_t)b * q_sb + (int64_t)h * q_sh + j * 8);
+  const u32x4 craw = ld16(cb + (int64_t)(h / G) * cb_sh + ((int64_t)j * K + c) * 8);
+  const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
+  const _Float16* ch = reinterpret_cast<const _Float16*>(&craw);
+  float sum = 0.f;
+#pragma unroll
+  for (int x = 0; x < 8; ++x) sum += bf16_bits_to_f32(qh[x]) * (float)ch[x];
+  lut[(int64_t)b * per_b + gid] = sum * scale;
+}
+
+// ============================================================================
+// Encode: idx[n, j] = argmin_c sum_e (x[n, 8j+e] - cb[j][c][e])^2, the sum in
+// fp32 in e order with separate multiply and add, first index on ties.
+// One thread per (vector, subspace); the head's codebook is staged in LDS.
+// ============================================================================
+constexpr int kEncThreads = 256;
+
+__global__ __launch_bounds__(kEncThreads) void pq_encode_kernel(const void* x, int x_dtype, int64_t rows_per_head,
+                                                                int64_t x_rs, const void* cb, int cb_f32,
+                                                                int64_t cb_sh, int M, int K, uint8_t* idx) {
+  __shared__ float cbs[16 * kPqKMax * 8];   // 128 KB: M <= 16 subspaces, K <= 256
+  const int head = blockIdx.y;
+  for (int e = threadIdx.x; e < M * K * 8; e += kEncThreads) {
+    const int64_t o = (int64_t)head * cb_sh + e;
+    cbs[e] = cb_f32 ? static_cast<const float*>(cb)[o] : (float)static_cast<const _Float16*>(cb)[o];
+  }
+  __syncthreads();
+  const int64_t gid = (int64_t)blockIdx.x * kEncThreads + threadIdx.x;
+  if (gid >= rows_per_head * M) return;
+  const int64_t n = gid / M;
+  const int j = (int)(gid - n * M);
+  const int64_t row = (int64_t)head * rows_per_head + n;
+  float xv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t o = row * x_rs + j * 8 + e;
+    xv[e] = x_dtype == 0 ? bf16_bits_to_f32(static_cast<const uint16_t*>(x)[o])
+                         : (x_dtype == 1 ? (float)static_cast<const _Float16*>(x)[o] : static_cast<const float*>(x)[o]);
+  }
+  float best = __builtin_inff();
+  int bi = 0;
+  const float* cj = cbs + j * K * 8;
+  for (int c = 0; c < K; ++c) {
+    float dist = 0.f;
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = xv[e] - cj[c * 8 + e];
+        dist = dist + d * d;
+      }
+    }
+    if (dist < best) {
+      best = dist;
+      bi = c;
+    }
+  }
+  idx[row * M + j] = (uint8_t)bi;
+}
+
+// out[row, 8j + e] = cb[j][idx[row, j]][e] (ProductQuantizer.dequantize, src/quantization.py:213-226).
+__global__ void pq_decode_vectors_kernel(const uint8_t* idx, int64_t rows_per_head, const void* cb, int cb_f32,
+                                         int64_t cb_sh, int M, int K, float* out) {
+  const int head = blockIdx.y;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= rows_per_head * M * 8) return;
+  const int64_t row = (int64_t)head * rows_per_head + gid / (M * 8);
+  const int r = (int)(gid % (M * 8));
+  const int j = r / 8, e = r % 8;
+  const int c = idx[row * M + j];
+  const int64_t o = (int64_t)head * cb_sh + ((int64_t)j * K + c) * 8 + e;
+  out[row * (M * 8) + r] = cb_f32 ? static_cast<const float*>(cb)[o] : (float)static_cast<const _Float16*>(cb)[o];
+}
+
+// ============================================================================
+// k-means centroid update, one workgroup per (head, subspace j), one thread
+// per cluster c: thread c walks the points in index order and sums the ones
+// labelled c, so every centroid is a sequential (deterministic) fp32 mean.
+// Empty clusters take the point reseed[head, j, c] drawn by the caller, as
+// src/quantization.py:128-130 re-initialises them.
+// ============================================================================
+constexpr int kKmThreads = 256;
+
+__global__ __launch_bounds__(kKmThreads) void pq_kmeans_update_kernel(const float* x, int64_t n, int M, int K,
+                                                                      const uint8_t* labels, const int64_t* reseed,
+                                                                      _Float16* cb_out, float* cb32) {
+  const int j = blockIdx.x % M;
+  const int head = blockIdx.x / M;
+  const int c = threadIdx.x;
+  const float* xh = x + (int64_t)head * n * (M * 8);
+  const uint8_t* lh = labels + (int64_t)head * n * M + j;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t cnt = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    if (lh[i * M] == c) {
+      const float* p = xh + i * (M * 8) + j * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] += p[e];
+      ++cnt;
+    }
+  }
+  if (c >= K) return;
+  const int64_t o = (((int64_t)head * M + j) * K + c) * 8;
+  const float* src = cnt ? nullptr : xh + reseed[((int64_t)head * M + j) * K + c] * (M * 8) + j * 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = cnt ? s[e] / (float)cnt : src[e];
+    cb32[o + e] = v;
+    cb_out[o + e] = (_Float16)v;
+  }
+}
+
+}  // namespace bytes_amd
+
+using namespace bytes_amd;
+
+extern "C" {
+
+int bytes_pq_decode_workspace_size(int B, int Hq, int Hk, int S, int D, int chunk_req, size_t* bytes) {
+  if (!bytes || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
+  if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  const int G = Hq / Hk, HG = (G + kPqHeads - 1) / kPqHeads;
+  const long units = (long)B * Hk * HG;
+  int chunk, ns;
+  pq_plan(S, units, chunk_req, &chunk, &ns);
+  *bytes = splitk_workspace_bytes(units, ns, D);
+  return 0;
+}
+
+// mode 0: LUT scores + PQ values (decode_attn_pq_lut_kv)
+// mode 1: LUT scores + dense bf16 values (decode_attn_pq_lut)
+// mode 2: scores from q and the key codebook + dense bf16 values (decode_attn_dequant)
+int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* kcb, const void* kidx,
+                         const void* vidx, const void* vcb, const void* v, void* out, int out_dtype, int B, int Hq,
+                         int Hk, int S, int D, int K, int64_t l_sb, int64_t l_sh, int64_t q_sb, int64_t q_sh,
+                         int64_t kcb_sh, int64_t ki_sb, int64_t ki_sh, int64_t ki_ss, int64_t vi_sb, int64_t vi_sh,
+                         int64_t vi_ss, int64_t vcb_sh, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb,
+                         int64_t o_sh, float scale, int chunk_req, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  if (mode < 0 || mode > 2 || !kidx || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0)
+    return (int)hipErrorInvalidValue;
+  if ((D != 64 && D != 128) || K <= 0 || K > kPqKMax || K % 4 != 0) return (int)hipErrorInvalidValue;
+  if (mode == 0 && (!lut || !vidx || !vcb)) return (int)hipErrorInvalidValue;
+  if (mode == 1 && (!lut || !v)) return (int)hipErrorInvalidValue;
+  if (mode == 2 && (!q || !kcb || !v)) return (int)hipErrorInvalidValue;
+  if (out_dtype < 0 || out_dtype > 2) return (int)hipErrorInvalidValue;
+  PqArgs a;
+  a.lut = static_cast<const float*>(lut);
+  a.l_sb = l_sb; a.l_sh = l_sh;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_sb; a.q_sh = q_sh;
+  a.kcb = static_cast<const _Float16*>(kcb);
+  a.kcb_sh = kcb_sh;
+  a.kidx = static_cast<const uint8_t*>(kidx);
+  a.ki_sb = ki_sb; a.ki_sh = ki_sh; a.ki_ss = ki_ss;
+  a.vidx = static_cast<const uint8_t*>(vidx);
+  a.vi_sb = vi_sb; a.vi_sh = vi_sh; a.vi_ss = vi_ss;
+  a.vcb = static_cast<const _Float16*>(vcb);
+  a.vcb_sh = vcb_sh;
+  a.v = static_cast<const uint16_t*>(v);
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.Hk = Hk; a.G = Hq / Hk; a.HG = (a.G + kPqHeads - 1) / kPqHeads; a.S = S; a.K = K;
+  a.scale_log2 = scale * kLog2e;
+  const long units = (long)B * Hk * a.HG;
+  if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
+  int ns;
+  pq_plan(S, units, chunk_req, &a.chunk, &ns);
+  if (ns > 1024) return (int)hipErrorInvalidConfiguration;
+  if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
+  a.o.out = out;
+  a.o.out_dtype = out_dtype;
+  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
+  // the merge kernel maps unit -> (b, hk, head group of kPqHeads)
+  a.o.Hk = Hk; a.o.HB = a.HG; a.o.G = a.G; a.o.hbs = kPqHeads;
+  splitk_carve(workspace, units, ns, a.o);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)(ns * units)), block(kPqWaves * 64);
+#define PQ_LAUNCH(DD, BL, QQ) hipLaunchKernelGGL((pq_decode_kernel<DD, BL, QQ>), grid, block, 0, st, a)
+  if (D == 128) {
+    if (mode == 0) PQ_LAUNCH(128, false, true);
+    else if (mode == 1) PQ_LAUNCH(128, false, false);
+    else PQ_LAUNCH(128, true, false);
+  } else {
+    if (mode == 0) PQ_LAUNCH(64, false, true);
+    else if (mode == 1) PQ_LAUNCH(64, false, false);
+    else PQ_LAUNCH(64, true, false);
+  }
+#undef PQ_LAUNCH
+  int rc = (int)hipGetLastError();
+  if (rc) return rc;
+  return splitk_combine(a.o, units, D, st);
+}
+
+int bytes_pq_build_lut(const void* q, const void* cb, void* lut, int B, int Hq, int Hk, int D, int K, int64_t q_sb,
+                       int64_t q_sh, int64_t cb_sh, float scale, void* stream) {
+  if (!q || !cb || !lut || B <= 0 || Hk <= 0 || Hq % Hk != 0 || D % 8 != 0 || K <= 0 || K > kPqKMax)
+    return (int)hipErrorInvalidValue;
+  if (B > 65535) return (int)hipErrorInvalidConfiguration;
+  const int M = D / 8;
+  const int64_t per_b = (int64_t)Hq * M * K;
+  const int th = 256;
+  dim3 grid((unsigned)((per_b + th - 1) / th), (unsigned)B);
+  hipLaunchKernelGGL(pq_lut_kernel, grid, dim3(th), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(q), q_sb, q_sh, static_cast<const _Float16*>(cb), cb_sh, Hq,
+                     Hq / Hk, M, K, scale, static_cast<float*>(lut));
+  return (int)hipGetLastError();
+}
+
+int bytes_pq_encode(const void* x, int x_dtype, int heads, int64_t rows_per_head, int64_t x_row_stride, int D,
+                    const void* cb, int cb_f32, int64_t cb_sh, int K, void* idx, void* stream) {
+  if (!x || !cb || !idx || heads <= 0 || rows_per_head < 0 || D % 8 != 0 || D / 8 > 16 || K <= 0 || K > kPqKMax)
+    return (int)hipErrorInvalidValue;
+  if (x_dtype < 0 || x_dtype > 2 || heads > 65535) return (int)hipErrorInvalidValue;
+  if (rows_per_head == 0) return 0;
+  const int M = D / 8;
+  const int64_t blocks = (rows_per_head * M + kEncThreads - 1) / kEncThreads;
+  if (blocks > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(pq_encode_kernel, dim3((unsigned)blocks, (unsigned)heads), dim3(kEncThreads), 0,
+                     static_cast<hipStream_t>(stream), x, x_dtype, rows_per_head, x_row_stride, cb, cb_f32 ? 1 : 0,
+                     cb_sh, M, K, static_cast<uint8_t*>(idx));
+  return (int)hipGetLastError();
+}
+
+int bytes_pq_decode_vectors(const void* idx, int heads, int64_t rows_per_head, int D, const void* cb, int cb_f32,
+                            int64_t cb_sh, int K, void* out, void* stream) {
+  if (!idx || !cb || !out || heads <= 0 || rows_per_head < 0 || D % 8 != 0 || K <= 0 || K > kPqKMax)
+    return (int)hipErrorInvalidValue;
+  if (heads > 65535) return (int)hipErrorInvalidConfiguration;
+  if (rows_per_head == 0) return 0;
+  const int64_t per = rows_per_head * D;
+  const int th = 256;
+  hipLaunchKernelGGL(pq_decode_vectors_kernel, dim3((unsigned)((per + th - 1) / th), (unsigned)heads), dim3(th), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(idx), rows_per_head, cb,
+                     cb_f32 ? 1 : 0, cb_sh, D / 8, K, static_cast<float*>(out));
+  return (int)hipGetLastError();
+}
+
+int bytes_pq_kmeans_update(const void* x, int heads, int64_t n, int D, int K, const void* labels, const void* reseed,
+                           void* cb_f16, void* cb_f32, void* stream) {
+  if (!x || !labels || !reseed || !cb_f16 || !cb_f32 || heads <= 0 || n <= 0 || D % 8 != 0 || K <= 0 ||
+      K > kKmThreads)
+    return (int)hipErrorInvalidValue;
+  const int M = D / 8;
+  const int64_t blocks = (int64_t)heads * M;
+  if (blocks > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(pq_kmeans_update_kernel, dim3((unsigned)blocks), dim3(kKmThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const float*>(x), n, M, K,
+                     static_cast<const uint8_t*>(labels), static_cast<const int64_t*>(reseed),
+                     static_cast<_Float16*>(cb_f16), static_cast<float*>(cb_f32));
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -33,7 +33,8 @@ struct SplitKOut {
   unsigned* counter;    // [kMaxUnits] arrival counters, zero between calls
   int nsplit;
   int fused;            // 1: the last-arriving workgroup of a unit merges
-  int Hk, HB, G;        // unit u -> b = u / (Hk*HB), hk, hb; query head = hk*G + hb*16 + h
+  int Hk, HB, G;        // unit u -> b = u / (Hk*HB), hk, hb; query head = hk*G + hb*hbs + h
+  int hbs = 16;         // query heads per head block
 };
 
 constexpr int kFusedSplitMax = 256;       // largest split count merged in-kernel

@@ -24,7 +24,7 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
   const int b = unit / (o.Hk * o.HB);
   const int rem = unit - b * o.Hk * o.HB;
   const int hk = rem / o.HB, hb = rem - (rem / o.HB) * o.HB;
-  const int nh = min(16, o.G - hb * 16);
+  const int nh = min(o.hbs, o.G - hb * o.hbs);
   if (h >= nh) return;
   const int ns = o.nsplit, tid = threadIdx.x, lane = tid & 63;
   const size_t base = (size_t)unit * ns * 16 + h;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
       T.x += v.x; T.y += v.y; T.z += v.z; T.w += v.w;
     }
     const float il = red[1][0];
-    const int hq = hk * o.G + hb * 16 + h, d = item * 4;
+    const int hq = hk * o.G + hb * o.hbs + h, d = item * 4;
     store_out(o, b, hq, d + 0, T.x * il);
     store_out(o, b, hq, d + 1, T.y * il);
     store_out(o, b, hq, d + 2, T.z * il);

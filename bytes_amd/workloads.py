@@ -119,3 +119,29 @@ def c4_quest(seed: int = 0, device="cpu", B: int = 1, Hq: int = 28, Hk: int = 4,
     return {"q": q.to(torch.bfloat16).to(device), "k": k.to(torch.bfloat16).to(device),
             "v": v.to(torch.bfloat16).to(device), "scale": 1.0 / math.sqrt(D), "needles": pos,
             "meta": {"seed": seed, "shape": (B, Hq, Hk, D, L), "n_needle": n_needle}}
+
+
+def c3_pq(seed: int = 0, device="cuda", B: int = 1, Hq: int = 28, Hk: int = 4, D: int = 128, L: int = 32768,
+          K: int = 256, n_train: int = 16384, iters: int = 10) -> Dict:
+    """BASELINE C3 inputs: q, K, V ~ N(0,1) bf16; per KV head, 16 subspaces of 8
+    dims with a K-entry fp16 codebook each for keys and for values, fitted by
+    k-means (`iters` iterations, seeded) on `n_train` fresh N(0,1) bf16 training
+    vectors per head; uint8 codes of K and V; the fp32 LUT of q against the key
+    codebooks with 1/sqrt(D) folded in.  Codebook fitting and encoding run on
+    the GPU kernels of bytes_amd.pq (setup, not part of a decode step)."""
+    from . import pq as PQ
+    g = _gen(seed)
+    q = randn_bf16((B, Hq, 1, D), g).to(device)
+    k = randn_bf16((B, Hk, L, D), g).to(device)
+    v = randn_bf16((B, Hk, L, D), g).to(device)
+    tk = randn_bf16((Hk, n_train, D), g).to(device)
+    tv = randn_bf16((Hk, n_train, D), g).to(device)
+    kcb = PQ.kmeans(tk, K, iters, generator=g).to(torch.float16)          # [Hk, M, K, 8]
+    vcb = PQ.kmeans(tv, K, iters, generator=g).to(torch.float16)
+    k_idx = PQ.pq_encode(k.transpose(0, 1).contiguous(), kcb).transpose(0, 1).contiguous()   # [B,Hk,L,M]
+    v_idx = PQ.pq_encode(v.transpose(0, 1).contiguous(), vcb).transpose(0, 1).contiguous()
+    scale = 1.0 / math.sqrt(D)
+    lut = PQ.pq_build_lut(q, kcb, scale)
+    return {"q": q, "k": k, "v": v, "k_cb": kcb, "v_cb": vcb, "k_idx": k_idx, "v_idx": v_idx, "lut": lut,
+            "scale": scale, "meta": {"seed": seed, "shape": (B, Hq, Hk, D, L), "K": K, "n_train": n_train,
+                                     "kmeans_iters": iters}}

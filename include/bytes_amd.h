@@ -176,6 +176,52 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
                             int Hk, int np, int D, int page, int pos, int local_w, int64_t q_sb, int64_t q_sh,
                             int64_t o_sb, int64_t o_sh, float scale, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Product-quantized decode attention (d_sub = 8, M = D/8 subspaces, K <= 256
+ * codewords, K % 4 == 0; codebooks fp16 [M, K, 8], per KV head when the head
+ * stride *_sh is non-zero; codes uint8 [B, Hk, S, M] with unit stride in M and
+ * token stride M).
+ *   mode 0  decode_attn_pq_lut_kv  src/attention_kernels.py:471-500 (kernel :397-469):
+ *           score_t = sum_j lut[b,h,j,kidx[t,j]]; values = concat_j vcb[j, vidx[t,j]]
+ *   mode 1  decode_attn_pq_lut     :365-392 (kernel :301-363): LUT scores, dense bf16 v
+ *   mode 2  decode_attn_dequant    :267-296 (kernel :187-265): scores q . k_hat with
+ *           k_hat = concat_j kcb[j, kidx[t,j]] (no scale), dense bf16 v
+ *   lut [B, Hq, M, K] fp32 (one head contiguous); q [B, Hq, D] bf16;
+ *   out [B, Hq, D] of out_dtype (0 bf16, 1 f16, 2 f32).  `scale` multiplies the
+ *   scores (the reference has none: pass 1.0).
+ * ------------------------------------------------------------------------- */
+int bytes_pq_decode_workspace_size(int B, int Hq, int Hk, int S, int D, int chunk, size_t* bytes);
+int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* kcb, const void* kidx,
+                         const void* vidx, const void* vcb, const void* v, void* out, int out_dtype, int B,
+                         int Hq, int Hk, int S, int D, int K, int64_t l_sb, int64_t l_sh, int64_t q_sb,
+                         int64_t q_sh, int64_t kcb_sh, int64_t ki_sb, int64_t ki_sh, int64_t ki_ss,
+                         int64_t vi_sb, int64_t vi_sh, int64_t vi_ss, int64_t vcb_sh, int64_t v_sb,
+                         int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scale, int chunk,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* PQ setup path.
+ * bytes_pq_build_lut: lut[b,h,j,c] = scale * sum_e q[b,h,8j+e] * cb[h/G][j][c][e] (fp32),
+ *   the LUT precompute of benchmarks/test_correctness.py:272-273.
+ * bytes_pq_encode: idx[r, j] = argmin_c sum_e (x[r, 8j+e] - cb[j][c][e])^2 in fp32
+ *   (e ascending, no fused multiply-add), first index on ties: the CPU rule of
+ *   src/quantization.py:203-211.  x [heads * rows_per_head, D] (dtype 0 bf16,
+ *   1 f16, 2 f32, row stride x_row_stride); codebook fp16 (cb_f32 = 0) or fp32.
+ * bytes_pq_decode_vectors: out[r, 8j+e] = cb[j][idx[r, j]][e] fp32
+ *   (src/quantization.py:213-226).
+ * bytes_pq_kmeans_update: one k-means centroid update (src/quantization.py:120-130)
+ *   for x [heads, n, D] fp32 with labels [heads, n, M] uint8: cb = mean of the
+ *   points of each cluster, summed in index order; an empty cluster takes the
+ *   point reseed[head, j, c] (int64).  Writes cb_f16 and cb_f32 [heads, M, K, 8].
+ * ------------------------------------------------------------------------- */
+int bytes_pq_build_lut(const void* q, const void* cb, void* lut, int B, int Hq, int Hk, int D, int K,
+                       int64_t q_sb, int64_t q_sh, int64_t cb_sh, float scale, void* stream);
+int bytes_pq_encode(const void* x, int x_dtype, int heads, int64_t rows_per_head, int64_t x_row_stride, int D,
+                    const void* cb, int cb_f32, int64_t cb_sh, int K, void* idx, void* stream);
+int bytes_pq_decode_vectors(const void* idx, int heads, int64_t rows_per_head, int D, const void* cb,
+                            int cb_f32, int64_t cb_sh, int K, void* out, void* stream);
+int bytes_pq_kmeans_update(const void* x, int heads, int64_t n, int D, int K, const void* labels,
+                           const void* reseed, void* cb_f16, void* cb_f32, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
