@@ -221,6 +221,53 @@ class QuestCase(Case):
                 f"(B{B} Hq{Hq} L{L})", run, 1)
 
 
+class PqCase(Case):
+    """BASELINE C3: PQ-LUT decode with quantized keys and values.  The LUT build
+    (q against the key codebooks) is part of the step; codebook fitting and
+    encoding are setup."""
+    kernel = "pq_decode_kernel"
+
+    def __init__(self, name, B=1, Hq=28, Hk=4, D=128, L=32768, K=256):
+        self.name, self.shape, self.K = name, (B, Hq, Hk, D, L), K
+        self.dtype = "u8 codes+fp16 codebooks+fp32 LUT"
+        self.workload = f"PQ-LUT KV decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} (16 x 8-dim subspaces, K={K})"
+
+    def bytes_per_step(self):
+        B, Hq, Hk, D, L = self.shape
+        M = D // 8
+        codes = 2 * B * Hk * L * M
+        lut = B * Hq * M * self.K * 4
+        cbs = 2 * Hk * M * self.K * 8 * 2
+        return codes + 2 * lut + cbs + B * Hq * D * 2 + B * Hq * D * 2
+
+    def make(self, dev):
+        from bytes_amd import workloads as W
+        x = W.c3_pq(seed=0, device=dev)
+        return {n: x[n] for n in ("q", "k_cb", "v_cb", "k_idx", "v_idx", "scale")}
+
+    def step(self, x):
+        from bytes_amd.pq import decode_attn_pq_lut_kv, pq_build_lut
+        lut = pq_build_lut(x["q"], x["k_cb"], x["scale"])
+        return decode_attn_pq_lut_kv(lut, x["k_idx"], x["v_idx"], x["v_cb"])
+
+    def cpu_sample(self):
+        from oracle import reference as R
+        B, Hq, Hk, D, L = self.shape
+        g = torch.Generator().manual_seed(0)
+        M = D // 8
+        q = torch.randn(1, Hq // Hk, 1, D, generator=g).to(torch.bfloat16)
+        kcb = torch.randn(1, M, self.K, 8, generator=g).half()
+        vcb = torch.randn(1, M, self.K, 8, generator=g).half()
+        ki = torch.randint(0, self.K, (1, 1, L, M), generator=g).to(torch.uint8)
+        vi = torch.randint(0, self.K, (1, 1, L, M), generator=g).to(torch.uint8)
+        units = B * Hk
+
+        def run():
+            lut = R.pq_build_lut(q, kcb, 1.0 / D ** 0.5)
+            return R.decode_attn_pq_lut_kv(lut, ki, vi, vcb)
+        return (f"one (b, kv-head) unit of {units}: oracle LUT build + pq_lut_kv over L={L}", run, units)
+
+
 class CopyCase(Case):
     """Plain device copy of known size: the calibration point for HBM byte counters
     (FETCH_SIZE / WRITE_SIZE of this kernel vs its exact 2 x nbytes traffic)."""
@@ -258,6 +305,7 @@ def cases():
         "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
         "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536),
         "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536),
+        "c3_pq": PqCase("c3_pq"),
         "c4_quest": QuestCase("c4_quest"),
         "c5_topk256": TopkCase("c5_topk256", 256),
         "c5_topk1024": TopkCase("c5_topk1024", 1024),
@@ -267,6 +315,18 @@ def cases():
 
 
 HEADLINE = "c2_kivi2"
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch of the config's dominant kernel, measured by the
+    FETCH_SIZE / WRITE_SIZE counter passes recorded in profiles/traffic.json
+    (each scaled by the same counter's reading for a copy of known size)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
 
 
 # ---------------------------------------------------------------------------
@@ -369,6 +429,10 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
                      "kernel": head.kernel, "algorithmic_bytes": r["bytes_per_step"]},
     }
+    tr = measured_traffic(head.name)
+    if tr is not None:
+        line["roofline"]["traffic"] = tr["traffic_bytes"]
+        line["roofline"]["traffic_source"] = tr["source"]
     if args.all:
         per = {}
         for name, c in allc.items():
