@@ -51,7 +51,7 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64,                                 # out strides (b, h)
         c_f32, c_vp),                                 # scaling, stream
     "bytes_topk_workspace_size": (c_i64, c_int, c_int, c_szp),
-    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
+    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
     "bytes_gather_attn_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
     "bytes_gather_attn": (
         c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, k, v, idx, out

@@ -152,7 +152,8 @@ static void gather_plan(int kb, long units, int chunk_req, int* chunk, int* ns) 
   if (chunk_req > 0) {
     c = chunk_req;
   } else {
-    const long target = 2L * device_cu_count();
+    // about one workgroup per CU: each wave then pipelines at least two tiles
+    const long target = device_cu_count();
     c = (int)(((long)kb * units + target - 1) / target);
   }
   c = (c + step - 1) / step * step;

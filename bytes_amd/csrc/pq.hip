@@ -84,11 +84,11 @@ __device__ __forceinline__ void pq_stage_dense_v(int lane, const u32x4 (&r)[Dens
 }
 
 // Codes of one tile, in registers:
-//  kc[blk*4+i]: the M key codes of tile row blk*16 + lg*4 + i (the score layout)
-//  vc[i]:       value code of row lane/16 + 4i, subspace lane%16 (the staging layout)
+//  kc: the M key codes of tile row lane % 32 (every lane scores whole rows)
+//  vc[i]: value code of row p / M, subspace p % M, for staging chunk p = lane + 64*i
 template <int D, bool QV>
 struct PqRegs {
-  u32x4 kc[8];
+  u32x4 kc;
   uint32_t vc[QV ? 8 : 1];
   u32x4 vd[QV ? 1 : DenseCfg<D>::CPL];
 };
@@ -97,22 +97,17 @@ template <int D, bool QV>
 __device__ __forceinline__ void pq_issue(const PqArgs& a, const uint8_t* kib, const uint8_t* vib, const uint16_t* vbase,
                                          int t0, int lane, PqRegs<D, QV>& r) {
   constexpr int M = D / 8;
-  const int lg = lane >> 4;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = min(t0 + blk * 16 + lg * 4 + i, a.S - 1);
-      const uint8_t* p = kib + (int64_t)t * a.ki_ss;
-      if (M == 16) {
-        r.kc[blk * 4 + i] = ld16(p);
-      } else {
-        const u32x2 h = *reinterpret_cast<const u32x2*>(p);
-        r.kc[blk * 4 + i] = u32x4{h[0], h[1], 0u, 0u};
-      }
+  {
+    const int t = min(t0 + (lane & 31), a.S - 1);
+    const uint8_t* p = kib + (int64_t)t * a.ki_ss;
+    if constexpr (M == 16) {
+      r.kc = ld16(p);
+    } else {
+      const u32x2 h = *reinterpret_cast<const u32x2*>(p);
+      r.kc = u32x4{h[0], h[1], 0u, 0u};
     }
+  }
   if constexpr (QV) {
-    // staging chunk p = lane + 64*i covers row p / M, subspace p % M
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int p = lane + 64 * i;
@@ -125,13 +120,40 @@ __device__ __forceinline__ void pq_issue(const PqArgs& a, const uint8_t* kib, co
   }
 }
 
+// One 32-row tile.  Scores: lane l sums the LUT entries of row l % 32 for head
+// slots l/32 and l/32 + 2 (subspaces in order), the wave passes them through
+// its tile buffer into the score-MFMA layout (head l%16, rows blk*16 + lg*4 + i),
+// then the V tile is built in the same buffer and the softmax/PV step runs.
 template <int D, bool QV>
 __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV>& r, uint32_t vmask, int lane, int nh,
                                         const float* lut, const char* vcb, char* vst, float& m_run, float& l_run,
                                         f32x4 (&acc)[D / 16]) {
   constexpr int M = D / 8;
-  const int l16 = lane & 15;
-  // V tile into LDS
+  const int l16 = lane & 15, lg = lane >> 4;
+  float* sc_lds = reinterpret_cast<float*>(vst);   // [kPqHeads][32]
+#pragma unroll
+  for (int rep = 0; rep < kPqHeads / 2; ++rep) {
+    const int h = (lane >> 5) + 2 * rep;
+    if (h < nh) {
+      const float* lh = lut + h * (M * kPqKMax);
+      float sc = 0.f;
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        const uint32_t code = (r.kc[j >> 2] >> ((j & 3) * 8)) & 0xFFu;
+        sc += lh[j * kPqKMax + code];
+      }
+      sc_lds[h * kTile + (lane & 31)] = sc;
+    }
+  }
+  wave_lds_sync();
+  f32x4 s[2];
+  const int hh = l16 < nh ? l16 : 0;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[blk][i] = sc_lds[hh * kTile + blk * 16 + lg * 4 + i];
+  wave_lds_sync();
+  // V tile into the same buffer
   if constexpr (QV) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -145,24 +167,27 @@ __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV>& r,
   } else {
     pq_stage_dense_v<D>(lane, r.vd, vst);
   }
-  // scores: lane (head l16, row group lg) sums its 8 rows' LUT entries in subspace order
-  f32x4 s[2];
-  const float* lh = lut + (l16 < nh ? l16 : 0) * (M * kPqKMax);
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 c = r.kc[blk * 4 + i];
-      float sc = 0.f;
-#pragma unroll
-      for (int j = 0; j < M; ++j) {
-        const uint32_t code = (c[j >> 2] >> ((j & 3) * 8)) & 0xFFu;
-        sc += lh[j * kPqKMax + code];
-      }
-      s[blk][i] = sc;
-    }
   wave_lds_sync();
   tile_softmax_pv<D, QV>(s, l16 < nh ? vmask : 0u, a.scale_log2, lane, vst, m_run, l_run, acc);
+}
+
+// Copy n 16-byte chunks global -> LDS with the workgroup, 8 loads in flight per thread.
+template <typename SRC, typename DST>
+__device__ __forceinline__ void stage_chunks(int n, SRC src, DST dst) {
+  constexpr int NT = kPqWaves * 64, BATCH = 8;
+  for (int e0 = threadIdx.x; e0 < n; e0 += NT * BATCH) {
+    u32x4 v[BATCH];
+#pragma unroll
+    for (int bb = 0; bb < BATCH; ++bb) {
+      const int e = e0 + bb * NT;
+      v[bb] = e < n ? ld16(src(e)) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int bb = 0; bb < BATCH; ++bb) {
+      const int e = e0 + bb * NT;
+      if (e < n) *reinterpret_cast<u32x4*>(dst(e)) = v[bb];
+    }
+  }
 }
 
 template <int D, bool BUILD_LUT, bool QV>
@@ -200,19 +225,28 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
       lut[(h * M + j) * kPqKMax + c] = sum;
     }
   } else {
-    for (int e = threadIdx.x; e < nh * M * (K / 4); e += kPqWaves * 64) {
-      const int h = e / (M * (K / 4)), r2 = e - h * (M * (K / 4));
-      const int j = r2 / (K / 4), c4 = r2 - j * (K / 4);
-      const float* src = a.lut + (int64_t)b * a.l_sb + (int64_t)(hq0 + h) * a.l_sh + j * K + c4 * 4;
-      *reinterpret_cast<u32x4*>(lut + (h * M + j) * kPqKMax + c4 * 4) = ld16(src);
-    }
+    const int K4 = K / 4;
+    stage_chunks(
+        nh * M * K4,
+        [&](int e) {
+          const int h = e / (M * K4), r2 = e - h * (M * K4);
+          const int j = r2 / K4, c4 = r2 - j * K4;
+          return a.lut + (int64_t)b * a.l_sb + (int64_t)(hq0 + h) * a.l_sh + j * K + c4 * 4;
+        },
+        [&](int e) {
+          const int h = e / (M * K4), r2 = e - h * (M * K4);
+          const int j = r2 / K4, c4 = r2 - j * K4;
+          return lut + (h * M + j) * kPqKMax + c4 * 4;
+        });
   }
-  if (QV) {
+  if constexpr (QV) {
     const _Float16* cb = a.vcb + (int64_t)hk * a.vcb_sh;
-    for (int e = threadIdx.x; e < M * K; e += kPqWaves * 64) {
-      const int j = e / K, c = e - j * K;
-      *reinterpret_cast<u32x4*>(vcb + ((j * kPqKMax + c) * 8) * 2) = ld16(cb + (int64_t)e * 8);
-    }
+    stage_chunks(
+        M * K, [&](int e) { return cb + (int64_t)e * 8; },
+        [&](int e) {
+          const int j = e / K, c = e - j * K;
+          return vcb + ((j * kPqKMax + c) * 8) * 2;
+        });
   }
 
   float m_run = kNegInf, l_run = 0.f;

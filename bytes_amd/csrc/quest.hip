@@ -56,49 +56,49 @@ __global__ void quest_minmax_kernel(const uint16_t* k, int64_t k_sb, int64_t k_s
 }
 
 constexpr int kQuestThreads = 256;
+constexpr int kQuestPages = 32;                    // pages per workgroup
+constexpr int kQuestSlots = kQuestThreads / kQuestPages;   // head slots per round
 
-// One thread per (b, hk, page), all G query heads of the group: the page's
-// min/max rows are read once and every head's bound is summed over d in order.
+// One workgroup per (b, kv head, 32 pages); thread (page, head slot).  The
+// pages' min/max rows are staged in LDS (rows padded to an odd number of
+// dwords, so the 32 pages a wave reads at one d sit in distinct banks) and
+// each (page, head) bound is summed over d in order.
 template <int D>
 __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                                                     const uint16_t* kmin, const uint16_t* kmax,
                                                                     int Hk, int G, int np, int page, int pos,
                                                                     int local_w, float scale, float* bound,
                                                                     int64_t o_sb, int64_t o_sh) {
+  constexpr int RW = D / 2 + 1;                    // dwords per padded row
+  __shared__ uint32_t mn_s[kQuestPages * RW];
+  __shared__ uint32_t mx_s[kQuestPages * RW];
   __shared__ float qs[16][D];
-  const int parts = (np + kQuestThreads - 1) / kQuestThreads;
+  const int parts = (np + kQuestPages - 1) / kQuestPages;
   const int bh = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
   const int b = bh / Hk, hk = bh - (bh / Hk) * Hk;
+  const int p0 = part * kQuestPages;
   for (int i = threadIdx.x; i < G * D; i += kQuestThreads) {
     const int g = i / D, d = i - (i / D) * D;
     qs[g][d] = bf16_bits_to_f32(q[(int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d]);
   }
-  __syncthreads();
-  const int p = part * kQuestThreads + threadIdx.x;
-  if (p >= np) return;
-  const int64_t row = ((int64_t)b * Hk + hk) * np + p;
-  const uint16_t* mnr = kmin + row * D;
-  const uint16_t* mxr = kmax + row * D;
-  float acc[16];
+  const int64_t row0 = ((int64_t)b * Hk + hk) * np;
+  constexpr int CH = D / 8;                        // 16-byte chunks per row
+  for (int e = threadIdx.x; e < kQuestPages * CH; e += kQuestThreads) {
+    const int pp = e / CH, c = e - (e / CH) * CH;
+    if (p0 + pp < np) {
+      const u32x4 a = ld16(kmin + (row0 + p0 + pp) * D + c * 8);
+      const u32x4 z = ld16(kmax + (row0 + p0 + pp) * D + c * 8);
 #pragma unroll
-  for (int c = 0; c < D / 8; ++c) {
-    const u32x4 a = ld16(mnr + c * 8), z = ld16(mxr + c * 8);
-    const uint16_t* ha = reinterpret_cast<const uint16_t*>(&a);
-    const uint16_t* hz = reinterpret_cast<const uint16_t*>(&z);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = c * 8 + j;
-      const float lo = bf16_bits_to_f32(ha[j]), hi = bf16_bits_to_f32(hz[j]);
-#pragma unroll
-      for (int g = 0; g < 16; ++g) {
-        if (g < G) {
-          const float qd = qs[g][d];
-          const float t = nmax(qd * lo, qd * hi);
-          acc[g] = d == 0 ? t : acc[g] + t;
-        }
+      for (int j = 0; j < 4; ++j) {
+        mn_s[pp * RW + c * 4 + j] = a[j];
+        mx_s[pp * RW + c * 4 + j] = z[j];
       }
     }
   }
+  __syncthreads();
+  const int pp = threadIdx.x % kQuestPages;
+  const int p = p0 + pp;
+  if (p >= np) return;
   // causal validity and the forced recent window, at page granularity
   const bool valid = (int64_t)p * page <= pos;
   bool recent = false;
@@ -106,14 +106,22 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     const int lo = max(pos - local_w + 1, 0) / page, hi = pos / page;
     recent = p >= lo && p <= hi;
   }
-#pragma unroll
-  for (int g = 0; g < 16; ++g) {
-    if (g < G) {
-      float v = acc[g] * scale;
-      if (!valid) v = kNegInf;
-      if (recent) v = __builtin_inff();
-      bound[(int64_t)b * o_sb + (int64_t)(hk * G + g) * o_sh + p] = v;
+  for (int g = threadIdx.x / kQuestPages; g < G; g += kQuestSlots) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int d2 = 0; d2 < D / 2; ++d2) {
+      const uint32_t a = mn_s[pp * RW + d2], z = mx_s[pp * RW + d2];
+      const float lo0 = __uint_as_float(a << 16), lo1 = __uint_as_float(a & 0xFFFF0000u);
+      const float hi0 = __uint_as_float(z << 16), hi1 = __uint_as_float(z & 0xFFFF0000u);
+      const float q0 = qs[g][2 * d2], q1 = qs[g][2 * d2 + 1];
+      const float t0 = nmax(q0 * lo0, q0 * hi0);
+      acc = d2 == 0 ? t0 : acc + t0;
+      acc = acc + nmax(q1 * lo1, q1 * hi1);
     }
+    float v = acc * scale;
+    if (!valid) v = kNegInf;
+    if (recent) v = __builtin_inff();
+    bound[(int64_t)b * o_sb + (int64_t)(hk * G + g) * o_sh + p] = v;
   }
 }
 
@@ -146,7 +154,7 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
   const int G = Hq / Hk;
   if (G > 16) return (int)hipErrorNotSupported;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
-  const int parts = (np + kQuestThreads - 1) / kQuestThreads;
+  const int parts = (np + kQuestPages - 1) / kQuestPages;
   const long grid = (long)B * Hk * parts;
   if (grid > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);

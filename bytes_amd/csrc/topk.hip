@@ -33,6 +33,9 @@ constexpr int kTopkMaxK = 8192;
 constexpr int kBins = 2048;            // digit = top 11 bits of the order key
 constexpr int kCandCap = 8192;         // candidate list capacity per row
 constexpr int kSortMax = 16384;        // LDS sort capacity (above list + candidates)
+constexpr int kShortRow = 16384;       // rows up to this length take the single-kernel exact path
+constexpr int kFullSortRow = 4096;     // ... and up to this length simply sort the whole row
+constexpr int kEqMax = 512;            // keys equal to the threshold handled by the bitmap path
 
 // Monotone key: larger score -> larger key.  NaN -> 0xFFFFFFFF, -0 -> +0.
 __device__ __forceinline__ uint32_t order_key(float x) {
@@ -91,13 +94,46 @@ __device__ __forceinline__ void load4(const float* x, int i, int n, uint32_t (&k
   }
 }
 
-// In-LDS bitonic sort of buf[0, P) into descending order (P a power of two).
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic merge steps with strides 32 .. 1 on the 64-element segments of buf,
+// one segment per wave at a time, in registers (xor shuffles); for the merge
+// of blocks of `size`, whose direction is descending where (index & size) == 0.
+// size <= 64 runs the whole network up to that size.
+template <int NT>
+__device__ __forceinline__ void bitonic_wave_steps(uint64_t* buf, int P, int size_lo, int size_hi) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int seg = w; seg < P / 64; seg += NW) {
+    const int i = seg * 64 + lane;
+    uint64_t x = buf[i];
+    for (int size = size_lo; size <= size_hi; size <<= 1) {
+      const bool desc = (i & size) == 0;
+      for (int stride = (size < 64 ? size : 64) >> 1; stride > 0; stride >>= 1) {
+        const uint64_t y = shfl_xor_u64(x, stride);
+        const bool keep_max = ((lane & stride) == 0) == desc;
+        x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+      }
+    }
+    buf[i] = x;
+  }
+}
+
+// In-LDS bitonic sort of buf[0, P) into descending order (P a power of two,
+// P >= 64).  Strides below 64 run inside a wave on xor shuffles; only strides
+// >= 64 go through LDS with a workgroup barrier.
 template <int NT>
 __device__ void bitonic_desc(uint64_t* buf, int P) {
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+  bitonic_wave_steps<NT>(buf, P, 2, 64);
+  __syncthreads();
+  for (int size = 128; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride >= 64; stride >>= 1) {
       for (int i = threadIdx.x; i < P / 2; i += NT) {
-        const int lo = (i / stride) * stride * 2 + (i % stride);
+        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
         const int hi = lo + stride;
         const bool desc = (lo & size) == 0;
         const uint64_t va = buf[lo], vb = buf[hi];
@@ -108,6 +144,8 @@ __device__ void bitonic_desc(uint64_t* buf, int P) {
       }
       __syncthreads();
     }
+    bitonic_wave_steps<NT>(buf, P, size, size);
+    __syncthreads();
   }
 }
 
@@ -252,11 +290,31 @@ __global__ __launch_bounds__(kPassThreads) void topk_filter_kernel(const float* 
     }
 }
 
+// Over an LDS histogram of 2048 digits (1024 threads, two digits each): the
+// digit holding the kr-th largest key and the count of keys in larger digits,
+// left in sel[0], sel[1].
+__device__ __forceinline__ void pick_digit(const uint32_t* hist, uint32_t kr, uint32_t* wsum, uint32_t* sel) {
+  const int tid = threadIdx.x;
+  const uint32_t c0 = hist[2 * tid], c1 = hist[2 * tid + 1];
+  uint32_t total;
+  const uint32_t incl = block_incl_scan<kTopkThreads>(c0 + c1, wsum, total);
+  const uint32_t above = total - incl;
+  if (above < kr && above + c1 >= kr) {
+    sel[0] = 2 * tid + 1;
+    sel[1] = above;
+  } else if (above + c1 < kr && above + c1 + c0 >= kr) {
+    sel[0] = 2 * tid;
+    sel[1] = above + c1;
+  }
+  __syncthreads();
+}
+
 // Exact selection over a whole row in one workgroup (used when the candidate
-// list overflowed): radix select, collection in index order, sort.
+// list overflowed): radix select, then either collection and sort by score or
+// (unsorted) collection straight into index order.
 template <bool VEC>
-__device__ void topk_row_exact(const float* x, int n, int k, uint64_t* sortbuf, uint32_t* hist, uint32_t* wsum,
-                               uint32_t* sel, int32_t* o) {
+__device__ void topk_row_exact(const float* x, int n, int k, int sorted, uint64_t* sortbuf, uint32_t* hist,
+                               uint32_t* wsum, uint32_t* sel, int32_t* o) {
   const int tid = threadIdx.x;
   uint32_t prefix = 0u, pmask = 0u;
   uint32_t kr = (uint32_t)k;
@@ -276,18 +334,7 @@ __device__ void topk_row_exact(const float* x, int n, int k, uint64_t* sortbuf, 
     }
     __syncthreads();
     // digit d with count(digits > d) < kr <= count(digits >= d); shift-relative digits
-    const uint32_t c0 = hist[2 * tid], c1 = hist[2 * tid + 1];
-    uint32_t total;
-    const uint32_t incl = block_incl_scan<kTopkThreads>(c0 + c1, wsum, total);
-    const uint32_t above = total - incl;
-    if (above < kr && above + c1 >= kr) {
-      sel[0] = 2 * tid + 1;
-      sel[1] = above;
-    } else if (above + c1 < kr && above + c1 + c0 >= kr) {
-      sel[0] = 2 * tid;
-      sel[1] = above + c1;
-    }
-    __syncthreads();
+    pick_digit(hist, kr, wsum, sel);
     kr -= sel[1];
     prefix |= sel[0] << shift;
     pmask |= dmask << shift;
@@ -295,7 +342,48 @@ __device__ void topk_row_exact(const float* x, int n, int k, uint64_t* sortbuf, 
   }
   const uint32_t T = prefix;
   const uint32_t need = kr;                      // keys equal to T to take, >= 1
-  int P = 2;
+  if (!sorted) {
+    // collection in index order: output slot = selected keys before this one
+    if (tid == 0) sel[3] = 0u;                   // keys equal to T taken so far
+    if (tid == 0) sel[2] = 0u;                   // output slots used so far
+    __syncthreads();
+    for (int base = 0; base < n; base += kTopkThreads * 4) {
+      const int i = base + tid * 4;
+      uint32_t key[4];
+      bool ok[4];
+      load4<VEC>(x, i, n, key, ok);
+      uint32_t ne = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ne += (ok[j] && key[j] == T) ? 1u : 0u;
+      uint32_t tot_eq;
+      uint32_t rank = block_incl_scan<kTopkThreads>(ne, wsum, tot_eq) - ne;
+      const uint32_t eq0 = sel[3];
+      bool take[4];
+      uint32_t nt = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        take[j] = ok[j] && key[j] > T;
+        if (ok[j] && key[j] == T) {
+          take[j] = eq0 + rank < need;
+          ++rank;
+        }
+        nt += take[j] ? 1u : 0u;
+      }
+      uint32_t tot_t;
+      uint32_t pos = sel[2] + block_incl_scan<kTopkThreads>(nt, wsum, tot_t) - nt;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (take[j]) o[pos++] = i + j;
+      __syncthreads();
+      if (tid == 0) {
+        sel[3] = eq0 + tot_eq;
+        sel[2] += tot_t;
+      }
+      __syncthreads();
+    }
+    return;
+  }
+  int P = 64;
   while (P < k) P <<= 1;
   for (int i = tid; i < P; i += kTopkThreads) sortbuf[i] = 0ull;
   if (tid == 0) {
@@ -333,32 +421,149 @@ __device__ void topk_row_exact(const float* x, int n, int k, uint64_t* sortbuf, 
 }
 
 // ---- 3. per-row selection and sort ----
+// sorted: output ordered by (score desc, index asc); else by index ascending.
 template <bool VEC>
 __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* scores, int64_t row_stride, int n,
                                                                    int k, TopkWs ws, int32_t* out,
-                                                                   int64_t out_stride) {
+                                                                   int64_t out_stride, int exact, int sorted) {
   extern __shared__ uint64_t sortbuf[];          // [kSortMax]
   __shared__ uint32_t hist[kBins];
   __shared__ uint32_t wsum[kTopkThreads / 64];
-  __shared__ uint32_t sel[4];
+  __shared__ uint32_t sel[8];
   const int row = blockIdx.x, tid = threadIdx.x;
-  const uint32_t A = ws.cnt[row * 2 + 0], Cn = ws.cnt[row * 2 + 1];
   int32_t* o = out + (int64_t)row * out_stride;
+  const float* x = scores + (int64_t)row * row_stride;
+  if (exact) {                                   // short rows: one pass of this kernel only
+    if (sorted && n <= kFullSortRow) {
+      // sort the whole row by (key desc, index asc)
+      int P = 64;
+      while (P < n) P <<= 1;
+      for (int i = tid; i < P; i += kTopkThreads) sortbuf[i] = i < n ? sort_val(order_key(x[i]), i) : 0ull;
+      __syncthreads();
+      bitonic_desc<kTopkThreads>(sortbuf, P);
+      for (int i = tid; i < k; i += kTopkThreads) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sortbuf[i]);
+    } else {
+      topk_row_exact<VEC>(x, n, k, sorted, sortbuf, hist, wsum, sel, o);
+    }
+    return;
+  }
+  const uint32_t A = ws.cnt[row * 2 + 0], Cn = ws.cnt[row * 2 + 1];
+  bool fallback = true;
   // lists are complete and consistent: fewer than k keys above the digit, the
   // candidates fill the rest and fit their list
   if (A < (uint32_t)k && A + Cn >= (uint32_t)k && Cn <= (uint32_t)kCandCap) {
-    const int m = (int)(A + Cn);
-    int P = 2;
-    while (P < m) P <<= 1;
+    fallback = false;
     const uint64_t* al = ws.above + (int64_t)row * k;
     const uint64_t* cl = ws.cand + (int64_t)row * kCandCap;
-    for (int i = tid; i < P; i += kTopkThreads)
-      sortbuf[i] = i < (int)A ? al[i] : (i < m ? cl[i - A] : 0ull);
+    // refine among the candidates (which share the top 11 key bits) on bits
+    // 20..10: keep the ones in larger digits and all of the threshold digit
+    constexpr int PC = kCandCap / kTopkThreads;
+    uint64_t cv[PC];
+#pragma unroll
+    for (int j = 0; j < PC; ++j) {
+      const int i = tid + j * kTopkThreads;
+      cv[j] = i < (int)Cn ? cl[i] : 0ull;
+    }
+    auto live = [&](int j) { return tid + j * kTopkThreads < (int)Cn; };
+    auto dg1 = [&](int j) { return (uint32_t)(cv[j] >> 42) & 0x7FFu; };     // key bits 20..10
+    auto dg2 = [&](int j) { return (uint32_t)(cv[j] >> 32) & 0x3FFu; };     // key bits 9..0
+    for (int b = tid; b < kBins; b += kTopkThreads) hist[b] = 0u;
     __syncthreads();
-    bitonic_desc<kTopkThreads>(sortbuf, P);
-    for (int i = tid; i < k; i += kTopkThreads) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sortbuf[i]);
-  } else {
-    topk_row_exact<VEC>(scores + (int64_t)row * row_stride, n, k, sortbuf, hist, wsum, sel, o);
+#pragma unroll
+    for (int j = 0; j < PC; ++j)
+      if (live(j)) atomicAdd(&hist[dg1(j)], 1u);
+    __syncthreads();
+    pick_digit(hist, (uint32_t)k - A, wsum, sel);
+    const uint32_t d1 = sel[0], above1 = sel[1];
+    if (sorted) {
+      uint32_t nk = 0;
+#pragma unroll
+      for (int j = 0; j < PC; ++j) nk += (live(j) && dg1(j) >= d1) ? 1u : 0u;
+      uint32_t kept;
+      uint32_t off = block_incl_scan<kTopkThreads>(nk, wsum, kept) - nk;
+      const int m = (int)(A + kept);
+      int P = 64;
+      while (P < m) P <<= 1;
+      for (int i = tid; i < P; i += kTopkThreads) sortbuf[i] = i < (int)A ? al[i] : 0ull;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < PC; ++j)
+        if (live(j) && dg1(j) >= d1) sortbuf[A + off++] = cv[j];
+      __syncthreads();
+      bitonic_desc<kTopkThreads>(sortbuf, P);
+      for (int i = tid; i < k; i += kTopkThreads) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sortbuf[i]);
+    } else {
+      // exact threshold: bits 9..0 among the candidates of digit d1
+      const uint32_t need1 = (uint32_t)k - A - above1;
+      for (int b = tid; b < kBins; b += kTopkThreads) hist[b] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < PC; ++j)
+        if (live(j) && dg1(j) == d1) atomicAdd(&hist[dg2(j)], 1u);
+      __syncthreads();
+      pick_digit(hist, need1, wsum, sel);
+      const uint32_t d2 = sel[0];
+      const uint32_t need = need1 - sel[1];        // keys equal to T to take (lowest indices)
+      if (tid == 0) sel[4] = (uint32_t)(cl[0] >> 53);   // the candidates' common top digit
+      if (tid == 0) sel[5] = 0u;
+      __syncthreads();
+      const uint32_t T = (sel[4] << 21) | (d1 << 10) | d2;
+      uint32_t* eql = reinterpret_cast<uint32_t*>(sortbuf);            // [kEqMax] indices equal to T
+      uint32_t* bits = eql + kEqMax;                                    // [ceil(n/32)] selection bitmap
+      const int W = (n + 31) / 32;
+      const bool fits = (size_t)(kEqMax + W) * 4 <= (size_t)kSortMax * 8;   // bitmap fits the LDS buffer
+#pragma unroll
+      for (int j = 0; j < PC; ++j)
+        if (live(j) && (uint32_t)(cv[j] >> 32) == T) {
+          const uint32_t slot = atomicAdd(&sel[5], 1u);
+          if (slot < (uint32_t)kEqMax) eql[slot] = 0xFFFFFFFFu - (uint32_t)cv[j];
+        }
+      if (fits)
+        for (int w = tid; w < W; w += kTopkThreads) bits[w] = 0u;
+      __syncthreads();
+      const uint32_t ceq = sel[5];
+      if (ceq <= (uint32_t)kEqMax && fits) {
+        for (int i = tid; i < (int)A; i += kTopkThreads) {
+          const uint32_t idx = 0xFFFFFFFFu - (uint32_t)al[i];
+          atomicOr(&bits[idx >> 5], 1u << (idx & 31));
+        }
+#pragma unroll
+        for (int j = 0; j < PC; ++j) {
+          if (!live(j)) continue;
+          const uint32_t key = (uint32_t)(cv[j] >> 32);
+          const uint32_t idx = 0xFFFFFFFFu - (uint32_t)cv[j];
+          bool take = key > T;
+          if (key == T) {
+            uint32_t r = 0;
+            for (uint32_t e = 0; e < ceq; ++e) r += eql[e] < idx ? 1u : 0u;
+            take = r < need;
+          }
+          if (take) atomicOr(&bits[idx >> 5], 1u << (idx & 31));
+        }
+        __syncthreads();
+        // compaction: thread t owns bitmap words [t*WPT, (t+1)*WPT)
+        const int WPT = (W + kTopkThreads - 1) / kTopkThreads;
+        uint32_t cnt = 0;
+        for (int w = tid * WPT; w < min(W, (tid + 1) * WPT); ++w) cnt += __popc(bits[w]);
+        uint32_t tot;
+        uint32_t pos = block_incl_scan<kTopkThreads>(cnt, wsum, tot) - cnt;
+        for (int w = tid * WPT; w < min(W, (tid + 1) * WPT); ++w) {
+          uint32_t m = bits[w];
+          while (m) {
+            const int bpos = __ffs(m) - 1;
+            m &= m - 1;
+            if (pos < (uint32_t)k) o[pos] = w * 32 + bpos;
+            ++pos;
+          }
+        }
+      } else {
+        fallback = true;
+      }
+    }
+  }
+  if (fallback) {
+    __syncthreads();
+    topk_row_exact<VEC>(x, n, k, sorted, sortbuf, hist, wsum, sel, o);
   }
   // leave the row's histogram and list counters at zero for the next call
   uint32_t* hr = ws.hist + (int64_t)row * kBins;
@@ -371,7 +576,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
 
 template <bool VEC>
 static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_stride, int k, int32_t* out,
-                       int64_t out_stride, const TopkWs& ws, hipStream_t st) {
+                       int64_t out_stride, int sorted, const TopkWs& ws, hipStream_t st) {
   static bool lds_set = false;   // the select kernel's dynamic LDS exceeds the 64 KB default
   if (!lds_set) {
     int rc = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_select_kernel<VEC>),
@@ -380,6 +585,13 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
     lds_set = true;
   }
   const int parts = (n + kSlice - 1) / kSlice;
+  const int exact = n <= kShortRow ? 1 : 0;
+  if (exact) {
+    if (rows > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(topk_select_kernel<VEC>, dim3((unsigned)rows), dim3(kTopkThreads), kSortMax * 8, st, scores,
+                       row_stride, n, k, ws, out, out_stride, exact, sorted);
+    return (int)hipGetLastError();
+  }
   for (int64_t r0 = 0; r0 < rows; r0 += kRowBatch) {
     const int nr = (int)(rows - r0 < kRowBatch ? rows - r0 : kRowBatch);
     const float* s = scores + r0 * row_stride;
@@ -390,7 +602,7 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
     hipLaunchKernelGGL(topk_filter_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, k, parts,
                        ws);
     hipLaunchKernelGGL(topk_select_kernel<VEC>, dim3((unsigned)nr), dim3(kTopkThreads), kSortMax * 8, st, s,
-                       row_stride, n, k, ws, o, out_stride);
+                       row_stride, n, k, ws, o, out_stride, exact, sorted);
     const int rc = (int)hipGetLastError();
     if (rc) return rc;
   }
@@ -410,8 +622,8 @@ int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes) {
   return 0;
 }
 
-int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, void* out, int64_t out_stride,
-               void* workspace, size_t workspace_bytes, void* stream) {
+int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, void* out,
+               int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
   if (!scores || !out || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
   if (k > kTopkMaxK) return (int)hipErrorNotSupported;
   if (rows == 0) return 0;
@@ -423,8 +635,8 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float* s = static_cast<const float*>(scores);
   int32_t* o = static_cast<int32_t*>(out);
-  return vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, ws, st)
-             : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, ws, st);
+  return vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, sorted ? 1 : 0, ws, st)
+             : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, sorted ? 1 : 0, ws, st);
 }
 
 }  // extern "C"

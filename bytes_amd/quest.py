@@ -74,12 +74,13 @@ def _npick(kb: int, page: int, np_: int) -> int:
 
 
 def quest_select_pages(q, kmin, kmax, S: int, kb: int, page: int, scaling: float, *, pos: Optional[int] = None,
-                       local_w: int = 0) -> torch.Tensor:
+                       local_w: int = 0, sorted: bool = True) -> torch.Tensor:
     """Page ids [B,H_q,npick] int32 of the top ceil(kb/page) page bounds, ordered
-    by bound descending, lowest page first among equal bounds."""
+    by bound descending with the lowest page first among equal bounds
+    (sorted=False: the same pages by ascending page id)."""
     bound = quest_page_scores(q, kmin, kmax, scaling, page=page, pos=S - 1 if pos is None else pos,
                               local_w=local_w)
-    return topk_indices(bound, _npick(kb, page, bound.shape[-1]))
+    return topk_indices(bound, _npick(kb, page, bound.shape[-1]), sorted=sorted)
 
 
 def _quest_select(q_blk, k_r, pos, S, kb, page, scaling, local_w=0):
@@ -110,6 +111,7 @@ def quest_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, sca
     if meta is None:
         meta = quest_page_minmax(k, page)
     p = S - 1 if pos is None else int(pos)
-    pid = quest_select_pages(q, meta[0], meta[1], S, kb, page, scaling, pos=p, local_w=local_w)
+    pid = quest_select_pages(q, meta[0], meta[1], S, kb, page, scaling, pos=p, local_w=local_w,
+                             sorted=return_pages)
     out = sparse_gather_attn(q, k, v, pid, scaling, page=page, limit=p + 1)
     return (out, pid) if return_pages else out

@@ -68,11 +68,13 @@ def group_scores(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tens
     return _score(q, k, scaling, group_sum=True)
 
 
-def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
-    """Indices of the k largest scores per row of [..., n] fp32, ordered by score
-    descending, lowest index first among equal scores (+0 == -0; NaN ranks
-    above +inf).  Returns int32 [..., k].  Replaces `scores.topk(k).indices`
-    (src/attention_kernels.py:1262) with a deterministic tie rule."""
+def topk_indices(scores: torch.Tensor, k: int, *, sorted: bool = True) -> torch.Tensor:
+    """Indices of the k largest scores per row of [..., n] fp32 under one total
+    order: score descending, lowest index first among equal scores (+0 == -0;
+    NaN ranks above +inf).  sorted=True orders the result by that order, like
+    `scores.topk(k).indices` (src/attention_kernels.py:1262) with a
+    deterministic tie rule; sorted=False returns the same set by ascending
+    index (cheaper: no sort).  Returns int32 [..., k]."""
     C.cuda_tensors(scores)
     C.dtype_in(scores, "scores", torch.float32)
     n = scores.shape[-1]
@@ -87,8 +89,8 @@ def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
     out = torch.empty((rows, k), dtype=torch.int32, device=scores.device)
     nbytes = size_query("bytes_topk_workspace_size", rows, n, int(k))
     ws = workspace(scores.device, nbytes, "topk")
-    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), ptr(out), out.stride(0), ptr(ws), ws.numel(),
-         stream_of(scores))
+    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), int(bool(sorted)), ptr(out), out.stride(0), ptr(ws),
+         ws.numel(), stream_of(scores))
     return out.reshape(*scores.shape[:-1], k)
 
 
@@ -156,14 +158,15 @@ def sparse_decode_scalar(q, k_score_or_packed, scale, zero, k_val, v_val, frac, 
     Returns [B,H_q,1,D] bf16."""
     scores = sparse_score_scalar(q, k_score_or_packed, scaling, score_bits=score_bits)
     kb = budget(frac, scores.shape[-1])
-    idx = topk_indices(scores, kb)
+    idx = topk_indices(scores, kb, sorted=False)      # attention does not depend on the order
     return sparse_gather_attn(q, k_val, v_val, idx, scaling)
 
 
 def token_topk_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float):
     """Group-shared token top-k decode: group-summed fp32 scores per KV head,
     the kb best tokens per (b, KV head), attention of every query head of the
-    group over them.  Returns (out [B,H_q,1,D] bf16, idx [B,H_k,kb] int32)."""
+    group over them.  Returns (out [B,H_q,1,D] bf16, idx [B,H_k,kb] int32 by
+    ascending token index)."""
     s = group_scores(q, k, scaling)
-    idx = topk_indices(s, kb)
+    idx = topk_indices(s, kb, sorted=False)
     return sparse_gather_attn(q, k, v, idx, scaling), idx

@@ -127,11 +127,12 @@ int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, i
  * `select_topk` :226-325) with one total order: score descending, lowest index
  * first among equal scores, +0 == -0, NaN above +inf.
  *   scores [rows, n] fp32 (row stride row_stride, unit stride along n)
- *   out    [rows, k] int32 (row stride out_stride), ordered by that order.
+ *   out    [rows, k] int32 (row stride out_stride): ordered by that order when
+ *          sorted != 0, else the same set by ascending index.
  * 1 <= k <= min(n, 8192); larger k returns hipErrorNotSupported.
  * ------------------------------------------------------------------------- */
 int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes);
-int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, void* out,
+int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, void* out,
                int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -56,12 +56,13 @@ def _tie_heavy(rows, n, seed):
     return s
 
 
+@pytest.mark.parametrize("sorted_out", [True, False])
 @pytest.mark.parametrize("rows,n,k", [(3, 1000, 1), (3, 1000, 17), (4, 4096, 256), (2, 1001, 1001),
-                                      (5, 333, 100), (28, 2048, 128), (2, 20000, 8192)])
-def test_topk_bit_exact_with_ties(dev, rows, n, k):
+                                      (5, 333, 100), (28, 2048, 128), (2, 20000, 8192), (3, 70000, 3000)])
+def test_topk_bit_exact_with_ties(dev, rows, n, k, sorted_out):
     s = _tie_heavy(rows, n, seed=n + k)
-    got = SP.topk_indices(s.to(dev), k).cpu()
-    ref = R.topk_indices(s, k)
+    got = SP.topk_indices(s.to(dev), k, sorted=sorted_out).cpu()
+    ref = R.topk_indices(s, k, sorted_by_score=sorted_out)
     assert got.dtype == torch.int32
     assert torch.equal(got.long(), ref)
 
@@ -86,8 +87,9 @@ def test_topk_crowded_digit_rows(dev, case):
     else:
         s = torch.full((3, 20000), 0.5)
     for k in (1, 100, 8192):
-        got = SP.topk_indices(s.to(dev), k).cpu().long()
-        assert torch.equal(got, R.topk_indices(s, k)), (case, k)
+        for so in (True, False):
+            got = SP.topk_indices(s.to(dev), k, sorted=so).cpu().long()
+            assert torch.equal(got, R.topk_indices(s, k, sorted_by_score=so)), (case, k, so)
 
 
 @pytest.mark.parametrize("k", [256, 1024, 4096])
@@ -96,8 +98,10 @@ def test_topk_c5_rows(dev, k):
     g = torch.Generator().manual_seed(k)
     s = torch.randn(64, 131072, generator=g)
     s[3, 1000:1100] = 5.0                                   # a tied block straddling the boundary
-    got = SP.topk_indices(s.to(dev), k).cpu().long()
-    assert torch.equal(got, R.topk_indices(s, k))
+    s[5, :] = s[5, :].round()                               # heavy ties at the threshold
+    for so in (True, False):
+        got = SP.topk_indices(s.to(dev), k, sorted=so).cpu().long()
+        assert torch.equal(got, R.topk_indices(s, k, sorted_by_score=so)), so
 
 
 def _gather_case(dev, B, Hq, Hk, S, D, kb, per_head, seed, chunk=0):
@@ -161,8 +165,8 @@ def test_token_topk_c5_full(dev, kb):
     s = SP.group_scores(q, k, sc)
     ref_s0 = R.group_scores(q[:1].cpu(), k[:1].cpu(), sc)
     assert (s[:1].cpu() - ref_s0).abs().max() <= SCORE_TOL
-    # selection bit-exact on the same scores
-    ref_idx = R.topk_indices(s.cpu(), kb)
+    # selection bit-exact on the same scores (the pipeline returns the set by ascending index)
+    ref_idx = R.topk_indices(s.cpu(), kb, sorted_by_score=False)
     assert torch.equal(idx.cpu().long(), ref_idx)
     # attention over the selected rows: dense oracle on the gathered rows
     B, Hk = k.shape[:2]
