@@ -49,9 +49,9 @@ SIGNATURES: Dict[str, Tuple] = {
         c_int, c_int, c_int, c_int, c_int, c_int,     # B, Hq, Hk, S, D, group_sum
         c_i64, c_i64, c_i64, c_i64, c_i64,            # q (b, h), k (b, h, s) strides
         c_i64, c_i64,                                 # out strides (b, h)
-        c_f32, c_vp),                                 # scaling, stream
+        c_f32, c_vp, c_vp),                           # scaling, histogram (or None), stream
     "bytes_topk_workspace_size": (c_i64, c_int, c_int, c_szp),
-    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
+    "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
     "bytes_gather_attn_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
     "bytes_gather_attn": (
         c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, k, v, idx, out

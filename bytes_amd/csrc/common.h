@@ -63,6 +63,15 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Monotone 32-bit ranking key of an fp32 score: larger score -> larger key;
+// every NaN -> 0xFFFFFFFF (above +inf), -0 -> the key of +0.
+__device__ __forceinline__ uint32_t score_order_key(float x) {
+  if (x != x) return 0xFFFFFFFFu;
+  uint32_t u = __float_as_uint(x);
+  if (x == 0.f) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Workgroup barrier that orders LDS only: outstanding global loads stay in
 // flight across it (a plain __syncthreads also waits for them).
 __device__ __forceinline__ void lds_barrier() {

@@ -26,6 +26,7 @@ struct ScoreArgs {
   int64_t k_sb, k_sh, k_ss;
   float* out;                // [B, Hq, S] (per head) or [B, Hk, S] (group sum); unit stride along S
   int64_t o_sb, o_sh;
+  uint32_t* hist;            // group sum only, optional: [B*Hk][2048] counts of the top 11 key bits
   int Hk, G, HB, S, tok_per_wg, parts, group_sum;
   float scaling;
 };
@@ -54,7 +55,7 @@ __device__ __forceinline__ void score_issue(const uint16_t* kbase, int64_t k_ss,
 
 template <int D>
 __device__ __forceinline__ void score_tile(const ScoreRegs<D>& r, const bf16x8 (&qa)[D / 32], int t, int lane,
-                                           const ScoreArgs& a, int b, int hk, int hq0, int nh) {
+                                           const ScoreArgs& a, int b, int hk, int hq0, int nh, uint32_t* hlds) {
   const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -75,7 +76,10 @@ __device__ __forceinline__ void score_tile(const ScoreRegs<D>& r, const bf16x8 (
       if (nh > 4) tot += p1;
       if (nh > 8) tot += p2;
       if (nh > 12) tot += p3;
-      if (lg == 0 && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)hk * a.o_sh + tok] = tot;
+      if (lg == 0 && tok < a.S) {
+        a.out[(int64_t)b * a.o_sb + (int64_t)hk * a.o_sh + tok] = tot;
+        if (hlds) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -110,22 +114,36 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   const int t_begin = part * a.tok_per_wg;
   const int t_end = min(t_begin + a.tok_per_wg, a.S);
   constexpr int STEP = kScoreWaves * kScoreIter;
+  __shared__ uint32_t hlds_mem[2048];
+  uint32_t* hlds = nullptr;
+  if (a.hist) {
+    for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64) hlds_mem[i] = 0u;
+    __syncthreads();
+    hlds = hlds_mem;
+  }
   int t = t_begin + w * kScoreIter;
-  if (t >= t_end) return;
-  // two register sets: the next iteration's rows are in flight while one is scored
-  ScoreRegs<D> r0, r1;
-  score_issue<D>(kbase, a.k_ss, a.S, t, lane, r0);
-  while (true) {
-    const bool more1 = t + STEP < t_end;
-    score_issue<D>(kbase, a.k_ss, a.S, more1 ? t + STEP : t, lane, r1);
-    score_tile<D>(r0, qa, t, lane, a, b, hk, hq0, nh);
-    t += STEP;
-    if (!more1) break;
-    const bool more0 = t + STEP < t_end;
-    score_issue<D>(kbase, a.k_ss, a.S, more0 ? t + STEP : t, lane, r0);
-    score_tile<D>(r1, qa, t, lane, a, b, hk, hq0, nh);
-    t += STEP;
-    if (!more0) break;
+  if (t < t_end) {
+    // two register sets: the next iteration's rows are in flight while one is scored
+    ScoreRegs<D> r0, r1;
+    score_issue<D>(kbase, a.k_ss, a.S, t, lane, r0);
+    while (true) {
+      const bool more1 = t + STEP < t_end;
+      score_issue<D>(kbase, a.k_ss, a.S, more1 ? t + STEP : t, lane, r1);
+      score_tile<D>(r0, qa, t, lane, a, b, hk, hq0, nh, hlds);
+      t += STEP;
+      if (!more1) break;
+      const bool more0 = t + STEP < t_end;
+      score_issue<D>(kbase, a.k_ss, a.S, more0 ? t + STEP : t, lane, r0);
+      score_tile<D>(r1, qa, t, lane, a, b, hk, hq0, nh, hlds);
+      t += STEP;
+      if (!more0) break;
+    }
+  }
+  if (a.hist) {
+    __syncthreads();
+    uint32_t* hr = a.hist + ((int64_t)b * a.Hk + hk) * 2048;
+    for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64)
+      if (hlds_mem[i]) atomicAdd(hr + i, hlds_mem[i]);
   }
 }
 
@@ -137,7 +155,7 @@ extern "C" {
 
 int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, int Hk, int S, int D, int group_sum,
                        int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss, int64_t o_sb,
-                       int64_t o_sh, float scaling, void* stream) {
+                       int64_t o_sh, float scaling, void* hist, void* stream) {
   if (!q || !k || !out || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
   ScoreArgs a;
@@ -147,9 +165,11 @@ int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, i
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
   a.out = static_cast<float*>(out);
   a.o_sb = o_sb; a.o_sh = o_sh;
+  a.hist = static_cast<uint32_t*>(hist);
   a.Hk = Hk; a.G = Hq / Hk; a.HB = (a.G + 15) / 16; a.S = S;
   a.group_sum = group_sum ? 1 : 0;
   if (a.group_sum && a.G > 16) return (int)hipErrorNotSupported;
+  if (a.hist && !a.group_sum) return (int)hipErrorInvalidValue;
   a.scaling = scaling;
   const long units = (long)B * Hk * a.HB;
   // about 8 workgroups per CU in total, each a multiple of one iteration of all waves

@@ -37,13 +37,7 @@ constexpr int kShortRow = 16384;       // rows up to this length take the single
 constexpr int kFullSortRow = 4096;     // ... and up to this length simply sort the whole row
 constexpr int kEqMax = 512;            // keys equal to the threshold handled by the bitmap path
 
-// Monotone key: larger score -> larger key.  NaN -> 0xFFFFFFFF, -0 -> +0.
-__device__ __forceinline__ uint32_t order_key(float x) {
-  if (x != x) return 0xFFFFFFFFu;
-  uint32_t u = __float_as_uint(x);
-  if (x == 0.f) u = 0u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
+__device__ __forceinline__ uint32_t order_key(float x) { return score_order_key(x); }
 
 // Sort value: descending order of (key, ~index) = key desc, index asc.
 __device__ __forceinline__ uint64_t sort_val(uint32_t key, int idx) {
@@ -425,7 +419,8 @@ __device__ void topk_row_exact(const float* x, int n, int k, int sorted, uint64_
 template <bool VEC>
 __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* scores, int64_t row_stride, int n,
                                                                    int k, TopkWs ws, int32_t* out,
-                                                                   int64_t out_stride, int exact, int sorted) {
+                                                                   int64_t out_stride, int exact, int sorted,
+                                                                   int hist_ready) {
   extern __shared__ uint64_t sortbuf[];          // [kSortMax]
   __shared__ uint32_t hist[kBins];
   __shared__ uint32_t wsum[kTopkThreads / 64];
@@ -444,6 +439,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
       for (int i = tid; i < k; i += kTopkThreads) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sortbuf[i]);
     } else {
       topk_row_exact<VEC>(x, n, k, sorted, sortbuf, hist, wsum, sel, o);
+    }
+    if (hist_ready) {                            // a histogram the caller built: leave it at zero
+      uint32_t* hr = ws.hist + (int64_t)row * kBins;
+      for (int b = tid; b < kBins; b += kTopkThreads) hr[b] = 0u;
     }
     return;
   }
@@ -576,7 +575,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
 
 template <bool VEC>
 static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_stride, int k, int32_t* out,
-                       int64_t out_stride, int sorted, const TopkWs& ws, hipStream_t st) {
+                       int64_t out_stride, int sorted, int hist_ready, const TopkWs& ws, hipStream_t st) {
   static bool lds_set = false;   // the select kernel's dynamic LDS exceeds the 64 KB default
   if (!lds_set) {
     int rc = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_select_kernel<VEC>),
@@ -589,7 +588,7 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
   if (exact) {
     if (rows > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(topk_select_kernel<VEC>, dim3((unsigned)rows), dim3(kTopkThreads), kSortMax * 8, st, scores,
-                       row_stride, n, k, ws, out, out_stride, exact, sorted);
+                       row_stride, n, k, ws, out, out_stride, exact, sorted, hist_ready);
     return (int)hipGetLastError();
   }
   for (int64_t r0 = 0; r0 < rows; r0 += kRowBatch) {
@@ -597,12 +596,13 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
     const float* s = scores + r0 * row_stride;
     int32_t* o = out + r0 * out_stride;
     const unsigned grid = (unsigned)(nr * parts);
-    hipLaunchKernelGGL(topk_hist_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, parts,
-                       ws.hist);
+    if (!hist_ready)
+      hipLaunchKernelGGL(topk_hist_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, parts,
+                         ws.hist);
     hipLaunchKernelGGL(topk_filter_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, k, parts,
                        ws);
     hipLaunchKernelGGL(topk_select_kernel<VEC>, dim3((unsigned)nr), dim3(kTopkThreads), kSortMax * 8, st, s,
-                       row_stride, n, k, ws, o, out_stride, exact, sorted);
+                       row_stride, n, k, ws, o, out_stride, exact, sorted, hist_ready);
     const int rc = (int)hipGetLastError();
     if (rc) return rc;
   }
@@ -622,21 +622,23 @@ int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes) {
   return 0;
 }
 
-int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, void* out,
-               int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, int hist_ready,
+               void* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
   if (!scores || !out || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
   if (k > kTopkMaxK) return (int)hipErrorNotSupported;
   if (rows == 0) return 0;
   const long parts = (n + kSlice - 1) / kSlice;
   if (kRowBatch * parts > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
   if (!workspace || workspace_bytes < topk_ws_bytes(k)) return (int)hipErrorInvalidValue;
+  if (hist_ready && rows > kRowBatch) return (int)hipErrorInvalidValue;
   const TopkWs ws = topk_ws_carve(workspace, k);
   const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0) && (row_stride % 4 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float* s = static_cast<const float*>(scores);
   int32_t* o = static_cast<int32_t*>(out);
-  return vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, sorted ? 1 : 0, ws, st)
-             : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, sorted ? 1 : 0, ws, st);
+  const int so = sorted ? 1 : 0, hr = hist_ready ? 1 : 0;
+  return vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st)
+             : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st);
 }
 
 }  // extern "C"

@@ -14,6 +14,7 @@ from . import _checks as C
 from ._lib import HIP_ERROR_NOT_SUPPORTED, call, lib, ptr, size_query, stream_of, workspace
 
 TOPK_MAX = 8192
+TOPK_HIST_ROWS = 128          # rows whose digit histogram fits the top-k workspace's fixed region
 
 
 def _qk_shapes(q: torch.Tensor, k: torch.Tensor):
@@ -33,7 +34,7 @@ def _qk_shapes(q: torch.Tensor, k: torch.Tensor):
     return B, Hq, Hk, S, D
 
 
-def _score(q, k_score, scaling, group_sum: bool) -> torch.Tensor:
+def _score(q, k_score, scaling, group_sum: bool, hist=None) -> torch.Tensor:
     B, Hq, Hk, S, D = _qk_shapes(q, k_score)
     if k_score.dtype != torch.bfloat16:
         raise ValueError(f"k_score: dtype {k_score.dtype} not supported (bf16)")
@@ -45,7 +46,7 @@ def _score(q, k_score, scaling, group_sum: bool) -> torch.Tensor:
     out = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
     call("bytes_sparse_score", ptr(qs), ptr(k), ptr(out), B, Hq, Hk, S, D, int(group_sum),
          qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), out.stride(0), out.stride(1),
-         float(scaling), stream_of(q))
+         float(scaling), hist, stream_of(q))
     return out
 
 
@@ -75,6 +76,14 @@ def topk_indices(scores: torch.Tensor, k: int, *, sorted: bool = True) -> torch.
     `scores.topk(k).indices` (src/attention_kernels.py:1262) with a
     deterministic tie rule; sorted=False returns the same set by ascending
     index (cheaper: no sort).  Returns int32 [..., k]."""
+    return _topk(scores, k, sorted=sorted)
+
+
+def _topk_workspace(device, rows: int, n: int, k: int) -> torch.Tensor:
+    return workspace(device, size_query("bytes_topk_workspace_size", rows, n, int(k)), "topk")
+
+
+def _topk(scores: torch.Tensor, k: int, *, sorted: bool, ws=None, hist_ready: bool = False) -> torch.Tensor:
     C.cuda_tensors(scores)
     C.dtype_in(scores, "scores", torch.float32)
     n = scores.shape[-1]
@@ -87,10 +96,10 @@ def topk_indices(scores: torch.Tensor, k: int, *, sorted: bool = True) -> torch.
         s = s.contiguous()
     rows = s.shape[0]
     out = torch.empty((rows, k), dtype=torch.int32, device=scores.device)
-    nbytes = size_query("bytes_topk_workspace_size", rows, n, int(k))
-    ws = workspace(scores.device, nbytes, "topk")
-    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), int(bool(sorted)), ptr(out), out.stride(0), ptr(ws),
-         ws.numel(), stream_of(scores))
+    if ws is None:
+        ws = _topk_workspace(scores.device, rows, n, k)
+    call("bytes_topk", ptr(s), rows, n, s.stride(0), int(k), int(bool(sorted)), int(bool(hist_ready)), ptr(out),
+         out.stride(0), ptr(ws), ws.numel(), stream_of(scores))
     return out.reshape(*scores.shape[:-1], k)
 
 
@@ -167,6 +176,13 @@ def token_topk_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int
     the kb best tokens per (b, KV head), attention of every query head of the
     group over them.  Returns (out [B,H_q,1,D] bf16, idx [B,H_k,kb] int32 by
     ascending token index)."""
-    s = group_scores(q, k, scaling)
-    idx = topk_indices(s, kb, sorted=False)
+    B, Hq, Hk, S, D = _qk_shapes(q, k)
+    if B * Hk <= TOPK_HIST_ROWS:
+        # the score kernel also counts the top-k digit histogram, in the top-k workspace
+        ws = _topk_workspace(q.device, B * Hk, S, kb)
+        s = _score(q, k, scaling, group_sum=True, hist=ptr(ws))
+        idx = _topk(s, kb, sorted=False, ws=ws, hist_ready=True)
+    else:
+        s = group_scores(q, k, scaling)
+        idx = topk_indices(s, kb, sorted=False)
     return sparse_gather_attn(q, k, v, idx, scaling), idx

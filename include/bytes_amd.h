@@ -115,10 +115,14 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
  *                  (the per-KV-head selection score of the token top-k path; G <= 16)
  *   q [B, Hq, D] bf16 (strides q_sb, q_sh); k [B, Hk, S, D] bf16 (strides k_*);
  *   out strides o_sb, o_sh (unit stride along S).  D in {64, 128}.
+ * hist (group_sum = 1 only, may be NULL): [B*Hk][2048] uint32, zero on entry,
+ *   receives the count of each score's top 11 order-key bits; pass the first
+ *   bytes of a bytes_topk workspace (its histogram region, B*Hk <= 128) and
+ *   call bytes_topk with hist_ready = 1 to skip its histogram pass.
  * ------------------------------------------------------------------------- */
 int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, int Hk, int S, int D,
                        int group_sum, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
-                       int64_t o_sb, int64_t o_sh, float scaling, void* stream);
+                       int64_t o_sb, int64_t o_sh, float scaling, void* hist, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Deterministic top-k per row.
@@ -130,10 +134,12 @@ int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, i
  *   out    [rows, k] int32 (row stride out_stride): ordered by that order when
  *          sorted != 0, else the same set by ascending index.
  * 1 <= k <= min(n, 8192); larger k returns hipErrorNotSupported.
+ * hist_ready = 1: the workspace's histogram region already holds the rows'
+ *   digit histograms (bytes_sparse_score with hist); rows <= 128.
  * ------------------------------------------------------------------------- */
 int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes);
-int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, void* out,
-               int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, int hist_ready,
+               void* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Gather attention over selected rows.
