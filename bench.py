@@ -87,6 +87,32 @@ class DenseCase(Case):
                 lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), units)
 
 
+class DenseFp8Case(DenseCase):
+    kernel = "dense_decode_kernel"
+    dtype = "fp8 e4m3fn K/V, bf16 q"
+
+    def __init__(self, name, B, Hq, Hk, D, L):
+        super().__init__(name, B, Hq, Hk, D, L)
+        self.workload = f"fp8 (e4m3fn) GQA decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L}"
+
+    def bytes_per_step(self):
+        B, Hq, Hk, D, L = self.shape
+        return 2 * B * Hk * L * D + 2 * B * Hq * D * 2
+
+    def make(self, dev):
+        x = super().make(dev)
+        x["k"], x["v"] = x["k"].to(torch.float8_e4m3fn), x["v"].to(torch.float8_e4m3fn)
+        return x
+
+    def step(self, inp):
+        from bytes_amd.attention_kernels import decode_attn_fp8
+        return decode_attn_fp8(inp["q"], inp["k"], inp["v"], inp["scale"])
+
+    def cpu_sample(self):
+        desc, fn, ratio = super().cpu_sample()
+        return desc + " (fp8 K/V as the oracle's fp32 values)", fn, ratio
+
+
 class KiviCase(Case):
     kernel = "kivi_decode_kernel"
 
@@ -140,13 +166,16 @@ class TopkCase(Case):
     query head of the group.  One step = score + top-k + gather."""
     kernel = "score_kernel"
 
-    def __init__(self, name, kb, B=8, Hq=24, Hk=8, D=128, L=131072):
-        self.name, self.kb, self.shape = name, kb, (B, Hq, Hk, D, L)
-        self.workload = f"token top-k decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} k={kb} (group-summed scores)"
+    def __init__(self, name, kb, B=8, Hq=24, Hk=8, D=128, L=131072, score_fp8=False):
+        self.name, self.kb, self.shape, self.score_fp8 = name, kb, (B, Hq, Hk, D, L), score_fp8
+        self.workload = (f"token top-k decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} k={kb} (group-summed scores"
+                         f"{' on fp8 e4m3fn score keys' if score_fp8 else ''})")
+        if score_fp8:
+            self.dtype = "bf16 (fp8 score keys)"
 
     def bytes_per_step(self):
         B, Hq, Hk, D, L = self.shape
-        keys = B * Hk * L * D * 2                 # score pass reads every key once
+        keys = B * Hk * L * D * (1 if self.score_fp8 else 2)   # score pass reads every key once
         scores = B * Hk * L * 4 * 2               # fp32 scores written, read by the top-k
         gather = 2 * B * Hk * self.kb * D * 2     # selected K and V rows
         return keys + scores + gather + 2 * B * Hq * D * 2
@@ -159,11 +188,14 @@ class TopkCase(Case):
         from bytes_amd import workloads as W
         B, Hq, Hk, D, L = self.shape
         x = W.c5_topk(seed=0, device=dev, B=B, Hq=Hq, Hk=Hk, D=D, L=L)
-        return {"q": x["q"], "k": x["k"], "v": x["v"], "scale": x["scale"]}
+        d = {"q": x["q"], "k": x["k"], "v": x["v"], "scale": x["scale"]}
+        if self.score_fp8:
+            d["k8"] = x["k"].to(torch.float8_e4m3fn)
+        return d
 
     def step(self, inp):
         from bytes_amd.sparse import token_topk_decode
-        return token_topk_decode(inp["q"], inp["k"], inp["v"], self.kb, inp["scale"])
+        return token_topk_decode(inp["q"], inp["k"], inp["v"], self.kb, inp["scale"], k_score=inp.get("k8"))
 
     def cpu_sample(self):
         from bytes_amd import workloads as W
@@ -311,6 +343,8 @@ def cases():
         "c5_topk1024": TopkCase("c5_topk1024", 1024),
         "c5_topk4096": TopkCase("c5_topk4096", 4096),
         "c5_dense": DenseCase("c5_dense", *W.SHAPES["c5_topk"]),
+        "c5_topk1024_fp8s": TopkCase("c5_topk1024_fp8s", 1024, score_fp8=True),
+        "dense_16k_fp8": DenseFp8Case("dense_16k_fp8", *W.SHAPES["dense_16k"]),
     }
 
 

@@ -33,6 +33,10 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64,                          # v strides (b, h, s)
         c_i64, c_i64,                                 # out strides (b, h)
         c_f32, c_int, c_vp, c_sz, c_vp),              # scale, chunk, workspace, bytes, stream
+    "bytes_decode_attn_fp8": (
+        c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int,
+        c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+        c_f32, c_int, c_vp, c_sz, c_vp),
     "bytes_kivi_quantize_pack": (c_vp, c_int, c_i64, c_int, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp),
     "bytes_kivi_dequant": (c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_int, c_vp, c_int, c_vp),
     "bytes_kivi_decode_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
@@ -45,7 +49,7 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64,                                 # out strides
         c_f32, c_int, c_vp, c_sz, c_vp),
     "bytes_sparse_score": (
-        c_vp, c_vp, c_vp,                             # q, k, out
+        c_vp, c_vp, c_int, c_vp,                      # q, k, k is fp8, out
         c_int, c_int, c_int, c_int, c_int, c_int,     # B, Hq, Hk, S, D, group_sum
         c_i64, c_i64, c_i64, c_i64, c_i64,            # q (b, h), k (b, h, s) strides
         c_i64, c_i64,                                 # out strides (b, h)
@@ -54,7 +58,7 @@ SIGNATURES: Dict[str, Tuple] = {
     "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
     "bytes_gather_attn_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
     "bytes_gather_attn": (
-        c_vp, c_vp, c_vp, c_vp, c_vp,                 # q, k, v, idx, out
+        c_vp, c_vp, c_vp, c_int, c_vp, c_vp,          # q, k, v, k/v are fp8, idx, out
         c_int, c_int, c_int, c_int, c_int, c_int, c_int,   # B, Hq, Hk, S, D, kb, per_head
         c_int, c_int,                                 # page, limit
         c_i64, c_i64,                                 # q strides

@@ -51,6 +51,41 @@ def decode_attn_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     return out.unsqueeze(2)
 
 
+def decode_attn_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 1.0,
+                    *, chunk: int = 0) -> torch.Tensor:
+    """softmax(scale * q.K^T) V with OCP float8_e4m3fn K and V.
+
+    Replaces src/attention_kernels.py:156-182: q [B,H_q,1,D] bf16; k, v
+    [B,H_k,S,D] float8_e4m3fn, widened to bf16 exactly inside the kernel; fp32
+    softmax and accumulation; no scale in the reference (`scale` defaults to
+    1.0).  Returns [B,H_q,1,D] in q's dtype (:171)."""
+    C.cuda_tensors(q, k, v)
+    C.ndim(q, 4, "q"), C.ndim(k, 4, "k"), C.ndim(v, 4, "v")
+    C.dtype_in(q, "q", torch.bfloat16)
+    C.dtype_in(k, "k", torch.float8_e4m3fn)
+    C.dtype_in(v, "v", torch.float8_e4m3fn)
+    B, Hq, one, D = q.shape
+    _, Hk, S, Dk = k.shape
+    if one != 1 or Dk != D or tuple(v.shape) != tuple(k.shape) or k.shape[0] != B:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if Hq % Hk != 0:
+        raise ValueError(f"H_q={Hq} is not a multiple of H_k={Hk}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if S == 0:
+        raise ValueError("empty KV cache (S == 0)")
+    qs = C.rows16(q.squeeze(2))
+    k, v = C.rows16(k), C.rows16(v)
+    out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    nbytes = size_query("bytes_decode_attn_bf16_workspace_size", B, Hq, Hk, S, D, int(chunk))
+    ws = workspace(q.device, nbytes)
+    call("bytes_decode_attn_fp8", ptr(qs), ptr(k), ptr(v), ptr(out), B, Hq, Hk, S, D,
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2),
+         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1),
+         float(scale), int(chunk), ptr(ws), ws.numel(), stream_of(q))
+    return out.unsqueeze(2)
+
+
 # Sparse decode operators of the same module (src/attention_kernels.py:1037-1263).
 from .sparse import (sparse_decode_scalar, sparse_gather_attn, sparse_score_scalar,  # noqa: E402,F401
                      topk_indices)

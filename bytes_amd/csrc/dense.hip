@@ -15,14 +15,18 @@
 //                                    are bank-conflict free)
 // The next tile's K and V loads are issued before the current tile is
 // computed (two-stage software pipeline).
+//
+// The fp8 entry point (src/attention_kernels.py:156-182, `decode_attn_fp8`:
+// OCP e4m3fn K and V, bf16 q, output in q's dtype, no scale) runs the same
+// kernel with K/V rows widened to bf16 (exactly) as they are staged in LDS.
 #include "dense_tile.h"
 
 namespace bytes_amd {
 
 struct DenseArgs {
   const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
+  const void* k;             // bf16 or fp8 e4m3fn rows
+  const void* v;
   int64_t q_sb, q_sh;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -31,7 +35,7 @@ struct DenseArgs {
   SplitKOut o;
 };
 
-template <int D>
+template <int D, bool FP8>
 __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(DenseArgs a) {
   using C = DenseCfg<D>;
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
@@ -51,8 +55,6 @@ __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(Dense
 
   const int t_begin = split * a.chunk;
   const int t_end = min(t_begin + a.chunk, a.S);
-  const uint16_t* kbase = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
-  const uint16_t* vbase = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
   char* wbuf = smem_raw + w * C::WAVE;
 
   float m_run = kNegInf, l_run = 0.f;
@@ -60,8 +62,17 @@ __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(Dense
 #pragma unroll
   for (int db = 0; db < C::DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  dense_wave_loop<D>(kbase, vbase, a.k_ss, a.v_ss, a.S, t_begin, t_end, w, lane, a.scale_log2, qb, wbuf, m_run,
-                     l_run, acc);
+  if constexpr (FP8) {
+    const uint8_t* kbase = static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const uint8_t* vbase = static_cast<const uint8_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    dense_wave_loop_fp8<D>(kbase, vbase, a.k_ss, a.v_ss, a.S, t_begin, t_end, w, lane, a.scale_log2, qb, wbuf,
+                           m_run, l_run, acc);
+  } else {
+    const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const uint16_t* vbase = static_cast<const uint16_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    dense_wave_loop<D>(kbase, vbase, a.k_ss, a.v_ss, a.S, t_begin, t_end, w, lane, a.scale_log2, qb, wbuf, m_run,
+                       l_run, acc);
+  }
 
   splitk_epilogue<D, kDenseWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b,
                                   hq0, nh);
@@ -105,10 +116,10 @@ int bytes_decode_attn_bf16_workspace_size(int B, int Hq, int Hk, int S, int D, i
   return 0;
 }
 
-int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* out, int B, int Hq, int Hk, int S,
-                           int D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
-                           int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scale,
-                           int chunk_req, void* workspace, size_t workspace_bytes, void* stream) {
+static int dense_decode(bool fp8, const void* q, const void* k, const void* v, void* out, int B, int Hq, int Hk,
+                        int S, int D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                        int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scale,
+                        int chunk_req, void* workspace, size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
   const int G = Hq / Hk, HB = (G + 15) / 16;
@@ -116,8 +127,8 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
   if (units > 65535) return (int)hipErrorInvalidConfiguration;
   DenseArgs a;
   a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
+  a.k = k;
+  a.v = v;
   a.q_sb = q_sb; a.q_sh = q_sh;
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
@@ -133,13 +144,33 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
   splitk_carve(workspace, units, ns, a.o, /*allow_fused=*/false);
   dim3 grid((unsigned)(ns * units));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
-    hipLaunchKernelGGL(dense_decode_kernel<64>, grid, dim3(kDenseWaves * 64), 0, st, a);
-  else
-    hipLaunchKernelGGL(dense_decode_kernel<128>, grid, dim3(kDenseWaves * 64), 0, st, a);
+  if (D == 64) {
+    if (fp8) hipLaunchKernelGGL((dense_decode_kernel<64, true>), grid, dim3(kDenseWaves * 64), 0, st, a);
+    else hipLaunchKernelGGL((dense_decode_kernel<64, false>), grid, dim3(kDenseWaves * 64), 0, st, a);
+  } else {
+    if (fp8) hipLaunchKernelGGL((dense_decode_kernel<128, true>), grid, dim3(kDenseWaves * 64), 0, st, a);
+    else hipLaunchKernelGGL((dense_decode_kernel<128, false>), grid, dim3(kDenseWaves * 64), 0, st, a);
+  }
   int rc = (int)hipGetLastError();
   if (rc) return rc;
   return splitk_combine(a.o, units, D, st);
+}
+
+int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* out, int B, int Hq, int Hk, int S,
+                           int D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                           int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scale,
+                           int chunk_req, void* workspace, size_t workspace_bytes, void* stream) {
+  return dense_decode(false, q, k, v, out, B, Hq, Hk, S, D, q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb,
+                      o_sh, scale, chunk_req, workspace, workspace_bytes, stream);
+}
+
+// K/V element strides are in fp8 elements (bytes).
+int bytes_decode_attn_fp8(const void* q, const void* k, const void* v, void* out, int B, int Hq, int Hk, int S,
+                          int D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                          int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scale,
+                          int chunk_req, void* workspace, size_t workspace_bytes, void* stream) {
+  return dense_decode(true, q, k, v, out, B, Hq, Hk, S, D, q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb,
+                      o_sh, scale, chunk_req, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -207,6 +207,86 @@ __device__ __forceinline__ void dense_wave_loop(const uint16_t* kbase, const uin
   }
 }
 
+// ---- fp8 (OCP e4m3fn) K/V rows, widened to bf16 while they are staged ----
+// 16 fp8 values -> 16 bf16 (two 16-byte LDS chunks).  v_cvt_pk_f32_fp8 decodes
+// e4m3fn exactly (NaN included); every e4m3 value is a bf16 value, so the
+// bf16 bits are the top half of the f32 bits.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+  const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8(w, HI);
+  return (__float_as_uint(f[0]) >> 16) | (__float_as_uint(f[1]) & 0xFFFF0000u);
+}
+__device__ __forceinline__ void fp8x16_to_bf16(const u32x4& in, u32x4& lo, u32x4& hi) {
+  lo = u32x4{fp8x2_to_bf16x2<false>(in[0]), fp8x2_to_bf16x2<true>(in[0]), fp8x2_to_bf16x2<false>(in[1]),
+             fp8x2_to_bf16x2<true>(in[1])};
+  hi = u32x4{fp8x2_to_bf16x2<false>(in[2]), fp8x2_to_bf16x2<true>(in[2]), fp8x2_to_bf16x2<false>(in[3]),
+             fp8x2_to_bf16x2<true>(in[3])};
+}
+
+template <int D>
+struct DenseRegs8 {
+  static constexpr int CPR8 = D / 16;                 // 16-byte fp8 chunks per row
+  static constexpr int CPL8 = kTile * CPR8 / 64;      // per lane per tile (each of K, V)
+  u32x4 k[CPL8];
+  u32x4 v[CPL8];
+};
+
+template <int D>
+__device__ __forceinline__ void dense_issue_fp8(const uint8_t* kbase, const uint8_t* vbase, int64_t k_ss, int64_t v_ss,
+                                                int S, int t0, int t_end, int lane, DenseRegs8<D>& r) {
+  using R = DenseRegs8<D>;
+  const bool live = t0 < t_end;
+#pragma unroll
+  for (int i = 0; i < R::CPL8; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / R::CPR8, pos = p - rr * R::CPR8;
+    const int row = live ? min(t0 + rr, S - 1) : S - 1;
+    const int col = live ? pos * 16 : 0;
+    r.k[i] = ld16(kbase + (int64_t)row * k_ss + col);
+    r.v[i] = ld16(vbase + (int64_t)row * v_ss + col);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void dense_stage_fp8(int lane, const DenseRegs8<D>& r, char* kst, char* vst) {
+  using R = DenseRegs8<D>;
+#pragma unroll
+  for (int i = 0; i < R::CPL8; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / R::CPR8, pos = p - rr * R::CPR8;
+    u32x4 k0, k1, v0, v1;
+    fp8x16_to_bf16(r.k[i], k0, k1);
+    fp8x16_to_bf16(r.v[i], v0, v1);
+    *reinterpret_cast<u32x4*>(kst + rr * (D * 2) + kswz<D>(rr, 2 * pos) * 16) = k0;
+    *reinterpret_cast<u32x4*>(kst + rr * (D * 2) + kswz<D>(rr, 2 * pos + 1) * 16) = k1;
+    *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, 2 * pos) * 16) = v0;
+    *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, 2 * pos + 1) * 16) = v1;
+  }
+}
+
+// The dense tile loop over fp8 rows (same pipeline as dense_wave_loop).
+template <int D>
+__device__ __forceinline__ void dense_wave_loop_fp8(const uint8_t* kbase, const uint8_t* vbase, int64_t k_ss,
+                                                    int64_t v_ss, int S, int t_begin, int t_end, int w, int lane,
+                                                    float scale_log2, const bf16x8 (&qb)[D / 32], char* wbuf,
+                                                    float& m_run, float& l_run, f32x4 (&acc)[D / 16]) {
+  constexpr int STEP = kDenseWaves * kTile;
+  char* kst = wbuf;
+  char* vst = wbuf + DenseCfg<D>::VT;
+  DenseRegs8<D> r;
+  int t = t_begin + w * kTile;
+  if (t >= t_end) return;
+  dense_issue_fp8<D>(kbase, vbase, k_ss, v_ss, S, t, t_end, lane, r);
+  for (; t < t_end; t += STEP) {
+    wave_lds_sync();
+    dense_stage_fp8<D>(lane, r, kst, vst);
+    dense_issue_fp8<D>(kbase, vbase, k_ss, v_ss, S, t + STEP, t_end, lane, r);
+    wave_lds_sync();
+    dense_compute<D>(range_mask(t, t_end), scale_log2, lane, qb, kst, vst, m_run, l_run, acc);
+  }
+}
+
 // Q rows as the MFMA B operand of the dense tile: lane holds Q[h = l16][d = kk*32 + lg*8 + j].
 template <int D>
 __device__ __forceinline__ void load_q_bf16(const uint16_t* qrow0, int64_t q_sh, int nh, int lane,

@@ -13,6 +13,8 @@
 // rows p*page + o clamped to S-1 (benchmarks/sparse_attention.py:358-363, the
 // Quest expansion), expanded while the list is staged.  Rows at or past
 // `limit` (the causal bound, S at decode) are masked.
+// K and V may be fp8 (OCP e4m3fn; the output is then bf16, :1044): rows are
+// widened to bf16 exactly while staged in LDS.
 // The index list of a unit is cut into split-K chunks; each workgroup stages
 // its chunk's row numbers in LDS, then its waves run the dense bf16 tile loop
 // with rows fetched through that list (prefetching the next tile's rows while
@@ -24,9 +26,9 @@ namespace bytes_amd {
 struct GatherArgs {
   const uint16_t* q;
   int64_t q_sb, q_sh;
-  const uint16_t* k;
+  const void* k;             // bf16 or fp8 e4m3fn rows
   int64_t k_sb, k_sh, k_ss;
-  const uint16_t* v;
+  const void* v;
   int64_t v_sb, v_sh, v_ss;
   const int32_t* idx;        // [B, Hq or Hk, kb], unit stride along kb
   int64_t i_sb, i_sh;
@@ -66,6 +68,23 @@ __device__ __forceinline__ void gather_issue(const uint16_t* kbase, const uint16
 }
 
 template <int D>
+__device__ __forceinline__ void gather_issue_fp8(const uint8_t* kbase, const uint8_t* vbase, int64_t k_ss,
+                                                 int64_t v_ss, const int32_t* rows, int j0, int n, int lane,
+                                                 DenseRegs8<D>& r) {
+  using R = DenseRegs8<D>;
+#pragma unroll
+  for (int i = 0; i < R::CPL8; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / R::CPR8, pos = p - rr * R::CPR8;
+    const int j = j0 + rr;
+    int row = j < n ? rows[j] : 0;
+    row = row < 0 ? 0 : row;
+    r.k[i] = ld16(kbase + (int64_t)row * k_ss + pos * 16);
+    r.v[i] = ld16(vbase + (int64_t)row * v_ss + pos * 16);
+  }
+}
+
+template <int D, bool FP8>
 __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(GatherArgs a) {
   using C = DenseCfg<D>;
   __shared__ __attribute__((aligned(16))) char smem_raw[GatherCfg<D>::kSmem];
@@ -121,23 +140,30 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
 #pragma unroll
   for (int db = 0; db < C::DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const uint16_t* kbase = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
-  const uint16_t* vbase = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
   char* kst = smem_raw + w * C::WAVE;
   char* vst = kst + C::VT;
   constexpr int STEP = kGatherWaves * kTile;
   int j = w * kTile;
   if (j < n) {
-    DenseRegs<D> r;
-    gather_issue<D>(kbase, vbase, a.k_ss, a.v_ss, rows, j, n, lane, r);
+    using Regs = typename std::conditional<FP8, DenseRegs8<D>, DenseRegs<D>>::type;
+    using Elem = typename std::conditional<FP8, uint8_t, uint16_t>::type;
+    const Elem* kbase = static_cast<const Elem*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const Elem* vbase = static_cast<const Elem*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    Regs r;
+    auto issue = [&](int j0) {
+      if constexpr (FP8) gather_issue_fp8<D>(kbase, vbase, a.k_ss, a.v_ss, rows, j0, n, lane, r);
+      else gather_issue<D>(kbase, vbase, a.k_ss, a.v_ss, rows, j0, n, lane, r);
+    };
+    issue(j);
     for (; j < n; j += STEP) {
       // rows of this tile that take part: inside the chunk and a valid index
       const int jj = j + (lane & 31);
       const bool ok = jj < n && rows[jj < n ? jj : 0] >= 0;
       const uint32_t vmask = (uint32_t)__ballot(ok);
       wave_lds_sync();
-      dense_stage<D>(lane, r, kst, vst);
-      gather_issue<D>(kbase, vbase, a.k_ss, a.v_ss, rows, j + STEP, n, lane, r);
+      if constexpr (FP8) dense_stage_fp8<D>(lane, r, kst, vst);
+      else dense_stage<D>(lane, r, kst, vst);
+      issue(j + STEP);
       wave_lds_sync();
       dense_compute<D>(vmask, a.scale_log2, lane, qb, kst, vst, m_run, l_run, acc);
     }
@@ -185,8 +211,8 @@ int bytes_gather_attn_workspace_size(int B, int Hq, int Hk, int kb, int D, int p
   return 0;
 }
 
-int bytes_gather_attn(const void* q, const void* k, const void* v, const void* idx, void* out, int B, int Hq, int Hk,
-                      int S, int D, int kb, int per_head, int page, int limit, int64_t q_sb, int64_t q_sh,
+int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, const void* idx, void* out, int B,
+                      int Hq, int Hk, int S, int D, int kb, int per_head, int page, int limit, int64_t q_sb, int64_t q_sh,
                       int64_t k_sb, int64_t k_sh, int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb, int64_t i_sh,
                       int64_t o_sb, int64_t o_sh, float scaling, int chunk_req, void* workspace,
                       size_t workspace_bytes, void* stream) {
@@ -201,9 +227,9 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, const void* i
   a.limit = limit;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
-  a.k = static_cast<const uint16_t*>(k);
+  a.k = k;
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
-  a.v = static_cast<const uint16_t*>(v);
+  a.v = v;
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
   a.idx = static_cast<const int32_t*>(idx);
   a.i_sb = i_sb; a.i_sh = i_sh;
@@ -226,10 +252,13 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, const void* i
   splitk_carve(workspace, units, ns, a.o);
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((unsigned)(ns * units)), block(kGatherWaves * 64);
-  if (D == 128)
-    hipLaunchKernelGGL(gather_decode_kernel<128>, grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL(gather_decode_kernel<64>, grid, block, 0, st, a);
+  if (D == 128) {
+    if (kv_fp8) hipLaunchKernelGGL((gather_decode_kernel<128, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gather_decode_kernel<128, false>), grid, block, 0, st, a);
+  } else {
+    if (kv_fp8) hipLaunchKernelGGL((gather_decode_kernel<64, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gather_decode_kernel<64, false>), grid, block, 0, st, a);
+  }
   int rc = (int)hipGetLastError();
   if (rc) return rc;
   return splitk_combine(a.o, units, D, st);

@@ -15,14 +15,17 @@
 // straight from HBM into the MFMA operand registers (no LDS round trip).  The
 // output tile lands with head (l/16)*4 + i and token l%16 in lane l, so the
 // group sum of up to four heads is a sum inside one lane.
-#include "common.h"
+//
+// fp8 (OCP e4m3fn) keys (`score_bits=8`, :1113) load 8 bytes per operand and
+// are widened to bf16 exactly in registers.
+#include "dense_tile.h"
 
 namespace bytes_amd {
 
 struct ScoreArgs {
   const uint16_t* q;
   int64_t q_sb, q_sh;
-  const uint16_t* k;
+  const void* k;             // bf16 or fp8 e4m3fn keys
   int64_t k_sb, k_sh, k_ss;
   float* out;                // [B, Hq, S] (per head) or [B, Hk, S] (group sum); unit stride along S
   int64_t o_sb, o_sh;
@@ -34,34 +37,50 @@ struct ScoreArgs {
 constexpr int kScoreWaves = 4;
 constexpr int kScoreIter = 64;   // tokens per wave iteration (4 MFMA column tiles)
 
-template <int D>
+template <int D, bool FP8>
 struct ScoreRegs {
-  u32x4 k[4][D / 32];        // [column tile][k-step]
+  typedef typename std::conditional<FP8, u32x2, u32x4>::type T;
+  T k[4][D / 32];            // [column tile][k-step]
 };
 
 // K rows t .. t+63 of one iteration as B operands (rows clamped to S-1).
-template <int D>
-__device__ __forceinline__ void score_issue(const uint16_t* kbase, int64_t k_ss, int S, int t, int lane,
-                                            ScoreRegs<D>& r) {
+template <int D, bool FP8>
+__device__ __forceinline__ void score_issue(const void* kbase, int64_t k_ss, int S, int t, int lane,
+                                            ScoreRegs<D, FP8>& r) {
   const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int row = min(t + c * 16 + l16, S - 1);
-    const uint16_t* p = kbase + (int64_t)row * k_ss + lg * 8;
+    if constexpr (FP8) {
+      const uint8_t* p = static_cast<const uint8_t*>(kbase) + (int64_t)row * k_ss + lg * 8;
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = ld16(p + kk * 32);
+      for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = *reinterpret_cast<const u32x2*>(p + kk * 32);
+    } else {
+      const uint16_t* p = static_cast<const uint16_t*>(kbase) + (int64_t)row * k_ss + lg * 8;
+#pragma unroll
+      for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = ld16(p + kk * 32);
+    }
   }
 }
 
-template <int D>
-__device__ __forceinline__ void score_tile(const ScoreRegs<D>& r, const bf16x8 (&qa)[D / 32], int t, int lane,
+template <bool FP8>
+__device__ __forceinline__ bf16x8 score_operand(const u32x4& w) { return __builtin_bit_cast(bf16x8, w); }
+template <bool FP8>
+__device__ __forceinline__ bf16x8 score_operand(const u32x2& w) {
+  const u32x4 b = {fp8x2_to_bf16x2<false>(w[0]), fp8x2_to_bf16x2<true>(w[0]), fp8x2_to_bf16x2<false>(w[1]),
+                   fp8x2_to_bf16x2<true>(w[1])};
+  return __builtin_bit_cast(bf16x8, b);
+}
+
+template <int D, bool FP8>
+__device__ __forceinline__ void score_tile(const ScoreRegs<D, FP8>& r, const bf16x8 (&qa)[D / 32], int t, int lane,
                                            const ScoreArgs& a, int b, int hk, int hq0, int nh, uint32_t* hlds) {
   const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) s = mfma_bf16(qa[kk], __builtin_bit_cast(bf16x8, r.k[c][kk]), s);
+    for (int kk = 0; kk < D / 32; ++kk) s = mfma_bf16(qa[kk], score_operand<FP8>(r.k[c][kk]), s);
     const int tok = t + c * 16 + l16;
     if (a.group_sum) {
       // heads lg*4 + i; group sum in head order, lane groups added in order
@@ -90,7 +109,7 @@ __device__ __forceinline__ void score_tile(const ScoreRegs<D>& r, const bf16x8 (
   }
 }
 
-template <int D>
+template <int D, bool FP8>
 __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
@@ -110,7 +129,8 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     for (int kk = 0; kk < D / 32; ++kk) qa[kk] = __builtin_bit_cast(bf16x8, live ? ld16(qp + kk * 32) : u32x4{0, 0, 0, 0});
   }
 
-  const uint16_t* kbase = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+  const void* kbase = FP8 ? (const void*)(static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh)
+                          : (const void*)(static_cast<const uint16_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh);
   const int t_begin = part * a.tok_per_wg;
   const int t_end = min(t_begin + a.tok_per_wg, a.S);
   constexpr int STEP = kScoreWaves * kScoreIter;
@@ -124,17 +144,17 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   int t = t_begin + w * kScoreIter;
   if (t < t_end) {
     // two register sets: the next iteration's rows are in flight while one is scored
-    ScoreRegs<D> r0, r1;
-    score_issue<D>(kbase, a.k_ss, a.S, t, lane, r0);
+    ScoreRegs<D, FP8> r0, r1;
+    score_issue<D, FP8>(kbase, a.k_ss, a.S, t, lane, r0);
     while (true) {
       const bool more1 = t + STEP < t_end;
-      score_issue<D>(kbase, a.k_ss, a.S, more1 ? t + STEP : t, lane, r1);
-      score_tile<D>(r0, qa, t, lane, a, b, hk, hq0, nh, hlds);
+      score_issue<D, FP8>(kbase, a.k_ss, a.S, more1 ? t + STEP : t, lane, r1);
+      score_tile<D, FP8>(r0, qa, t, lane, a, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more1) break;
       const bool more0 = t + STEP < t_end;
-      score_issue<D>(kbase, a.k_ss, a.S, more0 ? t + STEP : t, lane, r0);
-      score_tile<D>(r1, qa, t, lane, a, b, hk, hq0, nh, hlds);
+      score_issue<D, FP8>(kbase, a.k_ss, a.S, more0 ? t + STEP : t, lane, r0);
+      score_tile<D, FP8>(r1, qa, t, lane, a, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more0) break;
     }
@@ -153,15 +173,15 @@ using namespace bytes_amd;
 
 extern "C" {
 
-int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, int Hk, int S, int D, int group_sum,
-                       int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss, int64_t o_sb,
-                       int64_t o_sh, float scaling, void* hist, void* stream) {
+int bytes_sparse_score(const void* q, const void* k, int k_fp8, void* out, int B, int Hq, int Hk, int S, int D,
+                       int group_sum, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                       int64_t o_sb, int64_t o_sh, float scaling, void* hist, void* stream) {
   if (!q || !k || !out || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
   ScoreArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
-  a.k = static_cast<const uint16_t*>(k);
+  a.k = k;
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
   a.out = static_cast<float*>(out);
   a.o_sb = o_sb; a.o_sh = o_sh;
@@ -184,10 +204,14 @@ int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, i
   const long grid = units * a.parts;
   if (grid > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 128)
-    hipLaunchKernelGGL(score_kernel<128>, dim3((unsigned)grid), dim3(kScoreWaves * 64), 0, st, a);
-  else
-    hipLaunchKernelGGL(score_kernel<64>, dim3((unsigned)grid), dim3(kScoreWaves * 64), 0, st, a);
+  const dim3 g((unsigned)grid), blk(kScoreWaves * 64);
+  if (D == 128) {
+    if (k_fp8) hipLaunchKernelGGL((score_kernel<128, true>), g, blk, 0, st, a);
+    else hipLaunchKernelGGL((score_kernel<128, false>), g, blk, 0, st, a);
+  } else {
+    if (k_fp8) hipLaunchKernelGGL((score_kernel<64, true>), g, blk, 0, st, a);
+    else hipLaunchKernelGGL((score_kernel<64, false>), g, blk, 0, st, a);
+  }
   return (int)hipGetLastError();
 }
 

@@ -36,15 +36,16 @@ def _qk_shapes(q: torch.Tensor, k: torch.Tensor):
 
 def _score(q, k_score, scaling, group_sum: bool, hist=None) -> torch.Tensor:
     B, Hq, Hk, S, D = _qk_shapes(q, k_score)
-    if k_score.dtype != torch.bfloat16:
-        raise ValueError(f"k_score: dtype {k_score.dtype} not supported (bf16)")
+    if k_score.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+        raise ValueError(f"k_score: dtype {k_score.dtype} not supported (bf16 or float8_e4m3fn)")
+    fp8 = int(k_score.dtype == torch.float8_e4m3fn)
     if group_sum and Hq // Hk > 16:
         raise ValueError("group-summed scores support query groups of at most 16 heads")
     qs = C.rows16(q.squeeze(2))
     k = C.rows16(k_score)
     H = Hk if group_sum else Hq
     out = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
-    call("bytes_sparse_score", ptr(qs), ptr(k), ptr(out), B, Hq, Hk, S, D, int(group_sum),
+    call("bytes_sparse_score", ptr(qs), ptr(k), fp8, ptr(out), B, Hq, Hk, S, D, int(group_sum),
          qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), out.stride(0), out.stride(1),
          float(scaling), hist, stream_of(q))
     return out
@@ -55,10 +56,13 @@ def sparse_score_scalar(q: torch.Tensor, k_score: torch.Tensor, scaling: float, 
     """Pass 1: fp32 scores[b, h, t] = (q[b, h] . k[b, h // G, t]) * scaling.
 
     Replaces src/attention_kernels.py:1113-1133.  q [B,H_q,1,D] bf16;
-    k_score [B,H_k,S,D] bf16.  Returns [B,H_q,S] fp32.
+    k_score [B,H_k,S,D] bf16 (score_bits=16) or float8_e4m3fn (score_bits=8).
+    Returns [B,H_q,S] fp32.
     """
-    if score_bits != 16:
-        raise ValueError(f"score_bits={score_bits}: bf16 score keys (16) only")
+    want = {16: torch.bfloat16, 8: torch.float8_e4m3fn}.get(score_bits)
+    if want is None or k_score.dtype != want:
+        raise ValueError(f"score_bits={score_bits} with k_score {k_score.dtype}: use 16 with bf16 or 8 with "
+                         "float8_e4m3fn keys (packed 4/2-bit keys: sparse_score_packed)")
     return _score(q, k_score, scaling, group_sum=False)
 
 
@@ -108,10 +112,11 @@ def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: t
     """Pass 2: exact attention over the gathered rows.
 
     Replaces src/attention_kernels.py:1037-1059.  q [B,H_q,1,D] bf16; k, v
-    [B,H_k,S,D] bf16; idx [B,H_q,kb] (per query head, the reference layout) or
-    [B,H_k,kb] (one selection per KV head, shared by its query group), any
-    integer dtype.  Entries outside [0, S) are masked (sentinel rule of
-    benchmarks/sparse_attention.py:376).  Returns [B,H_q,1,D] bf16.
+    [B,H_k,S,D] bf16 or float8_e4m3fn; idx [B,H_q,kb] (per query head, the
+    reference layout) or [B,H_k,kb] (one selection per KV head, shared by its
+    query group), any integer dtype.  Entries outside [0, S) are masked
+    (sentinel rule of benchmarks/sparse_attention.py:376).  Returns
+    [B,H_q,1,D] bf16 (also for fp8 values, :1044).
 
     page > 1: idx holds page ids, each standing for rows p*page .. p*page+page-1
     clamped to S-1 (the Quest expansion, benchmarks/sparse_attention.py:360-363).
@@ -124,8 +129,8 @@ def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: t
         raise ValueError(f"limit={limit} outside [0, S]")
     B, Hq, Hk, S, D = _qk_shapes(q, k)
     C.cuda_tensors(q, v, idx)
-    C.dtype_in(k, "k", torch.bfloat16)
-    C.dtype_in(v, "v", torch.bfloat16)
+    C.dtype_in(k, "k", torch.bfloat16, torch.float8_e4m3fn)
+    C.dtype_in(v, "v", k.dtype)
     if tuple(v.shape) != tuple(k.shape):
         raise ValueError(f"shape mismatch: k {tuple(k.shape)}, v {tuple(v.shape)}")
     if idx.dim() != 3 or idx.shape[0] != B or idx.shape[1] not in (Hq, Hk):
@@ -145,7 +150,8 @@ def sparse_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: t
         page = 0                                    # plain row indices
     nbytes = size_query("bytes_gather_attn_workspace_size", B, Hq, Hk, kb * max(page, 1), D, per_head, int(chunk))
     ws = workspace(q.device, nbytes)
-    call("bytes_gather_attn", ptr(qs), ptr(k), ptr(v), ptr(idx), ptr(out), B, Hq, Hk, S, D, kb * max(page, 1),
+    call("bytes_gather_attn", ptr(qs), ptr(k), ptr(v), int(k.dtype == torch.float8_e4m3fn), ptr(idx), ptr(out),
+         B, Hq, Hk, S, D, kb * max(page, 1),
          per_head, page, S if limit is None else int(limit), qs.stride(0), qs.stride(1),
          k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
          idx.stride(0), idx.stride(1), out.stride(0), out.stride(1), float(scaling), int(chunk), ptr(ws),
@@ -162,27 +168,32 @@ def sparse_decode_scalar(q, k_score_or_packed, scale, zero, k_val, v_val, frac, 
                          group_size=32, BLOCK_N=128, BLOCK_K=64):
     """Two-pass sparse decode: score every key, keep the top kb = max(1, round(frac*S))
     per query head, attend exactly over them.  Replaces
-    src/attention_kernels.py:1252-1263 for bf16 score keys (score_bits=16);
-    `scale`/`zero`/`group_size` belong to the packed-score variant.
-    Returns [B,H_q,1,D] bf16."""
+    src/attention_kernels.py:1252-1263 for bf16 (score_bits=16) or fp8
+    (score_bits=8) score keys; `scale`/`zero`/`group_size` belong to the
+    packed-score variant.  Returns [B,H_q,1,D] bf16."""
     scores = sparse_score_scalar(q, k_score_or_packed, scaling, score_bits=score_bits)
     kb = budget(frac, scores.shape[-1])
     idx = topk_indices(scores, kb, sorted=False)      # attention does not depend on the order
     return sparse_gather_attn(q, k_val, v_val, idx, scaling)
 
 
-def token_topk_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float):
+def token_topk_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float, *,
+                      k_score: torch.Tensor = None):
     """Group-shared token top-k decode: group-summed fp32 scores per KV head,
     the kb best tokens per (b, KV head), attention of every query head of the
-    group over them.  Returns (out [B,H_q,1,D] bf16, idx [B,H_k,kb] int32 by
-    ascending token index)."""
-    B, Hq, Hk, S, D = _qk_shapes(q, k)
+    group over them.  `k_score` (default k) holds the keys the selection scores
+    use, e.g. a float8_e4m3fn copy of the cache.  Returns (out [B,H_q,1,D]
+    bf16, idx [B,H_k,kb] int32 by ascending token index)."""
+    ks = k if k_score is None else k_score
+    B, Hq, Hk, S, D = _qk_shapes(q, ks)
+    if tuple(ks.shape) != tuple(k.shape):
+        raise ValueError(f"k_score {tuple(ks.shape)} does not match k {tuple(k.shape)}")
     if B * Hk <= TOPK_HIST_ROWS:
         # the score kernel also counts the top-k digit histogram, in the top-k workspace
         ws = _topk_workspace(q.device, B * Hk, S, kb)
-        s = _score(q, k, scaling, group_sum=True, hist=ptr(ws))
+        s = _score(q, ks, scaling, group_sum=True, hist=ptr(ws))
         idx = _topk(s, kb, sorted=False, ws=ws, hist_ready=True)
     else:
-        s = group_scores(q, k, scaling)
+        s = group_scores(q, ks, scaling)
         idx = topk_indices(s, kb, sorted=False)
     return sparse_gather_attn(q, k, v, idx, scaling), idx

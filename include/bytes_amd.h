@@ -55,6 +55,19 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
                            float scale, int chunk, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* FP8 dense decode: replaces src/attention_kernels.py:156-182 (`decode_attn_fp8`,
+ * kernel :98-154).  Same arguments as bytes_decode_attn_bf16 with k, v OCP
+ * float8_e4m3fn (strides in elements = bytes), widened to bf16 exactly; out bf16
+ * (q's dtype).  Workspace size: bytes_decode_attn_bf16_workspace_size. */
+int bytes_decode_attn_fp8(const void* q, const void* k, const void* v, void* out,
+                          int B, int Hq, int Hk, int S, int D,
+                          int64_t q_sb, int64_t q_sh,
+                          int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                          int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                          int64_t o_sb, int64_t o_sh,
+                          float scale, int chunk, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* ---------------------------------------------------------------------------
  * KIVI asymmetric min/max quantize + pack along the last axis.
  * Replaces the external KIVI `triton_quantize_and_pack_along_last_dim(x, 32, bits)`
@@ -109,7 +122,8 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
 /* ---------------------------------------------------------------------------
  * Token scoring.
  * Replaces src/attention_kernels.py:1113-1133 (`sparse_score_scalar`, kernel
- * :1077-1110) for bf16 keys:
+ * :1077-1110) for bf16 keys (k_fp8 = 0) or OCP float8_e4m3fn keys (k_fp8 = 1,
+ * score_bits = 8; widened to bf16 exactly):
  *   group_sum = 0: out [B, Hq, S] fp32, out[b,h,t] = (q[b,h] . k[b,h/G,t]) * scaling
  *   group_sum = 1: out [B, Hk, S] fp32, out[b,hk,t] = sum_{g<G} (q[b,hk*G+g] . k[b,hk,t]) * scaling
  *                  (the per-KV-head selection score of the token top-k path; G <= 16)
@@ -120,7 +134,7 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
  *   bytes of a bytes_topk workspace (its histogram region, B*Hk <= 128) and
  *   call bytes_topk with hist_ready = 1 to skip its histogram pass.
  * ------------------------------------------------------------------------- */
-int bytes_sparse_score(const void* q, const void* k, void* out, int B, int Hq, int Hk, int S, int D,
+int bytes_sparse_score(const void* q, const void* k, int k_fp8, void* out, int B, int Hq, int Hk, int S, int D,
                        int group_sum, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
                        int64_t o_sb, int64_t o_sh, float scaling, void* hist, void* stream);
 
@@ -149,8 +163,9 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
  * over the kb entries idx_j in [0, S); other entries are ignored.
  *   per_head = 1: idx [B, Hq, kb] int32 (one list per query head, the reference layout)
  *   per_head = 0: idx [B, Hk, kb] int32 (one list per KV head, shared by its G query heads)
- *   idx strides i_sb, i_sh (unit stride along kb); k, v [B, Hk, S, D] bf16;
- *   out [B, Hq, D] bf16.  D in {64, 128}.
+ *   idx strides i_sb, i_sh (unit stride along kb); k, v [B, Hk, S, D] bf16, or OCP
+ *   float8_e4m3fn when kv_fp8 = 1 (widened to bf16 exactly); out [B, Hq, D] bf16.
+ *   D in {64, 128}.
  * page = 0: idx entries are rows.  page > 0: idx holds kb/page page ids per list,
  *   page id p standing for rows min(p*page + o, S-1), o < page (the Quest
  *   expansion, benchmarks/sparse_attention.py:358-363).
@@ -158,10 +173,11 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
  * ------------------------------------------------------------------------- */
 int bytes_gather_attn_workspace_size(int B, int Hq, int Hk, int kb, int D, int per_head, int chunk,
                                      size_t* bytes);
-int bytes_gather_attn(const void* q, const void* k, const void* v, const void* idx, void* out, int B, int Hq,
-                      int Hk, int S, int D, int kb, int per_head, int page, int limit, int64_t q_sb, int64_t q_sh, int64_t k_sb,
-                      int64_t k_sh, int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb,
-                      int64_t i_sh, int64_t o_sb, int64_t o_sh, float scaling, int chunk, void* workspace,
+int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, const void* idx, void* out,
+                      int B, int Hq, int Hk, int S, int D, int kb, int per_head, int page, int limit,
+                      int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                      int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t i_sb, int64_t i_sh,
+                      int64_t o_sb, int64_t o_sh, float scaling, int chunk, void* workspace,
                       size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
