@@ -28,17 +28,23 @@ def dtype_in(t: torch.Tensor, name: str, *dtypes: torch.dtype) -> None:
         raise ValueError(f"{name}: dtype {t.dtype} not supported (expected one of {dtypes})")
 
 
-def rows16(t: torch.Tensor) -> torch.Tensor:
-    """Unit stride on the last dim, every row start 16-byte aligned; copies on the
-    GPU when the given layout does not allow 128-bit row loads."""
+def rows16(t: torch.Tensor, align: int = 16) -> torch.Tensor:
+    """Unit stride on the last dim, every row start `align`-byte aligned (16 by
+    default: 128-bit row loads); copies on the GPU when the given layout does
+    not allow that."""
     es = t.element_size()
-    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+    ok = t.stride(-1) == 1 and t.data_ptr() % align == 0
     if ok:
         for d in range(t.dim() - 1):
-            if t.size(d) > 1 and (t.stride(d) * es) % 16 != 0:
+            if t.size(d) > 1 and (t.stride(d) * es) % align != 0:
                 ok = False
                 break
-    return t if ok else t.contiguous()
+    if ok:
+        return t
+    c = t.contiguous()
+    if c.data_ptr() % align != 0:
+        raise ValueError(f"tensor storage is not {align}-byte aligned")
+    return c
 
 
 def ndim(t: torch.Tensor, n: int, name: str) -> None:

@@ -49,11 +49,13 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64,                                 # out strides
         c_f32, c_int, c_vp, c_sz, c_vp),
     "bytes_sparse_score": (
-        c_vp, c_vp, c_int, c_vp,                      # q, k, k is fp8, out
+        c_vp, c_vp, c_int, c_vp, c_vp, c_vp,          # q, k, key mode, k scale, k min, out
         c_int, c_int, c_int, c_int, c_int, c_int,     # B, Hq, Hk, S, D, group_sum
         c_i64, c_i64, c_i64, c_i64, c_i64,            # q (b, h), k (b, h, s) strides
+        c_i64, c_i64, c_i64,                          # scale / min strides (b, h, s)
         c_i64, c_i64,                                 # out strides (b, h)
         c_f32, c_vp, c_vp),                           # scaling, histogram (or None), stream
+    "bytes_score_keys_pack": (c_vp, c_int, c_i64, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp),
     "bytes_topk_workspace_size": (c_i64, c_int, c_int, c_szp),
     "bytes_topk": (c_vp, c_i64, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_sz, c_vp),
     "bytes_gather_attn_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_szp),

@@ -17,12 +17,16 @@ TOPK_MAX = 8192
 TOPK_HIST_ROWS = 128          # rows whose digit histogram fits the top-k workspace's fixed region
 
 
-def _qk_shapes(q: torch.Tensor, k: torch.Tensor):
+def _qk_shapes(q: torch.Tensor, k: torch.Tensor, k_dim: int = None):
+    """Shapes of q [B,H_q,1,D] against keys [B,H_k,S,D]; k_dim overrides the
+    keys' last extent (packed codes store D*bits/8 bytes per row)."""
     C.cuda_tensors(q, k)
     C.ndim(q, 4, "q"), C.ndim(k, 4, "k")
     C.dtype_in(q, "q", torch.bfloat16)
     B, Hq, one, D = q.shape
     Bk, Hk, S, Dk = k.shape
+    if k_dim is not None:
+        Dk = k_dim
     if one != 1 or Dk != D or Bk != B:
         raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}")
     if Hq % Hk != 0:
@@ -34,20 +38,46 @@ def _qk_shapes(q: torch.Tensor, k: torch.Tensor):
     return B, Hq, Hk, S, D
 
 
-def _score(q, k_score, scaling, group_sum: bool, hist=None) -> torch.Tensor:
-    B, Hq, Hk, S, D = _qk_shapes(q, k_score)
-    if k_score.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
-        raise ValueError(f"k_score: dtype {k_score.dtype} not supported (bf16 or float8_e4m3fn)")
-    fp8 = int(k_score.dtype == torch.float8_e4m3fn)
+def _score(q, k_score, scaling, group_sum: bool, hist=None, packed=None) -> torch.Tensor:
+    """Launch the score kernel. packed = (scale, zero, bits) marks k_score as
+    uint8 4/2-bit codes along head_dim with bf16 per-32-dim scale/min."""
+    if packed is None:
+        B, Hq, Hk, S, D = _qk_shapes(q, k_score)
+        if k_score.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+            raise ValueError(f"k_score: dtype {k_score.dtype} not supported (bf16 or float8_e4m3fn)")
+        mode = int(k_score.dtype == torch.float8_e4m3fn)
+        sc = zr = None
+        m_strides = (0, 0, 0)
+    else:
+        scale, zero, bits = packed
+        if bits not in (4, 2):
+            raise ValueError(f"score_bits={bits}: packed keys are 4 or 2 bits")
+        C.dtype_in(k_score, "k_packed", torch.uint8)
+        nb = k_score.shape[-1]
+        if (nb * 8) % bits:
+            raise ValueError(f"k_packed last dim {nb} does not hold whole {bits}-bit codes")
+        B, Hq, Hk, S, D = _qk_shapes(q, k_score, k_dim=nb * 8 // bits)
+        for name, t in (("scale", scale), ("zero", zero)):
+            C.cuda_tensors(q, t)
+            C.dtype_in(t, name, torch.bfloat16)
+            if tuple(t.shape) != (B, Hk, S, D // 32):
+                raise ValueError(f"{name}: expected shape {(B, Hk, S, D // 32)}, got {tuple(t.shape)}")
+        mode = 2 if bits == 4 else 3
+        sc = C.rows16(scale, D // 32 * 2)
+        zr = C.rows16(zero, D // 32 * 2)
+        if sc.stride() != zr.stride():
+            sc, zr = sc.contiguous(), zr.contiguous()
+        m_strides = (sc.stride(0), sc.stride(1), sc.stride(2))
     if group_sum and Hq // Hk > 16:
         raise ValueError("group-summed scores support query groups of at most 16 heads")
     qs = C.rows16(q.squeeze(2))
     k = C.rows16(k_score)
     H = Hk if group_sum else Hq
     out = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
-    call("bytes_sparse_score", ptr(qs), ptr(k), fp8, ptr(out), B, Hq, Hk, S, D, int(group_sum),
-         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), out.stride(0), out.stride(1),
-         float(scaling), hist, stream_of(q))
+    call("bytes_sparse_score", ptr(qs), ptr(k), mode, ptr(sc) if sc is not None else None,
+         ptr(zr) if zr is not None else None, ptr(out), B, Hq, Hk, S, D, int(group_sum),
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), *m_strides,
+         out.stride(0), out.stride(1), float(scaling), hist, stream_of(q))
     return out
 
 
@@ -64,6 +94,53 @@ def sparse_score_scalar(q: torch.Tensor, k_score: torch.Tensor, scaling: float, 
         raise ValueError(f"score_bits={score_bits} with k_score {k_score.dtype}: use 16 with bf16 or 8 with "
                          "float8_e4m3fn keys (packed 4/2-bit keys: sparse_score_packed)")
     return _score(q, k_score, scaling, group_sum=False)
+
+
+def sparse_score_packed(q: torch.Tensor, k_packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor,
+                        scaling: float, *, score_bits: int = 4, group_size: int = 32,
+                        BLOCK_N: int = 128) -> torch.Tensor:
+    """Pass 1 on packed keys: fp32 scores[b, h, t] = (q[b, h] . k_hat[b, h // G, t]) * scaling
+    with k_hat = code * scale + zero per 32-dim group.
+
+    Replaces src/attention_kernels.py:1199-1222.  q [B,H_q,1,D] bf16;
+    k_packed uint8 [B,H_k,S,D*score_bits/8] (layout of
+    quantize_and_pack_score_keys); scale, zero bf16 [B,H_k,S,D/32] (the
+    dtype the packer gives bf16 keys).
+    group_size must be 32 (every reference caller's value).  Returns
+    [B,H_q,S] fp32."""
+    if group_size != 32:
+        raise ValueError(f"group_size={group_size} not supported (32)")
+    return _score(q, k_packed, scaling, group_sum=False, packed=(scale, zero, score_bits))
+
+
+def quantize_and_pack_score_keys(k: torch.Tensor, score_bits: int, group_size: int):
+    """Asymmetric min/max quantization of keys along head_dim in groups of 32,
+    packed to uint8 (element c at bits score_bits*(c % (8/score_bits)) of byte
+    c // (8/score_bits)).  Replaces src/attention_kernels.py:1225-1249:
+    k [B,H_k,S,D] bf16/fp16/fp32 -> (packed uint8 [B,H_k,S,D*score_bits/8],
+    scale [B,H_k,S,D/32], zero [B,H_k,S,D/32]) in k's dtype."""
+    C.cuda_tensors(k)
+    C.ndim(k, 4, "k")
+    if score_bits not in (4, 2):
+        raise ValueError("Unsupported score_bits")
+    if group_size != 32:
+        raise ValueError(f"group_size={group_size} not supported (32)")
+    dt = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}.get(k.dtype)
+    if dt is None:
+        raise ValueError(f"k: dtype {k.dtype} not supported (bf16, fp16 or fp32)")
+    B, Hk, S, D = k.shape
+    if D % 32:
+        raise ValueError(f"head_dim {D} is not a multiple of 32")
+    x = k.reshape(-1, D)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    rows = x.shape[0]
+    packed = torch.empty((B, Hk, S, D * score_bits // 8), dtype=torch.uint8, device=k.device)
+    scale = torch.empty((B, Hk, S, D // 32), dtype=k.dtype, device=k.device)
+    zero = torch.empty_like(scale)
+    call("bytes_score_keys_pack", ptr(x), dt, rows, D, x.stride(0) if rows else D, score_bits, ptr(packed),
+         ptr(scale), ptr(zero), stream_of(k))
+    return packed, scale, zero
 
 
 def group_scores(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tensor:
@@ -168,10 +245,14 @@ def sparse_decode_scalar(q, k_score_or_packed, scale, zero, k_val, v_val, frac, 
                          group_size=32, BLOCK_N=128, BLOCK_K=64):
     """Two-pass sparse decode: score every key, keep the top kb = max(1, round(frac*S))
     per query head, attend exactly over them.  Replaces
-    src/attention_kernels.py:1252-1263 for bf16 (score_bits=16) or fp8
-    (score_bits=8) score keys; `scale`/`zero`/`group_size` belong to the
-    packed-score variant.  Returns [B,H_q,1,D] bf16."""
-    scores = sparse_score_scalar(q, k_score_or_packed, scaling, score_bits=score_bits)
+    src/attention_kernels.py:1252-1263: bf16 (score_bits=16) or fp8
+    (score_bits=8) score keys, or packed 4/2-bit keys with their `scale` and
+    `zero` (score_bits=4/2, group_size=32).  Returns [B,H_q,1,D] bf16."""
+    if score_bits in (16, 8):
+        scores = sparse_score_scalar(q, k_score_or_packed, scaling, score_bits=score_bits)
+    else:
+        scores = sparse_score_packed(q, k_score_or_packed, scale, zero, scaling, score_bits=score_bits,
+                                     group_size=group_size)
     kb = budget(frac, scores.shape[-1])
     idx = topk_indices(scores, kb, sorted=False)      # attention does not depend on the order
     return sparse_gather_attn(q, k_val, v_val, idx, scaling)

@@ -122,21 +122,43 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
 /* ---------------------------------------------------------------------------
  * Token scoring.
  * Replaces src/attention_kernels.py:1113-1133 (`sparse_score_scalar`, kernel
- * :1077-1110) for bf16 keys (k_fp8 = 0) or OCP float8_e4m3fn keys (k_fp8 = 1,
- * score_bits = 8; widened to bf16 exactly):
+ * :1077-1110) and :1199-1222 (`sparse_score_packed`, kernel :1136-1196).
+ * k_mode selects the key format:
+ *   0  bf16 keys [B, Hk, S, D] (score_bits = 16)
+ *   1  OCP float8_e4m3fn keys [B, Hk, S, D] (score_bits = 8; widened to bf16 exactly)
+ *   2  4-bit codes uint8 [B, Hk, S, D/2], two per byte, element c at bits 4*(c%2)
+ *   3  2-bit codes uint8 [B, Hk, S, D/4], four per byte, element c at bits 2*(c%4)
+ *   modes 2/3: k_scale, k_min bf16 [B, Hk, S, D/32] (strides m_*; one pair per
+ *   32 dims, key = code * scale + min; the layout of bytes_score_keys_pack).
+ * Scores:
  *   group_sum = 0: out [B, Hq, S] fp32, out[b,h,t] = (q[b,h] . k[b,h/G,t]) * scaling
  *   group_sum = 1: out [B, Hk, S] fp32, out[b,hk,t] = sum_{g<G} (q[b,hk*G+g] . k[b,hk,t]) * scaling
  *                  (the per-KV-head selection score of the token top-k path; G <= 16)
- *   q [B, Hq, D] bf16 (strides q_sb, q_sh); k [B, Hk, S, D] bf16 (strides k_*);
- *   out strides o_sb, o_sh (unit stride along S).  D in {64, 128}.
+ *   q [B, Hq, D] bf16 (strides q_sb, q_sh); k strides k_* in storage elements
+ *   (bytes for modes 1-3); out strides o_sb, o_sh (unit stride along S).
+ *   D in {64, 128}.
  * hist (group_sum = 1 only, may be NULL): [B*Hk][2048] uint32, zero on entry,
  *   receives the count of each score's top 11 order-key bits; pass the first
  *   bytes of a bytes_topk workspace (its histogram region, B*Hk <= 128) and
  *   call bytes_topk with hist_ready = 1 to skip its histogram pass.
  * ------------------------------------------------------------------------- */
-int bytes_sparse_score(const void* q, const void* k, int k_fp8, void* out, int B, int Hq, int Hk, int S, int D,
-                       int group_sum, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
-                       int64_t o_sb, int64_t o_sh, float scaling, void* hist, void* stream);
+int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_scale, const void* k_min, void* out,
+                       int B, int Hq, int Hk, int S, int D, int group_sum, int64_t q_sb, int64_t q_sh, int64_t k_sb,
+                       int64_t k_sh, int64_t k_ss, int64_t m_sb, int64_t m_sh, int64_t m_ss, int64_t o_sb,
+                       int64_t o_sh, float scaling, void* hist, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Quantize and pack score keys along head_dim.
+ * Replaces src/attention_kernels.py:1225-1249 (`quantize_and_pack_score_keys`,
+ * group_size = 32, the size every caller uses: benchmarks/test_correctness.py:706,
+ * bench_sparse_crossover.py:188,201).  Per row and group of 32 dims, in fp32:
+ * scale = max(max - min, 1e-8) / (2^bits - 1), code = clamp(rint((x - min) / scale)).
+ *   x [rows, D] (x_dtype 0 bf16, 1 fp16, 2 fp32; row stride x_row_stride)
+ *   packed uint8 [rows, D*bits/8]; scale, mn [rows, D/32] in x's dtype
+ *   (rounded after the codes are chosen).  bits in {4, 2}, D % 32 == 0.
+ * ------------------------------------------------------------------------- */
+int bytes_score_keys_pack(const void* x, int x_dtype, int64_t rows, int D, int64_t x_row_stride, int bits,
+                          void* packed, void* scale, void* mn, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Deterministic top-k per row.

@@ -493,6 +493,53 @@ def sparse_gather_attn(q, k, v, idx, scaling: float):
     return o.reshape(B, Hq, 1, D).to(od)
 
 
+def score_keys_pack(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """Codes [..., D] (ints < 2^bits) -> uint8 [..., D*bits/8]: element c of a
+    row at bits ((c % (8/bits)) * bits) of byte c // (8/bits), the layout of
+    src/attention_kernels.py:1239-1245 (4-bit: lo | hi << 4; 2-bit: 4 per byte)."""
+    per = 8 // bits
+    c = codes.long().reshape(*codes.shape[:-1], -1, per)
+    out = torch.zeros(c.shape[:-1], dtype=torch.int64)
+    for i in range(per):
+        out |= (c[..., i] & ((1 << bits) - 1)) << (i * bits)
+    return out.to(torch.uint8)
+
+
+def score_keys_unpack(packed: torch.Tensor, bits: int) -> torch.Tensor:
+    """Inverse of score_keys_pack (the unpack loop of benchmarks/test_correctness.py:708-718)."""
+    per = 8 // bits
+    p = packed.long()
+    parts = [(p >> (i * bits)) & ((1 << bits) - 1) for i in range(per)]
+    return torch.stack(parts, dim=-1).reshape(*packed.shape[:-1], -1)
+
+
+def quantize_and_pack_score_keys(k: torch.Tensor, score_bits: int, group_size: int):
+    """Asym min/max quantization of the keys along head_dim in groups, packed to
+    uint8; scale and min rounded to k's dtype after the codes are formed.
+    Restates src/attention_kernels.py:1225-1249.  k [B,H,S,D] ->
+    (packed [B,H,S,D*bits/8] uint8, scale [B,H,S,D/g], zero [B,H,S,D/g])."""
+    B, H, S, D = k.shape
+    ng = D // group_size
+    kr = k.reshape(B, H, S, ng, group_size)
+    codes, scale, xmin = asym_quant_codes(kr, 2 ** score_bits, dim=-1)
+    packed = score_keys_pack(codes.reshape(B, H, S, D), score_bits)
+    return packed, scale.reshape(B, H, S, ng).to(k.dtype), xmin.reshape(B, H, S, ng).to(k.dtype)
+
+
+def score_keys_dequant(packed, scale, zero, score_bits: int, group_size: int) -> torch.Tensor:
+    """k_hat = code * scale + zero in fp32 (src/attention_kernels.py:1170-1187)."""
+    codes = score_keys_unpack(packed, score_bits).float()
+    B, H, S, D = codes.shape
+    s = scale.float().repeat_interleave(group_size, dim=-1)
+    z = zero.float().repeat_interleave(group_size, dim=-1)
+    return codes * s + z
+
+
+def sparse_score_packed(q, packed, scale, zero, scaling: float, score_bits: int = 4, group_size: int = 32):
+    """fp32 scores against dequantized packed keys (src/attention_kernels.py:1136-1222)."""
+    return sparse_score_scalar(q, score_keys_dequant(packed, scale, zero, score_bits, group_size), scaling)
+
+
 def budget(frac: float, S: int) -> int:
     """kb = max(1, round(frac*S)) with Python's round (src/attention_kernels.py:1261)."""
     return max(1, int(round(frac * S)))

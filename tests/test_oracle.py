@@ -287,3 +287,47 @@ def test_group_scores_and_gather():
     idx_kv = torch.randint(0, S, (B, Hk, 7), generator=torch.Generator().manual_seed(1))
     assert torch.equal(R.sparse_gather_attn(q, k, v, idx_kv, 0.25),
                        R.sparse_gather_attn(q, k, v, idx_kv.repeat_interleave(3, 1), 0.25))
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_score_keys_pack_exhaustive(bits):
+    """Every code in every slot of a byte survives pack -> unpack, and a hand
+    byte decodes as the reference loop (test_correctness.py:708-718) reads it."""
+    per = 8 // bits
+    codes = torch.cartesian_prod(*[torch.arange(2 ** bits)] * per).reshape(-1, per)
+    packed = R.score_keys_pack(codes, bits)
+    assert packed.shape == (codes.shape[0], 1)
+    assert torch.equal(R.score_keys_unpack(packed, bits), codes)
+    if bits == 4:
+        assert R.score_keys_pack(torch.tensor([[3, 12]]), 4).item() == 3 | (12 << 4)
+    else:
+        assert R.score_keys_pack(torch.tensor([[1, 2, 3, 0]]), 2).item() == 1 | (2 << 2) | (3 << 4)
+
+
+def test_quantize_and_pack_score_keys_closed_form():
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(2, 3, 5, 64, generator=g).to(torch.bfloat16)
+    k[0, 0, 0, :32] = 0.75                                   # constant group
+    for bits in (4, 2):
+        packed, sc, zr = R.quantize_and_pack_score_keys(k, bits, 32)
+        assert packed.dtype == torch.uint8 and packed.shape == (2, 3, 5, 64 * bits // 8)
+        assert sc.dtype == torch.bfloat16 and sc.shape == (2, 3, 5, 2)
+        codes = R.score_keys_unpack(packed, bits).reshape(2, 3, 5, 2, 32)
+        kf = k.float().reshape(2, 3, 5, 2, 32)
+        lo, hi = kf.amin(-1), kf.amax(-1)
+        # each group's extremes quantize to the end codes (non-constant groups)
+        for b_, h_, s_, gi in [(1, 2, 4, 1), (0, 1, 2, 0)]:
+            row = codes[b_, h_, s_, gi]
+            assert row[kf[b_, h_, s_, gi].argmin()] == 0
+            assert row[kf[b_, h_, s_, gi].argmax()] == 2 ** bits - 1
+        assert torch.all(codes[0, 0, 0, 0] == 0)
+        assert torch.equal(zr, lo.to(torch.bfloat16))
+        exp_scale = ((hi - lo).clamp(min=1e-8) / (2 ** bits - 1)).to(torch.bfloat16)
+        assert torch.equal(sc, exp_scale)
+        # dequantized keys are within half a step of the originals, plus what the
+        # bf16 rounding of scale (times the code) and of the minimum adds
+        dq = R.score_keys_dequant(packed, sc, zr, bits, 32)
+        step = sc.float().repeat_interleave(32, -1)
+        lvl = 2 ** bits - 1
+        bound = 0.5 * step + lvl * step * 2 ** -8 + 2 ** -8 * lo.repeat_interleave(32, -1).abs() + 1e-6
+        assert torch.all((dq - k.float()).abs() <= bound)
