@@ -166,36 +166,51 @@ class TopkCase(Case):
     query head of the group.  One step = score + top-k + gather."""
     kernel = "score_kernel"
 
-    def __init__(self, name, kb, B=8, Hq=24, Hk=8, D=128, L=131072, score_fp8=False):
-        self.name, self.kb, self.shape, self.score_fp8 = name, kb, (B, Hq, Hk, D, L), score_fp8
-        self.workload = (f"token top-k decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} k={kb} (group-summed scores"
-                         f"{' on fp8 e4m3fn score keys' if score_fp8 else ''})")
-        if score_fp8:
-            self.dtype = "bf16 (fp8 score keys)"
+    def __init__(self, name, kb, B=8, Hq=24, Hk=8, D=128, L=131072, score_bits=16):
+        self.name, self.kb, self.shape, self.score_bits = name, kb, (B, Hq, Hk, D, L), score_bits
+        keys = {16: "", 8: " on fp8 e4m3fn score keys", 4: " on packed 4-bit score keys",
+                2: " on packed 2-bit score keys"}[score_bits]
+        self.workload = f"token top-k decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} k={kb} (group-summed scores{keys})"
+        if score_bits != 16:
+            self.dtype = {8: "bf16 (fp8 score keys)", 4: "bf16 (int4 score keys)", 2: "bf16 (int2 score keys)"}[
+                score_bits]
+
+    def key_bytes(self):
+        """Bytes of score keys the score pass reads: codes plus, for packed keys,
+        the bf16 scale and min of every 32-dim group."""
+        B, Hq, Hk, D, L = self.shape
+        rows = B * Hk * L
+        if self.score_bits in (16, 8):
+            return rows * D * self.score_bits // 8
+        return rows * (D * self.score_bits // 8 + (D // 32) * 2 * 2)
 
     def bytes_per_step(self):
         B, Hq, Hk, D, L = self.shape
-        keys = B * Hk * L * D * (1 if self.score_fp8 else 2)   # score pass reads every key once
         scores = B * Hk * L * 4 * 2               # fp32 scores written, read by the top-k
         gather = 2 * B * Hk * self.kb * D * 2     # selected K and V rows
-        return keys + scores + gather + 2 * B * Hq * D * 2
+        return self.key_bytes() + scores + gather + 2 * B * Hq * D * 2
 
     def kernel_bytes(self):
         B, Hq, Hk, D, L = self.shape
-        return B * Hk * L * D * 2 + B * Hk * L * 4 + B * Hq * D * 2
+        return self.key_bytes() + B * Hk * L * 4 + B * Hq * D * 2
 
     def make(self, dev):
         from bytes_amd import workloads as W
+        from bytes_amd.sparse import quantize_and_pack_score_keys
         B, Hq, Hk, D, L = self.shape
         x = W.c5_topk(seed=0, device=dev, B=B, Hq=Hq, Hk=Hk, D=D, L=L)
         d = {"q": x["q"], "k": x["k"], "v": x["v"], "scale": x["scale"]}
-        if self.score_fp8:
-            d["k8"] = x["k"].to(torch.float8_e4m3fn)
+        if self.score_bits == 8:
+            d["ks"] = x["k"].to(torch.float8_e4m3fn)
+        elif self.score_bits in (4, 2):
+            d["ks"], d["ksc"], d["kzr"] = quantize_and_pack_score_keys(x["k"], self.score_bits, 32)
         return d
 
     def step(self, inp):
         from bytes_amd.sparse import token_topk_decode
-        return token_topk_decode(inp["q"], inp["k"], inp["v"], self.kb, inp["scale"], k_score=inp.get("k8"))
+        return token_topk_decode(inp["q"], inp["k"], inp["v"], self.kb, inp["scale"], k_score=inp.get("ks"),
+                                 score_scale=inp.get("ksc"), score_zero=inp.get("kzr"),
+                                 score_bits=self.score_bits if self.score_bits in (4, 2) else None)
 
     def cpu_sample(self):
         from bytes_amd import workloads as W
@@ -343,7 +358,9 @@ def cases():
         "c5_topk1024": TopkCase("c5_topk1024", 1024),
         "c5_topk4096": TopkCase("c5_topk4096", 4096),
         "c5_dense": DenseCase("c5_dense", *W.SHAPES["c5_topk"]),
-        "c5_topk1024_fp8s": TopkCase("c5_topk1024_fp8s", 1024, score_fp8=True),
+        "c5_topk1024_fp8s": TopkCase("c5_topk1024_fp8s", 1024, score_bits=8),
+        "c5_topk1024_int4s": TopkCase("c5_topk1024_int4s", 1024, score_bits=4),
+        "c5_topk1024_int2s": TopkCase("c5_topk1024_int2s", 1024, score_bits=2),
         "dense_16k_fp8": DenseFp8Case("dense_16k_fp8", *W.SHAPES["dense_16k"]),
     }
 

@@ -19,13 +19,23 @@
 // fp8 (OCP e4m3fn) keys (`score_bits=8`, :1113) load 8 bytes per operand and
 // are widened to bf16 exactly in registers.
 //
-// Packed 4/2-bit keys (`sparse_score_packed`, :1136-1222; layout of
-// `quantize_and_pack_score_keys`, :1225-1249: codes along head_dim, two or
-// four per byte, bf16 scale/min per 32-dim group) are scored group by group:
-// k-step kk of the MFMA covers exactly group kk, so
-//   score = sum_kk scale_kk * (q . code)_kk + min_kk * (sum of q over group kk)
-// with the integer codes as exact bf16 operands and both terms in fp32.
+// Packed 4/2-bit keys (`sparse_score_packed`, :1136-1222, layout of
+// `quantize_and_pack_score_keys`, :1225-1249: codes along head_dim, element c
+// at bits bits*(c % (8/bits)) of byte c // (8/bits), one bf16 scale/min per
+// 32 dims) use a different row map: MFMA row m stands for the pair
+// (group m / R, head m % R) with R = 16 / (D/32), and the A operand is q with
+// every entry outside row m's group set to zero.  One MFMA chain then yields
+// the per-group dot products (q . code)_g of R heads in separate rows, and
+// each lane applies its own group's scale and min:
+//   score = sum_g scale_g * (q . code)_g + min_g * (sum of q over group g).
+// A lane's codes are one contiguous run of its row (D*bits/32 bytes, one
+// load), all in one group.  Codes become bf16 operands by byte permutes
+// against the constant 0x43: bf16 0x43cc is 128 + cc exactly, so the MFMA
+// yields (q . code)_g + 128 * (sum of q)_g and the min term absorbs the
+// offset as (min_g - 128 * scale_g).  The permute order of the codes inside
+// an operand is applied to q as well.
 #include "dense_tile.h"
+#include "splitk.h"
 
 namespace bytes_amd {
 
@@ -36,178 +46,379 @@ struct ScoreArgs {
   int64_t q_sb, q_sh;
   const void* k;             // bf16, fp8 e4m3fn or packed codes (strides in storage elements)
   int64_t k_sb, k_sh, k_ss;
-  const uint16_t* ksc;       // packed modes: bf16 scale / min [B, Hk, S, D/32]
+  const uint16_t* ksc;       // packed keys: bf16 scale / min [B, Hk, S, D/32]
   const uint16_t* kmn;
   int64_t m_sb, m_sh, m_ss;
   float* out;                // [B, Hq, S] (per head) or [B, Hk, S] (group sum); unit stride along S
   int64_t o_sb, o_sh;
   uint32_t* hist;            // group sum only, optional: [B*Hk][2048] counts of the top 11 key bits
-  int Hk, G, HB, S, tok_per_wg, parts, group_sum;
+  int Hk, G, HPU, HB, S, tok_per_wg, parts, group_sum;   // HPU heads per unit, HB units per KV head
   float scaling;
 };
 
 constexpr int kScoreWaves = 4;
-constexpr int kScoreIter = 64;   // tokens per wave iteration (4 MFMA column tiles)
 
-template <int D, int KM>
-struct ScoreRegs {
-  typedef typename std::conditional<KM == kKeyBf16, u32x4,
-                                    typename std::conditional<KM == kKeyFp8, u32x2, uint32_t>::type>::type T;
-  T k[4][D / 32];            // [column tile][k-step]
-  u32x2 sc[KM >= kKeyP4 ? 4 : 1], mn[KM >= kKeyP4 ? 4 : 1];   // packed: bf16 scale/min of the 4 groups
+__device__ __forceinline__ void score_emit_sum(const ScoreArgs& a, float tot, int tok, int b, int hk, int lg,
+                                               uint32_t* hlds) {
+  if (lg == 0 && tok < a.S) {
+    a.out[(int64_t)b * a.o_sb + (int64_t)hk * a.o_sh + tok] = tot;
+    if (hlds) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
+  }
+}
+
+// ---- bf16 / fp8 keys ------------------------------------------------------
+
+template <int D, bool FP8>
+struct DenseKeys {
+  static constexpr int CT = 4;                 // 16-token column tiles per wave iteration
+  typedef typename std::conditional<FP8, u32x2, u32x4>::type T;
+  struct Regs {
+    T k[4][D / 32];          // [column tile][k-step]
+  };
+  const void* kbase;
+  bf16x8 qa[D / 32];
+
+  __device__ __forceinline__ void init(const ScoreArgs& a, int b, int hk, int hq0, int nh, int lane) {
+    const int l16 = lane & 15, lg = lane >> 4;
+    kbase = FP8 ? (const void*)(static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh)
+                : (const void*)(static_cast<const uint16_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh);
+    // Q as the A operand: lane holds Q[h = l16][dims (kk*4 + lg)*8 .. +8]
+    const bool live = l16 < nh;
+    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + (live ? l16 : 0)) * a.q_sh + lg * 8;
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk)
+      qa[kk] = __builtin_bit_cast(bf16x8, live ? ld16(qp + kk * 32) : u32x4{0, 0, 0, 0});
+  }
+
+  // K rows t .. t+63 of one iteration as B operands (rows clamped to S-1).
+  __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lane, Regs& r) const {
+    const int l16 = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int row = min(t + c * 16 + l16, a.S - 1);
+      if constexpr (FP8) {
+        const uint8_t* p = static_cast<const uint8_t*>(kbase) + (int64_t)row * a.k_ss + lg * 8;
+#pragma unroll
+        for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = *reinterpret_cast<const u32x2*>(p + kk * 32);
+      } else {
+        const uint16_t* p = static_cast<const uint16_t*>(kbase) + (int64_t)row * a.k_ss + lg * 8;
+#pragma unroll
+        for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = ld16(p + kk * 32);
+      }
+    }
+  }
+
+  static __device__ __forceinline__ bf16x8 operand(const u32x4& w) { return __builtin_bit_cast(bf16x8, w); }
+  static __device__ __forceinline__ bf16x8 operand(const u32x2& w) {
+    const u32x4 b = {fp8x2_to_bf16x2<false>(w[0]), fp8x2_to_bf16x2<true>(w[0]), fp8x2_to_bf16x2<false>(w[1]),
+                     fp8x2_to_bf16x2<true>(w[1])};
+    return __builtin_bit_cast(bf16x8, b);
+  }
+
+  __device__ __forceinline__ void tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
+                                       int nh, uint32_t* hlds) const {
+    const int l16 = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < D / 32; ++kk) s = mfma_bf16(qa[kk], operand(r.k[c][kk]), s);
+      const int tok = t + c * 16 + l16;
+      if (a.group_sum) {
+        // heads lg*4 + i; group sum in head order, lane groups added in order
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (lg * 4 + i < nh) part += s[i] * a.scaling;
+        const float p1 = __shfl(part, l16 + 16, 64);
+        const float p2 = __shfl(part, l16 + 32, 64);
+        const float p3 = __shfl(part, l16 + 48, 64);
+        float tot = part;
+        if (nh > 4) tot += p1;
+        if (nh > 8) tot += p2;
+        if (nh > 12) tot += p3;
+        score_emit_sum(a, tot, tok, b, hk, lg, hlds);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int h = lg * 4 + i;
+          if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = s[i] * a.scaling;
+        }
+      }
+    }
+  }
 };
 
-// K rows t .. t+63 of one iteration as B operands (rows clamped to S-1).
-template <int D, int KM>
-__device__ __forceinline__ void score_issue(const ScoreArgs& a, const void* kbase, const uint16_t* scb,
-                                            const uint16_t* mnb, int t, int lane, ScoreRegs<D, KM>& r) {
-  const int l16 = lane & 15, lg = lane >> 4;
+// ---- packed 4/2-bit keys --------------------------------------------------
+
+// Position, inside its run of 8 codes, of the code that lands in operand
+// element j after the byte permutes below (applied to q the same way).
+__device__ __forceinline__ int packed_perm(int bits, int j) {
+  return bits == 4 ? ((j & 3) * 2 + (j >> 2)) : ((j >> 1) + (j & 1) * 4);
+}
+
+constexpr uint32_t kBf16Hi128 = 0x43434343u;   // high byte of bf16 128 + cc (cc < 128)
+constexpr uint32_t kSelLo = 0x04010400u;       // [x.b0, 0x43, x.b1, 0x43]
+constexpr uint32_t kSelHi = 0x04030402u;       // [x.b2, 0x43, x.b3, 0x43]
+
+template <int D, int BITS, int NB, bool GS>
+struct PackedKeys {
+  static constexpr int NG = D / 32;            // groups per row = MFMA k-steps
+  static constexpr int R = 16 / NG;            // MFMA rows per group
+  static constexpr int LB = D * BITS / 32;     // bytes of one row per lane (D/4 codes)
+  static constexpr int NW = LB / 4;            // 32-bit words per lane
+  static constexpr int CT = 4;                 // 16-token column tiles per wave iteration (64 tokens)
+  typedef typename std::conditional<NW == 4, u32x4, typename std::conditional<NW == 2, u32x2, uint32_t>::type>::type T;
+  typedef typename std::conditional<NG == 4, u32x2, uint32_t>::type SR;
+  struct Regs {
+    T k[CT];                                   // [column tile]
+    SR srow, mrow;                             // scale / min row (NG bf16) of token t + lane
+  };
+  // Buffer resources over one KV head's codes and scale/min rows: every load
+  // is a 32-bit lane offset plus a uniform row offset, and rows at or past S
+  // read as zero (their scores are not stored).
+  __amdgpu_buffer_rsrc_t rk, rsc, rmn;
+  uint32_t koff;                               // lane part of the code offsets (bytes)
+  uint32_t k_row, m_row;                       // row strides (bytes)
+  bf16x8 qa[NB][NG];                           // [row block][k-step]
+  f32x4 qsum[NB];                              // sum of q over the lane's group, rows lg*4 + i
+
+  // 8 bf16 values (raw bits) reordered into operand order
+  static __device__ __forceinline__ bf16x8 permute_q(const uint16_t (&e)[8]) {
+    uint16_t o[8];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int row = min(t + c * 16 + l16, a.S - 1);
-    if constexpr (KM == kKeyFp8) {
-      const uint8_t* p = static_cast<const uint8_t*>(kbase) + (int64_t)row * a.k_ss + lg * 8;
+    for (int j = 0; j < 8; ++j) o[j] = e[packed_perm(BITS, j)];
+    const u32x4 w = {o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16), o[4] | ((uint32_t)o[5] << 16),
+                     o[6] | ((uint32_t)o[7] << 16)};
+    return __builtin_bit_cast(bf16x8, w);
+  }
+
+  __device__ __forceinline__ void init(const ScoreArgs& a, int b, int hk, int hq0, int nh, int lane) {
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int grp = lg * NG / 4;
+    k_row = (uint32_t)a.k_ss;
+    m_row = (uint32_t)a.m_ss * 2;
+    const uint32_t kspan = (uint32_t)((a.S - 1) * a.k_ss + LB * 4);
+    const uint32_t mspan = (uint32_t)(((a.S - 1) * a.m_ss + NG) * 2);
+    rk = buf_rsrc(static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh, kspan);
+    rsc = buf_rsrc(a.ksc + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh, mspan);
+    rmn = buf_rsrc(a.kmn + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh, mspan);
+    koff = (uint32_t)l16 * k_row + lg * LB;
+    const bool in_group = (l16 / R) == grp;
+    const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + lg * (D / 4);
+    if constexpr (GS) {
+      // group sum: rows (group, 0) and (group, 1) hold the bf16 high and low
+      // parts of sum_h q_h; the other rows are zero
+      const int slot = l16 % R;
 #pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = *reinterpret_cast<const u32x2*>(p + kk * 32);
-    } else if constexpr (KM == kKeyBf16) {
-      const uint16_t* p = static_cast<const uint16_t*>(kbase) + (int64_t)row * a.k_ss + lg * 8;
+      for (int kk = 0; kk < NG; ++kk) {
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int h = 0; h < nh; ++h) {
+          const u32x4 raw = ld16(qrow + (int64_t)(hq0 + h) * a.q_sh + kk * 8);
 #pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = ld16(p + kk * 32);
-    } else {
-      // group kk, dims kk*32 + lg*8 .. +8: 4 bytes (4-bit) or 2 bytes (2-bit)
-      constexpr int GB = KM == kKeyP4 ? 16 : 8;          // bytes per group
-      const uint8_t* p = static_cast<const uint8_t*>(kbase) + (int64_t)row * a.k_ss;
+          for (int j = 0; j < 4; ++j) {
+            acc[2 * j] += __uint_as_float(raw[j] << 16);
+            acc[2 * j + 1] += __uint_as_float(raw[j] & 0xFFFF0000u);
+          }
+        }
+        uint16_t e[8];
 #pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) {
-        if constexpr (KM == kKeyP4)
-          r.k[c][kk] = *reinterpret_cast<const uint32_t*>(p + kk * GB + lg * 4);
-        else
-          r.k[c][kk] = *reinterpret_cast<const uint16_t*>(p + kk * GB + lg * 2);
+        for (int j = 0; j < 8; ++j) {
+          const uint16_t hi = f32_to_bf16_bits(acc[j]);
+          const uint16_t lo = f32_to_bf16_bits(acc[j] - bf16_bits_to_f32(hi));
+          e[j] = !in_group ? (uint16_t)0 : (slot == 0 ? hi : (slot == 1 ? lo : (uint16_t)0));
+        }
+        qa[0][kk] = permute_q(e);
       }
-      // D/32 bf16 values per row: 8 bytes at D = 128, 4 bytes at D = 64
-      if constexpr (D == 128) {
-        r.sc[c] = *reinterpret_cast<const u32x2*>(scb + (int64_t)row * a.m_ss);
-        r.mn[c] = *reinterpret_cast<const u32x2*>(mnb + (int64_t)row * a.m_ss);
+    } else {
+      // per head: row m = (group m / R, head m % R) of block nb
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int h = nb * R + l16 % R;
+        const bool live = in_group && h < nh;
+        const uint16_t* qp = qrow + (int64_t)(hq0 + (live ? h : 0)) * a.q_sh;
+#pragma unroll
+        for (int kk = 0; kk < NG; ++kk) {
+          const u32x4 raw = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
+          uint16_t e[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            e[2 * j] = (uint16_t)(raw[j] & 0xFFFFu);
+            e[2 * j + 1] = (uint16_t)(raw[j] >> 16);
+          }
+          qa[nb][kk] = permute_q(e);
+        }
+      }
+    }
+    const u32x4 one = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};   // bf16 1.0 x 8
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NG; ++kk) s = mfma_bf16(qa[nb][kk], __builtin_bit_cast(bf16x8, one), s);
+      qsum[nb] = s;
+    }
+  }
+
+  __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lane, Regs& r) const {
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      const uint32_t row = (uint32_t)(t + c * 16);                  // wave-uniform
+      const uint32_t ko = koff + row * k_row;
+      if constexpr (NW == 4)
+        r.k[c] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0);
+      else if constexpr (NW == 2)
+        r.k[c] = __builtin_amdgcn_raw_buffer_load_b64(rk, ko, 0, 0);
+      else
+        r.k[c] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, 0, 0);
+    }
+    // scale and min rows of the iteration's 64 tokens, one row per lane; the
+    // tile hands each lane its (token, group) entry through LDS
+    const uint32_t so = ((uint32_t)t + lane) * m_row;
+    if constexpr (NG == 4) {
+      r.srow = __builtin_amdgcn_raw_buffer_load_b64(rsc, so, 0, 0);
+      r.mrow = __builtin_amdgcn_raw_buffer_load_b64(rmn, so, 0, 0);
+    } else {
+      r.srow = __builtin_amdgcn_raw_buffer_load_b32(rsc, so, 0, 0);
+      r.mrow = __builtin_amdgcn_raw_buffer_load_b32(rmn, so, 0, 0);
+    }
+  }
+
+  static __device__ __forceinline__ uint32_t word(const T& v, int i) {
+    if constexpr (NW == 1)
+      return v;
+    else
+      return v[i];
+  }
+
+  // the lane's D/4 codes as NG operands of 8 bf16 values 128 + code
+  static __device__ __forceinline__ void operands(const T& v, bf16x8 (&op)[NG]) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+      for (int kk = 0; kk < NG; ++kk) {
+        const uint32_t w = word(v, kk);
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        const u32x4 o = {__builtin_amdgcn_perm(kBf16Hi128, lo, kSelLo), __builtin_amdgcn_perm(kBf16Hi128, lo, kSelHi),
+                         __builtin_amdgcn_perm(kBf16Hi128, hi, kSelLo), __builtin_amdgcn_perm(kBf16Hi128, hi, kSelHi)};
+        op[kk] = __builtin_bit_cast(bf16x8, o);
+      }
+    } else {
+#pragma unroll
+      for (int wi = 0; wi < NG / 2; ++wi) {
+        const uint32_t w = word(v, wi);
+        const uint32_t x0 = w & 0x03030303u, x1 = (w >> 2) & 0x03030303u;
+        const uint32_t x2 = (w >> 4) & 0x03030303u, x3 = (w >> 6) & 0x03030303u;
+        const u32x4 lo = {__builtin_amdgcn_perm(kBf16Hi128, x0, kSelLo), __builtin_amdgcn_perm(kBf16Hi128, x1, kSelLo),
+                          __builtin_amdgcn_perm(kBf16Hi128, x2, kSelLo), __builtin_amdgcn_perm(kBf16Hi128, x3, kSelLo)};
+        const u32x4 hi = {__builtin_amdgcn_perm(kBf16Hi128, x0, kSelHi), __builtin_amdgcn_perm(kBf16Hi128, x1, kSelHi),
+                          __builtin_amdgcn_perm(kBf16Hi128, x2, kSelHi), __builtin_amdgcn_perm(kBf16Hi128, x3, kSelHi)};
+        op[2 * wi] = __builtin_bit_cast(bf16x8, lo);
+        op[2 * wi + 1] = __builtin_bit_cast(bf16x8, hi);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
+                                       int nh, uint32_t* hlds) const {
+    const int l16 = lane & 15, lg = lane >> 4;
+    // per wave: [token][group] words (bf16 scale low, bf16 min high)
+    __shared__ uint32_t sm_lds[kScoreWaves][64 * NG];
+    uint32_t* my = sm_lds[threadIdx.x >> 6];
+    {
+      uint32_t wv[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        uint32_t sw, mw;
+        if constexpr (NG == 4) {
+          sw = r.srow[g >> 1];
+          mw = r.mrow[g >> 1];
+        } else {
+          sw = r.srow;
+          mw = r.mrow;
+        }
+        wv[g] = (g & 1) ? __builtin_amdgcn_perm(mw, sw, 0x07060302u) : __builtin_amdgcn_perm(mw, sw, 0x05040100u);
+      }
+      wave_lds_sync();                         // the previous iteration's reads are done
+      if constexpr (NG == 4)
+        *reinterpret_cast<u32x4*>(my + lane * 4) = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      else
+        *reinterpret_cast<u32x2*>(my + lane * 2) = u32x2{wv[0], wv[1]};
+      wave_lds_sync();
+    }
+    const int grp = lg * NG / 4;
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      bf16x8 op[NG];
+      operands(r.k[c], op);
+      const uint32_t smc = my[(c * 16 + l16) * NG + grp];
+      const float sc = __uint_as_float(smc << 16);
+      const float mn = __uint_as_float(smc & 0xFFFF0000u);
+      const float mn128 = fmaf(-128.f, sc, mn);
+      const int tok = t + c * 16 + l16;
+      if constexpr (GS) {
+        f32x4 g = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NG; ++kk) g = mfma_bf16(qa[0][kk], op[kk], g);
+        // rows (group, 0/1) carry the high/low parts of the summed query; others are zero
+        float v = fmaf(sc, g[0] + g[1], mn128 * (qsum[0][0] + qsum[0][1]));
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        score_emit_sum(a, v * a.scaling, tok, b, hk, lg, hlds);
       } else {
-        r.sc[c] = u32x2{*reinterpret_cast<const uint32_t*>(scb + (int64_t)row * a.m_ss), 0u};
-        r.mn[c] = u32x2{*reinterpret_cast<const uint32_t*>(mnb + (int64_t)row * a.m_ss), 0u};
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          f32x4 g = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < NG; ++kk) g = mfma_bf16(qa[nb][kk], op[kk], g);
+          float p[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[i] = fmaf(sc, g[i], mn128 * qsum[nb][i]);
+          if constexpr (NG == 4) {
+            // lane group lg holds group lg of heads 0..3; reduce-scatter so that it ends with head lg
+            const bool up = lg >= 2;
+            const float k0 = up ? p[2] : p[0], k1 = up ? p[3] : p[1];
+            const float s0 = up ? p[0] : p[2], s1 = up ? p[1] : p[3];
+            const float a0 = k0 + __shfl_xor(s0, 32, 64), a1 = k1 + __shfl_xor(s1, 32, 64);
+            const bool odd = lg & 1;
+            const float tot = (odd ? a1 : a0) + __shfl_xor(odd ? a0 : a1, 16, 64);
+            const int h = nb * R + lg;
+            if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = tot * a.scaling;
+          } else {
+            // lane groups lg and lg^2 hold groups 0 and 1 of heads (lg&1)*4 + i
+            float tot[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tot[i] = p[i] + __shfl_xor(p[i], 32, 64);
+            const int i0 = (lg >> 1) * 2;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int h = nb * R + (lg & 1) * 4 + i0 + u;
+              const float val = i0 ? tot[2 + u] : tot[u];
+              if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = val * a.scaling;
+            }
+          }
+        }
       }
     }
   }
-}
+};
 
-template <int KM>
-__device__ __forceinline__ bf16x8 score_operand(const u32x4& w) { return __builtin_bit_cast(bf16x8, w); }
-template <int KM>
-__device__ __forceinline__ bf16x8 score_operand(const u32x2& w) {
-  const u32x4 b = {fp8x2_to_bf16x2<false>(w[0]), fp8x2_to_bf16x2<true>(w[0]), fp8x2_to_bf16x2<false>(w[1]),
-                   fp8x2_to_bf16x2<true>(w[1])};
-  return __builtin_bit_cast(bf16x8, b);
-}
-// 8 packed codes (4 or 2 bits each, element j at bits j*bits) -> 8 exact bf16 integers
-template <int KM>
-__device__ __forceinline__ bf16x8 score_operand(const uint32_t& w) {
-  constexpr int BITS = KM == kKeyP4 ? 4 : 2;
-  u32x4 b;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float c0 = (float)((w >> (2 * j * BITS)) & ((1u << BITS) - 1u));
-    const float c1 = (float)((w >> ((2 * j + 1) * BITS)) & ((1u << BITS) - 1u));
-    b[j] = (__float_as_uint(c0) >> 16) | (__float_as_uint(c1) & 0xFFFF0000u);
-  }
-  return __builtin_bit_cast(bf16x8, b);
-}
+// ---- driver ---------------------------------------------------------------
 
-__device__ __forceinline__ float bf16_at(const u32x2& v, int i) {
-  const uint32_t w = v[i >> 1];
-  return __uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16));
-}
-
-template <int D, int KM>
-__device__ __forceinline__ void score_tile(const ScoreRegs<D, KM>& r, const bf16x8 (&qa)[D / 32],
-                                           const f32x4 (&qsum)[D / 32], int t, int lane, const ScoreArgs& a, int b,
-                                           int hk, int hq0, int nh, uint32_t* hlds) {
-  const int l16 = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (KM >= kKeyP4) {
-      // per group: scale * (q . code) + min * (sum of q), groups in order
-#pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) {
-        const f32x4 g = mfma_bf16(qa[kk], score_operand<KM>(r.k[c][kk]), f32x4{0.f, 0.f, 0.f, 0.f});
-        const float sc = bf16_at(r.sc[c], kk), mn = bf16_at(r.mn[c], kk);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] += sc * g[i] + mn * qsum[kk][i];
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) s = mfma_bf16(qa[kk], score_operand<KM>(r.k[c][kk]), s);
-    }
-    const int tok = t + c * 16 + l16;
-    if (a.group_sum) {
-      // heads lg*4 + i; group sum in head order, lane groups added in order
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (lg * 4 + i < nh) part += s[i] * a.scaling;
-      const float p1 = __shfl(part, l16 + 16, 64);
-      const float p2 = __shfl(part, l16 + 32, 64);
-      const float p3 = __shfl(part, l16 + 48, 64);
-      float tot = part;
-      if (nh > 4) tot += p1;
-      if (nh > 8) tot += p2;
-      if (nh > 12) tot += p3;
-      if (lg == 0 && tok < a.S) {
-        a.out[(int64_t)b * a.o_sb + (int64_t)hk * a.o_sh + tok] = tot;
-        if (hlds) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h = lg * 4 + i;
-        if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = s[i] * a.scaling;
-      }
-    }
-  }
-}
-
-template <int D, int KM>
+template <class P>
 __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int l16 = lane & 15, lg = lane >> 4;
   const int unit = blockIdx.x / a.parts, part = blockIdx.x - unit * a.parts;
   const int b = unit / (a.Hk * a.HB);
   const int rem = unit - b * a.Hk * a.HB;
   const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
-  const int hq0 = hk * a.G + hb * 16;
-  const int nh = min(16, a.G - hb * 16);
+  const int hq0 = hk * a.G + hb * a.HPU;
+  const int nh = min(a.HPU, a.G - hb * a.HPU);
+  P pol;
+  pol.init(a, b, hk, hq0, nh, lane);
 
-  // Q as the A operand: lane holds Q[h = l16][dims (kk*4 + lg)*8 .. +8]
-  bf16x8 qa[D / 32];
-  {
-    const bool live = l16 < nh;
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + (live ? l16 : 0)) * a.q_sh + lg * 8;
-#pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) qa[kk] = __builtin_bit_cast(bf16x8, live ? ld16(qp + kk * 32) : u32x4{0, 0, 0, 0});
-  }
-
-  const void* kbase =
-      KM == kKeyBf16 ? (const void*)(static_cast<const uint16_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh)
-                     : (const void*)(static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh);
-  const uint16_t* scb = KM >= kKeyP4 ? a.ksc + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh : nullptr;
-  const uint16_t* mnb = KM >= kKeyP4 ? a.kmn + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh : nullptr;
-  // packed keys: sum of q over each 32-dim group, in the output layout (head lg*4+i)
-  f32x4 qsum[D / 32];
-  if constexpr (KM >= kKeyP4) {
-    const u32x4 one = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};   // bf16 1.0 x 8
-#pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk)
-      qsum[kk] = mfma_bf16(qa[kk], __builtin_bit_cast(bf16x8, one), f32x4{0.f, 0.f, 0.f, 0.f});
-  }
   const int t_begin = part * a.tok_per_wg;
   const int t_end = min(t_begin + a.tok_per_wg, a.S);
-  constexpr int STEP = kScoreWaves * kScoreIter;
+  constexpr int STEP = kScoreWaves * 16 * P::CT;
   __shared__ uint32_t hlds_mem[2048];
   uint32_t* hlds = nullptr;
   if (a.hist) {
@@ -215,20 +426,21 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     __syncthreads();
     hlds = hlds_mem;
   }
-  int t = t_begin + w * kScoreIter;
+  constexpr int ITER = 16 * P::CT;
+  int t = t_begin + w * ITER;
   if (t < t_end) {
     // two register sets: the next iteration's rows are in flight while one is scored
-    ScoreRegs<D, KM> r0, r1;
-    score_issue<D, KM>(a, kbase, scb, mnb, t, lane, r0);
+    typename P::Regs r0, r1;
+    pol.issue(a, t, lane, r0);
     while (true) {
       const bool more1 = t + STEP < t_end;
-      score_issue<D, KM>(a, kbase, scb, mnb, more1 ? t + STEP : t, lane, r1);
-      score_tile<D, KM>(r0, qa, qsum, t, lane, a, b, hk, hq0, nh, hlds);
+      pol.issue(a, more1 ? t + STEP : t, lane, r1);
+      pol.tile(a, r0, t, lane, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more1) break;
       const bool more0 = t + STEP < t_end;
-      score_issue<D, KM>(a, kbase, scb, mnb, more0 ? t + STEP : t, lane, r0);
-      score_tile<D, KM>(r1, qa, qsum, t, lane, a, b, hk, hq0, nh, hlds);
+      pol.issue(a, more0 ? t + STEP : t, lane, r0);
+      pol.tile(a, r1, t, lane, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more0) break;
     }
@@ -238,6 +450,20 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     uint32_t* hr = a.hist + ((int64_t)b * a.Hk + hk) * 2048;
     for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64)
       if (hlds_mem[i]) atomicAdd(hr + i, hlds_mem[i]);
+  }
+}
+
+template <int D, int BITS>
+static void launch_packed(const dim3& g, const dim3& blk, hipStream_t st, const ScoreArgs& a, int nb) {
+  if (a.group_sum) {
+    hipLaunchKernelGGL((score_kernel<PackedKeys<D, BITS, 1, true>>), g, blk, 0, st, a);
+  } else if constexpr (D == 128) {
+    if (nb == 1) hipLaunchKernelGGL((score_kernel<PackedKeys<128, BITS, 1, false>>), g, blk, 0, st, a);
+    else if (nb == 2) hipLaunchKernelGGL((score_kernel<PackedKeys<128, BITS, 2, false>>), g, blk, 0, st, a);
+    else hipLaunchKernelGGL((score_kernel<PackedKeys<128, BITS, 4, false>>), g, blk, 0, st, a);
+  } else {
+    if (nb == 1) hipLaunchKernelGGL((score_kernel<PackedKeys<64, BITS, 1, false>>), g, blk, 0, st, a);
+    else hipLaunchKernelGGL((score_kernel<PackedKeys<64, BITS, 2, false>>), g, blk, 0, st, a);
   }
 }
 
@@ -254,7 +480,8 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   if (!q || !k || !out || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
   if (k_mode < kKeyBf16 || k_mode > kKeyP2) return (int)hipErrorInvalidValue;
-  if (k_mode >= kKeyP4 && (!k_scale || !k_min)) return (int)hipErrorInvalidValue;
+  const bool packed = k_mode >= kKeyP4;
+  if (packed && (!k_scale || !k_min)) return (int)hipErrorInvalidValue;
   ScoreArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
@@ -266,7 +493,27 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   a.out = static_cast<float*>(out);
   a.o_sb = o_sb; a.o_sh = o_sh;
   a.hist = static_cast<uint32_t*>(hist);
-  a.Hk = Hk; a.G = Hq / Hk; a.HB = (a.G + 15) / 16; a.S = S;
+  a.Hk = Hk; a.G = Hq / Hk; a.S = S;
+  // packed keys: heads per row block R = 16 / (D/32); 1, 2 or 4 blocks per unit share the code widening
+  int nb = 1;
+  if (packed && !group_sum) {
+    const int R = 16 / (D / 32), nbmax = 16 / R;
+    nb = (a.G + R - 1) / R;
+    nb = nb <= 1 ? 1 : (nb <= 2 ? 2 : 4);
+    if (nb > nbmax) nb = nbmax;
+    a.HPU = R * nb;
+  } else {
+    a.HPU = 16;                  // bf16/fp8 keys; packed group sums fold every head of the group into q
+  }
+  if (packed) {
+    // one KV head's codes and scale/min rows are addressed with 32-bit offsets
+    const int64_t kspan = (int64_t)(S - 1) * k_ss + D * (k_mode == kKeyP4 ? 4 : 2) / 8;
+    const int64_t mspan = ((int64_t)(S - 1) * m_ss + D / 32) * 2;
+    // (a wave's last iteration reads up to 63 rows past S - 1)
+    if (k_ss <= 0 || m_ss <= 0 || kspan + 64L * k_ss >= (1LL << 32) || mspan + 128L * m_ss >= (1LL << 32))
+      return (int)hipErrorNotSupported;
+  }
+  a.HB = (a.G + a.HPU - 1) / a.HPU;
   a.group_sum = group_sum ? 1 : 0;
   if (a.group_sum && a.G > 16) return (int)hipErrorNotSupported;
   if (a.hist && !a.group_sum) return (int)hipErrorInvalidValue;
@@ -274,7 +521,7 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   const long units = (long)B * Hk * a.HB;
   // about 8 workgroups per CU in total, each a multiple of one iteration of all waves
   const long target = 8L * device_cu_count();
-  const int step = kScoreWaves * kScoreIter;
+  const int step = kScoreWaves * 64;
   long per = ((long)S * units + target - 1) / target;
   per = (per + step - 1) / step * step;
   if (per < step) per = step;
@@ -285,23 +532,21 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   if (grid > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 g((unsigned)grid), blk(kScoreWaves * 64);
-#define SCORE_LAUNCH(DD, KMV) hipLaunchKernelGGL((score_kernel<DD, KMV>), g, blk, 0, st, a)
   if (D == 128) {
     switch (k_mode) {
-      case kKeyBf16: SCORE_LAUNCH(128, kKeyBf16); break;
-      case kKeyFp8: SCORE_LAUNCH(128, kKeyFp8); break;
-      case kKeyP4: SCORE_LAUNCH(128, kKeyP4); break;
-      default: SCORE_LAUNCH(128, kKeyP2); break;
+      case kKeyBf16: hipLaunchKernelGGL((score_kernel<DenseKeys<128, false>>), g, blk, 0, st, a); break;
+      case kKeyFp8: hipLaunchKernelGGL((score_kernel<DenseKeys<128, true>>), g, blk, 0, st, a); break;
+      case kKeyP4: launch_packed<128, 4>(g, blk, st, a, nb); break;
+      default: launch_packed<128, 2>(g, blk, st, a, nb); break;
     }
   } else {
     switch (k_mode) {
-      case kKeyBf16: SCORE_LAUNCH(64, kKeyBf16); break;
-      case kKeyFp8: SCORE_LAUNCH(64, kKeyFp8); break;
-      case kKeyP4: SCORE_LAUNCH(64, kKeyP4); break;
-      default: SCORE_LAUNCH(64, kKeyP2); break;
+      case kKeyBf16: hipLaunchKernelGGL((score_kernel<DenseKeys<64, false>>), g, blk, 0, st, a); break;
+      case kKeyFp8: hipLaunchKernelGGL((score_kernel<DenseKeys<64, true>>), g, blk, 0, st, a); break;
+      case kKeyP4: launch_packed<64, 4>(g, blk, st, a, nb); break;
+      default: launch_packed<64, 2>(g, blk, st, a, nb); break;
     }
   }
-#undef SCORE_LAUNCH
   return (int)hipGetLastError();
 }
 

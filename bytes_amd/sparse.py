@@ -259,22 +259,34 @@ def sparse_decode_scalar(q, k_score_or_packed, scale, zero, k_val, v_val, frac, 
 
 
 def token_topk_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float, *,
-                      k_score: torch.Tensor = None):
+                      k_score: torch.Tensor = None, score_scale: torch.Tensor = None,
+                      score_zero: torch.Tensor = None, score_bits: int = None):
     """Group-shared token top-k decode: group-summed fp32 scores per KV head,
     the kb best tokens per (b, KV head), attention of every query head of the
     group over them.  `k_score` (default k) holds the keys the selection scores
-    use, e.g. a float8_e4m3fn copy of the cache.  Returns (out [B,H_q,1,D]
-    bf16, idx [B,H_k,kb] int32 by ascending token index)."""
+    use: a float8_e4m3fn copy of the cache, or packed 4/2-bit codes (uint8,
+    with score_scale, score_zero and score_bits as quantize_and_pack_score_keys
+    gives them).  Returns (out [B,H_q,1,D] bf16, idx [B,H_k,kb] int32 by
+    ascending token index)."""
     ks = k if k_score is None else k_score
-    B, Hq, Hk, S, D = _qk_shapes(q, ks)
-    if tuple(ks.shape) != tuple(k.shape):
-        raise ValueError(f"k_score {tuple(ks.shape)} does not match k {tuple(k.shape)}")
+    packed = None
+    if ks.dtype == torch.uint8:
+        if score_bits not in (4, 2) or score_scale is None or score_zero is None:
+            raise ValueError("packed score keys need score_bits 4 or 2 with score_scale and score_zero")
+        packed = (score_scale, score_zero, score_bits)
+        B, Hq, Hk, S, D = _qk_shapes(q, ks, k_dim=ks.shape[-1] * 8 // score_bits)
+        if tuple(ks.shape[:3]) != tuple(k.shape[:3]) or D != k.shape[-1]:
+            raise ValueError(f"packed score keys {tuple(ks.shape)} do not match k {tuple(k.shape)}")
+    else:
+        B, Hq, Hk, S, D = _qk_shapes(q, ks)
+        if tuple(ks.shape) != tuple(k.shape):
+            raise ValueError(f"k_score {tuple(ks.shape)} does not match k {tuple(k.shape)}")
     if B * Hk <= TOPK_HIST_ROWS:
         # the score kernel also counts the top-k digit histogram, in the top-k workspace
         ws = _topk_workspace(q.device, B * Hk, S, kb)
-        s = _score(q, ks, scaling, group_sum=True, hist=ptr(ws))
+        s = _score(q, ks, scaling, group_sum=True, hist=ptr(ws), packed=packed)
         idx = _topk(s, kb, sorted=False, ws=ws, hist_ready=True)
     else:
-        s = group_scores(q, ks, scaling)
+        s = _score(q, ks, scaling, group_sum=True, packed=packed)
         idx = topk_indices(s, kb, sorted=False)
     return sparse_gather_attn(q, k, v, idx, scaling), idx

@@ -48,15 +48,16 @@ def test_pack_bit_exact(dev, bits, dtype, B, Hk, S, D):
 @pytest.mark.parametrize("D", [128, 64])
 def test_every_position_scores_exactly(dev, bits, D):
     """One-hot queries pick one key element each: the score is code*scale + min,
-    which is exact in fp32 (an 8-bit by <= 4-bit product plus one rounding), so
-    it must equal the oracle's dequantized key bit for bit.  Pins the code
+    one rounding of an exact value in fp32 (an 8-bit by <= 4-bit product plus
+    min), so it must equal the oracle's dequantized key bit for bit.  Pins the code
     layout (element c at bits ((c % (8/bits)) * bits) of byte c // (8/bits))
     and the group of each scale/min."""
     S = 256
     g = torch.Generator().manual_seed(bits * 1000 + D)
     packed = torch.randint(0, 256, (1, 1, S, D * bits // 8), generator=g, dtype=torch.uint8)
     scale = (torch.rand(1, 1, S, D // 32, generator=g) * 0.5).to(torch.bfloat16)
-    zero = (torch.randn(1, 1, S, D // 32, generator=g)).to(torch.bfloat16)
+    z = torch.randn(1, 1, S, D // 32, generator=g)
+    zero = (z.sign() * (z.abs() + 0.05)).to(torch.bfloat16)      # |min| >= 0.05: min - 128*scale is exact in fp32
     q = torch.eye(D, dtype=torch.bfloat16).reshape(1, D, 1, D)
     s = AK.sparse_score_packed(q.to(dev), packed.to(dev), scale.to(dev), zero.to(dev), 1.0, score_bits=bits)
     ref = R.sparse_score_packed(q, packed, scale, zero, 1.0, score_bits=bits)
@@ -125,3 +126,26 @@ def test_packed_argument_errors(dev):
         AK.sparse_score_packed(q, p, s[..., :2], s, 1.0, score_bits=4)
     with pytest.raises(ValueError):
         AK.quantize_and_pack_score_keys(torch.zeros(1, 1, 4, 128, device=dev, dtype=torch.bfloat16), 3, 32)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("B,Hq,Hk,S,kb,D", [(2, 6, 2, 4096, 256, 128), (1, 24, 8, 3001, 100, 128),
+                                            (17, 24, 8, 1024, 64, 128), (2, 32, 2, 2000, 128, 64)])
+def test_token_topk_packed_score_keys(dev, bits, B, Hq, Hk, S, kb, D):
+    """Group-shared token top-k with packed selection keys: group-summed scores
+    against the oracle on the dequantized keys, indices bit-exact given the same
+    scores, attention over the exact bf16 cache (B*Hk = 136 rows, above the
+    fused-histogram limit of 128, takes the separate histogram pass)."""
+    x = W.dense(B, Hq, Hk, D, S, seed=S + bits)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    p, s, z = AK.quantize_and_pack_score_keys(k, bits, 32)
+    out, idx = SP.token_topk_decode(q, k, v, kb, x["scale"], k_score=p, score_scale=s, score_zero=z,
+                                    score_bits=bits)
+    g = SP._score(q, p, x["scale"], group_sum=True, packed=(s, z, bits)).cpu()
+    kd = R.score_keys_dequant(p.cpu(), s.cpu(), z.cpu(), bits, 32)
+    assert (g - R.group_scores(x["q"], kd, x["scale"])).abs().max() <= SCORE_TOL
+    ridx = R.topk_indices(g, kb, sorted_by_score=False)
+    assert torch.equal(idx.cpu().long(), ridx)
+    gi = ridx.unsqueeze(-1).expand(B, Hk, kb, D)
+    _check(out, R.decode_attn(x["q"], torch.gather(x["k"], 2, gi), torch.gather(x["v"], 2, gi), scale=x["scale"]),
+           f"token top-k {bits}-bit score keys B{B} S{S} kb{kb} D{D}")
