@@ -25,8 +25,9 @@
 //    turn into exact fp16 codes; one v_pk_fma_f16 applies scale and zero;
 //  * S^T = K_dq Q^T and O^T += V_dq^T P^T run on v_mfma_f32_16x16x32_f16 with
 //    fp32 accumulation and an fp32 online softmax.
-// The bf16 residual window is handled by the last split's waves with the dense
-// tile loop, ahead of that split's quantized chunk.
+// The bf16 residual window runs with the dense tile loop, as one extra split
+// per unit when the grid stays resident (its 2*R*D*2 bytes then do not
+// lengthen a quantized split), else ahead of the last split's chunk.
 #include "dense_tile.h"
 
 namespace bytes_amd {
@@ -122,6 +123,7 @@ struct KiviArgs {
   const uint16_t* vr;
   int64_t kr_sb, kr_sh, kr_ss, vr_sb, vr_sh, vr_ss;
   int Hk, G, HB, Sq, R, chunk, nsq;
+  int rsplit;               // 1: the residual window is split nsq of its own
   float scale_log2;
   SplitKOut o;
 };
@@ -398,10 +400,14 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The bf16 residual window [0, R) rides on the last split, ahead of its
-  // quantized chunk: dense tiles first, then (2-bit) the accumulator is moved
-  // to the 2-bit value layout so the quantized tiles continue the same state.
-  if (split == a.o.nsplit - 1 && a.R > 0) {
+  // The bf16 residual window [0, R) runs with the dense tile loop either as a
+  // split of its own (a.rsplit: split nsq, when the extra workgroups still fit
+  // on the device at once) or ahead of the last split's quantized chunk; then
+  // (2-bit) the accumulator moves to the 2-bit value layout so the quantized
+  // tiles continue the same state.
+  const bool resid_only = a.rsplit && a.R > 0 && split == a.nsq;
+  const bool resid_first = !a.rsplit && a.R > 0 && split == a.o.nsplit - 1;
+  if (resid_only || resid_first) {
     bf16x8 qb[D / 32];
     load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
     const uint16_t* kbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
@@ -409,7 +415,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
     dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, 0, a.R, w, lane, a.scale_log2, qb, wbuf, m_run, l_run,
                        acc);
-    if (BITS == 2) {
+    if (BITS == 2 && resid_first) {
       static_assert(D * 16 * 4 <= DenseCfg<D>::WAVE, "relayout buffer fits the wave's tile buffers");
       float* buf = reinterpret_cast<float*>(wbuf);
       wave_lds_sync();
@@ -428,7 +434,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
 
   const int Sq = a.Sq;
   const int t_begin = split * a.chunk;
-  const int t_end = min(t_begin + a.chunk, Sq);
+  const int t_end = resid_only ? t_begin : min(t_begin + a.chunk, Sq);
   if (t_begin < t_end) {
     const int g_lo = t_begin >> 5;
     const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
@@ -533,10 +539,12 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     }
   }
   splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
-                                 nh, BITS == 2 ? kDmapKivi2 : kDmapDense);
+                                 nh, (BITS == 2 && !resid_only) ? kDmapKivi2 : kDmapDense);
 }
 
-static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq) {
+// rsplit: the residual gets a split of its own when that keeps the whole grid
+// resident at two workgroups per CU; otherwise it rides on the last split.
+static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq, int* rsplit) {
   const int step = kKiviWaves * kKiviTile;
   int c;
   if (chunk_req > 0) {
@@ -550,7 +558,8 @@ static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int*
   if (c > kKiviChunkMax) c = kKiviChunkMax;
   *chunk = c;
   *nsq = Sq > 0 ? (Sq + c - 1) / c : 0;
-  (void)R;
+  const long resident = 2L * device_cu_count();
+  *rsplit = R > 0 && (*nsq == 0 || (long)(*nsq + 1) * units <= resident || (long)*nsq * units > resident);
 }
 
 }  // namespace bytes_amd
@@ -597,8 +606,9 @@ int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
   int chunk, nsq;
-  kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq);
-  *bytes = splitk_workspace_bytes(units, nsq > 0 ? nsq : 1, D);
+  int rsplit;
+  kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq, &rsplit);
+  *bytes = splitk_workspace_bytes(units, nsq + rsplit, D);
   return 0;
 }
 
@@ -634,8 +644,8 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.vr_sb = vr_sb; a.vr_sh = vr_sh; a.vr_ss = vr_ss;
   a.Hk = Hk; a.G = G; a.HB = HB; a.Sq = Sq; a.R = R;
   a.scale_log2 = scale * kLog2e;
-  kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq);
-  const int ns = a.nsq > 0 ? a.nsq : 1;
+  kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq, &a.rsplit);
+  const int ns = a.nsq + a.rsplit;                       // quantized chunks, then the residual's own split
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
   a.o.out = out;
