@@ -83,6 +83,23 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,         # kidx (b, h, s), vidx (b, h, s), vcb head stride
         c_i64, c_i64, c_i64, c_i64, c_i64,                       # v (b, h, s), out (b, h)
         c_f32, c_int, c_vp, c_sz, c_vp),                         # scale, chunk, workspace, bytes, stream
+    "bytes_pq_lut_decode_attn": (
+        c_vp, c_i64, c_i64,                                      # lut, strides (b, h)
+        c_vp, c_i64, c_i64, c_i64,                               # kidx, strides (batch|block, h, row)
+        c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,                  # vidx + strides, vcb, vcb head stride
+        c_vp, c_int, c_i64, c_i64, c_i64,                        # v, v is fp8, strides
+        c_vp, c_int, c_i64, c_i64, c_i64,                        # k_out, dtype, strides
+        c_vp, c_int, c_i64, c_i64, c_int,                        # q_out, dtype, strides (b, h), C
+        c_vp, c_i64, c_vp, c_int, c_int,                         # block table, row stride, lengths, bs, blocks
+        c_vp, c_int, c_i64, c_i64,                               # out, dtype, strides (b, h)
+        c_int, c_int, c_int, c_int, c_int, c_int,                # B, Hq, Hk, S, D, K
+        c_f32, c_int, c_vp, c_sz, c_vp),                         # scale, chunk, workspace, bytes, stream
+    "bytes_pq_lut_scores": (
+        c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64,           # lut + strides, kidx + strides
+        c_vp, c_int, c_i64, c_i64, c_i64,                        # k_out, dtype, strides
+        c_vp, c_int, c_i64, c_i64, c_int,                        # q_out, dtype, strides, C
+        c_vp, c_i64, c_i64,                                      # out [B, Hq, S], strides (b, h)
+        c_int, c_int, c_int, c_int, c_int, c_int, c_vp),         # B, Hq, Hk, S, D, K, stream
     "bytes_pq_build_lut": (c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_f32, c_vp),
     "bytes_pq_encode": (c_vp, c_int, c_int, c_i64, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
     "bytes_pq_decode_vectors": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),

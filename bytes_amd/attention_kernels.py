@@ -89,4 +89,6 @@ def decode_attn_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 # Sparse decode operators of the same module (src/attention_kernels.py:1037-1263).
 from .sparse import (quantize_and_pack_score_keys, sparse_decode_scalar, sparse_gather_attn,  # noqa: E402,F401
                      sparse_score_packed, sparse_score_scalar, topk_indices)
-from .pq import decode_attn_dequant, decode_attn_pq_lut, decode_attn_pq_lut_kv  # noqa: E402,F401
+from .pq import (decode_attn_dequant, decode_attn_pq_lut, decode_attn_pq_lut_asym,  # noqa: E402,F401
+                 decode_attn_pq_lut_kv, paged_attn_pq_lut_asym, paged_attn_pq_lut_kv, sparse_decode_pq_lut,
+                 sparse_score_pq_lut_asym)

@@ -4,6 +4,10 @@
 //   decode_attn_pq_lut_kv  :397-500  LUT-scored keys, codebook-reconstructed values
 //   decode_attn_pq_lut     :301-392  LUT-scored keys, dense V
 //   decode_attn_dequant    :187-296  codebook-reconstructed keys, dense V
+//   paged_attn_pq_lut_kv   :505-622  the LUT-KV decode over a paged cache
+//   decode_attn_pq_lut_asym :625-753 LUT scores + exact outlier channels, bf16/fp8 V
+//   paged_attn_pq_lut_asym :756-906  the same over a paged cache
+//   sparse_score_pq_lut_asym :909-984 per-key LUT + outlier scores (no softmax)
 // and, on the setup side, the LUT precompute of benchmarks/test_correctness.py
 // :272-273, ProductQuantizer.quantize/.dequantize (src/quantization.py:160-226)
 // and the k-means of src/quantization.py:102-132.
@@ -22,6 +26,15 @@
 // online softmax, rebuilds the V tile in LDS (16-byte codebook rows selected by
 // the value codes, or the bf16 V rows themselves), and accumulates O^T += V^T P^T
 // on MFMA, as the dense kernel does.
+//
+// Paged caches (block_table [B, max_blocks] int32, context_lens [B] int32):
+// token t of sequence b is row t % bs of block block_table[b][t / bs]; the
+// block index takes the place of the batch index in every cache stride.  The
+// grid covers max_blocks * bs tokens and each workgroup stops at its
+// sequence's length.  Outlier channels add sum_c q_out[b,h,c] * k_out[row,c]
+// (fp32) to each LUT score; fp8 values are widened to bf16 while staged.
+#include <string.h>
+
 #include "dense_tile.h"
 
 namespace bytes_amd {
@@ -29,6 +42,7 @@ namespace bytes_amd {
 constexpr int kPqWaves = 4;
 constexpr int kPqHeads = 4;     // query heads per unit
 constexpr int kPqKMax = 256;    // codewords per subspace
+constexpr int kPqOutMax = 16;   // outlier channels
 
 struct PqArgs {
   const float* lut;          // mode LUT: [B, Hq, M, K]
@@ -43,12 +57,43 @@ struct PqArgs {
   int64_t vi_sb, vi_sh, vi_ss;
   const _Float16* vcb;
   int64_t vcb_sh;
-  const uint16_t* v;         // dense V [B, Hk, S, D] bf16
+  const void* v;             // dense V [B, Hk, S, D] bf16 or fp8 e4m3fn
   int64_t v_sb, v_sh, v_ss;
-  int Hk, G, HG, S, K, chunk;
+  const void* kout;          // outlier keys [B, Hk, S, C] (bf16 / fp16 / fp32: ko_dt 0 / 1 / 2)
+  int64_t ko_sb, ko_sh, ko_ss;
+  const void* qout;          // outlier queries [B, Hq, C]
+  int64_t qo_sb, qo_sh;
+  int ko_dt, qo_dt, C;
+  const int* btab;           // paged: block table [B, *] (row stride bt_sb), null: contiguous cache
+  const int* clens;          // paged: sequence lengths [B]
+  int64_t bt_sb;
+  int bs, nblk;              // paged: rows per block, blocks in the cache
+  int Hk, G, HG, S, K, chunk;   // S: tokens (paged: max_blocks * bs)
   float scale_log2;
   SplitKOut o;
 };
+
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  return dt == 0 ? bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i])
+                 : (dt == 1 ? (float)static_cast<const _Float16*>(p)[i] : static_cast<const float*>(p)[i]);
+}
+
+// Cache block and row of token t of sequence b.
+__device__ __forceinline__ void pq_locate(const PqArgs& a, int b, int t, int& blk, int& row) {
+  if (a.btab) {
+    const int q = t / a.bs;
+    blk = min(max(a.btab[(int64_t)b * a.bt_sb + q], 0), a.nblk - 1);
+    row = t - q * a.bs;
+  } else {
+    blk = b;
+    row = t;
+  }
+}
+
+// Tokens of sequence b.
+__device__ __forceinline__ int pq_len(const PqArgs& a, int b) {
+  return a.btab ? max(0, min(a.clens[b], a.S)) : a.S;
+}
 
 template <int D, bool QV>
 struct PqCfg {
@@ -56,50 +101,37 @@ struct PqCfg {
   static constexpr int LUT = kPqHeads * M * kPqKMax * 4;          // fp32 LUTs of the unit's heads
   static constexpr int VCB = QV ? M * kPqKMax * 8 * 2 : 0;         // fp16 value codebook
   static constexpr int TILE = kTile * D * 2;                        // one wave's V tile
-  static constexpr int kSmem = LUT + VCB + kPqWaves * TILE;
+  static constexpr int QOUT = QV ? 0 : kPqHeads * kPqOutMax * 4;    // fp32 outlier queries (dense-V modes)
+  static constexpr int kSmem = LUT + VCB + kPqWaves * TILE + QOUT;
 };
 
-// Raw 16-bit V tile loads (dense V) for rows t0 .. t0+31 (clamped to S-1).
-template <int D>
-__device__ __forceinline__ void pq_issue_dense_v(const uint16_t* vbase, int64_t v_ss, int S, int t0, int lane,
-                                                 u32x4 (&r)[DenseCfg<D>::CPL]) {
-  using C = DenseCfg<D>;
-#pragma unroll
-  for (int i = 0; i < C::CPL; ++i) {
-    const int p = lane + 64 * i;
-    const int rr = p / C::CPR, pos = p - rr * C::CPR;
-    r[i] = ld16(vbase + (int64_t)min(t0 + rr, S - 1) * v_ss + pos * 8);
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void pq_stage_dense_v(int lane, const u32x4 (&r)[DenseCfg<D>::CPL], char* vst) {
-  using C = DenseCfg<D>;
-#pragma unroll
-  for (int i = 0; i < C::CPL; ++i) {
-    const int p = lane + 64 * i;
-    const int rr = p / C::CPR, pos = p - rr * C::CPR;
-    *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, pos) * 16) = r[i];
-  }
-}
-
-// Codes of one tile, in registers:
+// Codes and rows of one 32-token tile, in registers:
 //  kc: the M key codes of tile row lane % 32 (every lane scores whole rows)
 //  vc[i]: value code of row p / M, subspace p % M, for staging chunk p = lane + 64*i
-template <int D, bool QV>
+//  vd[i]: dense V chunk p = lane + 64*i (row p / chunks-per-row), bf16 or fp8
+//  ko: the outlier keys of tile row lane % 32
+template <int D, bool QV, bool VF8, bool OUT>
 struct PqRegs {
+  static constexpr int CPR = VF8 ? D / 16 : D / 8;   // 16-byte V chunks per row
+  static constexpr int CPL = kTile * CPR / 64;
   u32x4 kc;
   uint32_t vc[QV ? 8 : 1];
-  u32x4 vd[QV ? 1 : DenseCfg<D>::CPL];
+  u32x4 vd[QV ? 1 : CPL];
+  float ko[OUT ? kPqOutMax : 1];
 };
 
-template <int D, bool QV>
-__device__ __forceinline__ void pq_issue(const PqArgs& a, const uint8_t* kib, const uint8_t* vib, const uint16_t* vbase,
-                                         int t0, int lane, PqRegs<D, QV>& r) {
+// Issue the tile at t0 (rows clamped to len - 1).  Each lane locates its own
+// row lane % 32; rows of the V chunks come from the owning lane by shuffle.
+template <int D, bool QV, bool VF8, bool OUT>
+__device__ __forceinline__ void pq_issue(const PqArgs& a, int b, const uint8_t* kih, const uint8_t* vih,
+                                         const char* vh, const char* koh, int len, int t0, int lane,
+                                         PqRegs<D, QV, VF8, OUT>& r) {
+  using R = PqRegs<D, QV, VF8, OUT>;
   constexpr int M = D / 8;
+  int blk, row;
+  pq_locate(a, b, min(t0 + (lane & 31), len - 1), blk, row);
   {
-    const int t = min(t0 + (lane & 31), a.S - 1);
-    const uint8_t* p = kib + (int64_t)t * a.ki_ss;
+    const uint8_t* p = kih + (int64_t)blk * a.ki_sb + (int64_t)row * a.ki_ss;
     if constexpr (M == 16) {
       r.kc = ld16(p);
     } else {
@@ -107,16 +139,46 @@ __device__ __forceinline__ void pq_issue(const PqArgs& a, const uint8_t* kib, co
       r.kc = u32x4{h[0], h[1], 0u, 0u};
     }
   }
+  if constexpr (OUT) {
+    const int64_t o = (int64_t)blk * a.ko_sb + (int64_t)row * a.ko_ss;
+#pragma unroll
+    for (int c = 0; c < kPqOutMax; ++c) r.ko[c] = c < a.C ? load_any(koh, a.ko_dt, o + c) : 0.f;
+  }
   if constexpr (QV) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int p = lane + 64 * i;
       const int rr = p / M, j = p - (p / M) * M;
-      const int t = min(t0 + rr, a.S - 1);
-      r.vc[i] = (rr < kTile) ? vib[(int64_t)t * a.vi_ss + j] : 0u;
+      const int bq = __shfl(blk, rr & 31, 64), rq = __shfl(row, rr & 31, 64);
+      r.vc[i] = (rr < kTile) ? vih[(int64_t)bq * a.vi_sb + (int64_t)rq * a.vi_ss + j] : 0u;
     }
   } else {
-    pq_issue_dense_v<D>(vbase, a.v_ss, a.S, t0, lane, r.vd);
+    constexpr int ES = VF8 ? 1 : 2;
+#pragma unroll
+    for (int i = 0; i < R::CPL; ++i) {
+      const int p = lane + 64 * i;
+      const int rr = p / R::CPR, pos = p - rr * R::CPR;
+      const int bq = __shfl(blk, rr, 64), rq = __shfl(row, rr, 64);
+      r.vd[i] = ld16(vh + ((int64_t)bq * a.v_sb + (int64_t)rq * a.v_ss) * ES + pos * 16);
+    }
+  }
+}
+
+template <int D, bool QV, bool VF8, bool OUT>
+__device__ __forceinline__ void pq_stage_dense_v(int lane, const PqRegs<D, QV, VF8, OUT>& r, char* vst) {
+  using R = PqRegs<D, QV, VF8, OUT>;
+#pragma unroll
+  for (int i = 0; i < R::CPL; ++i) {
+    const int p = lane + 64 * i;
+    const int rr = p / R::CPR, pos = p - rr * R::CPR;
+    if constexpr (VF8) {
+      u32x4 v0, v1;
+      fp8x16_to_bf16(r.vd[i], v0, v1);
+      *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, 2 * pos) * 16) = v0;
+      *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, 2 * pos + 1) * 16) = v1;
+    } else {
+      *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, pos) * 16) = r.vd[i];
+    }
   }
 }
 
@@ -124,10 +186,10 @@ __device__ __forceinline__ void pq_issue(const PqArgs& a, const uint8_t* kib, co
 // slots l/32 and l/32 + 2 (subspaces in order), the wave passes them through
 // its tile buffer into the score-MFMA layout (head l%16, rows blk*16 + lg*4 + i),
 // then the V tile is built in the same buffer and the softmax/PV step runs.
-template <int D, bool QV>
-__device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV>& r, uint32_t vmask, int lane, int nh,
-                                        const float* lut, const char* vcb, char* vst, float& m_run, float& l_run,
-                                        f32x4 (&acc)[D / 16]) {
+template <int D, bool QV, bool VF8, bool OUT>
+__device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV, VF8, OUT>& r, uint32_t vmask, int lane,
+                                        int nh, const float* lut, const char* vcb, const float* qo, char* vst,
+                                        float& m_run, float& l_run, f32x4 (&acc)[D / 16]) {
   constexpr int M = D / 8;
   const int l16 = lane & 15, lg = lane >> 4;
   float* sc_lds = reinterpret_cast<float*>(vst);   // [kPqHeads][32]
@@ -141,6 +203,12 @@ __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV>& r,
       for (int j = 0; j < M; ++j) {
         const uint32_t code = (r.kc[j >> 2] >> ((j & 3) * 8)) & 0xFFu;
         sc += lh[j * kPqKMax + code];
+      }
+      if constexpr (OUT) {
+        float so = 0.f;
+#pragma unroll
+        for (int c = 0; c < kPqOutMax; ++c) so += qo[h * kPqOutMax + c] * r.ko[c];   // zero past C
+        sc += so;
       }
       sc_lds[h * kTile + (lane & 31)] = sc;
     }
@@ -165,7 +233,7 @@ __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV>& r,
       }
     }
   } else {
-    pq_stage_dense_v<D>(lane, r.vd, vst);
+    pq_stage_dense_v<D>(lane, r, vst);
   }
   wave_lds_sync();
   tile_softmax_pv<D, QV>(s, l16 < nh ? vmask : 0u, a.scale_log2, lane, vst, m_run, l_run, acc);
@@ -190,7 +258,7 @@ __device__ __forceinline__ void stage_chunks(int n, SRC src, DST dst) {
   }
 }
 
-template <int D, bool BUILD_LUT, bool QV>
+template <int D, bool BUILD_LUT, bool QV, bool VF8, bool OUT>
 __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   using C = PqCfg<D, QV>;
   constexpr int M = D / 8;
@@ -239,6 +307,14 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
           return lut + (h * M + j) * kPqKMax + c4 * 4;
         });
   }
+  float* qo = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB + kPqWaves * C::TILE);
+  if constexpr (OUT) {
+    for (int e = threadIdx.x; e < kPqHeads * kPqOutMax; e += kPqWaves * 64) {
+      const int h = e / kPqOutMax, c = e - h * kPqOutMax;
+      qo[e] = (h < nh && c < a.C) ? load_any(a.qout, a.qo_dt, (int64_t)b * a.qo_sb + (int64_t)(hq0 + h) * a.qo_sh + c)
+                                  : 0.f;
+    }
+  }
   if constexpr (QV) {
     const _Float16* cb = a.vcb + (int64_t)hk * a.vcb_sh;
     stage_chunks(
@@ -254,25 +330,98 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const int len = pq_len(a, b);
   const int t_begin = split * a.chunk;
-  const int t_end = min(t_begin + a.chunk, a.S);
-  const uint8_t* kib = a.kidx + (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh;
-  const uint8_t* vib = QV ? a.vidx + (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh : nullptr;
-  const uint16_t* vbase = QV ? nullptr : a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  const int t_end = min(t_begin + a.chunk, len);
+  // per-head bases; the row offsets (batch or block, row) are added per token
+  const uint8_t* kih = a.kidx + (int64_t)hk * a.ki_sh;
+  const uint8_t* vih = QV ? a.vidx + (int64_t)hk * a.vi_sh : nullptr;
+  const char* vh = QV ? nullptr : static_cast<const char*>(a.v) + (int64_t)hk * a.v_sh * (VF8 ? 1 : 2);
+  const char* koh = OUT ? static_cast<const char*>(a.kout) + (int64_t)hk * a.ko_sh * (a.ko_dt == 2 ? 4 : 2)
+                        : nullptr;
   char* vst = smem_raw + C::LUT + C::VCB + w * C::TILE;
   constexpr int STEP = kPqWaves * kTile;
   int t = t_begin + w * kTile;
-  PqRegs<D, QV> r;
-  if (t < t_end) pq_issue<D, QV>(a, kib, vib, vbase, t, lane, r);
+  PqRegs<D, QV, VF8, OUT> r;
+  if (t < t_end) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t, lane, r);
   __syncthreads();
   for (; t < t_end; t += STEP) {
-    PqRegs<D, QV> cur = r;
-    if (t + STEP < t_end) pq_issue<D, QV>(a, kib, vib, vbase, t + STEP, lane, r);
+    PqRegs<D, QV, VF8, OUT> cur = r;
+    if (t + STEP < t_end) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t + STEP, lane, r);
     wave_lds_sync();
-    pq_tile<D, QV>(a, cur, range_mask(t, t_end), lane, nh, lut, vcb, vst, m_run, l_run, acc);
+    pq_tile<D, QV, VF8, OUT>(a, cur, range_mask(t, t_end), lane, nh, lut, vcb, qo, vst, m_run, l_run, acc);
   }
   splitk_epilogue<D, kPqWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0, nh,
                                kDmapDense);
+}
+
+// ============================================================================
+// Per-key LUT scores: out[b, h, t] = sum_j lut[b, h, j, k_idx[t, j]] (j in
+// order) + sum_c q_out[b, h, c] * k_out[t, c] (C > 0), fp32.  A workgroup
+// stages the LUTs of one (b, kv head, group of <= 4 query heads) in LDS and
+// scores a run of tokens, one token per thread.
+// ============================================================================
+constexpr int kPqScoreThreads = 256;
+
+template <int M, bool OUT>
+__global__ __launch_bounds__(kPqScoreThreads, 2) void pq_score_kernel(PqArgs a, float* out, int64_t o_sb,
+                                                                      int64_t o_sh, int parts) {
+  __shared__ __attribute__((aligned(16))) float lut[kPqHeads * M * kPqKMax];
+  __shared__ float qo[kPqHeads * kPqOutMax];
+  const int unit = blockIdx.x / parts, part = blockIdx.x - unit * parts;
+  const int b = unit / (a.Hk * a.HG);
+  const int rem = unit - b * a.Hk * a.HG;
+  const int hk = rem / a.HG, hg = rem - (rem / a.HG) * a.HG;
+  const int hq0 = hk * a.G + hg * kPqHeads;
+  const int nh = min(kPqHeads, a.G - hg * kPqHeads);
+  const int K = a.K, K4 = K / 4;
+  for (int e = threadIdx.x; e < nh * M * K4; e += kPqScoreThreads) {
+    const int h = e / (M * K4), r2 = e - h * (M * K4);
+    const int j = r2 / K4, c4 = r2 - j * K4;
+    *reinterpret_cast<u32x4*>(lut + (h * M + j) * kPqKMax + c4 * 4) =
+        ld16(a.lut + (int64_t)b * a.l_sb + (int64_t)(hq0 + h) * a.l_sh + j * K + c4 * 4);
+  }
+  if constexpr (OUT) {
+    for (int e = threadIdx.x; e < kPqHeads * kPqOutMax; e += kPqScoreThreads) {
+      const int h = e / kPqOutMax, c = e - h * kPqOutMax;
+      qo[e] = (h < nh && c < a.C) ? load_any(a.qout, a.qo_dt, (int64_t)b * a.qo_sb + (int64_t)(hq0 + h) * a.qo_sh + c)
+                                  : 0.f;
+    }
+  }
+  __syncthreads();
+  const int per = a.chunk;
+  const int t_end = min((part + 1) * per, a.S);
+  const uint8_t* kib = a.kidx + (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh;
+  const char* kob = OUT ? static_cast<const char*>(a.kout) +
+                              ((int64_t)b * a.ko_sb + (int64_t)hk * a.ko_sh) * (a.ko_dt == 2 ? 4 : 2)
+                        : nullptr;
+  for (int t = part * per + threadIdx.x; t < t_end; t += kPqScoreThreads) {
+    u32x4 kc;
+    if constexpr (M == 16) {
+      kc = ld16(kib + (int64_t)t * a.ki_ss);
+    } else {
+      const u32x2 hh = *reinterpret_cast<const u32x2*>(kib + (int64_t)t * a.ki_ss);
+      kc = u32x4{hh[0], hh[1], 0u, 0u};
+    }
+    float ko[OUT ? kPqOutMax : 1];
+    if constexpr (OUT) {
+#pragma unroll
+      for (int c = 0; c < kPqOutMax; ++c) ko[c] = c < a.C ? load_any(kob, a.ko_dt, (int64_t)t * a.ko_ss + c) : 0.f;
+    }
+    for (int h = 0; h < nh; ++h) {
+      const float* lh = lut + h * (M * kPqKMax);
+      float sc = 0.f;
+#pragma unroll
+      for (int j = 0; j < M; ++j) sc += lh[j * kPqKMax + ((kc[j >> 2] >> ((j & 3) * 8)) & 0xFFu)];
+      if constexpr (OUT) {
+        float so = 0.f;
+#pragma unroll
+        for (int c = 0; c < kPqOutMax; ++c) so += qo[h * kPqOutMax + c] * ko[c];
+        sc += so;
+      }
+      out[(int64_t)b * o_sb + (int64_t)(hq0 + h) * o_sh + t] = sc;
+    }
+  }
 }
 
 static void pq_plan(int S, long units, int chunk_req, int* chunk, int* ns) {
@@ -431,6 +580,54 @@ int bytes_pq_decode_workspace_size(int B, int Hq, int Hk, int S, int D, int chun
   return 0;
 }
 
+// Launch the decode on a filled PqArgs (strides, pointers, modes set).
+// mode 0: LUT + PQ values, 1: LUT + dense V, 2: q + key codebook + dense V.
+static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S, int D, int K, void* out,
+                     int out_dtype, int64_t o_sb, int64_t o_sh, float scale, int chunk_req, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  a.Hk = Hk; a.G = Hq / Hk; a.HG = (a.G + kPqHeads - 1) / kPqHeads; a.S = S; a.K = K;
+  a.scale_log2 = scale * kLog2e;
+  const long units = (long)B * Hk * a.HG;
+  if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
+  int ns;
+  pq_plan(S, units, chunk_req, &a.chunk, &ns);
+  if (ns > 1024) return (int)hipErrorInvalidConfiguration;
+  if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
+  a.o.out = out;
+  a.o.out_dtype = out_dtype;
+  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
+  // the merge kernel maps unit -> (b, hk, head group of kPqHeads)
+  a.o.Hk = Hk; a.o.HB = a.HG; a.o.G = a.G; a.o.hbs = kPqHeads;
+  splitk_carve(workspace, units, ns, a.o);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)(ns * units)), block(kPqWaves * 64);
+  const bool outl = a.C > 0;
+#define PQ_LAUNCH(DD, BL, QQ, F8, OU) hipLaunchKernelGGL((pq_decode_kernel<DD, BL, QQ, F8, OU>), grid, block, 0, st, a)
+#define PQ_MODES(DD)                                          \
+  if (mode == 0) PQ_LAUNCH(DD, false, true, false, false);    \
+  else if (mode == 2) PQ_LAUNCH(DD, true, false, false, false); \
+  else if (!vf8 && !outl) PQ_LAUNCH(DD, false, false, false, false); \
+  else if (!vf8) PQ_LAUNCH(DD, false, false, false, true);   \
+  else if (!outl) PQ_LAUNCH(DD, false, false, true, false);  \
+  else PQ_LAUNCH(DD, false, false, true, true);
+  if (D == 128) {
+    PQ_MODES(128)
+  } else {
+    PQ_MODES(64)
+  }
+#undef PQ_MODES
+#undef PQ_LAUNCH
+  int rc = (int)hipGetLastError();
+  if (rc) return rc;
+  return splitk_combine(a.o, units, D, st);
+}
+
+static PqArgs pq_args_zero() {
+  PqArgs a;
+  memset(&a, 0, sizeof(a));
+  return a;
+}
+
 // mode 0: LUT scores + PQ values (decode_attn_pq_lut_kv)
 // mode 1: LUT scores + dense bf16 values (decode_attn_pq_lut)
 // mode 2: scores from q and the key codebook + dense bf16 values (decode_attn_dequant)
@@ -448,7 +645,7 @@ int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* k
   if (mode == 1 && (!lut || !v)) return (int)hipErrorInvalidValue;
   if (mode == 2 && (!q || !kcb || !v)) return (int)hipErrorInvalidValue;
   if (out_dtype < 0 || out_dtype > 2) return (int)hipErrorInvalidValue;
-  PqArgs a;
+  PqArgs a = pq_args_zero();
   a.lut = static_cast<const float*>(lut);
   a.l_sb = l_sb; a.l_sh = l_sh;
   a.q = static_cast<const uint16_t*>(q);
@@ -461,38 +658,97 @@ int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* k
   a.vi_sb = vi_sb; a.vi_sh = vi_sh; a.vi_ss = vi_ss;
   a.vcb = static_cast<const _Float16*>(vcb);
   a.vcb_sh = vcb_sh;
-  a.v = static_cast<const uint16_t*>(v);
+  a.v = v;
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
+  return pq_launch(a, mode, false, B, Hq, Hk, S, D, K, out, out_dtype, o_sb, o_sh, scale, chunk_req, workspace,
+                   workspace_bytes, stream);
+}
+
+int bytes_pq_lut_decode_attn(const void* lut, int64_t l_sb, int64_t l_sh, const void* kidx, int64_t ki_sb,
+                             int64_t ki_sh, int64_t ki_ss, const void* vidx, int64_t vi_sb, int64_t vi_sh,
+                             int64_t vi_ss, const void* vcb, int64_t vcb_sh, const void* v, int v_fp8, int64_t v_sb,
+                             int64_t v_sh, int64_t v_ss, const void* kout, int ko_dtype, int64_t ko_sb,
+                             int64_t ko_sh, int64_t ko_ss, const void* qout, int qo_dtype, int64_t qo_sb,
+                             int64_t qo_sh, int C, const int* block_table, int64_t bt_sb, const int* context_lens,
+                             int block_size, int num_blocks, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
+                             int B, int Hq, int Hk, int S, int D, int K, float scale, int chunk_req, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (!lut || !kidx || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
+  if ((D != 64 && D != 128) || K <= 0 || K > kPqKMax || K % 4 != 0) return (int)hipErrorInvalidValue;
+  const bool qv = vidx != nullptr;
+  if (qv == (v != nullptr) || (qv && (!vcb || v_fp8 || C > 0))) return (int)hipErrorInvalidValue;
+  if (C < 0 || C > kPqOutMax || (C > 0 && (!kout || !qout))) return C > kPqOutMax ? (int)hipErrorNotSupported
+                                                                                  : (int)hipErrorInvalidValue;
+  if (ko_dtype < 0 || ko_dtype > 2 || qo_dtype < 0 || qo_dtype > 2) return (int)hipErrorInvalidValue;
+  if (block_table && (!context_lens || block_size <= 0 || num_blocks <= 0 || S % block_size != 0))
+    return (int)hipErrorInvalidValue;
+  if (out_dtype < 0 || out_dtype > 2) return (int)hipErrorInvalidValue;
+  PqArgs a = pq_args_zero();
+  a.lut = static_cast<const float*>(lut);
+  a.l_sb = l_sb; a.l_sh = l_sh;
+  a.kidx = static_cast<const uint8_t*>(kidx);
+  a.ki_sb = ki_sb; a.ki_sh = ki_sh; a.ki_ss = ki_ss;
+  a.vidx = static_cast<const uint8_t*>(vidx);
+  a.vi_sb = vi_sb; a.vi_sh = vi_sh; a.vi_ss = vi_ss;
+  a.vcb = static_cast<const _Float16*>(vcb);
+  a.vcb_sh = vcb_sh;
+  a.v = v;
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.kout = kout;
+  a.ko_sb = ko_sb; a.ko_sh = ko_sh; a.ko_ss = ko_ss; a.ko_dt = ko_dtype;
+  a.qout = qout;
+  a.qo_sb = qo_sb; a.qo_sh = qo_sh; a.qo_dt = qo_dtype;
+  a.C = C;
+  a.btab = block_table;
+  a.bt_sb = bt_sb;
+  a.clens = context_lens;
+  a.bs = block_size;
+  a.nblk = num_blocks;
+  return pq_launch(a, qv ? 0 : 1, v_fp8 != 0, B, Hq, Hk, S, D, K, out, out_dtype, o_sb, o_sh, scale, chunk_req,
+                   workspace, workspace_bytes, stream);
+}
+
+int bytes_pq_lut_scores(const void* lut, int64_t l_sb, int64_t l_sh, const void* kidx, int64_t ki_sb, int64_t ki_sh,
+                        int64_t ki_ss, const void* kout, int ko_dtype, int64_t ko_sb, int64_t ko_sh, int64_t ko_ss,
+                        const void* qout, int qo_dtype, int64_t qo_sb, int64_t qo_sh, int C, void* out, int64_t o_sb,
+                        int64_t o_sh, int B, int Hq, int Hk, int S, int D, int K, void* stream) {
+  if (!lut || !kidx || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0) return (int)hipErrorInvalidValue;
+  if ((D != 64 && D != 128) || K <= 0 || K > kPqKMax || K % 4 != 0) return (int)hipErrorInvalidValue;
+  if (C < 0 || C > kPqOutMax || (C > 0 && (!kout || !qout))) return C > kPqOutMax ? (int)hipErrorNotSupported
+                                                                                  : (int)hipErrorInvalidValue;
+  if (ko_dtype < 0 || ko_dtype > 2 || qo_dtype < 0 || qo_dtype > 2) return (int)hipErrorInvalidValue;
+  PqArgs a = pq_args_zero();
+  a.lut = static_cast<const float*>(lut);
+  a.l_sb = l_sb; a.l_sh = l_sh;
+  a.kidx = static_cast<const uint8_t*>(kidx);
+  a.ki_sb = ki_sb; a.ki_sh = ki_sh; a.ki_ss = ki_ss;
+  a.kout = kout;
+  a.ko_sb = ko_sb; a.ko_sh = ko_sh; a.ko_ss = ko_ss; a.ko_dt = ko_dtype;
+  a.qout = qout;
+  a.qo_sb = qo_sb; a.qo_sh = qo_sh; a.qo_dt = qo_dtype;
+  a.C = C;
   a.Hk = Hk; a.G = Hq / Hk; a.HG = (a.G + kPqHeads - 1) / kPqHeads; a.S = S; a.K = K;
-  a.scale_log2 = scale * kLog2e;
   const long units = (long)B * Hk * a.HG;
-  if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
-  int ns;
-  pq_plan(S, units, chunk_req, &a.chunk, &ns);
-  if (ns > 1024) return (int)hipErrorInvalidConfiguration;
-  if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
-  a.o.out = out;
-  a.o.out_dtype = out_dtype;
-  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
-  // the merge kernel maps unit -> (b, hk, head group of kPqHeads)
-  a.o.Hk = Hk; a.o.HB = a.HG; a.o.G = a.G; a.o.hbs = kPqHeads;
-  splitk_carve(workspace, units, ns, a.o);
+  // runs of >= 2048 tokens per workgroup (the LUT staging is paid per workgroup), ~2 per CU
+  const long target = 2L * device_cu_count();
+  long per = ((long)S * units + target - 1) / target;
+  if (per < 2048) per = 2048;
+  per = (per + kPqScoreThreads - 1) / kPqScoreThreads * kPqScoreThreads;
+  if (per > S) per = (S + kPqScoreThreads - 1) / kPqScoreThreads * kPqScoreThreads;
+  a.chunk = (int)per;
+  const long parts = (S + per - 1) / per;
+  const long grid = units * parts;
+  if (grid > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)(ns * units)), block(kPqWaves * 64);
-#define PQ_LAUNCH(DD, BL, QQ) hipLaunchKernelGGL((pq_decode_kernel<DD, BL, QQ>), grid, block, 0, st, a)
+  float* o = static_cast<float*>(out);
   if (D == 128) {
-    if (mode == 0) PQ_LAUNCH(128, false, true);
-    else if (mode == 1) PQ_LAUNCH(128, false, false);
-    else PQ_LAUNCH(128, true, false);
+    if (C > 0) hipLaunchKernelGGL((pq_score_kernel<16, true>), dim3((unsigned)grid), dim3(kPqScoreThreads), 0, st, a, o, o_sb, o_sh, (int)parts);
+    else hipLaunchKernelGGL((pq_score_kernel<16, false>), dim3((unsigned)grid), dim3(kPqScoreThreads), 0, st, a, o, o_sb, o_sh, (int)parts);
   } else {
-    if (mode == 0) PQ_LAUNCH(64, false, true);
-    else if (mode == 1) PQ_LAUNCH(64, false, false);
-    else PQ_LAUNCH(64, true, false);
+    if (C > 0) hipLaunchKernelGGL((pq_score_kernel<8, true>), dim3((unsigned)grid), dim3(kPqScoreThreads), 0, st, a, o, o_sb, o_sh, (int)parts);
+    else hipLaunchKernelGGL((pq_score_kernel<8, false>), dim3((unsigned)grid), dim3(kPqScoreThreads), 0, st, a, o, o_sb, o_sh, (int)parts);
   }
-#undef PQ_LAUNCH
-  int rc = (int)hipGetLastError();
-  if (rc) return rc;
-  return splitk_combine(a.o, units, D, st);
+  return (int)hipGetLastError();
 }
 
 int bytes_pq_build_lut(const void* q, const void* cb, void* lut, int B, int Hq, int Hk, int D, int K, int64_t q_sb,

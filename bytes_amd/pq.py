@@ -152,6 +152,191 @@ def decode_attn_dequant(q: torch.Tensor, k_idx: torch.Tensor, centroids: torch.T
                    B=B, Hq=Hq, Hk=Hk, S=S, D=D, K=K, dev=q.device, chunk=chunk)
 
 
+# ---------------------------------------------------------------------------
+# outlier-aware (asymmetric) and paged variants
+# ---------------------------------------------------------------------------
+OUTLIER_MAX = 16
+_F8 = torch.float8_e4m3fn
+
+
+def _outliers(k_out: torch.Tensor, q_out: torch.Tensor, lead: tuple, B: int, Hq: int):
+    """-> (k_out rows with unit stride along C, q_out, C); C = 0 passes no pointers."""
+    C.cuda_tensors(k_out, q_out)
+    C.ndim(k_out, 4, "k_out"), C.ndim(q_out, 3, "q_out")
+    Cn = k_out.shape[-1]
+    if tuple(k_out.shape[:3]) != lead:
+        raise ValueError(f"k_out {tuple(k_out.shape)} does not match the key codes' {lead}")
+    if tuple(q_out.shape) != (B, Hq, Cn):
+        raise ValueError(f"q_out {tuple(q_out.shape)} must be [B, H_q, C] = {(B, Hq, Cn)}")
+    if Cn > OUTLIER_MAX:
+        raise ValueError(f"C={Cn} outlier channels above the supported {OUTLIER_MAX}")
+    for t, n in ((k_out, "k_out"), (q_out, "q_out")):
+        C.dtype_in(t, n, torch.bfloat16, torch.float16, torch.float32)
+    if Cn and k_out.stride(-1) != 1:
+        k_out = k_out.contiguous()
+    if Cn and q_out.stride(-1) != 1:
+        q_out = q_out.contiguous()
+    return k_out, q_out, Cn
+
+
+def _paging(block_table: torch.Tensor, context_lens: torch.Tensor, B: int, block_size: int, nblocks: int):
+    C.cuda_tensors(block_table, context_lens)
+    if block_table.dim() != 2 or block_table.shape[0] != B or context_lens.shape != (B,):
+        raise ValueError(f"block_table must be [B, max_blocks] and context_lens [B]; got "
+                         f"{tuple(block_table.shape)}, {tuple(context_lens.shape)}")
+    if block_size <= 0 or nblocks <= 0:
+        raise ValueError("empty paged cache")
+    bt = block_table.to(torch.int32)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    return bt, context_lens.to(torch.int32).contiguous(), block_table.shape[1] * block_size
+
+
+def _lut_decode(lut, k_idx, *, v_idx=None, vcb=None, v=None, k_out=None, q_out=None, Cn=0, paging=None,
+                out_dtype, Hk, S, K, chunk=0):
+    B, Hq, M, _ = lut.shape
+    D = M * D_SUB
+    dev = lut.device
+    out = torch.empty((B, Hq, D), dtype=out_dtype, device=dev)
+    ws = workspace(dev, size_query("bytes_pq_decode_workspace_size", B, Hq, Hk, S, D, int(chunk)))
+    z = lambda t, i: t.stride(i) if t is not None else 0    # noqa: E731
+    p = lambda t: ptr(t) if t is not None else None          # noqa: E731
+    vcb16, vcb_sh = vcb if vcb is not None else (None, 0)
+    ko = k_out if Cn else None
+    qo = q_out if Cn else None
+    bt, cl, bs, nblk = paging if paging is not None else (None, None, 0, 0)
+    call("bytes_pq_lut_decode_attn", ptr(lut), lut.stride(0), lut.stride(1),
+         ptr(k_idx), k_idx.stride(0), k_idx.stride(1), k_idx.stride(2),
+         p(v_idx), z(v_idx, 0), z(v_idx, 1), z(v_idx, 2), p(vcb16), vcb_sh,
+         p(v), int(v is not None and v.dtype == _F8), z(v, 0), z(v, 1), z(v, 2),
+         p(ko), dtype_code(ko) if ko is not None else 0, z(ko, 0), z(ko, 1), z(ko, 2),
+         p(qo), dtype_code(qo) if qo is not None else 0, z(qo, 0), z(qo, 1), int(Cn),
+         p(bt), z(bt, 0), p(cl), int(bs), int(nblk),
+         ptr(out), dtype_code(out), out.stride(0), out.stride(1),
+         B, Hq, Hk, S, D, K, 1.0, int(chunk), ptr(ws), ws.numel(), stream_of(lut))
+    return out.unsqueeze(2)
+
+
+def _dense_values(v: torch.Tensor, lead: tuple, D: int) -> torch.Tensor:
+    C.dtype_in(v, "v", torch.bfloat16, _F8)
+    if tuple(v.shape) != (*lead, D):
+        raise ValueError(f"v {tuple(v.shape)} does not match the key codes: expected {(*lead, D)}")
+    return C.rows16(v)
+
+
+def decode_attn_pq_lut_asym(lut: torch.Tensor, k_idx: torch.Tensor, k_out: torch.Tensor, q_out: torch.Tensor,
+                            v: torch.Tensor, BLOCK_N: int = 256, *, chunk: int = 0) -> torch.Tensor:
+    """LUT-scored keys plus exact outlier channels, dense V.
+
+    Replaces src/attention_kernels.py:713-753: score_t = sum_j lut[b,h,j,k_idx[t,j]]
+    + sum_c q_out[b,h,c] * k_out[b,h//G,t,c], softmax without a scale inside
+    (fold it into the LUT and q_out).  lut [B,H_q,M,K] fp32; k_idx [B,H_k,S,M];
+    k_out [B,H_k,S,C] and q_out [B,H_q,C] (C <= 16; C = 0 allowed); v
+    [B,H_k,S,D] bf16 or float8_e4m3fn.  Returns [B,H_q,1,D] in v's dtype, bf16
+    for fp8 values (:735)."""
+    lut, B, Hq, Hk, S, M, K = _lut_checks(lut, k_idx)
+    C.cuda_tensors(lut, v)
+    k_out, q_out, Cn = _outliers(k_out, q_out, (B, Hk, S), B, Hq)
+    v = _dense_values(v, (B, Hk, S), M * D_SUB)
+    od = torch.bfloat16 if v.dtype == _F8 else v.dtype
+    return _lut_decode(lut, _codes(k_idx, "k_idx"), v=v, k_out=k_out, q_out=q_out, Cn=Cn, out_dtype=od, Hk=Hk,
+                       S=S, K=K, chunk=chunk)
+
+
+def _paged_lut_checks(lut, k_idx_paged):
+    C.cuda_tensors(lut, k_idx_paged)
+    C.ndim(lut, 4, "lut"), C.ndim(k_idx_paged, 4, "k_idx_paged")
+    if lut.dtype != torch.float32:
+        lut = lut.float()
+    B, Hq, M, K = lut.shape
+    nblk, Hk, bs, Mk = k_idx_paged.shape
+    if Mk != M or Hq % Hk != 0:
+        raise ValueError(f"shape mismatch: lut {tuple(lut.shape)}, k_idx_paged {tuple(k_idx_paged.shape)}")
+    if M * D_SUB not in (64, 128):
+        raise ValueError(f"M={M} subspaces: head_dim {M * D_SUB} not supported (64 or 128)")
+    if not (0 < K <= 256 and K % 4 == 0):
+        raise ValueError(f"K={K} codewords not supported (multiple of 4, <= 256)")
+    if lut.stride(-1) != 1 or lut.stride(-2) != K or lut.data_ptr() % 16 != 0:
+        lut = lut.contiguous()
+    return lut, B, Hq, Hk, nblk, bs, M, K
+
+
+def paged_attn_pq_lut_kv(lut: torch.Tensor, k_idx_paged: torch.Tensor, v_idx_paged: torch.Tensor,
+                         v_centroids: torch.Tensor, block_table: torch.Tensor, context_lens: torch.Tensor,
+                         block_size: int = 16, *, chunk: int = 0) -> torch.Tensor:
+    """The LUT-KV decode over a paged cache.  Replaces
+    src/attention_kernels.py:588-622: k_idx_paged, v_idx_paged
+    [num_blocks,H_k,block_size,M]; block_table [B,max_blocks] (entries past a
+    sequence's blocks unused, e.g. -1); context_lens [B].  Returns
+    [B,H_q,1,D] in v_centroids' dtype."""
+    lut, B, Hq, Hk, nblk, bs, M, K = _paged_lut_checks(lut, k_idx_paged)
+    if bs != block_size:
+        raise ValueError(f"k_idx_paged rows per block {bs} != block_size {block_size}")
+    C.cuda_tensors(lut, v_idx_paged, v_centroids)
+    if tuple(v_idx_paged.shape[:3]) != (nblk, Hk, bs):
+        raise ValueError(f"v_idx_paged {tuple(v_idx_paged.shape)} does not match k_idx_paged")
+    vcb16, vsh, Mv, Kv = _codebook16(v_centroids, Hk, "v_centroids")
+    if Mv != M or v_idx_paged.shape[-1] != Mv or Kv != K:
+        raise ValueError("value codebook / codes must use the key's subspace and codeword counts")
+    bt, cl, S = _paging(block_table, context_lens, B, block_size, nblk)
+    return _lut_decode(lut, _codes(k_idx_paged, "k_idx_paged"), v_idx=_codes(v_idx_paged, "v_idx_paged"),
+                       vcb=(vcb16, vsh), paging=(bt, cl, block_size, nblk), out_dtype=v_centroids.dtype, Hk=Hk,
+                       S=S, K=K, chunk=chunk)
+
+
+def paged_attn_pq_lut_asym(lut: torch.Tensor, k_idx_paged: torch.Tensor, k_out_paged: torch.Tensor,
+                           q_out: torch.Tensor, v_paged: torch.Tensor, block_table: torch.Tensor,
+                           context_lens: torch.Tensor, block_size: int = 16, BLOCK_N: int = 256, *,
+                           chunk: int = 0) -> torch.Tensor:
+    """The outlier-aware LUT decode over a paged cache.  Replaces
+    src/attention_kernels.py:858-906: k_idx_paged [num_blocks,H_k,block_size,M],
+    k_out_paged [num_blocks,H_k,block_size,C], v_paged [num_blocks,H_k,block_size,D]
+    bf16 or float8_e4m3fn, q_out [B,H_q,C].  Returns [B,H_q,1,D] in v's dtype,
+    bf16 for fp8 values."""
+    lut, B, Hq, Hk, nblk, bs, M, K = _paged_lut_checks(lut, k_idx_paged)
+    if bs != block_size:
+        raise ValueError(f"k_idx_paged rows per block {bs} != block_size {block_size}")
+    C.cuda_tensors(lut, v_paged)
+    k_out_paged, q_out, Cn = _outliers(k_out_paged, q_out, (nblk, Hk, bs), B, Hq)
+    v_paged = _dense_values(v_paged, (nblk, Hk, bs), M * D_SUB)
+    bt, cl, S = _paging(block_table, context_lens, B, block_size, nblk)
+    od = torch.bfloat16 if v_paged.dtype == _F8 else v_paged.dtype
+    return _lut_decode(lut, _codes(k_idx_paged, "k_idx_paged"), v=v_paged, k_out=k_out_paged, q_out=q_out, Cn=Cn,
+                       paging=(bt, cl, block_size, nblk), out_dtype=od, Hk=Hk, S=S, K=K, chunk=chunk)
+
+
+def sparse_score_pq_lut_asym(lut: torch.Tensor, k_idx: torch.Tensor, k_out: torch.Tensor, q_out: torch.Tensor,
+                             BLOCK_N: int = 256) -> torch.Tensor:
+    """Per-key LUT + outlier scores [B,H_q,S] fp32 (no softmax).  Replaces
+    src/attention_kernels.py:960-984."""
+    lut, B, Hq, Hk, S, M, K = _lut_checks(lut, k_idx)
+    k_out, q_out, Cn = _outliers(k_out, q_out, (B, Hk, S), B, Hq)
+    k_idx = _codes(k_idx, "k_idx")
+    out = torch.empty((B, Hq, S), dtype=torch.float32, device=lut.device)
+    ko = k_out if Cn else None
+    qo = q_out if Cn else None
+    z = lambda t, i: t.stride(i) if t is not None else 0    # noqa: E731
+    call("bytes_pq_lut_scores", ptr(lut), lut.stride(0), lut.stride(1), ptr(k_idx), k_idx.stride(0),
+         k_idx.stride(1), k_idx.stride(2), ptr(ko) if Cn else None, dtype_code(ko) if Cn else 0, z(ko, 0), z(ko, 1),
+         z(ko, 2), ptr(qo) if Cn else None, dtype_code(qo) if Cn else 0, z(qo, 0), z(qo, 1), int(Cn), ptr(out),
+         out.stride(0), out.stride(1), B, Hq, Hk, S, M * D_SUB, K, stream_of(lut))
+    return out
+
+
+def sparse_decode_pq_lut(lut: torch.Tensor, k_idx: torch.Tensor, k_out: torch.Tensor, q_out: torch.Tensor,
+                         q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, frac: float, scaling: float,
+                         BLOCK_N: int = 256, BLOCK_K: int = 64) -> torch.Tensor:
+    """LUT + outlier scores over every key -> the kb = max(1, round(frac*S))
+    best per query head (ties to the lowest index) -> exact gathered attention
+    over k, v.  Replaces src/attention_kernels.py:1062-1074.  Returns
+    [B,H_q,1,D] bf16."""
+    from .sparse import budget, sparse_gather_attn, topk_indices
+    s = sparse_score_pq_lut_asym(lut, k_idx, k_out, q_out)
+    kb = budget(frac, s.shape[-1])
+    idx = topk_indices(s, kb, sorted=False)
+    return sparse_gather_attn(q, k, v, idx, scaling)
+
+
 def pq_build_lut(q: torch.Tensor, centroids: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
     """lut[b,h,j,c] = scale * sum_e q[b,h,8j+e] * centroids[h//G][j][c][e] (fp32):
     the reference's LUT precompute (benchmarks/test_correctness.py:272-273,

@@ -222,6 +222,50 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
                             int64_t o_sb, int64_t o_sh, float scale, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Product-quantized decode with paged caches, outlier channels and fp8 values.
+ * Replaces src/attention_kernels.py:
+ *   paged_attn_pq_lut_kv    :588-622 (kernel :505-586)   vidx + vcb, block_table
+ *   decode_attn_pq_lut_asym :713-753 (kernel :625-711)   v dense, k_out/q_out
+ *   paged_attn_pq_lut_asym  :858-906 (kernel :756-856)   the same, block_table
+ * Scores: sum_j lut[b,h,j,kidx[row,j]] + sum_{c<C} q_out[b,h,c] * k_out[row,c]
+ *   (fp32; C <= 16, C = 0: no outliers); softmax without a scale inside
+ *   (`scale` multiplies the scores: pass 1.0).
+ * Values: exactly one of  vidx (+ vcb, fp16 [M,K,8], per KV head when vcb_sh
+ *   != 0: reconstructed rows)  or  v (bf16, or float8_e4m3fn when v_fp8 = 1).
+ * Caches: block_table == NULL: contiguous [B, Hk, S, .] (strides *_sb, *_sh,
+ *   *_ss).  Otherwise paged [num_blocks, Hk, block_size, .] with *_sb the block
+ *   stride: token t of sequence b is row t % block_size of block
+ *   block_table[b * bt_sb + t / block_size]; sequence b has context_lens[b]
+ *   tokens (int32, device memory); S = max_blocks * block_size bounds every
+ *   length.  Block ids are clamped into [0, num_blocks).
+ * k_out / q_out dtypes: 0 bf16, 1 fp16, 2 fp32 (unit stride along C).
+ * out [B, Hq, D] of out_dtype; workspace from bytes_pq_decode_workspace_size
+ * (same S), in the split-K workspace family.
+ * ------------------------------------------------------------------------- */
+int bytes_pq_lut_decode_attn(const void* lut, int64_t l_sb, int64_t l_sh, const void* kidx, int64_t ki_sb,
+                             int64_t ki_sh, int64_t ki_ss, const void* vidx, int64_t vi_sb, int64_t vi_sh,
+                             int64_t vi_ss, const void* vcb, int64_t vcb_sh, const void* v, int v_fp8, int64_t v_sb,
+                             int64_t v_sh, int64_t v_ss, const void* kout, int ko_dtype, int64_t ko_sb,
+                             int64_t ko_sh, int64_t ko_ss, const void* qout, int qo_dtype, int64_t qo_sb,
+                             int64_t qo_sh, int C, const int* block_table, int64_t bt_sb, const int* context_lens,
+                             int block_size, int num_blocks, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
+                             int B, int Hq, int Hk, int S, int D, int K, float scale, int chunk, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Per-key LUT + outlier scores.
+ * Replaces src/attention_kernels.py:960-984 (`sparse_score_pq_lut_asym`,
+ * kernel :909-958): out[b,h,t] = sum_j lut[b,h,j,kidx[b,h/G,t,j]]
+ *   + sum_{c<C} q_out[b,h,c] * k_out[b,h/G,t,c], fp32 [B, Hq, S] (strides
+ *   o_sb, o_sh; unit stride along S).  Layouts as bytes_pq_lut_decode_attn
+ *   (contiguous caches).
+ * ------------------------------------------------------------------------- */
+int bytes_pq_lut_scores(const void* lut, int64_t l_sb, int64_t l_sh, const void* kidx, int64_t ki_sb, int64_t ki_sh,
+                        int64_t ki_ss, const void* kout, int ko_dtype, int64_t ko_sb, int64_t ko_sh, int64_t ko_ss,
+                        const void* qout, int qo_dtype, int64_t qo_sb, int64_t qo_sh, int C, void* out, int64_t o_sb,
+                        int64_t o_sh, int B, int Hq, int Hk, int S, int D, int K, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Product-quantized decode attention (d_sub = 8, M = D/8 subspaces, K <= 256
  * codewords, K % 4 == 0; codebooks fp16 [M, K, 8], per KV head when the head
  * stride *_sh is non-zero; codes uint8 [B, Hk, S, M] with unit stride in M and

@@ -356,6 +356,83 @@ def decode_attn_dequant(q, k_idx, centroids, v, d_sub: int = 8):
     return decode_attn(q, kh, v, scale=1.0, out_dtype=q.dtype)
 
 
+def pq_asym_scores(lut, k_idx, k_out, q_out) -> torch.Tensor:
+    """LUT scores plus the exact outlier channels:
+    s[b,h,t] = sum_j lut[b,h,j,k_idx[t,j]] + sum_c q_out[b,h,c] * k_out[b,h//G,t,c] (fp32).
+
+    Restates paths A and B of src/attention_kernels.py:660-685 (decode) and
+    :943-955 (`sparse_score_pq_lut_asym`).  Pinned by: per-token Python loop
+    (benchmarks/test_correctness.py:455-466 form) and equality with full-width
+    q.k when the LUT comes from the same codebook.
+    """
+    s = pq_lut_scores(lut, k_idx)
+    C = k_out.shape[-1]
+    if C > 0:
+        G = lut.shape[1] // k_idx.shape[1]
+        ko = repeat_kv(k_out.float(), G)                                   # [B,Hq,S,C]
+        s = s + (ko * q_out.float()[:, :, None, :]).sum(-1)
+    return s
+
+
+def decode_attn_pq_lut_asym(lut, k_idx, k_out, q_out, v):
+    """LUT + outlier scores, dense bf16 or float8_e4m3fn V, no scale inside.
+
+    Restates src/attention_kernels.py:625-753 (`decode_attn_pq_lut_asym`);
+    output dtype = v.dtype, bf16 for fp8 values (:735)."""
+    B, Hq, M, K = lut.shape
+    Hk = k_idx.shape[1]
+    G = Hq // Hk
+    s = pq_asym_scores(lut, k_idx, k_out, q_out)
+    o = _softmax_attend(s.reshape(B, Hk, G, -1), v.float())
+    od = torch.bfloat16 if v.dtype == torch.float8_e4m3fn else v.dtype
+    return o.reshape(B, Hq, 1, -1).to(od)
+
+
+def paged_rows(x_paged: torch.Tensor, block_table: torch.Tensor, b: int, n: int, block_size: int) -> torch.Tensor:
+    """Rows 0..n-1 of sequence b from a paged cache [blocks, H, block_size, ...]:
+    token t is row t % block_size of block block_table[b, t // block_size]
+    (src/attention_kernels.py:536-545 / :813-819).  Returns [1, H, n, ...]."""
+    t = torch.arange(n)
+    blk = block_table[b, t // block_size].long()
+    return x_paged[blk, :, t % block_size].transpose(0, 1).unsqueeze(0)
+
+
+def paged_attn_pq_lut_kv(lut, k_idx_paged, v_idx_paged, v_centroids, block_table, context_lens, block_size=16):
+    """Restates src/attention_kernels.py:505-622: the LUT-KV decode of each
+    sequence over its context_lens[b] tokens gathered through the block table."""
+    outs = []
+    for b in range(lut.shape[0]):
+        n = int(context_lens[b])
+        ki = paged_rows(k_idx_paged, block_table, b, n, block_size)
+        vi = paged_rows(v_idx_paged, block_table, b, n, block_size)
+        outs.append(decode_attn_pq_lut_kv(lut[b:b + 1], ki, vi, v_centroids))
+    return torch.cat(outs, 0)
+
+
+def paged_attn_pq_lut_asym(lut, k_idx_paged, k_out_paged, q_out, v_paged, block_table, context_lens,
+                           block_size=16):
+    """Restates src/attention_kernels.py:756-906: the asymmetric PQ-LUT decode
+    of each sequence over its context_lens[b] tokens gathered through the
+    block table."""
+    outs = []
+    for b in range(lut.shape[0]):
+        n = int(context_lens[b])
+        ki = paged_rows(k_idx_paged, block_table, b, n, block_size)
+        ko = paged_rows(k_out_paged, block_table, b, n, block_size)
+        vv = paged_rows(v_paged, block_table, b, n, block_size)
+        outs.append(decode_attn_pq_lut_asym(lut[b:b + 1], ki, ko, q_out[b:b + 1], vv))
+    return torch.cat(outs, 0)
+
+
+def sparse_decode_pq_lut(lut, k_idx, k_out, q_out, q, k, v, frac: float, scaling: float):
+    """LUT + outlier scores -> top-kb per query head (ties to the lowest
+    index) -> exact gathered attention.  Restates
+    src/attention_kernels.py:1062-1074 with the build's deterministic top-k."""
+    s = pq_asym_scores(lut, k_idx, k_out, q_out)
+    kb = budget(frac, s.shape[-1])
+    return sparse_gather_attn(q, k, v, topk_indices(s, kb), scaling)
+
+
 # ---------------------------------------------------------------------------
 # a10: deterministic top-k (total order: score desc, index asc)
 # ---------------------------------------------------------------------------

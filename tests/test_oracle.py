@@ -331,3 +331,66 @@ def test_quantize_and_pack_score_keys_closed_form():
         lvl = 2 ** bits - 1
         bound = 0.5 * step + lvl * step * 2 ** -8 + 2 ** -8 * lo.repeat_interleave(32, -1).abs() + 1e-6
         assert torch.all((dq - k.float()).abs() <= bound)
+
+
+# ---------------------------------------------------------------- PQ asym / paged
+def test_pq_asym_scores_loop_and_full_width():
+    """Per-token loop (benchmarks/test_correctness.py:455-466 form) and, with a
+    LUT built from the key codebook, equality with q . [k_hat, k_out]."""
+    g = torch.Generator().manual_seed(7)
+    B, Hq, Hk, S, M, K, C = 2, 4, 2, 9, 8, 8, 2
+    cb = torch.randn(M, K, 8, generator=g)
+    q = torch.randn(B, Hq, 1, M * 8, generator=g).to(torch.bfloat16)
+    k_idx = torch.randint(0, K, (B, Hk, S, M), generator=g, dtype=torch.uint8)
+    k_out = torch.randn(B, Hk, S, C, generator=g).to(torch.bfloat16)
+    q_out = torch.randn(B, Hq, C, generator=g).to(torch.bfloat16)
+    lut = R.pq_build_lut(q, cb)
+    s = R.pq_asym_scores(lut, k_idx, k_out, q_out)
+    G = Hq // Hk
+    for b in range(B):
+        for h in range(Hq):
+            for t in range(S):
+                ref = sum(float(lut[b, h, j, int(k_idx[b, h // G, t, j])]) for j in range(M))
+                ref += sum(float(q_out[b, h, c]) * float(k_out[b, h // G, t, c]) for c in range(C))
+                assert abs(float(s[b, h, t]) - ref) < 1e-4
+    khat = torch.stack([R.pq_decode(k_idx[:, h], cb) for h in range(Hk)], 1)          # [B,Hk,S,D]
+    qf = torch.cat([q.float(), q_out.float().unsqueeze(2)], -1)
+    kf = torch.cat([khat, k_out.float()], -1)
+    full = torch.matmul(qf.reshape(B, Hk, G, -1), kf.transpose(-1, -2)).reshape(B, Hq, S)
+    assert torch.allclose(s, full, atol=1e-4)
+    # C = 0 reduces to the LUT decode
+    v = torch.randn(B, Hk, S, M * 8, generator=g).to(torch.bfloat16)
+    a = R.decode_attn_pq_lut_asym(lut, k_idx, k_out[..., :0], q_out[..., :0], v)
+    assert torch.equal(a, R.decode_attn_pq_lut(lut, k_idx, v))
+
+
+def test_paged_rows_follow_the_block_table():
+    """A cache split into shuffled blocks and read back through the table
+    (src/attention_kernels.py:536-545 rule) reproduces the contiguous rows, so
+    the paged decodes equal the contiguous ones per sequence."""
+    g = torch.Generator().manual_seed(3)
+    Hk, bs, M, K = 2, 16, 8, 8
+    lens = [45, 78]
+    nb = [(n + bs - 1) // bs for n in lens]
+    perm = torch.randperm(sum(nb), generator=g)
+    table = torch.full((2, max(nb)), -1, dtype=torch.int32)
+    k_idx = torch.randint(0, K, (2, Hk, max(lens), M), generator=g, dtype=torch.uint8)
+    v_idx = torch.randint(0, K, (2, Hk, max(lens), M), generator=g, dtype=torch.uint8)
+    kp = torch.zeros(sum(nb), Hk, bs, M, dtype=torch.uint8)
+    vp = torch.zeros_like(kp)
+    c = 0
+    for b in range(2):
+        for i in range(nb[b]):
+            table[b, i] = int(perm[c])
+            c += 1
+        for t in range(lens[b]):
+            kp[table[b, t // bs], :, t % bs] = k_idx[b, :, t]
+            vp[table[b, t // bs], :, t % bs] = v_idx[b, :, t]
+    for b in range(2):
+        assert torch.equal(R.paged_rows(kp, table, b, lens[b], bs)[0], k_idx[b, :, :lens[b]])
+    cb = torch.randn(M, K, 8, generator=g)
+    lut = torch.randn(2, 4, M, K, generator=g)
+    out = R.paged_attn_pq_lut_kv(lut, kp, vp, cb, table, torch.tensor(lens), bs)
+    for b in range(2):
+        ref = R.decode_attn_pq_lut_kv(lut[b:b + 1], k_idx[b:b + 1, :, :lens[b]], v_idx[b:b + 1, :, :lens[b]], cb)
+        assert torch.equal(out[b:b + 1], ref)
