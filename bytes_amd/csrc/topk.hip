@@ -21,7 +21,8 @@
 //     the workgroup instead runs an exact radix select over the whole row
 //     (11/11/10-bit digits), collects in index order and sorts the k results.
 // Step 3 also clears the histogram and list counters, which are zero between
-// calls.
+// calls.  Short rows, and unsorted selections larger than the lists hold
+// (k > 8192), run step 3's exact path alone.
 #include "common.h"
 
 namespace bytes_amd {
@@ -143,7 +144,7 @@ __device__ void bitonic_desc(uint64_t* buf, int P) {
   }
 }
 
-constexpr int kRowBatch = 128;         // rows per launch group (fixed histogram region)
+constexpr int kRowBatch = 1024;        // rows per launch group (fixed histogram region, 8 MiB)
 
 // Workspace: a fixed-size region of per-row histograms and list counters for
 // kRowBatch rows, zero between calls (the select kernel clears what it used),
@@ -158,17 +159,24 @@ struct TopkWs {
 
 constexpr size_t kTopkZeroBytes = (size_t)kRowBatch * kBins * 4 + (size_t)kRowBatch * 2 * 4;
 
-inline size_t topk_ws_bytes(int k) {
-  return kTopkZeroBytes + (size_t)kRowBatch * k * 8 + (size_t)kRowBatch * kCandCap * 8;
+// Lists for the rows of one launch group (min(rows, kRowBatch)) follow the
+// fixed zero region.  k above kTopkMaxK (unsorted output only) runs the
+// one-workgroup-per-row exact path, which needs the zeroed region alone.
+inline size_t topk_ws_bytes(int64_t rows, int k) {
+  if (k > kTopkMaxK) return kTopkZeroBytes;
+  const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
+  return kTopkZeroBytes + r * k * 8 + r * kCandCap * 8;
 }
 
-inline TopkWs topk_ws_carve(void* ws, int k) {
+inline TopkWs topk_ws_carve(void* ws, int64_t rows, int k) {
+  if (k > kTopkMaxK) k = 0;                      // exact path: no lists
+  const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
   char* p = static_cast<char*>(ws);
   TopkWs t;
   t.hist = reinterpret_cast<uint32_t*>(p);
   t.cnt = reinterpret_cast<uint32_t*>(p + (size_t)kRowBatch * kBins * 4);
   t.above = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes);
-  t.cand = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes + (size_t)kRowBatch * k * 8);
+  t.cand = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes + r * k * 8);
   return t;
 }
 
@@ -584,7 +592,9 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
     lds_set = true;
   }
   const int parts = (n + kSlice - 1) / kSlice;
-  const int exact = n <= kShortRow ? 1 : 0;
+  // short rows, and k beyond the list capacity (unsorted output: the exact
+  // path writes the selection straight to `out` in index order)
+  const int exact = (n <= kShortRow || k > kTopkMaxK) ? 1 : 0;
   if (exact) {
     if (rows > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(topk_select_kernel<VEC>, dim3((unsigned)rows), dim3(kTopkThreads), kSortMax * 8, st, scores,
@@ -617,21 +627,20 @@ extern "C" {
 
 int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes) {
   if (!bytes || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
-  if (k > kTopkMaxK) return (int)hipErrorNotSupported;
-  *bytes = topk_ws_bytes(k);
+  *bytes = topk_ws_bytes(rows, k);
   return 0;
 }
 
 int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, int hist_ready,
                void* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
   if (!scores || !out || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
-  if (k > kTopkMaxK) return (int)hipErrorNotSupported;
+  if (k > kTopkMaxK && sorted) return (int)hipErrorNotSupported;
   if (rows == 0) return 0;
   const long parts = (n + kSlice - 1) / kSlice;
   if (kRowBatch * parts > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
-  if (!workspace || workspace_bytes < topk_ws_bytes(k)) return (int)hipErrorInvalidValue;
+  if (!workspace || workspace_bytes < topk_ws_bytes(rows, k)) return (int)hipErrorInvalidValue;
   if (hist_ready && rows > kRowBatch) return (int)hipErrorInvalidValue;
-  const TopkWs ws = topk_ws_carve(workspace, k);
+  const TopkWs ws = topk_ws_carve(workspace, rows, k);
   const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0) && (row_stride % 4 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float* s = static_cast<const float*>(scores);

@@ -13,8 +13,8 @@ import torch
 from . import _checks as C
 from ._lib import HIP_ERROR_NOT_SUPPORTED, call, lib, ptr, size_query, stream_of, workspace
 
-TOPK_MAX = 8192
-TOPK_HIST_ROWS = 128          # rows whose digit histogram fits the top-k workspace's fixed region
+TOPK_MAX = 8192               # largest k of the score-ordered (sorted=True) output
+TOPK_HIST_ROWS = 1024         # rows whose digit histogram fits the top-k workspace's fixed region
 
 
 def _qk_shapes(q: torch.Tensor, k: torch.Tensor, k_dim: int = None):
@@ -170,8 +170,9 @@ def _topk(scores: torch.Tensor, k: int, *, sorted: bool, ws=None, hist_ready: bo
     n = scores.shape[-1]
     if not 1 <= k <= n:
         raise ValueError(f"k={k} outside [1, {n}]")
-    if k > TOPK_MAX:
-        raise ValueError(f"k={k} above the supported maximum {TOPK_MAX}")
+    if k > TOPK_MAX and sorted:
+        raise ValueError(f"sorted output supports k <= {TOPK_MAX} (k={k}); sorted=False returns the same set "
+                         "by ascending index for any k")
     s = scores.reshape(-1, n)
     if s.stride(-1) != 1:
         s = s.contiguous()

@@ -139,7 +139,7 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
  *   D in {64, 128}.
  * hist (group_sum = 1 only, may be NULL): [B*Hk][2048] uint32, zero on entry,
  *   receives the count of each score's top 11 order-key bits; pass the first
- *   bytes of a bytes_topk workspace (its histogram region, B*Hk <= 128) and
+ *   bytes of a bytes_topk workspace (its histogram region, B*Hk <= 1024) and
  *   call bytes_topk with hist_ready = 1 to skip its histogram pass.
  * ------------------------------------------------------------------------- */
 int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_scale, const void* k_min, void* out,
@@ -169,9 +169,10 @@ int bytes_score_keys_pack(const void* x, int x_dtype, int64_t rows, int D, int64
  *   scores [rows, n] fp32 (row stride row_stride, unit stride along n)
  *   out    [rows, k] int32 (row stride out_stride): ordered by that order when
  *          sorted != 0, else the same set by ascending index.
- * 1 <= k <= min(n, 8192); larger k returns hipErrorNotSupported.
+ * 1 <= k <= n; sorted output needs k <= 8192 (else hipErrorNotSupported),
+ * unsorted output takes any k.
  * hist_ready = 1: the workspace's histogram region already holds the rows'
- *   digit histograms (bytes_sparse_score with hist); rows <= 128.
+ *   digit histograms (bytes_sparse_score with hist); rows <= 1024.
  * ------------------------------------------------------------------------- */
 int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes);
 int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, int hist_ready,

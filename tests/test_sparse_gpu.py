@@ -58,13 +58,24 @@ def _tie_heavy(rows, n, seed):
 
 @pytest.mark.parametrize("sorted_out", [True, False])
 @pytest.mark.parametrize("rows,n,k", [(3, 1000, 1), (3, 1000, 17), (4, 4096, 256), (2, 1001, 1001),
-                                      (5, 333, 100), (28, 2048, 128), (2, 20000, 8192), (3, 70000, 3000)])
+                                      (5, 333, 100), (28, 2048, 128), (2, 20000, 8192), (3, 70000, 3000),
+                                      (1100, 17000, 100)])
 def test_topk_bit_exact_with_ties(dev, rows, n, k, sorted_out):
     s = _tie_heavy(rows, n, seed=n + k)
     got = SP.topk_indices(s.to(dev), k, sorted=sorted_out).cpu()
     ref = R.topk_indices(s, k, sorted_by_score=sorted_out)
     assert got.dtype == torch.int32
     assert torch.equal(got.long(), ref)
+
+
+@pytest.mark.parametrize("rows,n,k", [(3, 40000, 10000), (2, 65536, 16384), (2, 9000, 9000), (130, 20000, 12000)])
+def test_topk_large_k_unsorted(dev, rows, n, k):
+    """k above the sorted-output limit: the same set, by ascending index."""
+    s = _tie_heavy(rows, n, seed=n + k)
+    got = SP.topk_indices(s.to(dev), k, sorted=False).cpu()
+    assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=False))
+    with pytest.raises(ValueError):
+        SP.topk_indices(s.to(dev), k, sorted=True)
 
 
 def test_topk_unaligned_rows(dev):
