@@ -450,92 +450,97 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     const _Float16* vsb = a.vs + bh * (int64_t)Sq * C::NGV;
     const _Float16* vmb = a.vm + bh * (int64_t)Sq * C::NGV;
 
-    // Every value tile of this wave (a chunk holds at most two per wave) is
-    // requested up front, so it is in flight while the key chunk is staged.
-    constexpr int STEP = kKiviWaves * kKiviTile;
-    constexpr int NTW = kKiviChunkMax / STEP;
-    const int tw = t_begin + w * kKiviTile;
-    KiviRegs<D, BITS> rg[NTW];
-#pragma unroll
-    for (int it = 0; it < NTW; ++it) {
-      const int t = tw + it * STEP;
-      kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[it]);
-    }
-
-    // Q as the fp16 B operand (scaled by scale*log2e):
+    // Q as the fp16 B operand (scaled by scale*log2e), loaded first:
     //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
-    f16x8 qh[D / 32];
+    u32x4 qraw[D / 32];
     {
       const bool live = l16 < nh;
       const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * a.q_sh + lg * (D / 4);
 #pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) {
-        u32x4 raw = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
-        const bf16x8 qv = __builtin_bit_cast(bf16x8, raw);
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
-      }
+      for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
     }
 
-    // Stage the chunk's key codes: channel rows of (t_end - t_begin)*BITS/8 bytes,
-    // consecutive threads covering consecutive 16-byte pieces of a row, so every
-    // request is a whole cache line.
-    {
-      constexpr int NT = kKiviWaves * 64;
-      constexpr int PER = D * C::KPIECES / NT;
-      const int pieces = (t_end - t_begin) * BITS / 128;
-      const uint32_t* kqb = a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32;
-      const int64_t wk = Sq * BITS / 32;
-      u32x4 kv[PER];
+    // The chunk is staged in two halves of kKiviChunkMax/2 tokens, each the
+    // first (it = 0) or second (it = 1) tile of every wave.  Requests go out
+    // in the order key half 0, value tiles 0, key half 1, value tiles 1, so
+    // the first tiles start as soon as their own bytes have arrived while the
+    // second half is still in flight.
+    //   keys: channel rows of 16-byte pieces, consecutive threads covering
+    //   consecutive pieces of a row; key scales/zeros two groups per 4-byte word.
+    constexpr int STEP = kKiviWaves * kKiviTile;
+    constexpr int NTW = kKiviChunkMax / STEP;
+    static_assert(NTW == 2, "two halves, one tile per wave each");
+    constexpr int NT = kKiviWaves * 64;
+    constexpr int HP = C::KPIECES / 2;               // key pieces per channel per half
+    constexpr int PERH = D * HP / NT;                // key pieces per thread per half
+    constexpr int WRH = C::KMG / 4;                  // meta words per (scale|zero, channel) per half
+    constexpr int PERMH = 2 * D * WRH / NT;
+    const int pieces = (t_end - t_begin) * BITS / 128;
+    const int nwr = ngs >> 1;
+    const uint32_t* kqb = a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32;
+    const int64_t wk = Sq * BITS / 32;
+    const int tw = t_begin + w * kKiviTile;
+    u32x4 kv[NTW][PERH];
+    uint32_t mv[NTW][PERMH];
+    KiviRegs<D, BITS> rg[NTW];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
+    for (int ph = 0; ph < NTW; ++ph) {
+#pragma unroll
+      for (int i = 0; i < PERH; ++i) {
         const int pc = threadIdx.x + NT * i;
-        const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
-        kv[i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
+        const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
+        kv[ph][i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
       }
-      // key scales/zeros: rows (sm, ch) of ngs fp16, two groups per 4-byte load
-      constexpr int WR = C::KMG / 2;
-      constexpr int PERM = 2 * D * WR / NT;
-      const int nwr = ngs >> 1;
-      uint32_t mv[PERM];
 #pragma unroll
-      for (int i = 0; i < PERM; ++i) {
+      for (int i = 0; i < PERMH; ++i) {
         const int pc = threadIdx.x + NT * i;
-        const int row = pc / WR, wi = pc - row * WR;
+        const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
         const int sm = row / D, ch = row - sm * D;
         const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? a.km : a.ks) + (bh * D + ch) * ngk + g_lo);
-        mv[i] = src[min(wi, nwr - 1)];
+        mv[ph][i] = src[min(wi, nwr - 1)];
+      }
+      const int t = tw + ph * STEP;
+      kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[ph]);
+    }
+
+    f16x8 qh[D / 32];
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, qraw[kk]);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
+    }
+
+    _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
+#pragma unroll
+    for (int ph = 0; ph < NTW; ++ph) {
+      // this half's key codes and scales/zeros into LDS
+#pragma unroll
+      for (int i = 0; i < PERH; ++i) {
+        const int pc = threadIdx.x + NT * i;
+        const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
+        if (q < pieces) *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[ph][i];
       }
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
+      for (int i = 0; i < PERMH; ++i) {
         const int pc = threadIdx.x + NT * i;
-        const int ch = pc / C::KPIECES, q = pc - ch * C::KPIECES;
-        if (q < pieces) *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[i];
-      }
-      _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
-#pragma unroll
-      for (int i = 0; i < PERM; ++i) {
-        const int pc = threadIdx.x + NT * i;
-        const int row = pc / WR, wi = pc - row * WR;
+        const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
         const int sm = row / D, ch = row - sm * D;
         if (wi < nwr) {
           _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
-          dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] & 0xFFFFu));
-          dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[i] >> 16));
+          dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] & 0xFFFFu));
+          dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
         }
       }
-    }
-    __syncthreads();
-
-#pragma unroll
-    for (int it = 0; it < NTW; ++it) {
-      const int t = tw + it * STEP;
-      if (t >= t_end) break;
-      wave_lds_sync();
-      kivi_stage<D, BITS>(lane, rg[it], vst, vml);
-      wave_lds_sync();
-      const int off = t - t_begin;
-      kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
+      __syncthreads();
+      const int t = tw + ph * STEP;
+      if (t < t_end) {
+        wave_lds_sync();
+        kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
+        wave_lds_sync();
+        const int off = t - t_begin;
+        kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
+      }
     }
   }
   splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
