@@ -151,10 +151,10 @@ def stream_of(t: torch.Tensor) -> int:
 
 # ---------------------------------------------------------------------------
 # Workspaces: zero-initialised byte buffers, one per (device, family).  The
-# split-K decode kernels (dense, KIVI, gather) share the "splitk" family: they
-# leave their arrival counters at zero when they finish.  The top-k kernels
-# keep a histogram and list counters that they also leave at zero, in a
-# buffer of their own ("topk").  A buffer is cleared only when it is
+# split-K decode kernels (dense, KIVI, gather, PQ) share the "splitk" family
+# for their per-split partials.  The top-k kernels keep a histogram and list
+# counters that they leave at zero when they finish, in a buffer of their own
+# ("topk").  A buffer is cleared only when it is
 # (re)allocated; it grows on demand, and the usual warm-up call before a graph
 # capture sizes it.  Calls that share a buffer must be ordered on one stream
 # (the reference harness runs everything on the current stream).

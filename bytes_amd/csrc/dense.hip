@@ -141,7 +141,7 @@ static int dense_decode(bool fp8, const void* q, const void* k, const void* v, v
   a.o.out_dtype = kOutBF16;
   a.o.o_sb = o_sb; a.o.o_sh = o_sh;
   a.o.Hk = Hk; a.o.HB = HB; a.o.G = G;
-  splitk_carve(workspace, units, ns, a.o, /*allow_fused=*/false);
+  splitk_carve(workspace, units, ns, a.o);
   dim3 grid((unsigned)(ns * units));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64) {

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKO
 }
 
 int splitk_combine(const SplitKOut& o, long units, int D, hipStream_t stream) {
-  if (o.nsplit <= 1 || o.fused) return 0;
+  if (o.nsplit <= 1) return 0;
   if (o.nsplit > kSplitMax) return (int)hipErrorInvalidValue;
   dim3 grid((unsigned)units, 16);
   if (D == 64)
