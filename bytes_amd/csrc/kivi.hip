@@ -124,6 +124,7 @@ struct KiviArgs {
   int64_t kr_sb, kr_sh, kr_ss, vr_sb, vr_sh, vr_ss;
   int Hk, G, HB, Sq, R, chunk, nsq;
   int rsplit;               // 1: the residual window is split nsq of its own
+  int rchunk;               // rsplit == 0: residual tokens per piece (pieces ride on the last splits)
   float scale_log2;
   SplitKOut o;
 };
@@ -402,19 +403,23 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
 
   // The bf16 residual window [0, R) runs with the dense tile loop either as a
   // split of its own (a.rsplit: split nsq, when the extra workgroups still fit
-  // on the device at once) or ahead of the last split's quantized chunk; then
+  // on the device at once) or in pieces of a.rchunk tokens ahead of the
+  // quantized chunks of the last splits (piece i on split nsplit-1-i); then
   // (2-bit) the accumulator moves to the 2-bit value layout so the quantized
   // tiles continue the same state.
   const bool resid_only = a.rsplit && a.R > 0 && split == a.nsq;
-  const bool resid_first = !a.rsplit && a.R > 0 && split == a.o.nsplit - 1;
+  const int rpiece = a.o.nsplit - 1 - split;
+  const int r_begin = resid_only ? 0 : rpiece * a.rchunk;
+  const int r_end = resid_only ? a.R : min(r_begin + a.rchunk, a.R);
+  const bool resid_first = !a.rsplit && a.R > 0 && r_begin < r_end;
   if (resid_only || resid_first) {
     bf16x8 qb[D / 32];
     load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
     const uint16_t* kbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
     const uint16_t* vbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
     char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
-    dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, 0, a.R, w, lane, a.scale_log2, qb, wbuf, m_run, l_run,
-                       acc);
+    dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, r_begin, r_end, w, lane, a.scale_log2, qb, wbuf, m_run,
+                       l_run, acc);
     if (BITS == 2 && resid_first) {
       static_assert(D * 16 * 4 <= DenseCfg<D>::WAVE, "relayout buffer fits the wave's tile buffers");
       float* buf = reinterpret_cast<float*>(wbuf);
@@ -651,6 +656,13 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.scale_log2 = scale * kLog2e;
   kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq, &a.rsplit);
   const int ns = a.nsq + a.rsplit;                       // quantized chunks, then the residual's own split
+  // otherwise the residual is cut into up to 4 pieces of whole 32-token tiles
+  {
+    const int pieces = a.nsq < 4 ? (a.nsq > 0 ? a.nsq : 1) : 4;
+    const int per = (R + pieces - 1) / pieces;
+    a.rchunk = (per + kTile - 1) / kTile * kTile;
+    if (a.rchunk < kTile) a.rchunk = kTile;
+  }
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
   a.o.out = out;
