@@ -36,6 +36,16 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// 16-byte load issued by every lane (p must be readable for all of them),
+// zeroed afterwards where !live.  A load under a lane mask makes the compiler
+// merge its result with the masked-off value right after the load, which waits
+// for every load issued before it; loading unconditionally keeps such loads in
+// flight together.
+__device__ __forceinline__ u32x4 ld16_live(const void* p, bool live) {
+  const u32x4 v = ld16(p);
+  return live ? v : u32x4{0, 0, 0, 0};
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }

@@ -296,7 +296,7 @@ __device__ __forceinline__ void load_q_bf16(const uint16_t* qrow0, int64_t q_sh,
   const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * q_sh + lg * 8;
 #pragma unroll
   for (int kk = 0; kk < D / 32; ++kk) {
-    u32x4 raw = live ? ld16(qp + kk * 32) : u32x4{0, 0, 0, 0};
+    u32x4 raw = ld16_live(qp + kk * 32, live);
     qb[kk] = __builtin_bit_cast(bf16x8, raw);
   }
 }

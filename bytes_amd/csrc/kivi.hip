@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
       const bool live = l16 < nh;
       const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * a.q_sh + lg * (D / 4);
 #pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
+      for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = ld16_live(qp + kk * 8, live);
     }
 
     // The chunk is staged in two halves of kKiviChunkMax/2 tokens, each the
@@ -506,6 +506,9 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
       }
       const int t = tw + ph * STEP;
       kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[ph]);
+      // keep the compiler from interleaving the two halves' requests: the
+      // first tiles wait only for what was issued before this point
+      __builtin_amdgcn_sched_barrier(0);
     }
 
     f16x8 qh[D / 32];
@@ -519,30 +522,31 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
 #pragma unroll
     for (int ph = 0; ph < NTW; ++ph) {
-      // this half's key codes and scales/zeros into LDS
+      // this half's key codes and scales/zeros into LDS, stored unconditionally
+      // (pieces and groups past the chunk end hold clamped copies no tile
+      // reads): a store under a lane mask lets the compiler sink the load
+      // feeding it down to the store, behind waits for every earlier load
 #pragma unroll
       for (int i = 0; i < PERH; ++i) {
         const int pc = threadIdx.x + NT * i;
         const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
-        if (q < pieces) *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[ph][i];
+        *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[ph][i];
       }
 #pragma unroll
       for (int i = 0; i < PERMH; ++i) {
         const int pc = threadIdx.x + NT * i;
         const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
         const int sm = row / D, ch = row - sm * D;
-        if (wi < nwr) {
-          _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
-          dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] & 0xFFFFu));
-          dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
-        }
+        _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
+        dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] & 0xFFFFu));
+        dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
       }
       __syncthreads();
       const int t = tw + ph * STEP;
+      wave_lds_sync();
+      kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
+      wave_lds_sync();
       if (t < t_end) {
-        wave_lds_sync();
-        kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
-        wave_lds_sync();
         const int off = t - t_begin;
         kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
       }

@@ -87,7 +87,7 @@ struct DenseKeys {
     const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + (live ? l16 : 0)) * a.q_sh + lg * 8;
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk)
-      qa[kk] = __builtin_bit_cast(bf16x8, live ? ld16(qp + kk * 32) : u32x4{0, 0, 0, 0});
+      qa[kk] = __builtin_bit_cast(bf16x8, ld16_live(qp + kk * 32, live));
   }
 
   // K rows t .. t+63 of one iteration as B operands (rows clamped to S-1).
@@ -239,7 +239,7 @@ struct PackedKeys {
         const uint16_t* qp = qrow + (int64_t)(hq0 + (live ? h : 0)) * a.q_sh;
 #pragma unroll
         for (int kk = 0; kk < NG; ++kk) {
-          const u32x4 raw = live ? ld16(qp + kk * 8) : u32x4{0, 0, 0, 0};
+          const u32x4 raw = ld16_live(qp + kk * 8, live);
           uint16_t e[8];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {

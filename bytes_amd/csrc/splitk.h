@@ -21,8 +21,8 @@ struct SplitKOut {
   void* out;            // [B, Hq, D] with element strides o_sb, o_sh (d stride 1)
   int out_dtype;        // OutDtype
   int64_t o_sb, o_sh;
-  float* part_acc;      // [units][nsplit][16][D]
-  float* part_ml;       // [units][nsplit][16][2]
+  float* part_acc;      // [units][16][nsplit][D]: a head's splits are contiguous
+  float* part_ml;       // [units][16][nsplit][2]
   int nsplit;
   int Hk, HB, G;        // unit u -> b = u / (Hk*HB), hk, hb; query head = hk*G + hb*hbs + h
   int hbs = 16;         // query heads per head block
@@ -147,16 +147,16 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
     }
     return;
   }
-  const size_t row0 = ((size_t)unit * o.nsplit + split) * 16;
   for (int e = threadIdx.x; e < nh * D; e += NT) {
     const int h = e / D, d = e - h * D;
     float A = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * 16 + h];
-    o.part_acc[(row0 + h) * D + d] = A;
+    const size_t row = ((size_t)unit * 16 + h) * o.nsplit + split;
+    o.part_acc[row * D + d] = A;
     if (d == 0) {
-      o.part_ml[(row0 + h) * 2 + 0] = wm[h];
-      o.part_ml[(row0 + h) * 2 + 1] = wf[NW * 16 + h];
+      o.part_ml[row * 2 + 0] = wm[h];
+      o.part_ml[row * 2 + 1] = wf[NW * 16 + h];
     }
   }
 }

@@ -1,125 +1,114 @@
 // Deterministic merge of split-K flash-decode partials (see splitk.h).
 //
-// One workgroup per (unit, head): out = sum_s f_s acc_s / sum_s f_s l_s with
-// f_s = 2^(m_s - max_s m_s).  Splits are assigned to thread groups by a fixed
-// rule and the group sums are added in a fixed order, so the result is
-// bit-reproducible run to run.
+// out = sum_s f_s acc_s / sum_s f_s l_s with f_s = 2^(m_s - max_s m_s).
+//
+// One wave per (unit, head, 64-dim slice of the head row): a launch of
+// units x heads x D/64 single-wave workgroups, no LDS and no barrier.  The
+// 64 lanes are 16 float4 items of the slice x 4 split groups; lane (g, item)
+// takes splits g, g+4, ... of each block of 64 splits, and all of a block's
+// loads (the acc rows and every split's (m, l)) are issued before any is
+// used, so a block costs one memory round trip.  Split groups are folded by
+// a fixed butterfly, so the result is bit-reproducible run to run.
 #include "splitk.h"
 
 namespace bytes_amd {
 
-constexpr int kCombineThreads = 256;
 constexpr int kSplitMax = 1024;
-constexpr int kSplitPerLane = kSplitMax / 64;
+constexpr int kCombItems = 16;                    // float4 items per wave (64 dims)
+constexpr int kCombGroups = 64 / kCombItems;      // split groups per wave
 
-template <int D>
-__global__ __launch_bounds__(kCombineThreads) void splitk_combine_kernel(SplitKOut o) {
-  constexpr int ITEMS = D / 4;                      // float4 items per head row
-  constexpr int GROUPS = kCombineThreads / ITEMS;   // split groups
-  constexpr int PF = 8;                             // acc loads per thread issued up front
-  __shared__ float fw[kSplitMax];
-  __shared__ float red[2][64];
-  __shared__ float4 gacc[GROUPS][ITEMS];
-  const int unit = blockIdx.x, h = blockIdx.y;
+template <int D, int PF>
+__global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
+  static_assert(kCombGroups * PF <= 64, "one block of at most 64 splits per pass");
+  const int unit = blockIdx.x, h = blockIdx.y, slice = blockIdx.z;
   const int b = unit / (o.Hk * o.HB);
   const int rem = unit - b * o.Hk * o.HB;
   const int hk = rem / o.HB, hb = rem - (rem / o.HB) * o.HB;
   const int nh = min(o.hbs, o.G - hb * o.hbs);
   if (h >= nh) return;
-  const int ns = o.nsplit, tid = threadIdx.x, lane = tid & 63;
-  const size_t base = (size_t)unit * ns * 16 + h;
+  const int lane = threadIdx.x, item = lane % kCombItems, g = lane / kCombItems;
+  const int ns = o.nsplit;
+  const size_t hrow = ((size_t)unit * 16 + h) * ns;   // row of split 0 of this head
+  const float4* src = reinterpret_cast<const float4*>(o.part_acc + hrow * D) + slice * kCombItems + item;
+  const float2* mlp = reinterpret_cast<const float2*>(o.part_ml) + hrow;
+  constexpr int ROW4 = D / 4;
 
-  // Issue the first PF acc rows of this thread's splits and (wave 0) every
-  // split's (m, l) before consuming any of them: one memory round trip.
-  const int item = tid % ITEMS, g = tid / ITEMS;
-  const float4* src = reinterpret_cast<const float4*>(o.part_acc + base * D) + item;
-  const size_t stride4 = (size_t)16 * D / 4;
+  // Block 0: every load unconditional (split index clamped to ns - 1, the
+  // surplus weighted by 0), all in flight together.
+  float2 mlv = mlp[min(lane, ns - 1)];
   float4 pv[PF];
 #pragma unroll
-  for (int u = 0; u < PF; ++u) {
-    const int s = g + u * GROUPS;
-    pv[u] = s < ns ? src[(size_t)s * stride4] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  float m_loc = kNegInf;
-  float mv[kSplitPerLane], lv[kSplitPerLane];
-#pragma unroll
-  for (int k = 0; k < kSplitPerLane; ++k) {
-    const int s = lane + 64 * k;
-    if (tid < 64 && s < ns) {
-      const float2 ml = *reinterpret_cast<const float2*>(o.part_ml + (base + (size_t)s * 16) * 2);
-      mv[k] = ml.x;
-      lv[k] = ml.y;
-    } else {
-      mv[k] = kNegInf;
-      lv[k] = 0.f;
-    }
-    m_loc = fmaxf(m_loc, mv[k]);
-  }
-  if (tid < 64) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m_loc = fmaxf(m_loc, shfl_xor_f(m_loc, off));
-    const float Ms = (m_loc == kNegInf) ? 0.f : m_loc;
-    float l_loc = 0.f;
-#pragma unroll
-    for (int k = 0; k < kSplitPerLane; ++k) {
-      const int s = lane + 64 * k;
-      if (s < ns) {
-        const float f = fast_exp2(mv[k] - Ms);
-        fw[s] = f;
-        l_loc += f * lv[k];
-      }
-    }
-    red[0][lane] = l_loc;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float L = 0.f;
-    for (int i = 0; i < 64; ++i) L += red[0][i];
-    red[1][0] = 1.f / L;
-  }
+  for (int u = 0; u < PF; ++u) pv[u] = src[(size_t)min(g + u * kCombGroups, ns - 1) * ROW4];
 
-  // weighted sum: thread (group g, item) takes splits s = g, g+GROUPS, ... in order
-  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+  float M;
+  if (ns <= 64) {
+    M = lane < ns ? mlv.x : kNegInf;
+  } else {
+    M = kNegInf;
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, mlp[s].x);
+  }
 #pragma unroll
-  for (int u = 0; u < PF; ++u) {
-    const int s = g + u * GROUPS;
-    if (s < ns) {
-      const float f = fw[s];
-      A.x += f * pv[u].x; A.y += f * pv[u].y; A.z += f * pv[u].z; A.w += f * pv[u].w;
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f(M, off));
+  if (M == kNegInf) M = 0.f;
+
+  float L = 0.f;
+  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    if (s0 > 0) {
+      mlv = mlp[min(s0 + lane, ns - 1)];
+#pragma unroll
+      for (int u = 0; u < PF; ++u) pv[u] = src[(size_t)min(s0 + g + u * kCombGroups, ns - 1) * ROW4];
+    }
+    const bool in = s0 + lane < ns;
+    const float f = in ? fast_exp2(mlv.x - M) : 0.f;
+    L += in ? f * mlv.y : 0.f;
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int s = g + u * kCombGroups;
+      const float w = __shfl(f, s, 64);     // 0 for splits past ns
+      A.x += w * pv[u].x; A.y += w * pv[u].y; A.z += w * pv[u].z; A.w += w * pv[u].w;
     }
   }
-  for (int s = g + PF * GROUPS; s < ns; s += GROUPS) {
-    const float4 v = src[(size_t)s * stride4];
-    const float f = fw[s];
-    A.x += f * v.x; A.y += f * v.y; A.z += f * v.z; A.w += f * v.w;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) L += shfl_xor_f(L, off);
+#pragma unroll
+  for (int off = kCombItems; off < 64; off <<= 1) {
+    A.x += shfl_xor_f(A.x, off); A.y += shfl_xor_f(A.y, off); A.z += shfl_xor_f(A.z, off); A.w += shfl_xor_f(A.w, off);
   }
-  gacc[g][item] = A;
-  __syncthreads();
   if (g == 0) {
-    float4 T = gacc[0][item];
-    for (int gg = 1; gg < GROUPS; ++gg) {
-      const float4 v = gacc[gg][item];
-      T.x += v.x; T.y += v.y; T.z += v.z; T.w += v.w;
-    }
-    const float il = red[1][0];
-    const int hq = hk * o.G + hb * o.hbs + h, d = item * 4;
-    store_out(o, b, hq, d + 0, T.x * il);
-    store_out(o, b, hq, d + 1, T.y * il);
-    store_out(o, b, hq, d + 2, T.z * il);
-    store_out(o, b, hq, d + 3, T.w * il);
+    const float il = 1.f / L;
+    const int hq = hk * o.G + hb * o.hbs + h, d = (slice * kCombItems + item) * 4;
+    store_out(o, b, hq, d + 0, A.x * il);
+    store_out(o, b, hq, d + 1, A.y * il);
+    store_out(o, b, hq, d + 2, A.z * il);
+    store_out(o, b, hq, d + 3, A.w * il);
   }
+}
+
+template <int D>
+static void launch_combine(const SplitKOut& o, dim3 grid, hipStream_t stream) {
+  // acc loads per lane per block: enough for min(ns, 64) splits over the 4 groups
+  const int need = ((o.nsplit < 64 ? o.nsplit : 64) + kCombGroups - 1) / kCombGroups;
+  if (need <= 2)
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 2>), grid, dim3(64), 0, stream, o);
+  else if (need <= 4)
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 4>), grid, dim3(64), 0, stream, o);
+  else if (need <= 8)
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 8>), grid, dim3(64), 0, stream, o);
+  else
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 16>), grid, dim3(64), 0, stream, o);
 }
 
 int splitk_combine(const SplitKOut& o, long units, int D, hipStream_t stream) {
   if (o.nsplit <= 1) return 0;
   if (o.nsplit > kSplitMax) return (int)hipErrorInvalidValue;
-  dim3 grid((unsigned)units, 16);
+  if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  // one wave per (unit, query head of the unit's head block, 64-dim slice)
+  const dim3 grid((unsigned)units, (unsigned)(o.G < o.hbs ? o.G : o.hbs), (unsigned)(D / 64));
   if (D == 64)
-    hipLaunchKernelGGL(splitk_combine_kernel<64>, grid, dim3(kCombineThreads), 0, stream, o);
-  else if (D == 128)
-    hipLaunchKernelGGL(splitk_combine_kernel<128>, grid, dim3(kCombineThreads), 0, stream, o);
+    launch_combine<64>(o, grid, stream);
   else
-    return (int)hipErrorInvalidValue;
+    launch_combine<128>(o, grid, stream);
   return (int)hipGetLastError();
 }
 
