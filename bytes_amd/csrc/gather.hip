@@ -113,6 +113,10 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
     irow = a.idx + (int64_t)b * a.i_sb + (int64_t)hk * a.i_sh;
   }
 
+  // Q first: its load is then in flight with the index loads below
+  bf16x8 qb[C::KK];
+  load_q_bf16<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, nh, lane, qb);
+
   const int p_begin = split * a.chunk;
   const int n = min(a.chunk, a.kb - p_begin);
   for (int i = threadIdx.x; i < n; i += kGatherWaves * 64) {
@@ -130,9 +134,6 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
     }
     rows[i] = (ok && r < a.limit) ? (int)r : -1;
   }
-
-  bf16x8 qb[C::KK];
-  load_q_bf16<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, nh, lane, qb);
   __syncthreads();
 
   float m_run = kNegInf, l_run = 0.f;

@@ -77,22 +77,41 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
   const int bh = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
   const int b = bh / Hk, hk = bh - (bh / Hk) * Hk;
   const int p0 = part * kQuestPages;
-  for (int i = threadIdx.x; i < G * D; i += kQuestThreads) {
+  // Every load is issued before any LDS store that consumes one (indices
+  // clamped, so no load sits under a lane mask): one memory round trip.
+  constexpr int QPT = 16 * D / kQuestThreads;      // query elements per thread (G <= 16)
+  constexpr int CH = D / 8;                        // 16-byte chunks per row
+  constexpr int MPT = kQuestPages * CH / kQuestThreads;   // min/max chunks per thread
+  uint16_t qv[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = min((int)threadIdx.x + u * kQuestThreads, G * D - 1);
     const int g = i / D, d = i - (i / D) * D;
-    qs[g][d] = bf16_bits_to_f32(q[(int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d]);
+    qv[u] = q[(int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d];
   }
   const int64_t row0 = ((int64_t)b * Hk + hk) * np;
-  constexpr int CH = D / 8;                        // 16-byte chunks per row
-  for (int e = threadIdx.x; e < kQuestPages * CH; e += kQuestThreads) {
-    const int pp = e / CH, c = e - (e / CH) * CH;
-    if (p0 + pp < np) {
-      const u32x4 a = ld16(kmin + (row0 + p0 + pp) * D + c * 8);
-      const u32x4 z = ld16(kmax + (row0 + p0 + pp) * D + c * 8);
+  u32x4 av[MPT], zv[MPT];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        mn_s[pp * RW + c * 4 + j] = a[j];
-        mx_s[pp * RW + c * 4 + j] = z[j];
-      }
+  for (int u = 0; u < MPT; ++u) {
+    const int e = threadIdx.x + u * kQuestThreads;
+    const int pp = e / CH, c = e - (e / CH) * CH;
+    const int64_t r = row0 + min(p0 + pp, np - 1);  // pages past np: copies nothing reads
+    av[u] = ld16(kmin + r * D + c * 8);
+    zv[u] = ld16(kmax + r * D + c * 8);
+  }
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = threadIdx.x + u * kQuestThreads;   // < 16 * D: rows past G are unused
+    qs[i / D][i - (i / D) * D] = bf16_bits_to_f32(qv[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < MPT; ++u) {
+    const int e = threadIdx.x + u * kQuestThreads;
+    const int pp = e / CH, c = e - (e / CH) * CH;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mn_s[pp * RW + c * 4 + j] = av[u][j];
+      mx_s[pp * RW + c * 4 + j] = zv[u][j];
     }
   }
   __syncthreads();

@@ -5,7 +5,7 @@
 // One wave per (unit, head, 64-dim slice of the head row): a launch of
 // units x heads x D/64 single-wave workgroups, no LDS and no barrier.  The
 // 64 lanes are 16 float4 items of the slice x 4 split groups; lane (g, item)
-// takes splits g, g+4, ... of each block of 64 splits, and all of a block's
+// takes splits g, g+4, ... of each block of up to 128 splits, and all of a block's
 // loads (the acc rows and every split's (m, l)) are issued before any is
 // used, so a block costs one memory round trip.  Split groups are folded by
 // a fixed butterfly, so the result is bit-reproducible run to run.
@@ -19,7 +19,9 @@ constexpr int kCombGroups = 64 / kCombItems;      // split groups per wave
 
 template <int D, int PF>
 __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
-  static_assert(kCombGroups * PF <= 64, "one block of at most 64 splits per pass");
+  constexpr int BLK = kCombGroups * PF;           // splits per block
+  constexpr int MB = (BLK + 63) / 64;             // (m, l) pairs per lane per block
+  static_assert(BLK <= 128, "at most two (m, l) pairs per lane");
   const int unit = blockIdx.x, h = blockIdx.y, slice = blockIdx.z;
   const int b = unit / (o.Hk * o.HB);
   const int rem = unit - b * o.Hk * o.HB;
@@ -35,17 +37,25 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
 
   // Block 0: every load unconditional (split index clamped to ns - 1, the
   // surplus weighted by 0), all in flight together.
-  float2 mlv = mlp[min(lane, ns - 1)];
+  float2 mlv[MB];
   float4 pv[PF];
+#pragma unroll
+  for (int k = 0; k < MB; ++k) mlv[k] = mlp[min(lane + 64 * k, ns - 1)];
 #pragma unroll
   for (int u = 0; u < PF; ++u) pv[u] = src[(size_t)min(g + u * kCombGroups, ns - 1) * ROW4];
 
-  float M;
-  if (ns <= 64) {
-    M = lane < ns ? mlv.x : kNegInf;
+  float M = kNegInf;
+  if (ns <= BLK) {
+#pragma unroll
+    for (int k = 0; k < MB; ++k) M = fmaxf(M, lane + 64 * k < ns ? mlv[k].x : kNegInf);
   } else {
-    M = kNegInf;
-    for (int s = lane; s < ns; s += 64) M = fmaxf(M, mlp[s].x);
+    for (int s = lane; s < ns; s += 256) {
+      float m4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) m4[k] = mlp[min(s + 64 * k, ns - 1)].x;   // clamped repeats are harmless
+#pragma unroll
+      for (int k = 0; k < 4; ++k) M = fmaxf(M, m4[k]);
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f(M, off));
@@ -53,19 +63,24 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
 
   float L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < ns; s0 += 64) {
+  for (int s0 = 0; s0 < ns; s0 += BLK) {
     if (s0 > 0) {
-      mlv = mlp[min(s0 + lane, ns - 1)];
+#pragma unroll
+      for (int k = 0; k < MB; ++k) mlv[k] = mlp[min(s0 + lane + 64 * k, ns - 1)];
 #pragma unroll
       for (int u = 0; u < PF; ++u) pv[u] = src[(size_t)min(s0 + g + u * kCombGroups, ns - 1) * ROW4];
     }
-    const bool in = s0 + lane < ns;
-    const float f = in ? fast_exp2(mlv.x - M) : 0.f;
-    L += in ? f * mlv.y : 0.f;
+    float f[MB];
+#pragma unroll
+    for (int k = 0; k < MB; ++k) {
+      const bool in = s0 + lane + 64 * k < ns;
+      f[k] = in ? fast_exp2(mlv[k].x - M) : 0.f;
+      L += in ? f[k] * mlv[k].y : 0.f;
+    }
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
-      const int s = g + u * kCombGroups;
-      const float w = __shfl(f, s, 64);     // 0 for splits past ns
+      // split g + 4u of the block: its weight sits in lane (g + 4u) % 64, pair u / 16
+      const float w = __shfl(f[u / 16], (g + u * kCombGroups) & 63, 64);   // 0 past ns
       A.x += w * pv[u].x; A.y += w * pv[u].y; A.z += w * pv[u].z; A.w += w * pv[u].w;
     }
   }
@@ -87,16 +102,18 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
 
 template <int D>
 static void launch_combine(const SplitKOut& o, dim3 grid, hipStream_t stream) {
-  // acc loads per lane per block: enough for min(ns, 64) splits over the 4 groups
-  const int need = ((o.nsplit < 64 ? o.nsplit : 64) + kCombGroups - 1) / kCombGroups;
+  // acc loads per lane per block: enough for min(ns, 128) splits over the 4 groups
+  const int need = ((o.nsplit < 128 ? o.nsplit : 128) + kCombGroups - 1) / kCombGroups;
   if (need <= 2)
     hipLaunchKernelGGL((splitk_combine_kernel<D, 2>), grid, dim3(64), 0, stream, o);
   else if (need <= 4)
     hipLaunchKernelGGL((splitk_combine_kernel<D, 4>), grid, dim3(64), 0, stream, o);
   else if (need <= 8)
     hipLaunchKernelGGL((splitk_combine_kernel<D, 8>), grid, dim3(64), 0, stream, o);
-  else
+  else if (need <= 16)
     hipLaunchKernelGGL((splitk_combine_kernel<D, 16>), grid, dim3(64), 0, stream, o);
+  else
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 32>), grid, dim3(64), 0, stream, o);
 }
 
 int splitk_combine(const SplitKOut& o, long units, int D, hipStream_t stream) {

@@ -90,7 +90,7 @@ def test_dense_back_to_back_calls_share_the_workspace(dev):
 
 
 def test_dense_many_splits_use_the_merge_kernel(dev):
-    # chunk 128 over 40000 tokens: 313 splits, above the in-kernel merge limit
+    # chunk 128 over 40000 tokens: 313 splits, several blocks of the merge kernel
     x = W.dense(1, 8, 1, 128, 40000, seed=9)
     out = AK.decode_attn_bf16(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), 0.09, chunk=128)
     _check(out, R.decode_attn(x["q"], x["k"], x["v"], scale=0.09), "313 splits")

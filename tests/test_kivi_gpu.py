@@ -119,5 +119,5 @@ def test_decode_back_to_back_calls(dev):
 
 
 def test_decode_many_splits_use_the_merge_kernel(dev):
-    # chunk 256 over 69120 packed tokens: 270 splits, above the in-kernel merge limit
+    # chunk 256 over 69120 packed tokens: 270 splits, several blocks of the merge kernel
     _decode_case(dev, 2, 1, 7, 1, 128, 69120 + 32, 32, seed=6, chunk=256)
