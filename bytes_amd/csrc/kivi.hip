@@ -210,6 +210,28 @@ __device__ __forceinline__ f16x8 deq_fp8(uint32_t lo, uint32_t hi, u32x4 s, u32x
   return __builtin_bit_cast(f16x8, r);
 }
 
+// 8 fp4 nibbles (2-bit codes c -> value c/2) -> the 8 codes as fp16 (exact).
+__device__ __forceinline__ f16x8 codes_fp4(uint32_t dw) {
+  const u32x4 r = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 0)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 1)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 2)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 3))};
+  return __builtin_bit_cast(f16x8, r);
+}
+
+// lo/hi: 4 bytes each holding a 4-bit code (fp8 e4m3 value c*2^-9) -> the 8
+// codes as fp16, k-slots in the order of deq_fp8.
+__device__ __forceinline__ f16x8 codes_fp8(uint32_t lo, uint32_t hi) {
+  const u32x4 r = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true))};
+  return __builtin_bit_cast(f16x8, r);
+}
+
+// Elementwise fp16 product of an operand and 8 fp16 scales.
+__device__ __forceinline__ f16x8 scale8(f16x8 x, u32x4 s) { return x * __builtin_bit_cast(f16x8, s); }
+
 template <int D>
 using VMetaReg = typename std::conditional<(D >= 128), u32x4, u32x2>::type;
 
@@ -257,10 +279,19 @@ __device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg
 // One 64-token tile: scores from the workgroup's staged key chunk (kc points at
 // this tile's first byte of channel row 0), online softmax, value accumulation
 // from the wave's staged value tile.
+//
+// Scales are folded into the other MFMA operand, so codes enter the MFMAs as
+// exact fp16 integers:
+//   keys   s[t][h] = sum_c (q[h][c] sc[c][g]) code[t][c] + sum_c q[h][c] zero[c][g]
+//          (g = key group of t; the second sum is one MFMA chain on the zeros,
+//          whose A rows are all equal, and initialises the score tile);
+//   values o[c][h] += sum_t code[t][c] (p[h][t] vs[t][g]) + sum_t p[h][t] vm[t][g]
+//          (g = value group of channel c; the second sum accumulates in zv,
+//          rows = groups, and is added to acc once after the last tile).
 template <int D, int BITS>
 __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[D / 32], const char* kc,
                                           const char* vst, const char* vmeta_lds, const char* kmeta, float& m_run,
-                                          float& l_run, f32x4 (&acc)[D / 16]) {
+                                          float& l_run, f32x4 (&acc)[D / 16], f32x4& zv) {
   using C = KiviCfg<D, BITS>;
   const int l16 = lane & 15, lg = lane >> 4;
   constexpr int KMG = C::KMG;
@@ -274,31 +305,42 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
 #pragma unroll
   for (int u = 0; u < 4; ++u) sc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int blk = 0; blk < 4; ++blk) {
-    // 2-bit: blk = sub-tile sg (blk < 2); 4-bit: blk = 16-token block tb
-    if (BITS == 2 && blk >= 2) break;
-    const int grp = grp0 + (BITS == 2 ? blk : (blk >> 1));
-    u32x4 ksp[C::KK], kzp[C::KK];
+  for (int sg = 0; sg < 2; ++sg) {
+    // key group sg of the tile (tokens 32sg .. 32sg+31): Q scaled by the
+    // group's channel scales, and the zero term as the initial scores
+    const int grp = grp0 + sg;
+    f16x8 qs[C::KK];
+    f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) {
       const int off = (grp * D + lg * (D / 4) + kk * 8) * 2;
-      ksp[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kms) + off);
-      kzp[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kmz) + off);
+      const u32x4 ks = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kms) + off);
+      const u32x4 kz = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kmz) + off);
+      qs[kk] = scale8(qh[kk], ks);
+      z = mfma_f16(__builtin_bit_cast(f16x8, kz), qh[kk], z);
     }
+    // 2-bit: one 32-token block per group, even/odd tokens in sc[2sg], sc[2sg+1]
+    // 4-bit: two 16-token blocks per group, sc[2sg], sc[2sg+1]
+    sc[sg * 2 + 0] = z;
+    sc[sg * 2 + 1] = z;
 #pragma unroll
-    for (int rd = 0; rd < C::KK / 2; ++rd) {
-      const int ch = lg * (D / 4) + rd * 16 + l16;
-      const u32x2 x = tr4(kc + ch * C::KCROW + blk * 8);
+    for (int bb = 0; bb < (BITS == 2 ? 1 : 2); ++bb) {
+      const int blk = BITS == 2 ? sg : sg * 2 + bb;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int kk = rd * 2 + half;
-        if (BITS == 2) {
-          const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
-          sc[blk * 2 + 0] = mfma_f16(deq_fp4(e, ksp[kk], kzp[kk]), qh[kk], sc[blk * 2 + 0]);
-          sc[blk * 2 + 1] = mfma_f16(deq_fp4(od, ksp[kk], kzp[kk]), qh[kk], sc[blk * 2 + 1]);
-        } else {
-          const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
-          sc[blk] = mfma_f16(deq_fp8(lo, hi, ksp[kk], kzp[kk]), qh[kk], sc[blk]);
+      for (int rd = 0; rd < C::KK / 2; ++rd) {
+        const int ch = lg * (D / 4) + rd * 16 + l16;
+        const u32x2 x = tr4(kc + ch * C::KCROW + blk * 8);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int kk = rd * 2 + half;
+          if (BITS == 2) {
+            const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
+            sc[sg * 2 + 0] = mfma_f16(codes_fp4(e), qs[kk], sc[sg * 2 + 0]);
+            sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
+          } else {
+            const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
+            sc[blk] = mfma_f16(codes_fp8(lo, hi), qs[kk], sc[blk]);
+          }
         }
       }
     }
@@ -327,6 +369,7 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   m_run = m_new;
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
+  zv *= alpha;
 
   // P^T as the B operand, k-slot jj of sub-tile sg:
   //   2-bit: token 32sg + 8lg + jj  -> p[(sg*2 + jj%2)*4 + jj/2]
@@ -344,11 +387,15 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   const char* vml = vmeta_lds;
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    u32x4 vsp[C::NGV], vzp[C::NGV];
+    // P^T scaled by each value group's token scales; the zero term on MFMA
+    // rows = groups (lane row l16 reads group l16 % NGV, rows >= NGV unused)
+    f16x8 pg[C::NGV];
 #pragma unroll
-    for (int g = 0; g < C::NGV; ++g) {
-      vsp[g] = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16);
-      vzp[g] = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, g, sg * 32) * 2 + lg * 16);
+    for (int g = 0; g < C::NGV; ++g)
+      pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
+    {
+      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, l16 % C::NGV, sg * 32) * 2 + lg * 16);
+      zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
     }
     if (BITS == 2) {
       // cb = 32-channel block; one tr read covers cb pair (2rd, 2rd+1)
@@ -360,10 +407,10 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
         const int ca = 2 * rd, cbb = 2 * rd + 1;
         const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
         const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
-        acc[ca * 2 + 0] = mfma_f16(deq_fp4(e0, vsp[ca], vzp[ca]), pb[sg], acc[ca * 2 + 0]);
-        acc[cbb * 2 + 0] = mfma_f16(deq_fp4(e1, vsp[cbb], vzp[cbb]), pb[sg], acc[cbb * 2 + 0]);
-        acc[ca * 2 + 1] = mfma_f16(deq_fp4(o0, vsp[ca], vzp[ca]), pb[sg], acc[ca * 2 + 1]);
-        acc[cbb * 2 + 1] = mfma_f16(deq_fp4(o1, vsp[cbb], vzp[cbb]), pb[sg], acc[cbb * 2 + 1]);
+        acc[ca * 2 + 0] = mfma_f16(codes_fp4(e0), pg[ca], acc[ca * 2 + 0]);
+        acc[cbb * 2 + 0] = mfma_f16(codes_fp4(e1), pg[cbb], acc[cbb * 2 + 0]);
+        acc[ca * 2 + 1] = mfma_f16(codes_fp4(o0), pg[ca], acc[ca * 2 + 1]);
+        acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
       }
     } else {
       // cb = 16-channel block; one tr read covers cb pair (2rd, 2rd+1), both in group rd
@@ -374,8 +421,8 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
         const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
         const uint32_t lo0 = x[0] & 0x0F0F0F0Fu, hi0 = (x[0] >> 4) & 0x0F0F0F0Fu;
         const uint32_t lo1 = x[1] & 0x0F0F0F0Fu, hi1 = (x[1] >> 4) & 0x0F0F0F0Fu;
-        acc[2 * rd] = mfma_f16(deq_fp8(lo0, hi0, vsp[rd], vzp[rd]), pb[sg], acc[2 * rd]);
-        acc[2 * rd + 1] = mfma_f16(deq_fp8(lo1, hi1, vsp[rd], vzp[rd]), pb[sg], acc[2 * rd + 1]);
+        acc[2 * rd] = mfma_f16(codes_fp8(lo0, hi0), pg[rd], acc[2 * rd]);
+        acc[2 * rd + 1] = mfma_f16(codes_fp8(lo1, hi1), pg[rd], acc[2 * rd + 1]);
       }
     }
   }
@@ -466,10 +513,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     }
 
     // The chunk is staged in two halves of kKiviChunkMax/2 tokens, each the
-    // first (it = 0) or second (it = 1) tile of every wave.  Requests go out
-    // in the order key half 0, value tiles 0, key half 1, value tiles 1, so
-    // the first tiles start as soon as their own bytes have arrived while the
-    // second half is still in flight.
+    // first (ph = 0) or second (ph = 1) tile of every wave.
     //   keys: channel rows of 16-byte pieces, consecutive threads covering
     //   consecutive pieces of a row; key scales/zeros two groups per 4-byte word.
     constexpr int STEP = kKiviWaves * kKiviTile;
@@ -488,8 +532,8 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     u32x4 kv[NTW][PERH];
     uint32_t mv[NTW][PERMH];
     KiviRegs<D, BITS> rg[NTW];
-#pragma unroll
-    for (int ph = 0; ph < NTW; ++ph) {
+    auto issue = [&](auto phc) {
+      constexpr int ph = decltype(phc)::value;
 #pragma unroll
       for (int i = 0; i < PERH; ++i) {
         const int pc = threadIdx.x + NT * i;
@@ -506,10 +550,10 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
       }
       const int t = tw + ph * STEP;
       kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[ph]);
-      // keep the compiler from interleaving the two halves' requests: the
-      // first tiles wait only for what was issued before this point
+      // keep the compiler from moving requests across this point
       __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    issue(std::integral_constant<int, 0>());
 
     f16x8 qh[D / 32];
 #pragma unroll
@@ -520,6 +564,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     }
 
     _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
+    f32x4 zv = {0.f, 0.f, 0.f, 0.f};   // value zero term: row g = value group, column = head
 #pragma unroll
     for (int ph = 0; ph < NTW; ++ph) {
       // this half's key codes and scales/zeros into LDS, stored unconditionally
@@ -542,13 +587,30 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
         dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
       }
       __syncthreads();
+      // The second half is requested only once the first has arrived: every
+      // workgroup's first half then reaches the head of the memory queues
+      // before any second half, and the second half streams in while the
+      // first tiles run.
+      if (ph == 0) issue(std::integral_constant<int, 1>());
       const int t = tw + ph * STEP;
       wave_lds_sync();
       kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
       wave_lds_sync();
       if (t < t_end) {
         const int off = t - t_begin;
-        kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc);
+        kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc,
+                           zv);
+      }
+    }
+    // acc[db][i] holds a channel of value group db / 2 (both layouts): add
+    // that group's zero term, held by lane l16 of row group 0 at element g
+#pragma unroll
+    for (int g = 0; g < C::NGV; ++g) {
+      const float zg = __shfl(zv[g], l16, 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * g][i] += zg;
+        acc[2 * g + 1][i] += zg;
       }
     }
   }

@@ -78,10 +78,15 @@ __device__ __forceinline__ void store_out(const SplitKOut& o, int b, int hq, int
   }
 }
 
+// Floats per (wave, head-dim) row of the epilogue's accumulator copy: 16 heads
+// plus one pad float, so the merge's reads at consecutive d (stride kAccRow)
+// and the lane groups' writes fall in distinct LDS banks.
+constexpr int kAccRow = 17;
+
 // LDS floats needed by splitk_epilogue (the wave merge).
 template <int D, int NW>
 constexpr int splitk_smem_floats() {
-  return NW * 16 * 2 + NW * D * 16 + NW * 16 + 16;
+  return NW * 16 * 2 + NW * D * kAccRow + NW * 16 + 16;
 }
 
 // Head-dim position of accumulator element acc[db][i] held by lane group lg.
@@ -115,11 +120,11 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
 #pragma unroll
   for (int db = 0; db < D / 16; ++db)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wacc[(w * D + acc_d(dmap, db, lg, i)) * 16 + l16] = acc[db][i];
+    for (int i = 0; i < 4; ++i) wacc[(w * D + acc_d(dmap, db, lg, i)) * kAccRow + l16] = acc[db][i];
   __syncthreads();
 
   // per-head merge factors of the waves, computed once
-  float* wf = wacc + NW * D * 16;   // [NW][16] factors, then [16] L
+  float* wf = wacc + NW * D * kAccRow;   // [NW][16] factors, then [16] L
   if (threadIdx.x < 16) {
     const int h = threadIdx.x;
     float M = kNegInf;
@@ -142,7 +147,7 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
       const int h = e / D, d = e - h * D;
       float A = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * 16 + h];
+      for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * kAccRow + h];
       store_out(o, b, hq0 + h, d, A / wf[NW * 16 + h]);
     }
     return;
@@ -151,7 +156,7 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
     const int h = e / D, d = e - h * D;
     float A = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * 16 + h];
+    for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * kAccRow + h];
     const size_t row = ((size_t)unit * 16 + h) * o.nsplit + split;
     o.part_acc[row * D + d] = A;
     if (d == 0) {
