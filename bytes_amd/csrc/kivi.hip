@@ -123,8 +123,8 @@ struct KiviArgs {
   const uint16_t* vr;
   int64_t kr_sb, kr_sh, kr_ss, vr_sb, vr_sh, vr_ss;
   int Hk, G, HB, Sq, R, chunk, nsq;
-  int rsplit;               // 1: the residual window is split nsq of its own
-  int rchunk;               // rsplit == 0: residual tokens per piece (pieces ride on the last splits)
+  int rsplit;               // > 0: the residual window has splits nsq .. nsq+rsplit-1 of its own (128 tokens each)
+  int rchunk;               // rsplit == 0: residual tokens per piece (<= 128; pieces ride on the last splits)
   float scale_log2;
   SplitKOut o;
 };
@@ -132,6 +132,7 @@ struct KiviArgs {
 constexpr int kKiviWaves = 4;
 constexpr int kKiviTile = 64;
 constexpr int kKiviChunkMax = 512;   // tokens per workgroup (multiple of 256)
+constexpr int kResidPerSplit = 128;  // residual tokens per split at most (one 32-token tile per wave)
 
 template <int D, int BITS>
 struct KiviCfg {
@@ -448,25 +449,141 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The bf16 residual window [0, R) runs with the dense tile loop either as a
-  // split of its own (a.rsplit: split nsq, when the extra workgroups still fit
-  // on the device at once) or in pieces of a.rchunk tokens ahead of the
-  // quantized chunks of the last splits (piece i on split nsplit-1-i); then
-  // (2-bit) the accumulator moves to the 2-bit value layout so the quantized
-  // tiles continue the same state.
-  const bool resid_only = a.rsplit && a.R > 0 && split == a.nsq;
+  // The bf16 residual window [0, R) runs as dense 32-token tiles, at most one
+  // per wave (the host keeps every split's share at or below 128 tokens),
+  // either on splits of its own (a.rsplit > 0: splits nsq.., 128 tokens each,
+  // when the extra workgroups still fit on the device at once) or in pieces
+  // of a.rchunk tokens ahead of the quantized chunks of the last splits
+  // (piece i on split nsplit-1-i); then (2-bit) the accumulator moves to the
+  // 2-bit value layout so the quantized tiles continue the same state.  The
+  // residual tile, Q and the first half of the quantized chunk are requested
+  // together, in that order, so the residual tile waits only for its own rows
+  // and the chunk arrives meanwhile.
+  const bool resid_only = a.rsplit > 0 && split >= a.nsq;
   const int rpiece = a.o.nsplit - 1 - split;
-  const int r_begin = resid_only ? 0 : rpiece * a.rchunk;
-  const int r_end = resid_only ? a.R : min(r_begin + a.rchunk, a.R);
-  const bool resid_first = !a.rsplit && a.R > 0 && r_begin < r_end;
-  if (resid_only || resid_first) {
+  const int r_begin = resid_only ? (split - a.nsq) * kResidPerSplit : rpiece * a.rchunk;
+  const int r_end = min(r_begin + (resid_only ? kResidPerSplit : a.rchunk), a.R);
+  const bool resid_first = a.rsplit == 0 && a.R > 0 && r_begin < r_end;
+  const bool resid = resid_only || resid_first;
+  const uint16_t* rkbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
+  const uint16_t* rvbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
+  static_assert(kResidPerSplit == kKiviWaves * kTile, "one residual tile per wave");
+  const int rt = r_begin + w * kTile;
+  // Lanes of head columns past nh load head hq0's query instead of zeros:
+  // their scores and accumulators are computed and never stored, and no
+  // select on a loaded value has to wait for the load at the end of these
+  // conditional blocks.
+  DenseRegs<D> rr;
+  u32x4 qbraw[D / 32];
+  const bool qlive = l16 < nh;
+  if (resid) {
+    if (rt < r_end) dense_issue<D>(rkbase, rvbase, a.kr_ss, a.vr_ss, a.R, rt, r_end, lane, rr);
+    const uint16_t* qp = qrow0 + (int64_t)(qlive ? l16 : 0) * a.q_sh + lg * 8;
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) qbraw[kk] = ld16(qp + kk * 32);
+  }
+
+  const int Sq = a.Sq;
+  const int t_begin = split * a.chunk;
+  const int t_end = resid_only ? t_begin : min(t_begin + a.chunk, Sq);
+  const bool quant = t_begin < t_end;
+  const int g_lo = t_begin >> 5;
+  const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
+  const int64_t bh = (int64_t)b * a.Hk + hk;
+  const int ngk = Sq >> 5;
+
+  char* kchunk = smem_raw;
+  char* kmeta = smem_raw + C::KCBYTES;
+  char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;
+  char* vml = vst + C::VBYTES;
+
+  // The first half is requested on every path, so that each wait counts the
+  // same requests whatever the path (the counts of a wait after paths that
+  // issued different requests are those of the shortest).  A split without
+  // quantized tokens (a residual-only split, or Sq == 0 with no quantized
+  // cache at all) requests 16 bytes at its own query row instead.
+  const void* dummy = qrow0;
+  const uint32_t* vqb = quant ? a.vq + bh * (int64_t)Sq * (D * BITS / 32) : static_cast<const uint32_t*>(dummy);
+  const _Float16* vsb = quant ? a.vs + bh * (int64_t)Sq * C::NGV : static_cast<const _Float16*>(dummy);
+  const _Float16* vmb = quant ? a.vm + bh * (int64_t)Sq * C::NGV : static_cast<const _Float16*>(dummy);
+
+  // Q as the fp16 B operand (scaled by scale*log2e):
+  //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
+  u32x4 qraw[D / 32];
+
+  // The chunk is staged in two halves of kKiviChunkMax/2 tokens, each the
+  // first (ph = 0) or second (ph = 1) tile of every wave.
+  //   keys: channel rows of 16-byte pieces, consecutive threads covering
+  //   consecutive pieces of a row; key scales/zeros two groups per 4-byte word.
+  constexpr int STEP = kKiviWaves * kKiviTile;
+  constexpr int NTW = kKiviChunkMax / STEP;
+  static_assert(NTW == 2, "two halves, one tile per wave each");
+  constexpr int NT = kKiviWaves * 64;
+  constexpr int HP = C::KPIECES / 2;               // key pieces per channel per half
+  constexpr int PERH = D * HP / NT;                // key pieces per thread per half
+  constexpr int WRH = C::KMG / 4;                  // meta words per (scale|zero, channel) per half
+  constexpr int PERMH = 2 * D * WRH / NT;
+  const int pieces = quant ? (t_end - t_begin) * BITS / 128 : 1;
+  const int nwr = quant ? ngs >> 1 : 1;
+  const uint32_t* kqb =
+      quant ? a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32 : static_cast<const uint32_t*>(dummy);
+  const int64_t wk = quant ? Sq * BITS / 32 : 0;
+  const int64_t mrow = quant ? ngk : 0;           // key scale/zero row stride (0: dummy)
+  const _Float16* ksb = quant ? a.ks + g_lo : static_cast<const _Float16*>(dummy);
+  const _Float16* kmb = quant ? a.km + g_lo : static_cast<const _Float16*>(dummy);
+  const int tw = t_begin + w * kKiviTile;
+  u32x4 kv[NTW][PERH];
+  uint32_t mv[NTW][PERMH];
+  KiviRegs<D, BITS> rg[NTW];
+  auto issue = [&](auto phc) {
+    constexpr int ph = decltype(phc)::value;
+#pragma unroll
+    for (int i = 0; i < PERH; ++i) {
+      const int pc = threadIdx.x + NT * i;
+      const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
+      kv[ph][i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < PERMH; ++i) {
+      const int pc = threadIdx.x + NT * i;
+      const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
+      const int sm = row / D, ch = row - sm * D;
+      const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? kmb : ksb) + (bh * D + ch) * mrow);
+      mv[ph][i] = src[min(wi, nwr - 1)];
+    }
+    const int t = tw + ph * STEP;
+    kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[ph]);
+    // keep the compiler from moving requests across this point
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto issue_first = [&]() {
+    const uint16_t* qp = qrow0 + (int64_t)(qlive ? l16 : 0) * a.q_sh + lg * (D / 4);
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = ld16(qp + kk * 8);
+    issue(std::integral_constant<int, 0>());
+  };
+  // 4-bit D=128 keeps the first half's registers out of the residual tile's
+  // live range (together they exceed the 256 VGPRs of two waves per SIMD)
+  constexpr bool kEarly = !(BITS == 4 && D == 128);
+  if (kEarly) issue_first();
+
+  if (resid) {
+    // Q as the bf16 B operand of the dense tile: lane holds Q[h = l16][d = kk*32 + lg*8 + j]
     bf16x8 qb[D / 32];
-    load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
-    const uint16_t* kbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
-    const uint16_t* vbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) qb[kk] = __builtin_bit_cast(bf16x8, qbraw[kk]);
     char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
-    dense_wave_loop<D>(kbase, vbase, a.kr_ss, a.vr_ss, a.R, r_begin, r_end, w, lane, a.scale_log2, qb, wbuf, m_run,
-                       l_run, acc);
+    char* kst = wbuf;
+    char* rvst = wbuf + DenseCfg<D>::VT;
+    // one tile per wave at most, and no loop: at a loop head the wait for the
+    // tile's rows would also count the back edge's requests and so wait for
+    // the quantized chunk too
+    if (rt < r_end) {
+      wave_lds_sync();
+      dense_stage<D>(lane, rr, kst, rvst);
+      wave_lds_sync();
+      dense_compute<D>(range_mask(rt, r_end), a.scale_log2, lane, qb, kst, rvst, m_run, l_run, acc);
+    }
     if (BITS == 2 && resid_first) {
       static_assert(D * 16 * 4 <= DenseCfg<D>::WAVE, "relayout buffer fits the wave's tile buffers");
       float* buf = reinterpret_cast<float*>(wbuf);
@@ -483,78 +600,9 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
     }
     __syncthreads();   // the key chunk below reuses this LDS
   }
+  if (!kEarly) issue_first();
 
-  const int Sq = a.Sq;
-  const int t_begin = split * a.chunk;
-  const int t_end = resid_only ? t_begin : min(t_begin + a.chunk, Sq);
-  if (t_begin < t_end) {
-    const int g_lo = t_begin >> 5;
-    const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
-    const int64_t bh = (int64_t)b * a.Hk + hk;
-    const int ngk = Sq >> 5;
-
-    char* kchunk = smem_raw;
-    char* kmeta = smem_raw + C::KCBYTES;
-    char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;
-    char* vml = vst + C::VBYTES;
-
-    const uint32_t* vqb = a.vq + bh * (int64_t)Sq * (D * BITS / 32);
-    const _Float16* vsb = a.vs + bh * (int64_t)Sq * C::NGV;
-    const _Float16* vmb = a.vm + bh * (int64_t)Sq * C::NGV;
-
-    // Q as the fp16 B operand (scaled by scale*log2e), loaded first:
-    //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
-    u32x4 qraw[D / 32];
-    {
-      const bool live = l16 < nh;
-      const uint16_t* qp = qrow0 + (int64_t)(live ? l16 : 0) * a.q_sh + lg * (D / 4);
-#pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = ld16_live(qp + kk * 8, live);
-    }
-
-    // The chunk is staged in two halves of kKiviChunkMax/2 tokens, each the
-    // first (ph = 0) or second (ph = 1) tile of every wave.
-    //   keys: channel rows of 16-byte pieces, consecutive threads covering
-    //   consecutive pieces of a row; key scales/zeros two groups per 4-byte word.
-    constexpr int STEP = kKiviWaves * kKiviTile;
-    constexpr int NTW = kKiviChunkMax / STEP;
-    static_assert(NTW == 2, "two halves, one tile per wave each");
-    constexpr int NT = kKiviWaves * 64;
-    constexpr int HP = C::KPIECES / 2;               // key pieces per channel per half
-    constexpr int PERH = D * HP / NT;                // key pieces per thread per half
-    constexpr int WRH = C::KMG / 4;                  // meta words per (scale|zero, channel) per half
-    constexpr int PERMH = 2 * D * WRH / NT;
-    const int pieces = (t_end - t_begin) * BITS / 128;
-    const int nwr = ngs >> 1;
-    const uint32_t* kqb = a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32;
-    const int64_t wk = Sq * BITS / 32;
-    const int tw = t_begin + w * kKiviTile;
-    u32x4 kv[NTW][PERH];
-    uint32_t mv[NTW][PERMH];
-    KiviRegs<D, BITS> rg[NTW];
-    auto issue = [&](auto phc) {
-      constexpr int ph = decltype(phc)::value;
-#pragma unroll
-      for (int i = 0; i < PERH; ++i) {
-        const int pc = threadIdx.x + NT * i;
-        const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
-        kv[ph][i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
-      }
-#pragma unroll
-      for (int i = 0; i < PERMH; ++i) {
-        const int pc = threadIdx.x + NT * i;
-        const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
-        const int sm = row / D, ch = row - sm * D;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? a.km : a.ks) + (bh * D + ch) * ngk + g_lo);
-        mv[ph][i] = src[min(wi, nwr - 1)];
-      }
-      const int t = tw + ph * STEP;
-      kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[ph]);
-      // keep the compiler from moving requests across this point
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    issue(std::integral_constant<int, 0>());
-
+  if (quant) {
     f16x8 qh[D / 32];
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk) {
@@ -618,9 +666,11 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
                                  nh, (BITS == 2 && !resid_only) ? kDmapKivi2 : kDmapDense);
 }
 
-// rsplit: the residual gets a split of its own when that keeps the whole grid
-// resident at two workgroups per CU; otherwise it rides on the last split.
-static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq, int* rsplit) {
+// rsplit: the residual gets splits of its own (128 tokens each) when that keeps
+// the whole grid resident at two workgroups per CU, when the grid is past that
+// already, or when four pieces of at most 128 tokens cannot hold it; otherwise
+// it rides, in up to four pieces (rchunk tokens each), on the last splits.
+static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq, int* rsplit, int* rchunk) {
   const int step = kKiviWaves * kKiviTile;
   int c;
   if (chunk_req > 0) {
@@ -635,7 +685,18 @@ static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int*
   *chunk = c;
   *nsq = Sq > 0 ? (Sq + c - 1) / c : 0;
   const long resident = 2L * device_cu_count();
-  *rsplit = R > 0 && (*nsq == 0 || (long)(*nsq + 1) * units <= resident || (long)*nsq * units > resident);
+  const int nr = (R + kResidPerSplit - 1) / kResidPerSplit;    // residual splits if on its own
+  const int pieces = R > 0 ? (*nsq < 4 ? *nsq : 4) : 0;
+  const bool own = R > 0 && (*nsq == 0 || (long)(*nsq + nr) * units <= resident || (long)*nsq * units > resident ||
+                             (long)pieces * kResidPerSplit < R);
+  *rsplit = own ? nr : 0;
+  // pieces on the last splits: whole 32-token tiles, at most kResidPerSplit each
+  int rc = 0;
+  if (R > 0 && !own) {
+    const int per = (R + pieces - 1) / pieces;
+    rc = (per + kTile - 1) / kTile * kTile;
+  }
+  *rchunk = rc;
 }
 
 }  // namespace bytes_amd
@@ -682,8 +743,8 @@ int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
   int chunk, nsq;
-  int rsplit;
-  kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq, &rsplit);
+  int rsplit, rchunk;
+  kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq, &rsplit, &rchunk);
   *bytes = splitk_workspace_bytes(units, nsq + rsplit, D);
   return 0;
 }
@@ -720,15 +781,8 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.vr_sb = vr_sb; a.vr_sh = vr_sh; a.vr_ss = vr_ss;
   a.Hk = Hk; a.G = G; a.HB = HB; a.Sq = Sq; a.R = R;
   a.scale_log2 = scale * kLog2e;
-  kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq, &a.rsplit);
-  const int ns = a.nsq + a.rsplit;                       // quantized chunks, then the residual's own split
-  // otherwise the residual is cut into up to 4 pieces of whole 32-token tiles
-  {
-    const int pieces = a.nsq < 4 ? (a.nsq > 0 ? a.nsq : 1) : 4;
-    const int per = (R + pieces - 1) / pieces;
-    a.rchunk = (per + kTile - 1) / kTile * kTile;
-    if (a.rchunk < kTile) a.rchunk = kTile;
-  }
+  kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
+  const int ns = a.nsq + a.rsplit;                       // quantized chunks, then the residual's own splits
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
   a.o.out = out;

@@ -70,6 +70,9 @@ def _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=0, chunk=0):
     (2, 4, 4, 64, 1024 + 32, 32),       # D = 64, G = 1
     (1, 20, 1, 128, 640, 0),            # no residual, two head blocks
     (1, 4, 2, 128, 128, 128),           # residual only (Sq = 0)
+    (1, 4, 2, 128, 300, 300),           # residual only, three 128-token residual splits, ragged end
+    (1, 7, 1, 128, 1024 + 200, 200),    # residual pieces of 64 tokens (two tiles) on the last splits
+    (2, 8, 2, 128, 256 + 384, 384),     # more residual than four 128-token pieces hold: own splits
 ])
 def test_decode_small(dev, bits, B, Hq, Hk, D, L, Rw):
     _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
