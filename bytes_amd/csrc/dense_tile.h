@@ -97,14 +97,25 @@ __device__ __forceinline__ uint32_t range_mask(int t0, int t_end) {
   return n >= 32 ? 0xFFFFFFFFu : (n <= 0 ? 0u : ((1u << n) - 1u));
 }
 
+// Address of the 4 consecutive V elements (row, col .. col+3) of a tile staged
+// in vst (vswz layout).
+template <int D>
+struct StagedV {
+  const char* vst;
+  __device__ __forceinline__ const char* operator()(int hf, int row, int col) const {
+    return vst + row * (D * 2) + vswz<D>(row, col >> 3) * 16 + (col & 7) * 2;
+  }
+};
+
 // Online softmax and PV for one 32-row tile whose raw scores are s[blk][i]
-// (row blk*16 + lg*4 + i, head l%16; the layout of the score MFMA output) and
-// whose V rows are staged in vst (vswz layout); rows whose vmask bit is clear
-// get probability zero.  F16: V and P in fp16 (f16 MFMA), else bf16.
-template <int D, bool F16 = false>
-__device__ __forceinline__ void tile_softmax_pv(const f32x4 (&s)[2], uint32_t vmask, float scale_log2, int lane,
-                                                const char* vst, float& m_run, float& l_run,
-                                                f32x4 (&acc)[D / 16]) {
+// (row blk*16 + lg*4 + i, head l%16; the layout of the score MFMA output);
+// vaddr(hf, row, col) gives the LDS address of V elements (row, col .. col+3)
+// of the tile (hf = row / 16).  Rows whose vmask bit is clear get probability
+// zero.  F16: V and P in fp16 (f16 MFMA), else bf16.
+template <int D, bool F16 = false, class VA>
+__device__ __forceinline__ void tile_softmax_pv_at(const f32x4 (&s)[2], uint32_t vmask, float scale_log2, int lane,
+                                                   const VA& vaddr, float& m_run, float& l_run,
+                                                   f32x4 (&acc)[D / 16]) {
   using C = DenseCfg<D>;
   const int l16 = lane & 15, lg = lane >> 4;
   float x[8];
@@ -148,8 +159,7 @@ __device__ __forceinline__ void tile_softmax_pv(const f32x4 (&s)[2], uint32_t vm
     for (int hf = 0; hf < 2; ++hf) {
       const int row = hf * 16 + lg * 4 + (l16 >> 2);
       const int col = db * 16 + (l16 & 3) * 4;
-      const int chunk = col >> 3;
-      h[hf] = tr16(vst + row * (D * 2) + vswz<D>(row, chunk) * 16 + (col & 7) * 2);
+      h[hf] = tr16(vaddr(hf, row, col));
     }
     const u32x4 raw = {h[0][0], h[0][1], h[1][0], h[1][1]};
     if (F16)
@@ -157,6 +167,13 @@ __device__ __forceinline__ void tile_softmax_pv(const f32x4 (&s)[2], uint32_t vm
     else
       acc[db] = mfma_bf16(__builtin_bit_cast(bf16x8, raw), pb, acc[db]);
   }
+}
+
+template <int D, bool F16 = false>
+__device__ __forceinline__ void tile_softmax_pv(const f32x4 (&s)[2], uint32_t vmask, float scale_log2, int lane,
+                                                const char* vst, float& m_run, float& l_run,
+                                                f32x4 (&acc)[D / 16]) {
+  tile_softmax_pv_at<D, F16>(s, vmask, scale_log2, lane, StagedV<D>{vst}, m_run, l_run, acc);
 }
 
 // Scores (K rows staged in kst, Q in VGPRs), online softmax and PV for the

@@ -39,7 +39,7 @@
 
 namespace bytes_amd {
 
-constexpr int kPqWaves = 4;
+constexpr int kPqWaves = 8;    // two waves per SIMD at one workgroup per CU
 constexpr int kPqHeads = 4;     // query heads per unit
 constexpr int kPqKMax = 256;    // codewords per subspace
 constexpr int kPqOutMax = 16;   // outlier channels
@@ -100,9 +100,13 @@ struct PqCfg {
   static constexpr int M = D / 8;
   static constexpr int LUT = kPqHeads * M * kPqKMax * 4;          // fp32 LUTs of the unit's heads
   static constexpr int VCB = QV ? M * kPqKMax * 8 * 2 : 0;         // fp16 value codebook
-  static constexpr int TILE = kTile * D * 2;                        // one wave's V tile
+  static constexpr int SCORES = kPqHeads * kTile * 4;              // one wave's tile scores
+  // per wave: the tile scores, and (dense V) the V tile in the same buffer
+  static constexpr int TILE = QV ? SCORES : kTile * D * 2;
   static constexpr int QOUT = QV ? 0 : kPqHeads * kPqOutMax * 4;    // fp32 outlier queries (dense-V modes)
-  static constexpr int kSmem = LUT + VCB + kPqWaves * TILE + QOUT;
+  static constexpr int kSmem0 = LUT + VCB + kPqWaves * TILE + QOUT;
+  static constexpr int kEpi = splitk_smem_floats<D, kPqWaves>() * 4;
+  static constexpr int kSmem = kSmem0 > kEpi ? kSmem0 : kEpi;
 };
 
 // Codes and rows of one 32-token tile, in registers:
@@ -115,7 +119,7 @@ struct PqRegs {
   static constexpr int CPR = VF8 ? D / 16 : D / 8;   // 16-byte V chunks per row
   static constexpr int CPL = kTile * CPR / 64;
   u32x4 kc;
-  uint32_t vc[QV ? 8 : 1];
+  u32x4 vr[QV ? 2 : 1];   // quantized V: value codes of PV rows hf*16 + lg*4 + (l16 >> 2), hf = 0, 1
   u32x4 vd[QV ? 1 : CPL];
   float ko[OUT ? kPqOutMax : 1];
 };
@@ -140,17 +144,24 @@ __device__ __forceinline__ void pq_issue(const PqArgs& a, int b, const uint8_t* 
     }
   }
   if constexpr (OUT) {
+    // channels past C read channel C - 1; their query weights are zero
     const int64_t o = (int64_t)blk * a.ko_sb + (int64_t)row * a.ko_ss;
 #pragma unroll
-    for (int c = 0; c < kPqOutMax; ++c) r.ko[c] = c < a.C ? load_any(koh, a.ko_dt, o + c) : 0.f;
+    for (int c = 0; c < kPqOutMax; ++c) r.ko[c] = load_any(koh, a.ko_dt, o + min(c, a.C - 1));
   }
   if constexpr (QV) {
+    const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int p = lane + 64 * i;
-      const int rr = p / M, j = p - (p / M) * M;
-      const int bq = __shfl(blk, rr & 31, 64), rq = __shfl(row, rr & 31, 64);
-      r.vc[i] = (rr < kTile) ? vih[(int64_t)bq * a.vi_sb + (int64_t)rq * a.vi_ss + j] : 0u;
+    for (int hf = 0; hf < 2; ++hf) {
+      const int rr = hf * 16 + lg * 4 + (l16 >> 2);
+      const int bq = __shfl(blk, rr, 64), rq = __shfl(row, rr, 64);
+      const uint8_t* p = vih + (int64_t)bq * a.vi_sb + (int64_t)rq * a.vi_ss;
+      if constexpr (M == 16) {
+        r.vr[hf] = ld16(p);
+      } else {
+        const u32x2 h = *reinterpret_cast<const u32x2*>(p);
+        r.vr[hf] = u32x4{h[0], h[1], 0u, 0u};
+      }
     }
   } else {
     constexpr int ES = VF8 ? 1 : 2;
@@ -163,6 +174,20 @@ __device__ __forceinline__ void pq_issue(const PqArgs& a, int b, const uint8_t* 
     }
   }
 }
+
+// V elements (row, col .. col+3) of a quantized-V tile, read straight from
+// the value codebook in LDS: subspace j = col / 8, codeword = the row's code
+// j (the lane holds the codes of its two PV rows, hf = row / 16).
+template <int D>
+struct CodebookV {
+  const char* vcb;
+  const u32x4* vr;
+  __device__ __forceinline__ const char* operator()(int hf, int row, int col) const {
+    const int j = col >> 3;
+    const uint32_t code = (vr[hf][j >> 2] >> ((j & 3) * 8)) & 0xFFu;
+    return vcb + (((j * kPqKMax + (int)code) * 8) + (col & 7)) * 2;
+  }
+};
 
 template <int D, bool QV, bool VF8, bool OUT>
 __device__ __forceinline__ void pq_stage_dense_v(int lane, const PqRegs<D, QV, VF8, OUT>& r, char* vst) {
@@ -220,47 +245,38 @@ __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV, VF8
   for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[blk][i] = sc_lds[hh * kTile + blk * 16 + lg * 4 + i];
-  wave_lds_sync();
-  // V tile into the same buffer
   if constexpr (QV) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int p = lane + 64 * i;
-      const int rr = p / M, j = p - (p / M) * M;
-      if (rr < kTile) {
-        const u32x4 row = *reinterpret_cast<const u32x4*>(vcb + ((j * kPqKMax + r.vc[i]) * 8) * 2);
-        *reinterpret_cast<u32x4*>(vst + rr * (D * 2) + vswz<D>(rr, j) * 16) = row;
-      }
-    }
+    // V gathered from the codebook by the PV reads themselves
+    tile_softmax_pv_at<D, true>(s, l16 < nh ? vmask : 0u, a.scale_log2, lane, CodebookV<D>{vcb, r.vr}, m_run, l_run,
+                                acc);
   } else {
+    // V tile into the same buffer
+    wave_lds_sync();
     pq_stage_dense_v<D>(lane, r, vst);
+    wave_lds_sync();
+    tile_softmax_pv<D, false>(s, l16 < nh ? vmask : 0u, a.scale_log2, lane, vst, m_run, l_run, acc);
   }
-  wave_lds_sync();
-  tile_softmax_pv<D, QV>(s, l16 < nh ? vmask : 0u, a.scale_log2, lane, vst, m_run, l_run, acc);
 }
 
-// Copy n 16-byte chunks global -> LDS with the workgroup, 8 loads in flight per thread.
+// Copy n >= 1 16-byte chunks global -> LDS with the workgroup, 8 loads in
+// flight per thread.  Chunks past n repeat chunk n - 1 (same value, same
+// place): no load or store sits under a lane mask.
 template <typename SRC, typename DST>
 __device__ __forceinline__ void stage_chunks(int n, SRC src, DST dst) {
   constexpr int NT = kPqWaves * 64, BATCH = 8;
   for (int e0 = threadIdx.x; e0 < n; e0 += NT * BATCH) {
     u32x4 v[BATCH];
 #pragma unroll
-    for (int bb = 0; bb < BATCH; ++bb) {
-      const int e = e0 + bb * NT;
-      v[bb] = e < n ? ld16(src(e)) : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int bb = 0; bb < BATCH; ++bb) v[bb] = ld16(src(min(e0 + bb * NT, n - 1)));
 #pragma unroll
-    for (int bb = 0; bb < BATCH; ++bb) {
-      const int e = e0 + bb * NT;
-      if (e < n) *reinterpret_cast<u32x4*>(dst(e)) = v[bb];
-    }
+    for (int bb = 0; bb < BATCH; ++bb) *reinterpret_cast<u32x4*>(dst(min(e0 + bb * NT, n - 1))) = v[bb];
   }
 }
 
 template <int D, bool BUILD_LUT, bool QV, bool VF8, bool OUT>
 __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   using C = PqCfg<D, QV>;
+  using Regs = PqRegs<D, QV, VF8, OUT>;
   constexpr int M = D / 8;
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
   float* lut = reinterpret_cast<float*>(smem_raw);
@@ -274,23 +290,56 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   const int hq0 = hk * a.G + hg * kPqHeads;
   const int nh = min(kPqHeads, a.G - hg * kPqHeads);
 
-  // ---- stage the group's LUTs (and the value codebook) ----
+  const int len = pq_len(a, b);
+  const int t_begin = split * a.chunk;
+  const int t_end = min(t_begin + a.chunk, len);
+  // per-head bases; the row offsets (batch or block, row) are added per token
+  const uint8_t* kih = a.kidx + (int64_t)hk * a.ki_sh;
+  const uint8_t* vih = QV ? a.vidx + (int64_t)hk * a.vi_sh : nullptr;
+  const char* vh = QV ? nullptr : static_cast<const char*>(a.v) + (int64_t)hk * a.v_sh * (VF8 ? 1 : 2);
+  const char* koh = OUT ? static_cast<const char*>(a.kout) + (int64_t)hk * a.ko_sh * (a.ko_dt == 2 ? 4 : 2)
+                        : nullptr;
+  char* vst = smem_raw + C::LUT + C::VCB + w * C::TILE;
+  constexpr int STEP = kPqWaves * kTile;
+  int t = t_begin + w * kTile;
+  const bool any = t < t_end;          // wave-uniform; tiles past the end are issued clamped (len >= 1 then)
+
+  // The first tile's codes are requested before the LUTs are staged, so they
+  // arrive meanwhile.  Every later request is unconditional (rows clamped to
+  // len - 1 past the end), so each wait counts the same requests.
+  Regs r;
+  if (any) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t, lane, r);
+
+  // ---- stage the group's LUTs ----
   const int K = a.K;
   if (BUILD_LUT) {
     // LUT[h][j][c] = sum_e q[h][8j+e] * kcb[j][c][e], e ascending, fp32
+    // (entries in batches of 4 per thread, all loads of a batch in flight
+    // together; entries past n repeat entry n - 1)
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
-    for (int e = threadIdx.x; e < nh * M * K; e += kPqWaves * 64) {
-      const int h = e / (M * K), r2 = e - h * (M * K);
-      const int j = r2 / K, c = r2 - j * K;
-      const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + h) * a.q_sh + j * 8;
-      const u32x4 qraw = ld16(qp);
-      const u32x4 craw = ld16(cb + ((int64_t)j * K + c) * 8);
-      const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
-      const _Float16* ch = reinterpret_cast<const _Float16*>(&craw);
-      float sum = 0.f;
+    const int n = nh * M * K;
+    constexpr int NT = kPqWaves * 64, BATCH = 4;
+    for (int e0 = threadIdx.x; e0 < n; e0 += NT * BATCH) {
+      u32x4 qraw[BATCH], craw[BATCH];
+      int dst[BATCH];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) sum += bf16_bits_to_f32(qh[x]) * (float)ch[x];
-      lut[(h * M + j) * kPqKMax + c] = sum;
+      for (int bb = 0; bb < BATCH; ++bb) {
+        const int e = min(e0 + bb * NT, n - 1);
+        const int h = e / (M * K), r2 = e - h * (M * K);
+        const int j = r2 / K, c = r2 - j * K;
+        qraw[bb] = ld16(a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + h) * a.q_sh + j * 8);
+        craw[bb] = ld16(cb + ((int64_t)j * K + c) * 8);
+        dst[bb] = (h * M + j) * kPqKMax + c;
+      }
+#pragma unroll
+      for (int bb = 0; bb < BATCH; ++bb) {
+        const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw[bb]);
+        const _Float16* ch = reinterpret_cast<const _Float16*>(&craw[bb]);
+        float sum = 0.f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) sum += bf16_bits_to_f32(qh[x]) * (float)ch[x];
+        lut[dst[bb]] = sum;
+      }
     }
   } else {
     const int K4 = K / 4;
@@ -307,14 +356,6 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
           return lut + (h * M + j) * kPqKMax + c4 * 4;
         });
   }
-  float* qo = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB + kPqWaves * C::TILE);
-  if constexpr (OUT) {
-    for (int e = threadIdx.x; e < kPqHeads * kPqOutMax; e += kPqWaves * 64) {
-      const int h = e / kPqOutMax, c = e - h * kPqOutMax;
-      qo[e] = (h < nh && c < a.C) ? load_any(a.qout, a.qo_dt, (int64_t)b * a.qo_sb + (int64_t)(hq0 + h) * a.qo_sh + c)
-                                  : 0.f;
-    }
-  }
   if constexpr (QV) {
     const _Float16* cb = a.vcb + (int64_t)hk * a.vcb_sh;
     stage_chunks(
@@ -324,32 +365,30 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
           return vcb + ((j * kPqKMax + c) * 8) * 2;
         });
   }
+  float* qo = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB + kPqWaves * C::TILE);
+  if constexpr (OUT) {
+    for (int e = threadIdx.x; e < kPqHeads * kPqOutMax; e += kPqWaves * 64) {
+      const int h = e / kPqOutMax, c = e - h * kPqOutMax;
+      qo[e] = (h < nh && c < a.C) ? load_any(a.qout, a.qo_dt, (int64_t)b * a.qo_sb + (int64_t)(hq0 + h) * a.qo_sh + c)
+                                  : 0.f;
+    }
+  }
 
   float m_run = kNegInf, l_run = 0.f;
   f32x4 acc[D / 16];
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int len = pq_len(a, b);
-  const int t_begin = split * a.chunk;
-  const int t_end = min(t_begin + a.chunk, len);
-  // per-head bases; the row offsets (batch or block, row) are added per token
-  const uint8_t* kih = a.kidx + (int64_t)hk * a.ki_sh;
-  const uint8_t* vih = QV ? a.vidx + (int64_t)hk * a.vi_sh : nullptr;
-  const char* vh = QV ? nullptr : static_cast<const char*>(a.v) + (int64_t)hk * a.v_sh * (VF8 ? 1 : 2);
-  const char* koh = OUT ? static_cast<const char*>(a.kout) + (int64_t)hk * a.ko_sh * (a.ko_dt == 2 ? 4 : 2)
-                        : nullptr;
-  char* vst = smem_raw + C::LUT + C::VCB + w * C::TILE;
-  constexpr int STEP = kPqWaves * kTile;
-  int t = t_begin + w * kTile;
-  PqRegs<D, QV, VF8, OUT> r;
-  if (t < t_end) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t, lane, r);
   __syncthreads();
-  for (; t < t_end; t += STEP) {
-    PqRegs<D, QV, VF8, OUT> cur = r;
-    if (t + STEP < t_end) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t + STEP, lane, r);
-    wave_lds_sync();
-    pq_tile<D, QV, VF8, OUT>(a, cur, range_mask(t, t_end), lane, nh, lut, vcb, qo, vst, m_run, l_run, acc);
+  if (any) {
+    // tile t runs on the registers that arrived during the last tile, which
+    // are copied out first and refilled with tile t+STEP (clamped past the end)
+    for (; t < t_end; t += STEP) {
+      const Regs cur = r;
+      pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t + STEP, lane, r);
+      wave_lds_sync();
+      pq_tile<D, QV, VF8, OUT>(a, cur, range_mask(t, t_end), lane, nh, lut, vcb, qo, vst, m_run, l_run, acc);
+    }
   }
   splitk_epilogue<D, kPqWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0, nh,
                                kDmapDense);
