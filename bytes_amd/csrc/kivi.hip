@@ -129,18 +129,20 @@ struct KiviArgs {
   SplitKOut o;
 };
 
-constexpr int kKiviWaves = 4;
+// Waves per workgroup (template NW): 4 (512-token chunks, two workgroups per CU) or 8
+// (1024-token chunks, one per CU).  Chunk = waves * 128 tokens, staged in two
+// halves of one 64-token tile per wave.
 constexpr int kKiviTile = 64;
-constexpr int kKiviChunkMax = 512;   // tokens per workgroup (multiple of 256)
 constexpr int kResidPerSplit = 128;  // residual tokens per split at most (one 32-token tile per wave)
 
-template <int D, int BITS>
+template <int D, int BITS, int NW = 4>
 struct KiviCfg {
+  static constexpr int CHUNK = NW * 2 * kKiviTile;         // tokens per workgroup
   static constexpr int KK = D / 32;                        // MFMA k-steps over channels
-  static constexpr int KPIECES = kKiviChunkMax * BITS / 128;  // 16-byte key pieces per channel per chunk
+  static constexpr int KPIECES = CHUNK * BITS / 128;       // 16-byte key pieces per channel per chunk
   static constexpr int KCROW = KPIECES * 16 + 16;          // LDS bytes per channel row (+16: bank spread)
   static constexpr int KCBYTES = D * KCROW;                // staged key codes of one chunk
-  static constexpr int KMG = kKiviChunkMax / 32;           // key groups per chunk
+  static constexpr int KMG = CHUNK / 32;                   // key groups per chunk
   static constexpr int KMETA = 2 * KMG * D * 2;            // staged key scales + zeros
   static constexpr int VROW = D * BITS / 8;                // LDS bytes of one token's value codes
   static constexpr int VBYTES = kKiviTile * VROW;
@@ -148,9 +150,11 @@ struct KiviCfg {
   static constexpr int NGV = D / 32;                        // value groups per token
   static constexpr int VMBYTES = 2 * kKiviTile * NGV * 2;   // value scale + zero of one tile
   static constexpr int WAVE_BYTES = VBYTES + VMBYTES;
-  static constexpr int kQuant = KCBYTES + KMETA + kKiviWaves * WAVE_BYTES;
-  static constexpr int kDense = DenseCfg<D>::kSmem;
-  static constexpr int kSmem = kQuant > kDense ? kQuant : kDense;
+  static constexpr int kQuant = KCBYTES + KMETA + NW * WAVE_BYTES;
+  static constexpr int kDense = DenseCfg<D>::kSmem;        // residual tiles of waves 0-3 (and their merge)
+  static constexpr int kEpi = splitk_smem_floats<D, NW>() * 4;
+  static constexpr int kSmem0 = kQuant > kDense ? kQuant : kDense;
+  static constexpr int kSmem = kSmem0 > kEpi ? kSmem0 : kEpi;
 };
 
 // Position of the k-slot order inside an 8-channel block (4-bit keys interleave
@@ -289,11 +293,11 @@ __device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg
 //   values o[c][h] += sum_t code[t][c] (p[h][t] vs[t][g]) + sum_t p[h][t] vm[t][g]
 //          (g = value group of channel c; the second sum accumulates in zv,
 //          rows = groups, and is added to acc once after the last tile).
-template <int D, int BITS>
+template <int D, int BITS, int NW>
 __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[D / 32], const char* kc,
                                           const char* vst, const char* vmeta_lds, const char* kmeta, float& m_run,
                                           float& l_run, f32x4 (&acc)[D / 16], f32x4& zv) {
-  using C = KiviCfg<D, BITS>;
+  using C = KiviCfg<D, BITS, NW>;
   const int l16 = lane & 15, lg = lane >> 4;
   constexpr int KMG = C::KMG;
   const _Float16* kms = reinterpret_cast<const _Float16*>(kmeta);
@@ -429,9 +433,9 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   }
 }
 
-template <int D, int BITS>
-__global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArgs a) {
-  using C = KiviCfg<D, BITS>;
+template <int D, int BITS, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a) {
+  using C = KiviCfg<D, BITS, NW>;
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
@@ -467,7 +471,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
   const bool resid = resid_only || resid_first;
   const uint16_t* rkbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
   const uint16_t* rvbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
-  static_assert(kResidPerSplit == kKiviWaves * kTile, "one residual tile per wave");
+  static_assert(kResidPerSplit == 4 * kTile && NW >= 4, "one residual tile per wave of waves 0-3");
   const int rt = r_begin + w * kTile;
   // Lanes of head columns past nh load head hq0's query instead of zeros:
   // their scores and accumulators are computed and never stored, and no
@@ -511,14 +515,14 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
   //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
   u32x4 qraw[D / 32];
 
-  // The chunk is staged in two halves of kKiviChunkMax/2 tokens, each the
+  // The chunk is staged in two halves of C::CHUNK/2 tokens, each the
   // first (ph = 0) or second (ph = 1) tile of every wave.
   //   keys: channel rows of 16-byte pieces, consecutive threads covering
   //   consecutive pieces of a row; key scales/zeros two groups per 4-byte word.
-  constexpr int STEP = kKiviWaves * kKiviTile;
-  constexpr int NTW = kKiviChunkMax / STEP;
+  constexpr int STEP = NW * kKiviTile;
+  constexpr int NTW = C::CHUNK / STEP;
   static_assert(NTW == 2, "two halves, one tile per wave each");
-  constexpr int NT = kKiviWaves * 64;
+  constexpr int NT = NW * 64;
   constexpr int HP = C::KPIECES / 2;               // key pieces per channel per half
   constexpr int PERH = D * HP / NT;                // key pieces per thread per half
   constexpr int WRH = C::KMG / 4;                  // meta words per (scale|zero, channel) per half
@@ -646,7 +650,7 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
       wave_lds_sync();
       if (t < t_end) {
         const int off = t - t_begin;
-        kivi_tile<D, BITS>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc,
+        kivi_tile<D, BITS, NW>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc,
                            zv);
       }
     }
@@ -662,29 +666,39 @@ __global__ __launch_bounds__(kKiviWaves * 64, 2) void kivi_decode_kernel(KiviArg
       }
     }
   }
-  splitk_epilogue<D, kKiviWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
+  splitk_epilogue<D, NW>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
                                  nh, (BITS == 2 && !resid_only) ? kDmapKivi2 : kDmapDense);
 }
 
+// nw: 8-wave workgroups with 1024-token chunks (one per CU) when that grid
+// fills between half and all of the CUs in one go; else 4-wave workgroups with
+// chunks of up to 512 tokens (two per CU), whose pairs overlap one
+// workgroup's loads with the other's tiles across successive workgroups.
 // rsplit: the residual gets splits of its own (128 tokens each) when that keeps
-// the whole grid resident at two workgroups per CU, when the grid is past that
-// already, or when four pieces of at most 128 tokens cannot hold it; otherwise
-// it rides, in up to four pieces (rchunk tokens each), on the last splits.
-static void kivi_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq, int* rsplit, int* rchunk) {
-  const int step = kKiviWaves * kKiviTile;
+// the whole grid resident, when the grid is past that already, or when four
+// pieces of at most 128 tokens cannot hold it; otherwise it rides, in up to
+// four pieces (rchunk tokens each), on the last splits.
+static void kivi_plan(int Sq, int R, long units, int chunk_req, int* nw, int* chunk, int* nsq, int* rsplit,
+                      int* rchunk) {
+  const long cus = device_cu_count();
+  *nw = 4;
+  if (chunk_req <= 0 && Sq > 0) {
+    const long n8 = (long)((Sq + 1023) / 1024) * units;
+    if (2 * n8 >= cus && n8 <= cus) *nw = 8;
+  }
+  const int step = *nw * kKiviTile, cmax = *nw * 2 * kKiviTile;
+  const long resident = (8 / *nw) * cus;
   int c;
   if (chunk_req > 0) {
     c = (chunk_req + step - 1) / step * step;
   } else {
-    const long target = 2L * device_cu_count();
-    const long per = ((long)Sq * units + target - 1) / target;
+    const long per = ((long)Sq * units + resident - 1) / resident;
     c = (int)((per + step - 1) / step * step);
   }
   if (c < step) c = step;
-  if (c > kKiviChunkMax) c = kKiviChunkMax;
+  if (c > cmax) c = cmax;
   *chunk = c;
   *nsq = Sq > 0 ? (Sq + c - 1) / c : 0;
-  const long resident = 2L * device_cu_count();
   const int nr = (R + kResidPerSplit - 1) / kResidPerSplit;    // residual splits if on its own
   const int pieces = R > 0 ? (*nsq < 4 ? *nsq : 4) : 0;
   const bool own = R > 0 && (*nsq == 0 || (long)(*nsq + nr) * units <= resident || (long)*nsq * units > resident ||
@@ -742,9 +756,8 @@ int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D
   if ((D != 64 && D != 128) || (bits != 2 && bits != 4)) return (int)hipErrorInvalidValue;
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
-  int chunk, nsq;
-  int rsplit, rchunk;
-  kivi_plan(Sq, R, units, chunk_req, &chunk, &nsq, &rsplit, &rchunk);
+  int nw, chunk, nsq, rsplit, rchunk;
+  kivi_plan(Sq, R, units, chunk_req, &nw, &chunk, &nsq, &rsplit, &rchunk);
   *bytes = splitk_workspace_bytes(units, nsq + rsplit, D);
   return 0;
 }
@@ -781,7 +794,8 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.vr_sb = vr_sb; a.vr_sh = vr_sh; a.vr_ss = vr_ss;
   a.Hk = Hk; a.G = G; a.HB = HB; a.Sq = Sq; a.R = R;
   a.scale_log2 = scale * kLog2e;
-  kivi_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
+  int nw;
+  kivi_plan(Sq, R, units, chunk_req, &nw, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
   const int ns = a.nsq + a.rsplit;                       // quantized chunks, then the residual's own splits
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
@@ -791,15 +805,20 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.o.Hk = Hk; a.o.HB = HB; a.o.G = G;
   splitk_carve(workspace, units, ns, a.o);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)(ns * units)), block(kKiviWaves * 64);
-  if (D == 128 && bits == 2)
-    hipLaunchKernelGGL((kivi_decode_kernel<128, 2>), grid, block, 0, st, a);
-  else if (D == 128 && bits == 4)
-    hipLaunchKernelGGL((kivi_decode_kernel<128, 4>), grid, block, 0, st, a);
-  else if (D == 64 && bits == 2)
-    hipLaunchKernelGGL((kivi_decode_kernel<64, 2>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((kivi_decode_kernel<64, 4>), grid, block, 0, st, a);
+  const dim3 grid((unsigned)(ns * units)), block(nw * 64);
+#define KIVI_LAUNCH(DD, BB)                                                               \
+  if (nw == 8) hipLaunchKernelGGL((kivi_decode_kernel<DD, BB, 8>), grid, block, 0, st, a); \
+  else hipLaunchKernelGGL((kivi_decode_kernel<DD, BB, 4>), grid, block, 0, st, a);
+  if (D == 128 && bits == 2) {
+    KIVI_LAUNCH(128, 2)
+  } else if (D == 128 && bits == 4) {
+    KIVI_LAUNCH(128, 4)
+  } else if (D == 64 && bits == 2) {
+    KIVI_LAUNCH(64, 2)
+  } else {
+    KIVI_LAUNCH(64, 4)
+  }
+#undef KIVI_LAUNCH
   int rc = (int)hipGetLastError();
   if (rc) return rc;
   return splitk_combine(a.o, units, D, st);

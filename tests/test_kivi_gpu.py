@@ -112,6 +112,17 @@ def test_decode_c2_full(dev, bits):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("B,Hq,Hk,D,L,Rw", [
+    (2, 8, 4, 64, 16256 + 128, 128),      # 8-wave workgroups, residual on a split of its own
+    (1, 14, 2, 128, 65536 + 64, 64),      # 8-wave workgroups, residual pieces on the last splits
+])
+def test_decode_eight_wave_workgroups(dev, bits, B, Hq, Hk, D, L, Rw):
+    """Shapes whose 1024-token grid fills half to all of the CUs take the
+    eight-wave, 1024-token-chunk kernel (on a 256-CU device)."""
+    _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
+
+
 def test_decode_back_to_back_calls(dev):
     """The in-kernel split merge leaves its arrival counters at zero: consecutive
     calls with new data (and a different plan in between) on the shared
