@@ -454,15 +454,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // The bf16 residual window [0, R) runs as dense 32-token tiles, at most one
-  // per wave (the host keeps every split's share at or below 128 tokens),
-  // either on splits of its own (a.rsplit > 0: splits nsq.., 128 tokens each,
-  // when the extra workgroups still fit on the device at once) or in pieces
-  // of a.rchunk tokens ahead of the quantized chunks of the last splits
-  // (piece i on split nsplit-1-i); then (2-bit) the accumulator moves to the
-  // 2-bit value layout so the quantized tiles continue the same state.  The
-  // residual tile, Q and the first half of the quantized chunk are requested
-  // together, in that order, so the residual tile waits only for its own rows
-  // and the chunk arrives meanwhile.
+  // per wave of waves 0-3 (the host keeps every split's share at or below 128
+  // tokens), either on splits of its own (a.rsplit > 0: splits nsq.., 128
+  // tokens each, when the extra workgroups still fit on the device at once)
+  // or in pieces of a.rchunk tokens on the last splits (piece i on split
+  // nsplit-1-i), after their quantized tiles: the residual rows are requested
+  // once the second half is staged and arrive during the last tiles; (2-bit)
+  // the accumulator then moves to the dense layout for the residual tile.
   const bool resid_only = a.rsplit > 0 && split >= a.nsq;
   const int rpiece = a.o.nsplit - 1 - split;
   const int r_begin = resid_only ? (split - a.nsq) * kResidPerSplit : rpiece * a.rchunk;
@@ -475,17 +473,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   const int rt = r_begin + w * kTile;
   // Lanes of head columns past nh load head hq0's query instead of zeros:
   // their scores and accumulators are computed and never stored, and no
-  // select on a loaded value has to wait for the load at the end of these
-  // conditional blocks.
+  // select on a loaded value has to wait for the load at the end of the
+  // conditional blocks that issue it.
   DenseRegs<D> rr;
   u32x4 qbraw[D / 32];
   const bool qlive = l16 < nh;
-  if (resid) {
-    if (rt < r_end) dense_issue<D>(rkbase, rvbase, a.kr_ss, a.vr_ss, a.R, rt, r_end, lane, rr);
+  const bool rtile = resid && rt < r_end;         // this wave has a residual tile
+  auto issue_resid = [&]() {
+    dense_issue<D>(rkbase, rvbase, a.kr_ss, a.vr_ss, a.R, rt, r_end, lane, rr);
     const uint16_t* qp = qrow0 + (int64_t)(qlive ? l16 : 0) * a.q_sh + lg * 8;
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk) qbraw[kk] = ld16(qp + kk * 32);
-  }
+  };
 
   const int Sq = a.Sq;
   const int t_begin = split * a.chunk;
@@ -566,45 +565,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
     for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = ld16(qp + kk * 8);
     issue(std::integral_constant<int, 0>());
   };
-  // 4-bit D=128 keeps the first half's registers out of the residual tile's
-  // live range (together they exceed the 256 VGPRs of two waves per SIMD)
-  constexpr bool kEarly = !(BITS == 4 && D == 128);
-  if (kEarly) issue_first();
+  issue_first();
+  if (!quant && rtile) issue_resid();             // residual-only split
 
-  if (resid) {
-    // Q as the bf16 B operand of the dense tile: lane holds Q[h = l16][d = kk*32 + lg*8 + j]
-    bf16x8 qb[D / 32];
-#pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) qb[kk] = __builtin_bit_cast(bf16x8, qbraw[kk]);
-    char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
-    char* kst = wbuf;
-    char* rvst = wbuf + DenseCfg<D>::VT;
-    // one tile per wave at most, and no loop: at a loop head the wait for the
-    // tile's rows would also count the back edge's requests and so wait for
-    // the quantized chunk too
-    if (rt < r_end) {
-      wave_lds_sync();
-      dense_stage<D>(lane, rr, kst, rvst);
-      wave_lds_sync();
-      dense_compute<D>(range_mask(rt, r_end), a.scale_log2, lane, qb, kst, rvst, m_run, l_run, acc);
-    }
-    if (BITS == 2 && resid_first) {
-      static_assert(D * 16 * 4 <= DenseCfg<D>::WAVE, "relayout buffer fits the wave's tile buffers");
-      float* buf = reinterpret_cast<float*>(wbuf);
-      wave_lds_sync();
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) buf[(db * 16 + lg * 4 + i) * 16 + l16] = acc[db][i];
-      wave_lds_sync();
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[db][i] = buf[acc_d(kDmapKivi2, db, lg, i) * 16 + l16];
-    }
-    __syncthreads();   // the key chunk below reuses this LDS
-  }
-  if (!kEarly) issue_first();
 
   if (quant) {
     f16x8 qh[D / 32];
@@ -647,6 +610,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
       const int t = tw + ph * STEP;
       wave_lds_sync();
       kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
+      if (ph == 1 && rtile) issue_resid();        // arrives during the last tiles
       wave_lds_sync();
       if (t < t_end) {
         const int off = t - t_begin;
@@ -666,8 +630,39 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
       }
     }
   }
+
+  if (resid) {
+    __syncthreads();   // every wave is done with the chunk's LDS, which the residual tiles reuse
+    if (rtile) {
+      char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
+      char* kst = wbuf;
+      char* rvst = wbuf + DenseCfg<D>::VT;
+      if (BITS == 2 && quant) {
+        // 2-bit value layout -> dense layout, through the wave's buffer
+        static_assert(D * 16 * 4 <= DenseCfg<D>::WAVE, "relayout buffer fits the wave's tile buffers");
+        float* buf = reinterpret_cast<float*>(wbuf);
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) buf[acc_d(kDmapKivi2, db, lg, i) * 16 + l16] = acc[db][i];
+        wave_lds_sync();
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[db][i] = buf[(db * 16 + lg * 4 + i) * 16 + l16];
+      }
+      // Q as the bf16 B operand of the dense tile: lane holds Q[h = l16][d = kk*32 + lg*8 + j]
+      bf16x8 qb[D / 32];
+#pragma unroll
+      for (int kk = 0; kk < D / 32; ++kk) qb[kk] = __builtin_bit_cast(bf16x8, qbraw[kk]);
+      wave_lds_sync();
+      dense_stage<D>(lane, rr, kst, rvst);
+      wave_lds_sync();
+      dense_compute<D>(range_mask(rt, r_end), a.scale_log2, lane, qb, kst, rvst, m_run, l_run, acc);
+    }
+  }
   splitk_epilogue<D, NW>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0,
-                                 nh, (BITS == 2 && !resid_only) ? kDmapKivi2 : kDmapDense);
+                                 nh, (BITS == 2 && quant && !rtile) ? kDmapKivi2 : kDmapDense);
 }
 
 // nw: 8-wave workgroups with 1024-token chunks (one per CU) when that grid
