@@ -581,6 +581,162 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
   }
 }
 
+// ---- short rows: one wave per row ----
+// Many rows of at most kWaveRow elements with k <= kWaveK: the row's order keys
+// stay in the wave's registers (lane holds elements PER*lane .. +PER), the
+// three digit passes histogram them in the wave's LDS and pick the digit with
+// a suffix scan over the lanes, and the selection is compacted in index order
+// (unsorted) or into an LDS list that an in-wave bitonic sort orders by
+// (score desc, index asc).  No workgroup barrier anywhere.
+constexpr int kWaveRow = 4096;
+constexpr int kWaveK = 256;
+constexpr int kWaveRowsPerWG = 4;
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(v, off, 64);
+    if (lane >= off) v += y;
+  }
+  return v;
+}
+
+template <bool VEC, int PER>
+__global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const float* scores, int64_t row_stride,
+                                                                        int64_t rows, int n, int k, int32_t* out,
+                                                                        int64_t out_stride, int sorted,
+                                                                        uint32_t* ghist) {
+  static_assert(PER % 4 == 0 && 64 * PER <= kWaveRow, "keys per lane");
+  __shared__ __attribute__((aligned(16))) uint32_t hist_s[kWaveRowsPerWG][kBins];
+  __shared__ uint64_t sb_s[kWaveRowsPerWG][kWaveK];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaveRowsPerWG + w;
+  if (row >= rows) return;                       // wave-uniform
+  uint32_t* hist = hist_s[w];
+  uint64_t* sb = sb_s[w];
+  const float* x = scores + row * row_stride;
+  int32_t* o = out + row * out_stride;
+
+  uint32_t key[PER];
+  const int i0 = PER * lane;                     // this lane's first element
+#pragma unroll
+  for (int j = 0; j < PER / 4; ++j) {
+    uint32_t kq[4];
+    bool okq[4];
+    load4<VEC>(x, i0 + 4 * j, n, kq, okq);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
+  }
+  auto valid = [&](int q) { return i0 + q < n; };
+
+  uint32_t prefix = 0u, pmask = 0u, kr = (uint32_t)k;
+#pragma unroll 1
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+    u32x4* h4 = reinterpret_cast<u32x4*>(hist) + lane * 8;      // this lane's 32 bins
+#pragma unroll
+    for (int q = 0; q < 8; ++q) h4[q] = u32x4{0u, 0u, 0u, 0u};
+    wave_lds_sync();
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      if (valid(q) && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> shift) & dmask], 1u);
+    wave_lds_sync();
+    uint32_t c[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const u32x4 v = h4[q];
+      c[4 * q] = v[0]; c[4 * q + 1] = v[1]; c[4 * q + 2] = v[2]; c[4 * q + 3] = v[3];
+    }
+    uint32_t s = 0;
+#pragma unroll
+    for (int b = 0; b < 32; ++b) s += c[b];
+    // inclusive suffix sum over lanes (bins above this lane's range included)
+    uint32_t suf = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = __shfl_down(suf, off, 64);
+      if (lane + off < 64) suf += y;
+    }
+    const uint32_t above_lane = suf - s;         // keys in digits above this lane's bins
+    // digit d: count(digits > d) < kr <= count(digits >= d)
+    const bool mine = above_lane < kr && kr <= suf;
+    uint32_t acc = above_lane, d = 0u, above = 0u;
+    bool got = false;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+      if (!got && acc + c[b] >= kr) {
+        got = true;
+        d = 32u * lane + b;
+        above = acc;
+      }
+      acc += c[b];
+    }
+    const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
+    d = __shfl(d, src, 64);
+    above = __shfl(above, src, 64);
+    kr -= above;
+    prefix |= d << shift;
+    pmask |= dmask << shift;
+    wave_lds_sync();
+  }
+  const uint32_t T = prefix, need = kr;          // keys equal to T to take (>= 1)
+  if (ghist) {                                   // a histogram the caller built: leave it at zero
+    u32x4* gh = reinterpret_cast<u32x4*>(ghist + row * kBins) + lane * 8;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) gh[q] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // compaction in index order (lane, q): slot = selected keys before this one
+  uint32_t ne = 0u, ng = 0u;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    ne += (valid(q) && key[q] == T) ? 1u : 0u;
+    ng += (valid(q) && key[q] > T) ? 1u : 0u;
+  }
+  uint32_t rank = wave_incl_scan(ne, lane) - ne;          // keys equal to T before this lane
+  const uint32_t take_eq = rank >= need ? 0u : (need - rank < ne ? need - rank : ne);
+  const uint32_t nt = ng + take_eq;
+  uint32_t pos = wave_incl_scan(nt, lane) - nt;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const bool v = valid(q);
+    bool take = v && key[q] > T;
+    if (v && key[q] == T) {
+      take = rank < need;
+      ++rank;
+    }
+    if (take) {
+      if (sorted) sb[pos] = sort_val(key[q], i0 + q);
+      else o[pos] = i0 + q;
+      ++pos;
+    }
+  }
+  if (!sorted) return;
+
+  // in-wave bitonic sort of sb[0, P) into descending order (padding zeros sort last)
+  int P = 64;
+  while (P < k) P <<= 1;
+  for (int i = k + lane; i < P; i += 64) sb[i] = 0ull;
+  wave_lds_sync();
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+      for (int p = lane; p < P / 2; p += 64) {
+        const int lo = ((p & ~(stride - 1)) << 1) | (p & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t va = sb[lo], vb = sb[hi];
+        if ((va < vb) == desc) {
+          sb[lo] = vb;
+          sb[hi] = va;
+        }
+      }
+      wave_lds_sync();
+    }
+  }
+  for (int i = lane; i < k; i += 64) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sb[i]);
+}
+
 template <bool VEC>
 static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_stride, int k, int32_t* out,
                        int64_t out_stride, int sorted, int hist_ready, const TopkWs& ws, hipStream_t st) {
@@ -592,6 +748,22 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
     lds_set = true;
   }
   const int parts = (n + kSlice - 1) / kSlice;
+  // one wave per row when there are more rows than CUs: the one-workgroup
+  // path (16 waves per row, one workgroup per CU at a time) then runs in
+  // several generations, while four rows per workgroup all stay resident;
+  // with fewer rows the 16-wave workgroups finish each row sooner
+  if (n <= kWaveRow && k <= kWaveK && rows > device_cu_count()) {
+    const int64_t g = (rows + kWaveRowsPerWG - 1) / kWaveRowsPerWG;
+    if (g > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+    uint32_t* gh = hist_ready ? ws.hist : nullptr;
+    if (n <= 2048)
+      hipLaunchKernelGGL((topk_wave_kernel<VEC, 32>), dim3((unsigned)g), dim3(64 * kWaveRowsPerWG), 0, st, scores,
+                         row_stride, rows, n, k, out, out_stride, sorted, gh);
+    else
+      hipLaunchKernelGGL((topk_wave_kernel<VEC, 64>), dim3((unsigned)g), dim3(64 * kWaveRowsPerWG), 0, st, scores,
+                         row_stride, rows, n, k, out, out_stride, sorted, gh);
+    return (int)hipGetLastError();
+  }
   // short rows, and k beyond the list capacity (unsorted output: the exact
   // path writes the selection straight to `out` in index order)
   const int exact = (n <= kShortRow || k > kTopkMaxK) ? 1 : 0;

@@ -78,6 +78,29 @@ def test_topk_large_k_unsorted(dev, rows, n, k):
         SP.topk_indices(s.to(dev), k, sorted=True)
 
 
+@pytest.mark.parametrize("sorted_out", [True, False])
+@pytest.mark.parametrize("rows,n,k", [(600, 2048, 128), (600, 1000, 1), (300, 4096, 256), (700, 2051, 17),
+                                      (260, 64, 64), (1000, 4095, 200)])
+def test_topk_many_short_rows(dev, rows, n, k, sorted_out):
+    """More rows than CUs with n <= 4096 and k <= 256: the one-wave-per-row
+    selection (ties, +-0, NaN, +-inf and all-equal rows included)."""
+    s = _tie_heavy(rows, n, seed=n + k + rows)
+    s[2] = 0.5                                             # an all-equal row
+    s[3, : n // 2] = float("inf")                          # more infinities than k
+    got = SP.topk_indices(s.to(dev), k, sorted=sorted_out).cpu()
+    assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=sorted_out))
+
+
+def test_topk_many_short_rows_unaligned(dev):
+    s = _tie_heavy(400, 1500, seed=11)
+    big = torch.zeros(400 * 1500 + 1)
+    big[1:] = s.reshape(-1)
+    view = big.to(dev)[1:].reshape(400, 1500)              # rows not 16-byte aligned
+    for srt in (True, False):
+        assert torch.equal(SP.topk_indices(view, 100, sorted=srt).cpu().long(),
+                           R.topk_indices(s, 100, sorted_by_score=srt))
+
+
 def test_topk_unaligned_rows(dev):
     s = _tie_heavy(6, 2051, seed=3)
     big = torch.zeros(6 * 2051 + 1)
