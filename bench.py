@@ -446,8 +446,9 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (every configuration is one GPU's "
-              "shard; see DESIGN.md for how the path would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU only: every configuration is one GPU's share "
+              "of the work (units of (batch, KV head) split across GPUs, no cross-GPU traffic in the "
+              "step). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)

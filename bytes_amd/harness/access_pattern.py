@@ -51,7 +51,7 @@ def main(argv=None):
     ap.add_argument("--page", type=int, default=16)
     ap.add_argument("--runs", type=int, default=50)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--output-json", default="gpurun_out/access_pattern.json")
+    ap.add_argument("--output-json", default="harness_out/access_pattern.json")
     a = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)

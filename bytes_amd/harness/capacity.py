@@ -47,7 +47,7 @@ def main(argv=None):
     ap.add_argument("--Hk", type=int, default=8)
     ap.add_argument("--D", type=int, default=128)
     ap.add_argument("--verify", action="store_true", help="allocate the computed batch once")
-    ap.add_argument("--output-json", default="gpurun_out/sparse_capacity.json")
+    ap.add_argument("--output-json", default="harness_out/sparse_capacity.json")
     a = ap.parse_args(argv)
     free, total = torch.cuda.mem_get_info(0)
     res = {"gpu": torch.cuda.get_device_name(0), "free_bytes": free, "total_bytes": total}

@@ -106,7 +106,7 @@ def main(argv=None):
     ap.add_argument("--Hk", type=int, default=8)
     ap.add_argument("--runs", type=int, default=50)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--output-json", default="gpurun_out/sparse_crossover.json")
+    ap.add_argument("--output-json", default="harness_out/sparse_crossover.json")
     a = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     s_grid = [4096, 16384, 65536] if a.quick else S_GRID

@@ -28,7 +28,7 @@ def main(argv=None):
     ap.add_argument("--Hq", type=int, default=64)
     ap.add_argument("--Hk", type=int, default=8)
     ap.add_argument("--runs", type=int, default=50)
-    ap.add_argument("--output-json", default="gpurun_out/score_ablation.json")
+    ap.add_argument("--output-json", default="harness_out/score_ablation.json")
     a = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
