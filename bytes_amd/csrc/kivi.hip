@@ -361,6 +361,9 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   mx = fmaxf(mx, shfl_xor_f(mx, 32));
   const float m_new = fmaxf(m_run, mx);
   const float alpha = fast_exp2(m_run - m_new);
+  // before a workgroup's first tile every lane's state is empty (m = -inf,
+  // acc = 0): the rescale is skipped on that wave-uniform condition
+  const bool rescale = __ballot(m_run != kNegInf) != 0;
   float p[16];
   float psum = 0.f;
 #pragma unroll
@@ -372,9 +375,11 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
     }
   l_run = l_run * alpha + psum;
   m_run = m_new;
+  if (rescale) {
 #pragma unroll
-  for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
-  zv *= alpha;
+    for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
+    zv *= alpha;
+  }
 
   // P^T as the B operand, k-slot jj of sub-tile sg:
   //   2-bit: token 32sg + 8lg + jj  -> p[(sg*2 + jj%2)*4 + jj/2]
