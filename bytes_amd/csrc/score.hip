@@ -58,30 +58,47 @@ struct ScoreArgs {
 
 constexpr int kScoreWaves = 4;
 
+// Score stores go through a buffer resource over the unit's output rows
+// [row0, row0 + rows), and a lane that must not store gets an offset past the
+// resource (the store is dropped).  The store instruction is then issued on
+// every path, with no branch around it, so the waits for the next rows'
+// loads count the same requests in every iteration.  (The host keeps each
+// unit's output span below 2^31 bytes.)
+__device__ __forceinline__ void score_store(const ScoreArgs& a, int b, int row0, int rows, int r, int tok, bool ok,
+                                            float v) {
+  float* base = a.out + (int64_t)b * a.o_sb + (int64_t)row0 * a.o_sh;
+  const uint32_t span = (uint32_t)(((int64_t)(rows - 1) * a.o_sh + a.S) * 4);
+  const uint32_t off = ok ? (uint32_t)(((int64_t)r * a.o_sh + tok) * 4) : 0x80000000u;
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), buf_rsrc(base, span), (int)off, 0, 0);
+}
+
 __device__ __forceinline__ void score_emit_sum(const ScoreArgs& a, float tot, int tok, int b, int hk, int lg,
                                                uint32_t* hlds) {
-  if (lg == 0 && tok < a.S) {
-    a.out[(int64_t)b * a.o_sb + (int64_t)hk * a.o_sh + tok] = tot;
-    if (hlds) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
-  }
+  const bool ok = lg == 0 && tok < a.S;
+  score_store(a, b, hk, 1, 0, tok, ok, tot);
+  if (hlds && ok) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
 }
 
 // ---- bf16 / fp8 keys ------------------------------------------------------
 
-template <int D, bool FP8>
+template <int D, bool FP8, bool GS>
 struct DenseKeys {
   static constexpr int CT = 4;                 // 16-token column tiles per wave iteration
   typedef typename std::conditional<FP8, u32x2, u32x4>::type T;
   struct Regs {
     T k[4][D / 32];          // [column tile][k-step]
   };
-  const void* kbase;
+  static constexpr int ES = FP8 ? 1 : 2;       // bytes per key element
+  __amdgpu_buffer_rsrc_t rk;   // the unit's key rows (rows at or past S read zero)
+  uint32_t koff, row_bytes;    // this lane's byte offset in a tile row block; bytes per token row
   bf16x8 qa[D / 32];
 
   __device__ __forceinline__ void init(const ScoreArgs& a, int b, int hk, int hq0, int nh, int lane) {
     const int l16 = lane & 15, lg = lane >> 4;
-    kbase = FP8 ? (const void*)(static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh)
-                : (const void*)(static_cast<const uint16_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh);
+    row_bytes = (uint32_t)(a.k_ss * ES);
+    rk = buf_rsrc(static_cast<const uint8_t*>(a.k) + ((int64_t)b * a.k_sb + (int64_t)hk * a.k_sh) * ES,
+                  (uint32_t)((int64_t)a.S * a.k_ss * ES));
+    koff = (uint32_t)l16 * row_bytes + lg * 8 * ES;
     // Q as the A operand: lane holds Q[h = l16][dims (kk*4 + lg)*8 .. +8]
     const bool live = l16 < nh;
     const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + (live ? l16 : 0)) * a.q_sh + lg * 8;
@@ -90,20 +107,19 @@ struct DenseKeys {
       qa[kk] = __builtin_bit_cast(bf16x8, ld16_live(qp + kk * 32, live));
   }
 
-  // K rows t .. t+63 of one iteration as B operands (rows clamped to S-1).
+  // K rows t .. t+63 of one iteration as B operands: buffer loads with the
+  // iteration's row offset in the scalar offset (rows past S read zero).
   __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lane, Regs& r) const {
-    const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int row = min(t + c * 16 + l16, a.S - 1);
-      if constexpr (FP8) {
-        const uint8_t* p = static_cast<const uint8_t*>(kbase) + (int64_t)row * a.k_ss + lg * 8;
+      // row block in the (scalar) offset, k-step in the instruction's immediate
+      const uint32_t soff = (uint32_t)(t + c * 16) * row_bytes;
 #pragma unroll
-        for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = *reinterpret_cast<const u32x2*>(p + kk * 32);
-      } else {
-        const uint16_t* p = static_cast<const uint16_t*>(kbase) + (int64_t)row * a.k_ss + lg * 8;
-#pragma unroll
-        for (int kk = 0; kk < D / 32; ++kk) r.k[c][kk] = ld16(p + kk * 32);
+      for (int kk = 0; kk < D / 32; ++kk) {
+        if constexpr (FP8)
+          r.k[c][kk] = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)(koff + kk * 32 * ES), (int)soff, 0);
+        else
+          r.k[c][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(koff + kk * 32 * ES), (int)soff, 0);
       }
     }
   }
@@ -124,7 +140,7 @@ struct DenseKeys {
 #pragma unroll
       for (int kk = 0; kk < D / 32; ++kk) s = mfma_bf16(qa[kk], operand(r.k[c][kk]), s);
       const int tok = t + c * 16 + l16;
-      if (a.group_sum) {
+      if constexpr (GS) {
         // heads lg*4 + i; group sum in head order, lane groups added in order
         float part = 0.f;
 #pragma unroll
@@ -142,7 +158,7 @@ struct DenseKeys {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int h = lg * 4 + i;
-          if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = s[i] * a.scaling;
+          score_store(a, b, hq0, nh, h, tok, h < nh && tok < a.S, s[i] * a.scaling);
         }
       }
     }
@@ -382,7 +398,7 @@ struct PackedKeys {
             const bool odd = lg & 1;
             const float tot = (odd ? a1 : a0) + __shfl_xor(odd ? a0 : a1, 16, 64);
             const int h = nb * R + lg;
-            if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = tot * a.scaling;
+            score_store(a, b, hq0, nh, h, tok, h < nh && tok < a.S, tot * a.scaling);
           } else {
             // lane groups lg and lg^2 hold groups 0 and 1 of heads (lg&1)*4 + i
             float tot[4];
@@ -393,7 +409,7 @@ struct PackedKeys {
             for (int u = 0; u < 2; ++u) {
               const int h = nb * R + (lg & 1) * 4 + i0 + u;
               const float val = i0 ? tot[2 + u] : tot[u];
-              if (h < nh && tok < a.S) a.out[(int64_t)b * a.o_sb + (int64_t)(hq0 + h) * a.o_sh + tok] = val * a.scaling;
+              score_store(a, b, hq0, nh, h, tok, h < nh && tok < a.S, val * a.scaling);
             }
           }
         }
@@ -427,19 +443,27 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     hlds = hlds_mem;
   }
   constexpr int ITER = 16 * P::CT;
-  int t = t_begin + w * ITER;
+  // wave-uniform (the compiler cannot see it from threadIdx), so the loop runs
+  // on scalar branches rather than an exec-mask loop
+  int t = __builtin_amdgcn_readfirstlane(t_begin + w * ITER);
   if (t < t_end) {
-    // two register sets: the next iteration's rows are in flight while one is scored
+    // two register sets: the next iteration's rows are in flight while one is
+    // scored.  The scheduling barriers keep each request batch ahead of the
+    // tile that follows it (left alone, the compiler moves the requests below
+    // the tile's first use of the current rows, so only one batch is ever in
+    // flight).
     typename P::Regs r0, r1;
     pol.issue(a, t, lane, r0);
     while (true) {
       const bool more1 = t + STEP < t_end;
       pol.issue(a, more1 ? t + STEP : t, lane, r1);
+      __builtin_amdgcn_sched_barrier(0);
       pol.tile(a, r0, t, lane, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more1) break;
       const bool more0 = t + STEP < t_end;
       pol.issue(a, more0 ? t + STEP : t, lane, r0);
+      __builtin_amdgcn_sched_barrier(0);
       pol.tile(a, r1, t, lane, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more0) break;
@@ -451,6 +475,14 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64)
       if (hlds_mem[i]) atomicAdd(hr + i, hlds_mem[i]);
   }
+}
+
+template <int D, bool FP8>
+static void launch_dense(const dim3& g, const dim3& blk, hipStream_t st, const ScoreArgs& a) {
+  if (a.group_sum)
+    hipLaunchKernelGGL((score_kernel<DenseKeys<D, FP8, true>>), g, blk, 0, st, a);
+  else
+    hipLaunchKernelGGL((score_kernel<DenseKeys<D, FP8, false>>), g, blk, 0, st, a);
 }
 
 template <int D, int BITS>
@@ -517,6 +549,14 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   a.group_sum = group_sum ? 1 : 0;
   if (a.group_sum && a.G > 16) return (int)hipErrorNotSupported;
   if (a.hist && !a.group_sum) return (int)hipErrorInvalidValue;
+  // each unit's output rows must fit one buffer resource with room for the
+  // out-of-range offset of dropped stores, and (dense keys) the unit's key
+  // rows plus one iteration of 64 rows must stay below 2^32 bytes of offset
+  if (((int64_t)((a.group_sum ? 1 : a.HPU) - 1) * o_sh + S) * 4 >= ((int64_t)1 << 31))
+    return (int)hipErrorNotSupported;
+  if ((k_mode == kKeyBf16 || k_mode == kKeyFp8) &&
+      ((int64_t)S + 64) * k_ss * (k_mode == kKeyBf16 ? 2 : 1) >= ((int64_t)1 << 32))
+    return (int)hipErrorNotSupported;
   a.scaling = scaling;
   const long units = (long)B * Hk * a.HB;
   // about 8 workgroups per CU in total, each a multiple of one iteration of all waves
@@ -534,15 +574,15 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   const dim3 g((unsigned)grid), blk(kScoreWaves * 64);
   if (D == 128) {
     switch (k_mode) {
-      case kKeyBf16: hipLaunchKernelGGL((score_kernel<DenseKeys<128, false>>), g, blk, 0, st, a); break;
-      case kKeyFp8: hipLaunchKernelGGL((score_kernel<DenseKeys<128, true>>), g, blk, 0, st, a); break;
+      case kKeyBf16: launch_dense<128, false>(g, blk, st, a); break;
+      case kKeyFp8: launch_dense<128, true>(g, blk, st, a); break;
       case kKeyP4: launch_packed<128, 4>(g, blk, st, a, nb); break;
       default: launch_packed<128, 2>(g, blk, st, a, nb); break;
     }
   } else {
     switch (k_mode) {
-      case kKeyBf16: hipLaunchKernelGGL((score_kernel<DenseKeys<64, false>>), g, blk, 0, st, a); break;
-      case kKeyFp8: hipLaunchKernelGGL((score_kernel<DenseKeys<64, true>>), g, blk, 0, st, a); break;
+      case kKeyBf16: launch_dense<64, false>(g, blk, st, a); break;
+      case kKeyFp8: launch_dense<64, true>(g, blk, st, a); break;
       case kKeyP4: launch_packed<64, 4>(g, blk, st, a, nb); break;
       default: launch_packed<64, 2>(g, blk, st, a, nb); break;
     }
