@@ -143,7 +143,10 @@ struct KiviCfg {
   static constexpr int KCROW = KPIECES * 16 + 16;          // LDS bytes per channel row (+16: bank spread)
   static constexpr int KCBYTES = D * KCROW;                // staged key codes of one chunk
   static constexpr int KMG = CHUNK / 32;                   // key groups per chunk
-  static constexpr int KMETA = 2 * KMG * D * 2;            // staged key scales + zeros
+  // staged key scales + zeros, one row of KMP fp16 per (scale|zero, group): the
+  // 8-halfword pad puts the staging stores of a wave's eight groups in distinct banks
+  static constexpr int KMP = D + 8;
+  static constexpr int KMETA = 2 * KMG * KMP * 2;
   static constexpr int VROW = D * BITS / 8;                // LDS bytes of one token's value codes
   static constexpr int VBYTES = kKiviTile * VROW;
   static constexpr int VDMA = VBYTES / 1024;               // 16-byte value chunks per lane per tile
@@ -301,7 +304,7 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   const int l16 = lane & 15, lg = lane >> 4;
   constexpr int KMG = C::KMG;
   const _Float16* kms = reinterpret_cast<const _Float16*>(kmeta);
-  const _Float16* kmz = kms + KMG * D;
+  const _Float16* kmz = kms + KMG * C::KMP;
 
   // ---------------- scores ----------------
   // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
@@ -318,7 +321,7 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
     f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) {
-      const int off = (grp * D + lg * (D / 4) + kk * 8) * 2;
+      const int off = (grp * C::KMP + lg * (D / 4) + kk * 8) * 2;
       const u32x4 ks = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kms) + off);
       const u32x4 kz = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kmz) + off);
       qs[kk] = scale8(qh[kk], ks);
@@ -602,9 +605,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
         const int pc = threadIdx.x + NT * i;
         const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
         const int sm = row / D, ch = row - sm * D;
-        _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * D + kslot_pos<BITS>(ch);
+        _Float16* dst = km_lds + (sm * C::KMG + 2 * wi) * C::KMP + kslot_pos<BITS>(ch);
         dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] & 0xFFFFu));
-        dst[D] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
+        dst[C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
       }
       __syncthreads();
       // The second half is requested only once the first has arrived: every

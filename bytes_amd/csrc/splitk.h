@@ -78,15 +78,17 @@ __device__ __forceinline__ void store_out(const SplitKOut& o, int b, int hq, int
   }
 }
 
-// Floats per (wave, head-dim) row of the epilogue's accumulator copy: 16 heads
-// plus one pad float, so the merge's reads at consecutive d (stride kAccRow)
-// and the lane groups' writes fall in distinct LDS banks.
-constexpr int kAccRow = 17;
+// Floats per (wave, head) row of the epilogue's accumulator copy: D plus four
+// pad floats, so the 16-byte writes of lanes with consecutive heads (row
+// pitch = 4 banks mod 64) and the merge's reads at consecutive d fall in
+// distinct LDS banks.
+template <int D>
+constexpr int acc_pitch() { return D + 4; }
 
 // LDS floats needed by splitk_epilogue (the wave merge).
 template <int D, int NW>
 constexpr int splitk_smem_floats() {
-  return NW * 16 * 2 + NW * D * kAccRow + NW * 16 + 16;
+  return NW * 16 * 2 + NW * 16 * acc_pitch<D>();
 }
 
 // Head-dim position of accumulator element acc[db][i] held by lane group lg.
@@ -101,12 +103,18 @@ __device__ __forceinline__ int acc_d(int dmap, int db, int lg, int i) {
 // the four lanes l%16 + 16*j; l_run: this lane's partial denominator;
 // acc[db][i]: O^T[d = acc_d(dmap, db, l/16, i)][h = l%16].
 // All threads of the workgroup must call this (it contains barriers).
+//
+// Every wave copies its state to LDS (acc as 16-byte runs of four consecutive
+// d), then each thread merges four consecutive d of one head over the waves,
+// computing that head's wave factors itself (no third barrier), in wave order.
 template <int D, int NW>
 __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], float* smem,
                                 const SplitKOut& o, int unit, int split, int b, int hq0, int nh,
                                 int dmap = kDmapDense) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
   constexpr int NT = NW * 64;
+  constexpr int P = acc_pitch<D>();
+  constexpr int D4 = D / 4;
   l_run += shfl_xor_f(l_run, 16);
   l_run += shfl_xor_f(l_run, 32);
   float* wm = smem;
@@ -117,51 +125,44 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
     wm[w * 16 + l16] = m_run;
     wl[w * 16 + l16] = l_run;
   }
+  f32x4* row = reinterpret_cast<f32x4*>(wacc + (w * 16 + l16) * P);
+  if (dmap == kDmapKivi2) {
+    // acc[2k][i], acc[2k+1][i] hold d = 32k + 8lg + 2i + {0, 1}
 #pragma unroll
-  for (int db = 0; db < D / 16; ++db)
+    for (int k = 0; k < D / 32; ++k) {
+      row[8 * k + 2 * lg] = f32x4{acc[2 * k][0], acc[2 * k + 1][0], acc[2 * k][1], acc[2 * k + 1][1]};
+      row[8 * k + 2 * lg + 1] = f32x4{acc[2 * k][2], acc[2 * k + 1][2], acc[2 * k][3], acc[2 * k + 1][3]};
+    }
+  } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wacc[(w * D + acc_d(dmap, db, lg, i)) * kAccRow + l16] = acc[db][i];
+    for (int db = 0; db < D / 16; ++db) row[4 * db + lg] = acc[db];
+  }
   __syncthreads();
 
-  // per-head merge factors of the waves, computed once
-  float* wf = wacc + NW * D * kAccRow;   // [NW][16] factors, then [16] L
-  if (threadIdx.x < 16) {
-    const int h = threadIdx.x;
+  for (int e = threadIdx.x; e < nh * D4; e += NT) {
+    const int h = e / D4, d4 = e - h * D4;
     float M = kNegInf;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, wm[ww * 16 + h]);
     const float Ms = (M == kNegInf) ? 0.f : M;
     float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
       const float f = fast_exp2(wm[ww * 16 + h] - Ms);
-      wf[ww * 16 + h] = f;
       L += f * wl[ww * 16 + h];
+      A += f * reinterpret_cast<const f32x4*>(wacc + (ww * 16 + h) * P)[d4];
     }
-    wf[NW * 16 + h] = L;
-    wm[h] = M;   // wave 0's slot is free now: holds the merged max
-  }
-  __syncthreads();
-  if (o.nsplit <= 1) {
-    for (int e = threadIdx.x; e < nh * D; e += NT) {
-      const int h = e / D, d = e - h * D;
-      float A = 0.f;
+    if (o.nsplit <= 1) {
 #pragma unroll
-      for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * kAccRow + h];
-      store_out(o, b, hq0 + h, d, A / wf[NW * 16 + h]);
-    }
-    return;
-  }
-  for (int e = threadIdx.x; e < nh * D; e += NT) {
-    const int h = e / D, d = e - h * D;
-    float A = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) A += wf[ww * 16 + h] * wacc[(ww * D + d) * kAccRow + h];
-    const size_t row = ((size_t)unit * 16 + h) * o.nsplit + split;
-    o.part_acc[row * D + d] = A;
-    if (d == 0) {
-      o.part_ml[row * 2 + 0] = wm[h];
-      o.part_ml[row * 2 + 1] = wf[NW * 16 + h];
+      for (int j = 0; j < 4; ++j) store_out(o, b, hq0 + h, 4 * d4 + j, A[j] / L);
+    } else {
+      const size_t r = ((size_t)unit * 16 + h) * o.nsplit + split;
+      reinterpret_cast<f32x4*>(o.part_acc + r * D)[d4] = A;
+      if (d4 == 0) {
+        o.part_ml[r * 2 + 0] = M;
+        o.part_ml[r * 2 + 1] = L;
+      }
     }
   }
 }
