@@ -140,8 +140,13 @@ struct KiviCfg {
   static constexpr int CHUNK = NW * 2 * kKiviTile;         // tokens per workgroup
   static constexpr int KK = D / 32;                        // MFMA k-steps over channels
   static constexpr int KPIECES = CHUNK * BITS / 128;       // 16-byte key pieces per channel per chunk
-  static constexpr int KCROW = KPIECES * 16 + 16;          // LDS bytes per channel row (+16: bank spread)
-  static constexpr int KCBYTES = D * KCROW;                // staged key codes of one chunk
+  // Key codes are staged per half chunk ([half][channel][row]) so that the
+  // first half's block, read by no wave once the second half is staged, can
+  // hold the dense residual tiles of the first waves (RES_EARLY of them).
+  static constexpr int KCROW = KPIECES / 2 * 16 + 16;      // LDS bytes per channel row of a half (+16: bank spread)
+  static constexpr int KHALF = D * KCROW;
+  static constexpr int KCBYTES = 2 * KHALF;                // staged key codes of one chunk
+  static constexpr int RES_EARLY = KHALF / DenseCfg<D>::WAVE;
   static constexpr int KMG = CHUNK / 32;                   // key groups per chunk
   // staged key scales + zeros, one row of KMP fp16 per (scale|zero, group): the
   // 8-halfword pad puts the staging stores of a wave's eight groups in distinct banks
@@ -597,8 +602,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
 #pragma unroll
       for (int i = 0; i < PERH; ++i) {
         const int pc = threadIdx.x + NT * i;
-        const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
-        *reinterpret_cast<u32x4*>(kchunk + ch * C::KCROW + q * 16) = kv[ph][i];
+        const int ch = pc / HP, q = pc - (pc / HP) * HP;
+        *reinterpret_cast<u32x4*>(kchunk + ph * C::KHALF + ch * C::KCROW + q * 16) = kv[ph][i];
       }
 #pragma unroll
       for (int i = 0; i < PERMH; ++i) {
@@ -622,7 +627,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
       wave_lds_sync();
       if (t < t_end) {
         const int off = t - t_begin;
-        kivi_tile<D, BITS, NW>((t >> 5) - g_lo, lane, qh, kchunk + off * BITS / 8, vst, vml, kmeta, m_run, l_run, acc,
+        kivi_tile<D, BITS, NW>((t >> 5) - g_lo, lane, qh, kchunk + ph * C::KHALF + (off - ph * STEP) * BITS / 8, vst, vml,
+                               kmeta, m_run, l_run, acc,
                            zv);
       }
     }
@@ -640,7 +646,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   }
 
   if (resid) {
-    __syncthreads();   // every wave is done with the chunk's LDS, which the residual tiles reuse
+    // Wave w's residual tile uses LDS bytes [w, w+1) * DenseCfg<D>::WAVE.  With
+    // quantized tiles, waves below RES_EARLY find those bytes in the first
+    // half's key block, which no wave reads once the second half is staged:
+    // when the split's residual tiles all fit there they run right after the
+    // wave's own tiles, while other waves still work on theirs.  Otherwise every
+    // wave first finishes with the chunk.  Without quantized tiles the LDS is
+    // not otherwise in use before the epilogue.
+    const int ntiles = (r_end - r_begin + kTile - 1) / kTile;
+    if (quant && ntiles > C::RES_EARLY) __syncthreads();
     if (rtile) {
       char* wbuf = smem_raw + w * DenseCfg<D>::WAVE;
       char* kst = wbuf;

@@ -116,10 +116,14 @@ def test_decode_c2_full(dev, bits):
 @pytest.mark.parametrize("B,Hq,Hk,D,L,Rw", [
     (2, 8, 4, 64, 16256 + 128, 128),      # 8-wave workgroups, residual on a split of its own
     (1, 14, 2, 128, 65536 + 64, 64),      # 8-wave workgroups, residual pieces on the last splits
+    (2, 8, 2, 128, 65536 + 200, 200),     # 64-token pieces: two residual tiles per split (4-bit: both
+                                          # right after the waves' own tiles; 2-bit: after the chunk)
 ])
 def test_decode_eight_wave_workgroups(dev, bits, B, Hq, Hk, D, L, Rw):
     """Shapes whose 1024-token grid fills half to all of the CUs take the
-    eight-wave, 1024-token-chunk kernel (on a 256-CU device)."""
+    eight-wave, 1024-token-chunk kernel (on a 256-CU device).  Residual tiles
+    that fit in the first half's key block run without waiting for the other
+    waves; larger pieces wait for the whole chunk."""
     _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
 
 
