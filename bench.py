@@ -270,8 +270,9 @@ class QuestCase(Case):
 
 class PqCase(Case):
     """BASELINE C3: PQ-LUT decode with quantized keys and values.  The LUT build
-    (q against the key codebooks) is part of the step; codebook fitting and
-    encoding are setup."""
+    (q against the key codebooks) is part of the step, fused into the decode
+    launch (decode_attn_pq_kv_fused, bit-identical to pq_build_lut followed by
+    decode_attn_pq_lut_kv); codebook fitting and encoding are setup."""
     kernel = "pq_decode_kernel"
 
     def __init__(self, name, B=1, Hq=28, Hk=4, D=128, L=32768, K=256):
@@ -283,9 +284,8 @@ class PqCase(Case):
         B, Hq, Hk, D, L = self.shape
         M = D // 8
         codes = 2 * B * Hk * L * M
-        lut = B * Hq * M * self.K * 4
         cbs = 2 * Hk * M * self.K * 8 * 2
-        return codes + 2 * lut + cbs + B * Hq * D * 2 + B * Hq * D * 2
+        return codes + cbs + B * Hq * D * 2 + B * Hq * D * 2
 
     def make(self, dev):
         from bytes_amd import workloads as W
@@ -293,9 +293,8 @@ class PqCase(Case):
         return {n: x[n] for n in ("q", "k_cb", "v_cb", "k_idx", "v_idx", "scale")}
 
     def step(self, x):
-        from bytes_amd.pq import decode_attn_pq_lut_kv, pq_build_lut
-        lut = pq_build_lut(x["q"], x["k_cb"], x["scale"])
-        return decode_attn_pq_lut_kv(lut, x["k_idx"], x["v_idx"], x["v_cb"])
+        from bytes_amd.pq import decode_attn_pq_kv_fused
+        return decode_attn_pq_kv_fused(x["q"], x["k_cb"], x["k_idx"], x["v_idx"], x["v_cb"], x["scale"])
 
     def cpu_sample(self):
         from oracle import reference as R

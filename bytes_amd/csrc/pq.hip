@@ -70,6 +70,7 @@ struct PqArgs {
   int bs, nblk;              // paged: rows per block, blocks in the cache
   int Hk, G, HG, S, K, chunk;   // S: tokens (paged: max_blocks * bs)
   float scale_log2;
+  float lut_scale;           // LUTs built in the kernel: entries are lut_scale * (q . codeword)
   SplitKOut o;
 };
 
@@ -313,32 +314,45 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   // ---- stage the group's LUTs ----
   const int K = a.K;
   if (BUILD_LUT) {
-    // LUT[h][j][c] = sum_e q[h][8j+e] * kcb[j][c][e], e ascending, fp32
-    // (entries in batches of 4 per thread, all loads of a batch in flight
-    // together; entries past n repeat entry n - 1)
+    // LUT[h][j][c] = lut_scale * sum_e q[h][8j+e] * kcb[j][c][e], e ascending,
+    // fp32.  The unit's q rows go to LDS as fp32 (in the tile buffers, unused
+    // until the tile loop); every thread requests all of its codewords at once
+    // (entries past n repeat entry n - 1) and scores each against the heads.
+    static_assert(kPqWaves * C::TILE >= kPqHeads * D * 4, "q rows fit in the tile buffers");
+    constexpr int NT = kPqWaves * 64, CPT = (M * kPqKMax + NT - 1) / NT;
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
-    const int n = nh * M * K;
-    constexpr int NT = kPqWaves * 64, BATCH = 4;
-    for (int e0 = threadIdx.x; e0 < n; e0 += NT * BATCH) {
-      u32x4 qraw[BATCH], craw[BATCH];
-      int dst[BATCH];
+    const int n = M * K;
+    u32x4 craw[CPT];
 #pragma unroll
-      for (int bb = 0; bb < BATCH; ++bb) {
-        const int e = min(e0 + bb * NT, n - 1);
-        const int h = e / (M * K), r2 = e - h * (M * K);
-        const int j = r2 / K, c = r2 - j * K;
-        qraw[bb] = ld16(a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + h) * a.q_sh + j * 8);
-        craw[bb] = ld16(cb + ((int64_t)j * K + c) * 8);
-        dst[bb] = (h * M + j) * kPqKMax + c;
-      }
+    for (int i = 0; i < CPT; ++i) craw[i] = ld16(cb + (int64_t)min((int)threadIdx.x + NT * i, n - 1) * 8);
+    float* qs = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB);
+    if (threadIdx.x < kPqHeads * M) {
+      const int h = threadIdx.x / M, j = threadIdx.x - (threadIdx.x / M) * M;
+      const u32x4 qraw = ld16(a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + min(h, nh - 1)) * a.q_sh + j * 8);
+      const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
 #pragma unroll
-      for (int bb = 0; bb < BATCH; ++bb) {
-        const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw[bb]);
-        const _Float16* ch = reinterpret_cast<const _Float16*>(&craw[bb]);
+      for (int x = 0; x < 8; ++x) qs[(h * M + j) * 8 + x] = bf16_bits_to_f32(qh[x]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int e = min((int)threadIdx.x + NT * i, n - 1);
+      const int j = e / K, c = e - j * K;
+      const _Float16* ch = reinterpret_cast<const _Float16*>(&craw[i]);
+#pragma unroll
+      for (int h = 0; h < kPqHeads; ++h) {
+        const f32x4 q0 = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8);
+        const f32x4 q1 = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8 + 4);
         float sum = 0.f;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) sum += bf16_bits_to_f32(qh[x]) * (float)ch[x];
-        lut[dst[bb]] = sum;
+        sum += q0[0] * (float)ch[0];
+        sum += q0[1] * (float)ch[1];
+        sum += q0[2] * (float)ch[2];
+        sum += q0[3] * (float)ch[3];
+        sum += q1[0] * (float)ch[4];
+        sum += q1[1] * (float)ch[5];
+        sum += q1[2] * (float)ch[6];
+        sum += q1[3] * (float)ch[7];
+        lut[(h * M + j) * kPqKMax + c] = sum * a.lut_scale;
       }
     }
   } else {
@@ -620,7 +634,8 @@ int bytes_pq_decode_workspace_size(int B, int Hq, int Hk, int S, int D, int chun
 }
 
 // Launch the decode on a filled PqArgs (strides, pointers, modes set).
-// mode 0: LUT + PQ values, 1: LUT + dense V, 2: q + key codebook + dense V.
+// mode 0: LUT + PQ values, 1: LUT + dense V, 2: q + key codebook + dense V,
+// 3: q + key codebook + PQ values.
 static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S, int D, int K, void* out,
                      int out_dtype, int64_t o_sb, int64_t o_sh, float scale, int chunk_req, void* workspace,
                      size_t workspace_bytes, void* stream) {
@@ -645,6 +660,7 @@ static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S
 #define PQ_MODES(DD)                                          \
   if (mode == 0) PQ_LAUNCH(DD, false, true, false, false);    \
   else if (mode == 2) PQ_LAUNCH(DD, true, false, false, false); \
+  else if (mode == 3) PQ_LAUNCH(DD, true, true, false, false); \
   else if (!vf8 && !outl) PQ_LAUNCH(DD, false, false, false, false); \
   else if (!vf8) PQ_LAUNCH(DD, false, false, false, true);   \
   else if (!outl) PQ_LAUNCH(DD, false, false, true, false);  \
@@ -670,6 +686,9 @@ static PqArgs pq_args_zero() {
 // mode 0: LUT scores + PQ values (decode_attn_pq_lut_kv)
 // mode 1: LUT scores + dense bf16 values (decode_attn_pq_lut)
 // mode 2: scores from q and the key codebook + dense bf16 values (decode_attn_dequant)
+// mode 3: mode 0 with the LUT built inside the kernel from q and the key
+//         codebook, entries scale * (q . codeword) exactly as bytes_pq_build_lut
+//         writes them (the softmax then takes the scores unscaled)
 int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* kcb, const void* kidx,
                          const void* vidx, const void* vcb, const void* v, void* out, int out_dtype, int B, int Hq,
                          int Hk, int S, int D, int K, int64_t l_sb, int64_t l_sh, int64_t q_sb, int64_t q_sh,
@@ -677,14 +696,17 @@ int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* k
                          int64_t vi_ss, int64_t vcb_sh, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb,
                          int64_t o_sh, float scale, int chunk_req, void* workspace, size_t workspace_bytes,
                          void* stream) {
-  if (mode < 0 || mode > 2 || !kidx || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0)
+  if (mode < 0 || mode > 3 || !kidx || !out || B <= 0 || Hk <= 0 || Hq % Hk != 0 || S <= 0)
     return (int)hipErrorInvalidValue;
   if ((D != 64 && D != 128) || K <= 0 || K > kPqKMax || K % 4 != 0) return (int)hipErrorInvalidValue;
   if (mode == 0 && (!lut || !vidx || !vcb)) return (int)hipErrorInvalidValue;
   if (mode == 1 && (!lut || !v)) return (int)hipErrorInvalidValue;
   if (mode == 2 && (!q || !kcb || !v)) return (int)hipErrorInvalidValue;
+  if (mode == 3 && (!q || !kcb || !vidx || !vcb)) return (int)hipErrorInvalidValue;
   if (out_dtype < 0 || out_dtype > 2) return (int)hipErrorInvalidValue;
   PqArgs a = pq_args_zero();
+  a.lut_scale = mode == 3 ? scale : 1.f;
+  if (mode == 3) scale = 1.f;
   a.lut = static_cast<const float*>(lut);
   a.l_sb = l_sb; a.l_sh = l_sh;
   a.q = static_cast<const uint16_t*>(q);

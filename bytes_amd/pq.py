@@ -56,7 +56,7 @@ def _codes(idx: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def _decode(mode: int, *, lut=None, q=None, kcb=None, k_idx, v_idx=None, vcb=None, v=None, out_dtype, B, Hq, Hk,
-            S, D, K, dev, chunk=0):
+            S, D, K, dev, chunk=0, scale=1.0):
     out = torch.empty((B, Hq, D), dtype=out_dtype, device=dev)
     nbytes = size_query("bytes_pq_decode_workspace_size", B, Hq, Hk, S, D, int(chunk))
     ws = workspace(dev, nbytes)
@@ -67,7 +67,7 @@ def _decode(mode: int, *, lut=None, q=None, kcb=None, k_idx, v_idx=None, vcb=Non
     call("bytes_pq_decode_attn", mode, p(lut), p(q), p(kcb16), ptr(k_idx), p(v_idx), p(vcb16), p(v), ptr(out),
          dtype_code(out), B, Hq, Hk, S, D, K, z(lut, 0), z(lut, 1), z(q, 0), z(q, 1), kcb_sh,
          k_idx.stride(0), k_idx.stride(1), k_idx.stride(2), z(v_idx, 0), z(v_idx, 1), z(v_idx, 2), vcb_sh,
-         z(v, 0), z(v, 1), z(v, 2), out.stride(0), out.stride(1), 1.0, int(chunk), ptr(ws), ws.numel(),
+         z(v, 0), z(v, 1), z(v, 2), out.stride(0), out.stride(1), float(scale), int(chunk), ptr(ws), ws.numel(),
          stream_of(k_idx))
     return out.unsqueeze(2)
 
@@ -111,6 +111,42 @@ def decode_attn_pq_lut_kv(lut: torch.Tensor, k_idx: torch.Tensor, v_idx: torch.T
     return _decode(0, lut=lut, k_idx=_codes(k_idx, "k_idx"), v_idx=_codes(v_idx, "v_idx"), vcb=(vcb16, vsh),
                    out_dtype=v_centroids.dtype, B=B, Hq=Hq, Hk=Hk, S=S, D=M * D_SUB, K=K, dev=lut.device,
                    chunk=chunk)
+
+
+def decode_attn_pq_kv_fused(q: torch.Tensor, k_centroids: torch.Tensor, k_idx: torch.Tensor, v_idx: torch.Tensor,
+                            v_centroids: torch.Tensor, scale: float = 1.0, d_sub_v: int = 8, *,
+                            chunk: int = 0) -> torch.Tensor:
+    """pq_build_lut(q, k_centroids, scale) followed by decode_attn_pq_lut_kv, in
+    one launch: every workgroup builds its heads' LUTs in LDS from q and the key
+    codebook, entry for entry as pq_build_lut writes them
+    (benchmarks/test_correctness.py:272-273), then runs the decode of
+    src/attention_kernels.py:471-500.  The result is bit-identical to the two
+    calls.  q [B,H_q,1,D] bf16; k_centroids, v_centroids [M,K,8] or
+    [H_k,M,K,8]; k_idx, v_idx [B,H_k,S,M].  Returns [B,H_q,1,D] in v_centroids'
+    dtype."""
+    if d_sub_v != D_SUB:
+        raise ValueError(f"d_sub_v={d_sub_v} not supported (8)")
+    C.cuda_tensors(q, k_centroids, k_idx, v_idx, v_centroids)
+    C.ndim(q, 4, "q"), C.ndim(k_idx, 4, "k_idx")
+    C.dtype_in(q, "q", torch.bfloat16)
+    B, Hq, one, D = q.shape
+    Bk, Hk, S, M = k_idx.shape
+    if one != 1 or Bk != B or M * D_SUB != D or Hq % Hk != 0 or S == 0:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k_idx {tuple(k_idx.shape)}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if tuple(v_idx.shape[:3]) != (B, Hk, S):
+        raise ValueError(f"v_idx {tuple(v_idx.shape)} does not match k_idx {tuple(k_idx.shape)}")
+    kcb16, ksh, Mk, K = _codebook16(k_centroids, Hk, "k_centroids")
+    vcb16, vsh, Mv, Kv = _codebook16(v_centroids, Hk, "v_centroids")
+    if Mk != M or Mv != M or v_idx.shape[-1] != M or Kv != K:
+        raise ValueError("codebooks / codes must share the subspace and codeword counts")
+    if not (0 < K <= 256 and K % 4 == 0):
+        raise ValueError(f"K={K} codewords not supported (multiple of 4, <= 256)")
+    qs = C.rows16(q.squeeze(2))
+    return _decode(3, q=qs, kcb=(kcb16, ksh), k_idx=_codes(k_idx, "k_idx"), v_idx=_codes(v_idx, "v_idx"),
+                   vcb=(vcb16, vsh), out_dtype=v_centroids.dtype, B=B, Hq=Hq, Hk=Hk, S=S, D=D, K=K, dev=q.device,
+                   chunk=chunk, scale=scale)
 
 
 def decode_attn_pq_lut(lut: torch.Tensor, k_idx: torch.Tensor, v: torch.Tensor, *, chunk: int = 0) -> torch.Tensor:

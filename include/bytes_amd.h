@@ -276,9 +276,14 @@ int bytes_pq_lut_scores(const void* lut, int64_t l_sb, int64_t l_sh, const void*
  *   mode 1  decode_attn_pq_lut     :365-392 (kernel :301-363): LUT scores, dense bf16 v
  *   mode 2  decode_attn_dequant    :267-296 (kernel :187-265): scores q . k_hat with
  *           k_hat = concat_j kcb[j, kidx[t,j]] (no scale), dense bf16 v
+ *   mode 3  mode 0 with the LUT precompute fused (benchmarks/test_correctness.py:272-273
+ *           followed by :471-500): each workgroup builds lut = scale * (q . kcb) in LDS,
+ *           entry for entry as bytes_pq_build_lut, so the output is bit-identical to
+ *           bytes_pq_build_lut + mode 0; q, kcb, vidx, vcb required, lut unused
  *   lut [B, Hq, M, K] fp32 (one head contiguous); q [B, Hq, D] bf16;
  *   out [B, Hq, D] of out_dtype (0 bf16, 1 f16, 2 f32).  `scale` multiplies the
- *   scores (the reference has none: pass 1.0).
+ *   scores in modes 0-2 (the reference has none: pass 1.0) and the LUT entries in
+ *   mode 3.
  * ------------------------------------------------------------------------- */
 int bytes_pq_decode_workspace_size(int B, int Hq, int Hk, int S, int D, int chunk, size_t* bytes);
 int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* kcb, const void* kidx,

@@ -131,6 +131,31 @@ def test_c3_full(dev):
     _check(out2, R.decode_attn_dequant(qs, c["k_idx"], c["k_cb"], c["v"]), "C3 dequant")
 
 
+@pytest.mark.parametrize("B,Hq,Hk,S,D,K,per_head", [(1, 28, 4, 32768, 128, 256, True),   # C3
+                                                   (1, 7, 1, 1000, 128, 256, True),
+                                                   (2, 8, 2, 333, 64, 16, False),
+                                                   (2, 12, 2, 5000, 128, 64, True)])
+def test_fused_lut_build_matches_two_calls(dev, B, Hq, Hk, S, D, K, per_head):
+    """decode_attn_pq_kv_fused == pq_build_lut + decode_attn_pq_lut_kv, bit for
+    bit (same LUT entries, same decode), and within tolerance of the oracle."""
+    g = torch.Generator().manual_seed(S + K)
+    M = D // 8
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    shp = (Hk, M, K, 8) if per_head else (M, K, 8)
+    kcb, vcb = _rand_cb(shp, S + 3), _rand_cb(shp, S + 4)
+    k_idx = torch.randint(0, K, (B, Hk, S, M), generator=g).to(torch.uint8)
+    v_idx = torch.randint(0, K, (B, Hk, S, M), generator=g).to(torch.uint8)
+    d = {n: t.to(dev) for n, t in dict(q=q, kcb=kcb, vcb=vcb, k_idx=k_idx, v_idx=v_idx).items()}
+    scale = D ** -0.5
+    lut = PQ.pq_build_lut(d["q"], d["kcb"], scale)
+    two = PQ.decode_attn_pq_lut_kv(lut, d["k_idx"], d["v_idx"], d["vcb"])
+    fused = PQ.decode_attn_pq_kv_fused(d["q"], d["kcb"], d["k_idx"], d["v_idx"], d["vcb"], scale)
+    assert fused.shape == two.shape and fused.dtype == two.dtype
+    assert torch.equal(fused, two)
+    ref = R.decode_attn_pq_lut_kv(R.pq_build_lut(q, kcb, scale), k_idx, v_idx, vcb)
+    _check(fused, ref, f"fused B{B} Hq{Hq} Hk{Hk} S{S} D{D} K{K}")
+
+
 def test_kmeans_update_and_determinism(dev):
     g = torch.Generator().manual_seed(13)
     H, N, D, K = 2, 3000, 64, 32
