@@ -737,6 +737,127 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
   for (int i = lane; i < k; i += 64) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sb[i]);
 }
 
+// Rows of at most kSmallRow elements that the wave kernel does not take (few
+// rows, or larger k): one 256-thread workgroup per row, the row's order keys
+// in registers (thread t holds elements PER*t .. +PER, read from memory once),
+// three digit passes over a workgroup histogram, each with one block scan to
+// pick the digit, then one scan of packed (equal, greater) counts to place the
+// selection in index order, or into an LDS list sorted by (score desc, index
+// asc).  Four waves per barrier instead of sixteen.
+constexpr int kSmallThreads = 256;
+constexpr int kSmallRow = 4096;
+constexpr int kSmallSortK = 1024;
+
+template <bool VEC, int PER>
+__global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* scores, int64_t row_stride, int n,
+                                                                   int k, int32_t* out, int64_t out_stride,
+                                                                   int sorted, uint32_t* ghist) {
+  constexpr int NT = kSmallThreads;
+  constexpr int BPT = kBins / NT;                // histogram bins per thread
+  static_assert(PER % 4 == 0 && NT * PER <= kSmallRow && BPT % 4 == 0, "keys and bins per thread");
+  __shared__ __attribute__((aligned(16))) uint32_t hist[kBins];
+  __shared__ uint64_t sb[kSmallSortK];
+  __shared__ uint32_t wsum[NT / 64];
+  __shared__ uint32_t sel[2];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* x = scores + row * row_stride;
+  int32_t* o = out + row * out_stride;
+
+  uint32_t key[PER];
+  const int i0 = PER * tid;                      // this thread's first element
+#pragma unroll
+  for (int j = 0; j < PER / 4; ++j) {
+    uint32_t kq[4];
+    bool okq[4];
+    load4<VEC>(x, i0 + 4 * j, n, kq, okq);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
+  }
+  auto valid = [&](int q) { return i0 + q < n; };
+
+  uint32_t prefix = 0u, pmask = 0u, kr = (uint32_t)k;
+  u32x4* h4 = reinterpret_cast<u32x4*>(hist) + tid * (BPT / 4);   // this thread's bins
+#pragma unroll 1
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+#pragma unroll
+    for (int q = 0; q < BPT / 4; ++q) h4[q] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      if (valid(q) && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> shift) & dmask], 1u);
+    __syncthreads();
+    uint32_t c[BPT];
+#pragma unroll
+    for (int q = 0; q < BPT / 4; ++q) {
+      const u32x4 v = h4[q];
+      c[4 * q] = v[0]; c[4 * q + 1] = v[1]; c[4 * q + 2] = v[2]; c[4 * q + 3] = v[3];
+    }
+    uint32_t s = 0u;
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) s += c[b];
+    uint32_t total;
+    const uint32_t incl = block_incl_scan<NT>(s, wsum, total);
+    // digit d: count(digits > d) < kr <= count(digits >= d); exactly one thread
+    // and bin see the crossing
+    uint32_t acc = total - incl;                 // keys in the bins above this thread's
+#pragma unroll
+    for (int b = BPT - 1; b >= 0; --b) {
+      if (acc < kr && acc + c[b] >= kr) {
+        sel[0] = (uint32_t)(BPT * tid + b);
+        sel[1] = acc;
+      }
+      acc += c[b];
+    }
+    __syncthreads();
+    kr -= sel[1];
+    prefix |= sel[0] << shift;
+    pmask |= dmask << shift;
+  }
+  const uint32_t T = prefix, need = kr;          // keys equal to T to take (>= 1), lowest indices first
+  if (ghist) {                                   // a histogram the caller built: leave it at zero
+    u32x4* gh = reinterpret_cast<u32x4*>(ghist + row * kBins) + tid * (BPT / 4);
+#pragma unroll
+    for (int q = 0; q < BPT / 4; ++q) gh[q] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // placement in index order: one scan of (equal << 16 | greater), both < 2^16
+  uint32_t ne = 0u, ng = 0u;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    ne += (valid(q) && key[q] == T) ? 1u : 0u;
+    ng += (valid(q) && key[q] > T) ? 1u : 0u;
+  }
+  const uint32_t packed = (ne << 16) | ng;
+  uint32_t tot;
+  const uint32_t before = block_incl_scan<NT>(packed, wsum, tot) - packed;
+  uint32_t rank = before >> 16;                  // keys equal to T before this thread
+  uint32_t pos = (before & 0xFFFFu) + (rank < need ? rank : need);
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const bool v = valid(q);
+    bool take = v && key[q] > T;
+    if (v && key[q] == T) {
+      take = rank < need;
+      ++rank;
+    }
+    if (take) {
+      if (sorted) sb[pos] = sort_val(key[q], i0 + q);
+      else o[pos] = i0 + q;
+      ++pos;
+    }
+  }
+  if (!sorted) return;
+  int P = 64;
+  while (P < k) P <<= 1;
+  for (int i = k + tid; i < P; i += NT) sb[i] = 0ull;   // padding sorts last
+  __syncthreads();
+  bitonic_desc<NT>(sb, P);
+  for (int i = tid; i < k; i += NT) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sb[i]);
+}
+
 template <bool VEC>
 static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_stride, int k, int32_t* out,
                        int64_t out_stride, int sorted, int hist_ready, const TopkWs& ws, hipStream_t st) {
@@ -762,6 +883,22 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
     else
       hipLaunchKernelGGL((topk_wave_kernel<VEC, 64>), dim3((unsigned)g), dim3(64 * kWaveRowsPerWG), 0, st, scores,
                          row_stride, rows, n, k, out, out_stride, sorted, gh);
+    return (int)hipGetLastError();
+  }
+  // other rows of at most kSmallRow elements: a 256-thread workgroup per row
+  if (n <= kSmallRow && (!sorted || k <= kSmallSortK)) {
+    if (rows > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+    uint32_t* gh = hist_ready ? ws.hist : nullptr;
+    const dim3 grid((unsigned)rows), block(kSmallThreads);
+    if (n <= 1024)
+      hipLaunchKernelGGL((topk_small_kernel<VEC, 4>), grid, block, 0, st, scores, row_stride, n, k, out, out_stride,
+                         sorted, gh);
+    else if (n <= 2048)
+      hipLaunchKernelGGL((topk_small_kernel<VEC, 8>), grid, block, 0, st, scores, row_stride, n, k, out, out_stride,
+                         sorted, gh);
+    else
+      hipLaunchKernelGGL((topk_small_kernel<VEC, 16>), grid, block, 0, st, scores, row_stride, n, k, out,
+                         out_stride, sorted, gh);
     return (int)hipGetLastError();
   }
   // short rows, and k beyond the list capacity (unsorted output: the exact

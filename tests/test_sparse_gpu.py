@@ -91,6 +91,27 @@ def test_topk_many_short_rows(dev, rows, n, k, sorted_out):
     assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=sorted_out))
 
 
+@pytest.mark.parametrize("rows,n,k", [(1, 1, 1), (1, 3, 2), (5, 64, 64), (28, 2048, 1024), (3, 4096, 4096),
+                                      (4, 4096, 1024), (2, 3000, 2000), (280, 1500, 512), (7, 4095, 1)])
+def test_topk_small_rows(dev, rows, n, k):
+    """Rows of at most 4096 elements outside the one-wave path: one 256-thread
+    workgroup per row (sorted output up to k = 1024; larger sorted k takes the
+    whole-row sort)."""
+    s = _tie_heavy(rows, n, seed=3 * n + k)
+    if rows > 3:
+        s[2] = -1.5                                          # an all-equal row
+        s[3, : n // 2] = float("-inf")
+        s[3, n // 2:] = float("inf")
+    for so in (True, False):
+        got = SP.topk_indices(s.to(dev), k, sorted=so).cpu()
+        assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=so)), so
+    big = torch.zeros(rows * n + 1)
+    big[1:] = s.reshape(-1)
+    view = big.to(dev)[1:].reshape(rows, n)                  # rows not 16-byte aligned
+    assert torch.equal(SP.topk_indices(view, k, sorted=False).cpu().long(),
+                       R.topk_indices(s, k, sorted_by_score=False))
+
+
 def test_topk_many_short_rows_unaligned(dev):
     s = _tie_heavy(400, 1500, seed=11)
     big = torch.zeros(400 * 1500 + 1)
