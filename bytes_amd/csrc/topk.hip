@@ -739,11 +739,14 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
 
 // Rows of at most kSmallRow elements that the wave kernel does not take (few
 // rows, or larger k): one 256-thread workgroup per row, the row's order keys
-// in registers (thread t holds elements PER*t .. +PER, read from memory once),
-// three digit passes over a workgroup histogram, each with one block scan to
-// pick the digit, then one scan of packed (equal, greater) counts to place the
-// selection in index order, or into an LDS list sorted by (score desc, index
-// asc).  Four waves per barrier instead of sixteen.
+// in registers (thread t holds elements PER*t .. +PER, read from memory once).
+// The digit passes start at the highest bit in which the row's keys differ
+// (the bits above are common to every key), so rows of scores in a narrow
+// range take fewer passes and spread over the first histogram.  Each pass
+// histograms the keys that match the prefix so far, picks the digit from
+// wave suffix sums and the four wave totals (one barrier), and one scan of
+// packed (equal, greater) counts places the selection in index order, or into
+// an LDS list sorted by (score desc, index asc).
 constexpr int kSmallThreads = 256;
 constexpr int kSmallRow = 4096;
 constexpr int kSmallSortK = 1024;
@@ -752,14 +755,14 @@ template <bool VEC, int PER>
 __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* scores, int64_t row_stride, int n,
                                                                    int k, int32_t* out, int64_t out_stride,
                                                                    int sorted, uint32_t* ghist) {
-  constexpr int NT = kSmallThreads;
+  constexpr int NT = kSmallThreads, NW = NT / 64;
   constexpr int BPT = kBins / NT;                // histogram bins per thread
   static_assert(PER % 4 == 0 && NT * PER <= kSmallRow && BPT % 4 == 0, "keys and bins per thread");
   __shared__ __attribute__((aligned(16))) uint32_t hist[kBins];
   __shared__ uint64_t sb[kSmallSortK];
-  __shared__ uint32_t wsum[NT / 64];
+  __shared__ uint32_t wa[NW], wb[NW], wc[NW], wd[NW];
   __shared__ uint32_t sel[2];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t row = blockIdx.x;
   const float* x = scores + row * row_stride;
   int32_t* o = out + row * out_stride;
@@ -776,18 +779,45 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
   }
   auto valid = [&](int q) { return i0 + q < n; };
 
-  uint32_t prefix = 0u, pmask = 0u, kr = (uint32_t)k;
+  // key range of the row
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+  for (int q = 0; q < PER; ++q)
+    if (valid(q)) {
+      kmin = min(kmin, key[q]);
+      kmax = max(kmax, key[q]);
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off, 64));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+  }
+  if (lane == 0) {
+    wa[w] = kmin;
+    wb[w] = kmax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    kmin = min(kmin, wa[v]);
+    kmax = max(kmax, wb[v]);
+  }
+  const uint32_t diff = kmin ^ kmax;
+  const int hb = diff ? 31 - __builtin_clz(diff) : -1;        // highest differing bit
+  uint32_t pmask = hb < 0 ? 0xFFFFFFFFu : ~(uint32_t)((2ull << hb) - 1ull);
+  uint32_t prefix = kmin & pmask, kr = (uint32_t)k;
+
   u32x4* h4 = reinterpret_cast<u32x4*>(hist) + tid * (BPT / 4);   // this thread's bins
 #pragma unroll 1
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+  for (int hi = hb; hi >= 0; hi -= 11) {
+    const int lo = hi >= 10 ? hi - 10 : 0;
+    const uint32_t dmask = (1u << (hi - lo + 1)) - 1u;
 #pragma unroll
     for (int q = 0; q < BPT / 4; ++q) h4[q] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < PER; ++q)
-      if (valid(q) && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> shift) & dmask], 1u);
+      if (valid(q) && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> lo) & dmask], 1u);
     __syncthreads();
     uint32_t c[BPT];
 #pragma unroll
@@ -798,11 +828,20 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
     uint32_t s = 0u;
 #pragma unroll
     for (int b = 0; b < BPT; ++b) s += c[b];
-    uint32_t total;
-    const uint32_t incl = block_incl_scan<NT>(s, wsum, total);
-    // digit d: count(digits > d) < kr <= count(digits >= d); exactly one thread
-    // and bin see the crossing
-    uint32_t acc = total - incl;                 // keys in the bins above this thread's
+    // inclusive suffix sum over the wave's lanes, then the waves above
+    uint32_t suf = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_down((int)suf, off, 64);
+      if (lane + off < 64) suf += y;
+    }
+    if (lane == 0) wc[w] = suf;
+    __syncthreads();
+    uint32_t acc = suf - s;                      // keys in the bins above this thread's
+#pragma unroll
+    for (int v = 0; v < NW; ++v) acc += v > w ? wc[v] : 0u;
+    // digit d: count(digits > d) < kr <= count(digits >= d); exactly one
+    // thread and bin see the crossing
 #pragma unroll
     for (int b = BPT - 1; b >= 0; --b) {
       if (acc < kr && acc + c[b] >= kr) {
@@ -813,8 +852,8 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
     }
     __syncthreads();
     kr -= sel[1];
-    prefix |= sel[0] << shift;
-    pmask |= dmask << shift;
+    prefix |= sel[0] << lo;
+    pmask |= dmask << lo;
   }
   const uint32_t T = prefix, need = kr;          // keys equal to T to take (>= 1), lowest indices first
   if (ghist) {                                   // a histogram the caller built: leave it at zero
@@ -831,8 +870,12 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
     ng += (valid(q) && key[q] > T) ? 1u : 0u;
   }
   const uint32_t packed = (ne << 16) | ng;
-  uint32_t tot;
-  const uint32_t before = block_incl_scan<NT>(packed, wsum, tot) - packed;
+  const uint32_t incl = wave_incl_scan(packed, lane);
+  if (lane == 63) wd[w] = incl;
+  __syncthreads();
+  uint32_t before = incl - packed;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) before += v < w ? wd[v] : 0u;
   uint32_t rank = before >> 16;                  // keys equal to T before this thread
   uint32_t pos = (before & 0xFFFFu) + (rank < need ? rank : need);
 #pragma unroll
