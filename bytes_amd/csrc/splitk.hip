@@ -2,8 +2,11 @@
 //
 // out = sum_s f_s acc_s / sum_s f_s l_s with f_s = 2^(m_s - max_s m_s).
 //
-// One wave per (unit, head, 64-dim slice of the head row): a launch of
-// units x heads x D/64 single-wave workgroups, no LDS and no barrier.  The
+// One wave per (unit, head, 64-dim slice of the head row), no LDS and no
+// barrier.  The waves of a unit run on the XCD that ran its first split (the
+// split kernels deal runs of consecutive splits to each XCD, see
+// xcd_unit_split), where the partials are still in that XCD's L2: workgroup L
+// of the 1-D grid goes to XCD L % 8 and takes that XCD's (L / 8)-th wave.  The
 // 64 lanes are 16 float4 items of the slice x 4 split groups; lane (g, item)
 // takes splits g, g+4, ... of each block of up to 128 splits, and all of a block's
 // loads (the acc rows and every split's (m, l)) are issued before any is
@@ -17,12 +20,36 @@ constexpr int kSplitMax = 1024;
 constexpr int kCombItems = 16;                    // float4 items per wave (64 dims)
 constexpr int kCombGroups = 64 / kCombItems;      // split groups per wave
 
+// Units whose first split is on XCD x: [first[x], first[x + 1]), for a split
+// grid of units * ns workgroups mapped by xcd_unit_split.
+struct XcdUnits {
+  int first[kXcds + 1];
+};
+
+static XcdUnits xcd_units(long units, int ns) {
+  XcdUnits m;
+  const long N = units * ns, q = N / kXcds, r = N % kXcds;
+  for (int x = 0; x < kXcds; ++x) {
+    const long start = x * q + (x < r ? x : r);    // first split index dealt to XCD x
+    m.first[x] = (int)((start + ns - 1) / ns);
+  }
+  m.first[kXcds] = (int)units;
+  return m;
+}
+
 template <int D, int PF>
-__global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
+__global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o, XcdUnits xm) {
   constexpr int BLK = kCombGroups * PF;           // splits per block
   constexpr int MB = (BLK + 63) / 64;             // (m, l) pairs per lane per block
+  constexpr int NSL = D / 64;                     // 64-dim slices per head row
   static_assert(BLK <= 128, "at most two (m, l) pairs per lane");
-  const int unit = blockIdx.x, h = blockIdx.y, slice = blockIdx.z;
+  const int x = blockIdx.x % kXcds, kk = blockIdx.x / kXcds;
+  const int wu = (o.G < o.hbs ? o.G : o.hbs) * NSL;                  // waves per unit
+  const int uk = kk / wu;
+  const int unit = xm.first[x] + uk;
+  if (unit >= xm.first[x + 1]) return;
+  const int rw = kk - uk * wu;
+  const int h = rw / NSL, slice = rw - h * NSL;
   const int b = unit / (o.Hk * o.HB);
   const int rem = unit - b * o.Hk * o.HB;
   const int hk = rem / o.HB, hb = rem - (rem / o.HB) * o.HB;
@@ -101,31 +128,37 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o) {
 }
 
 template <int D>
-static void launch_combine(const SplitKOut& o, dim3 grid, hipStream_t stream) {
+static void launch_combine(const SplitKOut& o, const XcdUnits& xm, dim3 grid, hipStream_t stream) {
   // acc loads per lane per block: enough for min(ns, 128) splits over the 4 groups
   const int need = ((o.nsplit < 128 ? o.nsplit : 128) + kCombGroups - 1) / kCombGroups;
   if (need <= 2)
-    hipLaunchKernelGGL((splitk_combine_kernel<D, 2>), grid, dim3(64), 0, stream, o);
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 2>), grid, dim3(64), 0, stream, o, xm);
   else if (need <= 4)
-    hipLaunchKernelGGL((splitk_combine_kernel<D, 4>), grid, dim3(64), 0, stream, o);
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 4>), grid, dim3(64), 0, stream, o, xm);
   else if (need <= 8)
-    hipLaunchKernelGGL((splitk_combine_kernel<D, 8>), grid, dim3(64), 0, stream, o);
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 8>), grid, dim3(64), 0, stream, o, xm);
   else if (need <= 16)
-    hipLaunchKernelGGL((splitk_combine_kernel<D, 16>), grid, dim3(64), 0, stream, o);
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 16>), grid, dim3(64), 0, stream, o, xm);
   else
-    hipLaunchKernelGGL((splitk_combine_kernel<D, 32>), grid, dim3(64), 0, stream, o);
+    hipLaunchKernelGGL((splitk_combine_kernel<D, 32>), grid, dim3(64), 0, stream, o, xm);
 }
 
 int splitk_combine(const SplitKOut& o, long units, int D, hipStream_t stream) {
   if (o.nsplit <= 1) return 0;
   if (o.nsplit > kSplitMax) return (int)hipErrorInvalidValue;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
-  // one wave per (unit, query head of the unit's head block, 64-dim slice)
-  const dim3 grid((unsigned)units, (unsigned)(o.G < o.hbs ? o.G : o.hbs), (unsigned)(D / 64));
+  // one wave per (unit, query head of the unit's head block, 64-dim slice),
+  // eight interleaved per-XCD lists as long as the longest
+  const long wu = (long)(o.G < o.hbs ? o.G : o.hbs) * (D / 64);
+  const XcdUnits xm = xcd_units(units, o.nsplit);
+  long most = 0;
+  for (int x = 0; x < kXcds; ++x) most = xm.first[x + 1] - xm.first[x] > most ? xm.first[x + 1] - xm.first[x] : most;
+  if (most * wu * kXcds > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)(most * wu * kXcds));
   if (D == 64)
-    launch_combine<64>(o, grid, stream);
+    launch_combine<64>(o, xm, grid, stream);
   else
-    launch_combine<128>(o, grid, stream);
+    launch_combine<128>(o, xm, grid, stream);
   return (int)hipGetLastError();
 }
 
