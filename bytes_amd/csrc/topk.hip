@@ -74,19 +74,28 @@ __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum, 
   return r;
 }
 
+// Buffer resource over the n floats of a row: reads past the row return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* x, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, (int)((uint32_t)n * 4u), 0x00020000);
+}
+
+// Order keys of elements i .. i+3 of a row and whether each exists.  Loads go
+// through the row's buffer resource, unconditionally (past the row they read
+// zero), so no load sits under a branch and a thread's loads are all in flight
+// together.  VEC: one 16-byte load (the host sets it only for 16-byte-aligned
+// rows with n % 4 == 0, so a vector is never partly past the row).
 template <bool VEC>
-__device__ __forceinline__ void load4(const float* x, int i, int n, uint32_t (&key)[4], bool (&ok)[4]) {
-  if (VEC && i + 3 < n) {
-    const float4 v = *reinterpret_cast<const float4*>(x + i);
-    key[0] = order_key(v.x); key[1] = order_key(v.y); key[2] = order_key(v.z); key[3] = order_key(v.w);
-    ok[0] = ok[1] = ok[2] = ok[3] = true;
+__device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rs, int i, int n, uint32_t (&key)[4], bool (&ok)[4]) {
+  if constexpr (VEC) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, i * 4, 0, 0));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) key[j] = order_key(__uint_as_float(v[j]));
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ok[j] = i + j < n;
-      key[j] = ok[j] ? order_key(x[i + j]) : 0u;
-    }
+    for (int j = 0; j < 4; ++j) key[j] = order_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (i + j) * 4, 0, 0)));
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ok[j] = i + j < n;
 }
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
@@ -152,12 +161,16 @@ constexpr int kRowBatch = 1024;        // rows per launch group (fixed histogram
 // never moves, list data of an earlier call can never land in it.
 struct TopkWs {
   uint32_t* hist;    // [kRowBatch][kBins]
-  uint32_t* cnt;     // [kRowBatch][2]: above-list length, candidate count
+  uint32_t* cnt;     // [kRowBatch][kCntStride]: above-list length, candidate count
   uint64_t* above;   // [kRowBatch][k]
   uint64_t* cand;    // [kRowBatch][kCandCap]
 };
 
-constexpr size_t kTopkZeroBytes = (size_t)kRowBatch * kBins * 4 + (size_t)kRowBatch * 2 * 4;
+// A row's two list counters have a 128-byte line of their own: the filter
+// workgroups of a row (on every XCD) add to them with device-wide atomics,
+// which serialise per cache line.
+constexpr int kCntStride = 32;
+constexpr size_t kTopkZeroBytes = (size_t)kRowBatch * kBins * 4 + (size_t)kRowBatch * kCntStride * 4;
 
 // Lists for the rows of one launch group (min(rows, kRowBatch)) follow the
 // fixed zero region.  k above kTopkMaxK (unsorted output only) runs the
@@ -188,13 +201,14 @@ __global__ __launch_bounds__(kPassThreads) void topk_hist_kernel(const float* sc
   // scores points at the batch's first row; row indexes the batch's workspace rows
   const int row = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
   const float* x = scores + (int64_t)row * row_stride;
+  const auto rs = row_rsrc(x, n);
   constexpr int R = kSlice / (kPassThreads * 4);
   uint32_t key[R][4];
   bool ok[R][4];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = part * kSlice + (r * kPassThreads + threadIdx.x) * 4;
-    load4<VEC>(x, i < n ? i : n, n, key[r], ok[r]);
+    load4<VEC>(rs, i, n, key[r], ok[r]);
   }
   for (int b = threadIdx.x; b < kBins; b += kPassThreads) h[b] = 0u;
   __syncthreads();
@@ -243,13 +257,14 @@ __global__ __launch_bounds__(kPassThreads) void topk_filter_kernel(const float* 
   __shared__ uint32_t sel[4];
   const int row = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
   const float* x = scores + (int64_t)row * row_stride;
+  const auto rs = row_rsrc(x, n);
   constexpr int R = kSlice / (kPassThreads * 4);
   uint32_t key[R][4];
   bool ok[R][4];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = part * kSlice + (r * kPassThreads + threadIdx.x) * 4;
-    load4<VEC>(x, i < n ? i : n, n, key[r], ok[r]);
+    load4<VEC>(rs, i, n, key[r], ok[r]);
   }
   find_digit<kPassThreads>(ws.hist + (int64_t)row * kBins, (uint32_t)k, wsum, sel);
   const uint32_t d0 = sel[0];                   // digits are < kBins: a missing pick keeps every key out
@@ -267,8 +282,8 @@ __global__ __launch_bounds__(kPassThreads) void topk_filter_kernel(const float* 
   uint32_t oa = block_incl_scan<kPassThreads>(na, wsum, ta) - na;
   uint32_t oc = block_incl_scan<kPassThreads>(nc, wsum, tc) - nc;
   if (threadIdx.x == 0) {
-    sel[2] = ta ? atomicAdd(ws.cnt + row * 2 + 0, ta) : 0u;
-    sel[3] = tc ? atomicAdd(ws.cnt + row * 2 + 1, tc) : 0u;
+    sel[2] = ta ? atomicAdd(ws.cnt + row * kCntStride + 0, ta) : 0u;
+    sel[3] = tc ? atomicAdd(ws.cnt + row * kCntStride + 1, tc) : 0u;
   }
   __syncthreads();
   oa += sel[2];
@@ -318,6 +333,7 @@ template <bool VEC>
 __device__ void topk_row_exact(const float* x, int n, int k, int sorted, uint64_t* sortbuf, uint32_t* hist,
                                uint32_t* wsum, uint32_t* sel, int32_t* o) {
   const int tid = threadIdx.x;
+  const auto rs = row_rsrc(x, n);
   uint32_t prefix = 0u, pmask = 0u;
   uint32_t kr = (uint32_t)k;
 #pragma unroll 1
@@ -329,7 +345,7 @@ __device__ void topk_row_exact(const float* x, int n, int k, int sorted, uint64_
     for (int i = tid * 4; i < n; i += kTopkThreads * 4) {
       uint32_t key[4];
       bool ok[4];
-      load4<VEC>(x, i, n, key, ok);
+      load4<VEC>(rs, i, n, key, ok);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (ok[j] && (key[j] & pmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & dmask], 1u);
@@ -353,7 +369,7 @@ __device__ void topk_row_exact(const float* x, int n, int k, int sorted, uint64_
       const int i = base + tid * 4;
       uint32_t key[4];
       bool ok[4];
-      load4<VEC>(x, i, n, key, ok);
+      load4<VEC>(rs, i, n, key, ok);
       uint32_t ne = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) ne += (ok[j] && key[j] == T) ? 1u : 0u;
@@ -397,7 +413,7 @@ __device__ void topk_row_exact(const float* x, int n, int k, int sorted, uint64_
     const int i = base + tid * 4;
     uint32_t key[4];
     bool ok[4];
-    load4<VEC>(x, i, n, key, ok);
+    load4<VEC>(rs, i, n, key, ok);
     uint32_t ne = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) ne += (ok[j] && key[j] == T) ? 1u : 0u;
@@ -436,6 +452,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
   const int row = blockIdx.x, tid = threadIdx.x;
   int32_t* o = out + (int64_t)row * out_stride;
   const float* x = scores + (int64_t)row * row_stride;
+  const auto rs = row_rsrc(x, n);
   if (exact) {                                   // short rows: one pass of this kernel only
     if (sorted && n <= kFullSortRow) {
       // sort the whole row by (key desc, index asc)
@@ -454,7 +471,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
     }
     return;
   }
-  const uint32_t A = ws.cnt[row * 2 + 0], Cn = ws.cnt[row * 2 + 1];
+  const uint32_t A = ws.cnt[row * kCntStride + 0], Cn = ws.cnt[row * kCntStride + 1];
   bool fallback = true;
   // lists are complete and consistent: fewer than k keys above the digit, the
   // candidates fill the rest and fit their list
@@ -576,8 +593,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_select_kernel(const float* 
   uint32_t* hr = ws.hist + (int64_t)row * kBins;
   for (int b = tid; b < kBins; b += kTopkThreads) hr[b] = 0u;
   if (tid == 0) {
-    ws.cnt[row * 2 + 0] = 0u;
-    ws.cnt[row * 2 + 1] = 0u;
+    ws.cnt[row * kCntStride + 0] = 0u;
+    ws.cnt[row * kCntStride + 1] = 0u;
   }
 }
 
@@ -615,6 +632,7 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
   uint32_t* hist = hist_s[w];
   uint64_t* sb = sb_s[w];
   const float* x = scores + row * row_stride;
+  const auto rs = row_rsrc(x, n);
   int32_t* o = out + row * out_stride;
 
   uint32_t key[PER];
@@ -623,7 +641,7 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
   for (int j = 0; j < PER / 4; ++j) {
     uint32_t kq[4];
     bool okq[4];
-    load4<VEC>(x, i0 + 4 * j, n, kq, okq);
+    load4<VEC>(rs, i0 + 4 * j, n, kq, okq);
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
   }
@@ -765,6 +783,7 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t row = blockIdx.x;
   const float* x = scores + row * row_stride;
+  const auto rs = row_rsrc(x, n);
   int32_t* o = out + row * out_stride;
 
   uint32_t key[PER];
@@ -773,7 +792,7 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
   for (int j = 0; j < PER / 4; ++j) {
     uint32_t kq[4];
     bool okq[4];
-    load4<VEC>(x, i0 + 4 * j, n, kq, okq);
+    load4<VEC>(rs, i0 + 4 * j, n, kq, okq);
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
   }
@@ -993,7 +1012,7 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
   if (!workspace || workspace_bytes < topk_ws_bytes(rows, k)) return (int)hipErrorInvalidValue;
   if (hist_ready && rows > kRowBatch) return (int)hipErrorInvalidValue;
   const TopkWs ws = topk_ws_carve(workspace, rows, k);
-  const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0) && (row_stride % 4 == 0);
+  const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0) && (row_stride % 4 == 0) && (n % 4 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float* s = static_cast<const float*>(scores);
   int32_t* o = static_cast<int32_t*>(out);
