@@ -93,4 +93,21 @@ __device__ __forceinline__ void lds_barrier() {
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Touch every 8-byte word of a kernel's argument block at entry: the scalar
+// loads of the whole block are then issued together, one scalar-cache round
+// trip, instead of in batches at each first use (each a round trip of its
+// own before the first memory request can go out).  A macro, expanded in the
+// kernel body: reading the block through a helper's reference parameter makes
+// the compiler address every pointer the block holds as a flat pointer.
+#define PREFETCH_ARGS(args)                                                          \
+  do {                                                                               \
+    static_assert(sizeof(args) % 8 == 0, "argument block in 8-byte words");          \
+    constexpr int pf_n = (int)(sizeof(args) / 8);                                    \
+    u32x2 pf_v[pf_n];                                                                \
+    _Pragma("unroll") for (int pf_i = 0; pf_i < pf_n; ++pf_i)                        \
+      pf_v[pf_i] = reinterpret_cast<const u32x2*>(&(args))[pf_i];                    \
+    _Pragma("unroll") for (int pf_i = 0; pf_i < pf_n; ++pf_i)                        \
+      asm volatile("" : : "s"(pf_v[pf_i]));                                          \
+  } while (0)
+
 }  // namespace bytes_amd

@@ -37,13 +37,14 @@ struct DenseArgs {
 
 template <int D, bool FP8>
 __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(DenseArgs a) {
+  PREFETCH_ARGS(a);
   using C = DenseCfg<D>;
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   int unit, split;
-  xcd_unit_split(a.o.nsplit, unit, split);
+  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
   const int b = unit / (a.Hk * a.HB);
   const int rem = unit - b * a.Hk * a.HB;
   const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;

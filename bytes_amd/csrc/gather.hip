@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
   int32_t* rows = reinterpret_cast<int32_t*>(smem_raw + C::kSmem);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int unit, split;
-  xcd_unit_split(a.o.nsplit, unit, split);
+  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
 
   int b, hk, hq0, nh;
   const int32_t* irow;

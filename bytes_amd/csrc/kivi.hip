@@ -449,11 +449,12 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
 template <int D, int BITS, int NW>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a) {
   using C = KiviCfg<D, BITS, NW>;
+  PREFETCH_ARGS(a);
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   int unit, split;
-  xcd_unit_split(a.o.nsplit, unit, split);
+  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
   const int b = unit / (a.Hk * a.HB);
   const int rem = unit - b * a.Hk * a.HB;
   const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;

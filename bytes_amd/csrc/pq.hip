@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   char* vcb = smem_raw + C::LUT;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int unit, split;
-  xcd_unit_split(a.o.nsplit, unit, split);
+  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
   const int b = unit / (a.Hk * a.HG);
   const int rem = unit - b * a.Hk * a.HG;
   const int hk = rem / a.HG, hg = rem - (rem / a.HG) * a.HG;

@@ -422,6 +422,7 @@ struct PackedKeys {
 
 template <class P>
 __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a) {
+  PREFETCH_ARGS(a);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int unit = blockIdx.x / a.parts, part = blockIdx.x - unit * a.parts;
   const int b = unit / (a.Hk * a.HB);

@@ -26,6 +26,7 @@ struct SplitKOut {
   int nsplit;
   int Hk, HB, G;        // unit u -> b = u / (Hk*HB), hk, hb; query head = hk*G + hb*hbs + h
   int hbs = 16;         // query heads per head block
+  int nwg = 0;          // workgroups of the split grid (units * nsplit)
 };
 
 constexpr long kMaxUnits = 65535;         // grid.y limit
@@ -44,6 +45,7 @@ inline void splitk_carve(void* ws, long units, long nsplit, SplitKOut& o) {
   o.part_ml = reinterpret_cast<float*>(p);
   o.part_acc = reinterpret_cast<float*>(p + ml);
   o.nsplit = (int)nsplit;
+  o.nwg = (int)(units * nsplit);
 }
 
 // Workgroups of a 1-D grid are dealt round-robin over the XCDs (8 on MI355X),
@@ -52,14 +54,15 @@ inline void splitk_carve(void* ws, long units, long nsplit, SplitKOut& o) {
 // splits share cache lines of per-channel rows and metadata, which are then
 // fetched into one L2 instead of several.  A bijection for any grid size.
 constexpr int kXcds = 8;
-__device__ __forceinline__ void xcd_unit_split(int nsplit, int& unit, int& split) {
-  const int L = blockIdx.x, N = gridDim.x;
+__device__ __forceinline__ void xcd_unit_split(int nsplit, int N, int& unit, int& split) {
+  const int L = blockIdx.x;
   const int x = L % kXcds, k = L / kXcds;
   const int q = N / kXcds, r = N % kXcds;
   const int idx = x * q + min(x, r) + k;
   unit = idx / nsplit;
   split = idx - unit * nsplit;
 }
+
 
 // Raw buffer resource over [base, base + bytes) (out-of-range lanes read 0 and
 // drop stores).
