@@ -311,48 +311,64 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   Regs r;
   if (any) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t, lane, r);
 
-  // ---- stage the group's LUTs ----
+  // The value codebook (quantized V) is requested now, with the first tile's
+  // codes, so it arrives while the LUTs are built or staged; it is stored to
+  // LDS after them (chunks past M*K repeat the last one).
   const int K = a.K;
+  constexpr int VPT = (M * kPqKMax + kPqWaves * 64 - 1) / (kPqWaves * 64);   // codebook chunks per thread
+  u32x4 vraw[QV ? VPT : 1];
+  const _Float16* vcbh = QV ? a.vcb + (int64_t)hk * a.vcb_sh : nullptr;
+  if constexpr (QV) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) vraw[i] = ld16(vcbh + (int64_t)min((int)threadIdx.x + kPqWaves * 64 * i, M * K - 1) * 8);
+  }
+
+  // ---- stage the group's LUTs ----
   if (BUILD_LUT) {
     // LUT[h][j][c] = lut_scale * sum_e q[h][8j+e] * kcb[j][c][e], e ascending,
     // fp32.  The unit's q rows go to LDS as fp32 (in the tile buffers, unused
-    // until the tile loop); every thread requests all of its codewords at once
-    // (entries past n repeat entry n - 1) and scores each against the heads.
+    // until the tile loop).  Thread t scores codewords c = t % TPJ + TPJ*i of
+    // subspace j = t / TPJ against every head, so it reads its heads' q rows
+    // once; all of its codewords are requested at once (codewords past K
+    // repeat codeword K - 1 and land in LUT entries no code reads).
     static_assert(kPqWaves * C::TILE >= kPqHeads * D * 4, "q rows fit in the tile buffers");
-    constexpr int NT = kPqWaves * 64, CPT = (M * kPqKMax + NT - 1) / NT;
+    constexpr int NT = kPqWaves * 64, TPJ = NT / M, CPT = kPqKMax / TPJ;
+    static_assert(TPJ * M == NT && CPT * TPJ == kPqKMax, "threads per subspace");
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
-    const int n = M * K;
+    const int j = threadIdx.x / TPJ, c0 = threadIdx.x - j * TPJ;
     u32x4 craw[CPT];
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) craw[i] = ld16(cb + (int64_t)min((int)threadIdx.x + NT * i, n - 1) * 8);
+    for (int i = 0; i < CPT; ++i) craw[i] = ld16(cb + ((int64_t)j * K + min(c0 + TPJ * i, K - 1)) * 8);
     float* qs = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB);
     if (threadIdx.x < kPqHeads * M) {
-      const int h = threadIdx.x / M, j = threadIdx.x - (threadIdx.x / M) * M;
-      const u32x4 qraw = ld16(a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + min(h, nh - 1)) * a.q_sh + j * 8);
+      const int h = threadIdx.x / M, jq = threadIdx.x - (threadIdx.x / M) * M;
+      const u32x4 qraw = ld16(a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + min(h, nh - 1)) * a.q_sh + jq * 8);
       const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) qs[(h * M + j) * 8 + x] = bf16_bits_to_f32(qh[x]);
+      for (int x = 0; x < 8; ++x) qs[(h * M + jq) * 8 + x] = bf16_bits_to_f32(qh[x]);
     }
     __syncthreads();
+    f32x4 qv[kPqHeads][2];
+#pragma unroll
+    for (int h = 0; h < kPqHeads; ++h) {
+      qv[h][0] = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8);
+      qv[h][1] = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8 + 4);
+    }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int e = min((int)threadIdx.x + NT * i, n - 1);
-      const int j = e / K, c = e - j * K;
       const _Float16* ch = reinterpret_cast<const _Float16*>(&craw[i]);
 #pragma unroll
       for (int h = 0; h < kPqHeads; ++h) {
-        const f32x4 q0 = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8);
-        const f32x4 q1 = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8 + 4);
         float sum = 0.f;
-        sum += q0[0] * (float)ch[0];
-        sum += q0[1] * (float)ch[1];
-        sum += q0[2] * (float)ch[2];
-        sum += q0[3] * (float)ch[3];
-        sum += q1[0] * (float)ch[4];
-        sum += q1[1] * (float)ch[5];
-        sum += q1[2] * (float)ch[6];
-        sum += q1[3] * (float)ch[7];
-        lut[(h * M + j) * kPqKMax + c] = sum * a.lut_scale;
+        sum += qv[h][0][0] * (float)ch[0];
+        sum += qv[h][0][1] * (float)ch[1];
+        sum += qv[h][0][2] * (float)ch[2];
+        sum += qv[h][0][3] * (float)ch[3];
+        sum += qv[h][1][0] * (float)ch[4];
+        sum += qv[h][1][1] * (float)ch[5];
+        sum += qv[h][1][2] * (float)ch[6];
+        sum += qv[h][1][3] * (float)ch[7];
+        lut[(h * M + j) * kPqKMax + c0 + TPJ * i] = sum * a.lut_scale;
       }
     }
   } else {
@@ -371,13 +387,12 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
         });
   }
   if constexpr (QV) {
-    const _Float16* cb = a.vcb + (int64_t)hk * a.vcb_sh;
-    stage_chunks(
-        M * K, [&](int e) { return cb + (int64_t)e * 8; },
-        [&](int e) {
-          const int j = e / K, c = e - j * K;
-          return vcb + ((j * kPqKMax + c) * 8) * 2;
-        });
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = min((int)threadIdx.x + kPqWaves * 64 * i, M * K - 1);
+      const int j = e / K, c = e - j * K;
+      *reinterpret_cast<u32x4*>(vcb + ((j * kPqKMax + c) * 8) * 2) = vraw[i];
+    }
   }
   float* qo = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB + kPqWaves * C::TILE);
   if constexpr (OUT) {
