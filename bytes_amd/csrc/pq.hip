@@ -40,7 +40,7 @@
 namespace bytes_amd {
 
 constexpr int kPqWaves = 8;    // two waves per SIMD at one workgroup per CU
-constexpr int kPqHeads = 4;     // query heads per unit
+constexpr int kPqHeads = 4;     // query heads per unit (one 16-byte LUT entry holds all of them)
 constexpr int kPqKMax = 256;    // codewords per subspace
 constexpr int kPqOutMax = 16;   // outlier channels
 
@@ -208,10 +208,12 @@ __device__ __forceinline__ void pq_stage_dense_v(int lane, const PqRegs<D, QV, V
   }
 }
 
-// One 32-row tile.  Scores: lane l sums the LUT entries of row l % 32 for head
-// slots l/32 and l/32 + 2 (subspaces in order), the wave passes them through
-// its tile buffer into the score-MFMA layout (head l%16, rows blk*16 + lg*4 + i),
-// then the V tile is built in the same buffer and the softmax/PV step runs.
+// One 32-row tile.  Scores: lane l sums the LUT entries of row l % 32 over
+// half l/32 of the subspaces for the four heads at once (LUTs are kept
+// [subspace][code][head], one 16-byte read per subspace), the halves are
+// added, the wave passes the scores through its tile buffer into the
+// score-MFMA layout (head l%16, rows blk*16 + lg*4 + i), then the V tile is
+// built in the same buffer and the softmax/PV step runs.
 template <int D, bool QV, bool VF8, bool OUT>
 __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV, VF8, OUT>& r, uint32_t vmask, int lane,
                                         int nh, const float* lut, const char* vcb, const float* qo, char* vst,
@@ -219,25 +221,34 @@ __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV, VF8
   constexpr int M = D / 8;
   const int l16 = lane & 15, lg = lane >> 4;
   float* sc_lds = reinterpret_cast<float*>(vst);   // [kPqHeads][32]
+  // lane half hf sums subspaces hf*M/2 .. of its row for all four heads at
+  // once (the LUT keeps a (subspace, code)'s heads adjacent); the halves are
+  // added as (first + second) on both sides
+  constexpr int MH = M / 2;
+  const int hf = lane >> 5;
+  f32x4 ps = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int rep = 0; rep < kPqHeads / 2; ++rep) {
-    const int h = (lane >> 5) + 2 * rep;
-    if (h < nh) {
-      const float* lh = lut + h * (M * kPqKMax);
-      float sc = 0.f;
+  for (int jj = 0; jj < MH; ++jj) {
+    const uint32_t w = hf ? r.kc[MH / 4 + (jj >> 2)] : r.kc[jj >> 2];
+    const uint32_t code = (w >> ((jj & 3) * 8)) & 0xFFu;
+    ps += *reinterpret_cast<const f32x4*>(lut + ((hf * MH + jj) * kPqKMax + code) * kPqHeads);
+  }
+  f32x4 sc4;
 #pragma unroll
-      for (int j = 0; j < M; ++j) {
-        const uint32_t code = (r.kc[j >> 2] >> ((j & 3) * 8)) & 0xFFu;
-        sc += lh[j * kPqKMax + code];
-      }
-      if constexpr (OUT) {
-        float so = 0.f;
+  for (int h = 0; h < kPqHeads; ++h) {
+    const float o = shfl_xor_f(ps[h], 32);
+    sc4[h] = hf ? o + ps[h] : ps[h] + o;
+    if constexpr (OUT) {
+      float so = 0.f;
 #pragma unroll
-        for (int c = 0; c < kPqOutMax; ++c) so += qo[h * kPqOutMax + c] * r.ko[c];   // zero past C
-        sc += so;
-      }
-      sc_lds[h * kTile + (lane & 31)] = sc;
+      for (int c = 0; c < kPqOutMax; ++c) so += qo[h * kPqOutMax + c] * r.ko[c];   // zero past C
+      sc4[h] += so;
     }
+  }
+#pragma unroll
+  for (int rep = 0; rep < 2; ++rep) {
+    const int h = hf * 2 + rep;
+    if (h < nh) sc_lds[h * kTile + (lane & 31)] = hf ? sc4[2 + rep] : sc4[rep];
   }
   wave_lds_sync();
   f32x4 s[2];
@@ -357,6 +368,7 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const _Float16* ch = reinterpret_cast<const _Float16*>(&craw[i]);
+      f32x4 e4;
 #pragma unroll
       for (int h = 0; h < kPqHeads; ++h) {
         float sum = 0.f;
@@ -368,23 +380,33 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
         sum += qv[h][1][1] * (float)ch[5];
         sum += qv[h][1][2] * (float)ch[6];
         sum += qv[h][1][3] * (float)ch[7];
-        lut[(h * M + j) * kPqKMax + c0 + TPJ * i] = sum * a.lut_scale;
+        e4[h] = sum * a.lut_scale;
       }
+      *reinterpret_cast<f32x4*>(lut + (j * kPqKMax + c0 + TPJ * i) * kPqHeads) = e4;
     }
   } else {
-    const int K4 = K / 4;
-    stage_chunks(
-        nh * M * K4,
-        [&](int e) {
-          const int h = e / (M * K4), r2 = e - h * (M * K4);
-          const int j = r2 / K4, c4 = r2 - j * K4;
-          return a.lut + (int64_t)b * a.l_sb + (int64_t)(hq0 + h) * a.l_sh + j * K + c4 * 4;
-        },
-        [&](int e) {
-          const int h = e / (M * K4), r2 = e - h * (M * K4);
-          const int j = r2 / K4, c4 = r2 - j * K4;
-          return lut + (h * M + j) * kPqKMax + c4 * 4;
-        });
+    // the caller's LUTs, transposed so the heads of one (subspace, code) are
+    // adjacent; chunks past n repeat the last one (same values, same place)
+    const int K4 = K / 4, n = nh * M * K4;
+    constexpr int NT = kPqWaves * 64, BATCH = 8;
+    for (int e0 = threadIdx.x; e0 < n; e0 += NT * BATCH) {
+      u32x4 v[BATCH];
+#pragma unroll
+      for (int bb = 0; bb < BATCH; ++bb) {
+        const int e = min(e0 + bb * NT, n - 1);
+        const int h = e / (M * K4), r2 = e - h * (M * K4);
+        const int j = r2 / K4, c4 = r2 - j * K4;
+        v[bb] = ld16(a.lut + (int64_t)b * a.l_sb + (int64_t)(hq0 + h) * a.l_sh + j * K + c4 * 4);
+      }
+#pragma unroll
+      for (int bb = 0; bb < BATCH; ++bb) {
+        const int e = min(e0 + bb * NT, n - 1);
+        const int h = e / (M * K4), r2 = e - h * (M * K4);
+        const int j = r2 / K4, c4 = r2 - j * K4;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) lut[(j * kPqKMax + c4 * 4 + x) * kPqHeads + h] = __uint_as_float(v[bb][x]);
+      }
+    }
   }
   if constexpr (QV) {
 #pragma unroll
