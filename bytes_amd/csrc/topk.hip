@@ -647,11 +647,27 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
   }
   auto valid = [&](int q) { return i0 + q < n; };
 
-  uint32_t prefix = 0u, pmask = 0u, kr = (uint32_t)k;
+  // the digit passes start at the highest bit in which the row's keys differ
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+  for (int q = 0; q < PER; ++q)
+    if (valid(q)) {
+      kmin = min(kmin, key[q]);
+      kmax = max(kmax, key[q]);
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off, 64));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+  }
+  const uint32_t diff = kmin ^ kmax;
+  const int hb = diff ? 31 - __builtin_clz(diff) : -1;
+  uint32_t pmask = hb < 0 ? 0xFFFFFFFFu : ~(uint32_t)((2ull << hb) - 1ull);
+  uint32_t prefix = kmin & pmask, kr = (uint32_t)k;
 #pragma unroll 1
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+  for (int hi = hb; hi >= 0; hi -= 11) {
+    const int shift = hi >= 10 ? hi - 10 : 0;
+    const uint32_t dmask = (1u << (hi - shift + 1)) - 1u;
     u32x4* h4 = reinterpret_cast<u32x4*>(hist) + lane * 8;      // this lane's 32 bins
 #pragma unroll
     for (int q = 0; q < 8; ++q) h4[q] = u32x4{0u, 0u, 0u, 0u};
