@@ -112,6 +112,22 @@ def test_topk_small_rows(dev, rows, n, k):
                        R.topk_indices(s, k, sorted_by_score=False))
 
 
+@pytest.mark.parametrize("rows,n,k", [(300, 2048, 128), (28, 2048, 128), (280, 4096, 600), (5, 1000, 17)])
+def test_topk_narrow_range_rows(dev, rows, n, k):
+    """Scores in a narrow range (every key shares its top bits; the digit
+    passes start below them), with exact ties and an all-equal row, on the
+    one-wave path (more rows than CUs, k <= 256) and the workgroup path."""
+    g = torch.Generator().manual_seed(rows + n + k)
+    s = 3.0 + torch.rand(rows, n, generator=g) * 0.5
+    s[0, 10:40] = 3.25                                       # a block of exact ties
+    s[1] = 3.125                                             # an all-equal row
+    if n > 100:
+        s[2, :5] = 3.0 + 2.0 ** -20                          # keys one ulp-scale apart
+    for so in (True, False):
+        got = SP.topk_indices(s.to(dev), k, sorted=so).cpu()
+        assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=so)), so
+
+
 def test_topk_many_short_rows_unaligned(dev):
     s = _tie_heavy(400, 1500, seed=11)
     big = torch.zeros(400 * 1500 + 1)
