@@ -28,7 +28,7 @@
 namespace bytes_amd {
 
 constexpr int kTopkThreads = 1024;     // select kernel
-constexpr int kPassThreads = 256;      // histogram and filter kernels
+constexpr int kPassThreads = 512;      // histogram and filter kernels (four 16-byte loads per thread)
 constexpr int kSlice = 8192;           // row elements per histogram / filter workgroup
 constexpr int kTopkMaxK = 8192;
 constexpr int kBins = 2048;            // digit = top 11 bits of the order key
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kPassThreads) void topk_hist_kernel(const float* sc
 }
 
 // The digit holding the k-th largest key of a row and the count of keys in
-// larger digits, from its histogram (thread t owns digits 8t .. 8t+7).
+// larger digits, from its histogram (thread t owns digits PER*t .. PER*t+PER-1, PER = kBins / NT).
 template <int NT>
 __device__ __forceinline__ void find_digit(const uint32_t* hr, uint32_t k, uint32_t* wsum, uint32_t* sel) {
   constexpr int PER = kBins / NT;
