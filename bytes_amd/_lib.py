@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
-from typing import Dict, Tuple
+from typing import Dict, List, Tuple
 
 import torch
 
@@ -104,6 +104,9 @@ SIGNATURES: Dict[str, Tuple] = {
     "bytes_pq_encode": (c_vp, c_int, c_int, c_i64, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
     "bytes_pq_decode_vectors": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
     "bytes_pq_kmeans_update": (c_vp, c_int, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp),
+    "bytes_select_mask": (c_vp, c_i64, c_int, c_i64, c_vp, c_int, c_int, c_int, c_vp),
+    "bytes_select_fill": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_i64, c_vp, c_int, c_i64, c_vp),
+    "bytes_select_pages": (c_vp, c_i64, c_int, c_int, c_i64, c_vp, c_vp),
 }
 _RESTYPES = {"bytes_error_string": ctypes.c_char_p}
 
@@ -158,8 +161,17 @@ def stream_of(t: torch.Tensor) -> int:
 # (re)allocated; it grows on demand, and the usual warm-up call before a graph
 # capture sizes it.  Calls that share a buffer must be ordered on one stream
 # (the reference harness runs everything on the current stream).
+#
+# A graph captured earlier keeps the address of the buffer it was captured
+# with, so a buffer that has been replaced by a larger one is never released:
+# it stays in _retired until the process ends, still zero at rest, and old
+# graphs keep replaying into memory that nothing else owns.  A buffer cannot
+# be created or grown while the current stream is capturing (the allocation
+# would come from the graph's pool and its zero fill would only run at
+# replay); that raises, and a warm-up call before the capture avoids it.
 # ---------------------------------------------------------------------------
 _ws: Dict[Tuple[int, str], torch.Tensor] = {}
+_retired: List[torch.Tensor] = []
 
 
 def workspace(device: torch.device, nbytes: int, family: str = "splitk") -> torch.Tensor:
@@ -167,7 +179,14 @@ def workspace(device: torch.device, nbytes: int, family: str = "splitk") -> torc
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), family)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"bytes_amd: the {family!r} workspace on cuda:{key[0]} needs {int(nbytes)} bytes "
+                f"(has {0 if buf is None else buf.numel()}) during graph capture; make one eager call "
+                "of the same shape before capturing")
         size = max(int(nbytes), 1 << 20)
+        if buf is not None:
+            _retired.append(buf)
         buf = torch.zeros(size, dtype=torch.uint8, device=dev)
         _ws[key] = buf
     return buf

@@ -66,17 +66,20 @@ constexpr int kQuestSlots = kQuestThreads / kQuestPages;   // head slots per rou
 template <int D>
 __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                                                     const uint16_t* kmin, const uint16_t* kmax,
-                                                                    int Hk, int G, int np, int page, int pos,
-                                                                    int local_w, float scale, float* bound,
-                                                                    int64_t o_sb, int64_t o_sh) {
+                                                                    int Hk, int G, int HB, int np, int page,
+                                                                    int pos, int local_w, float scale,
+                                                                    float* bound, int64_t o_sb, int64_t o_sh) {
   constexpr int RW = D / 2 + 1;                    // dwords per padded row
   __shared__ uint32_t mn_s[kQuestPages * RW];
   __shared__ uint32_t mx_s[kQuestPages * RW];
   __shared__ float qs[16][D];
   const int parts = (np + kQuestPages - 1) / kQuestPages;
-  const int bh = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const int bhb = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const int bh = bhb / HB, hb = bhb - (bhb / HB) * HB;
   const int b = bh / Hk, hk = bh - (bh / Hk) * Hk;
   const int p0 = part * kQuestPages;
+  // this workgroup's heads: query heads hk*G + g0 .. + GB - 1 (blocks of 16)
+  const int g0 = hb * 16, GB = min(16, G - g0);
   // Every load is issued before any LDS store that consumes one (indices
   // clamped, so no load sits under a lane mask): one memory round trip.
   constexpr int QPT = 16 * D / kQuestThreads;      // query elements per thread (G <= 16)
@@ -85,9 +88,9 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
   uint16_t qv[QPT];
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
-    const int i = min((int)threadIdx.x + u * kQuestThreads, G * D - 1);
+    const int i = min((int)threadIdx.x + u * kQuestThreads, GB * D - 1);
     const int g = i / D, d = i - (i / D) * D;
-    qv[u] = q[(int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d];
+    qv[u] = q[(int64_t)b * q_sb + (int64_t)(hk * G + g0 + g) * q_sh + d];
   }
   const int64_t row0 = ((int64_t)b * Hk + hk) * np;
   u32x4 av[MPT], zv[MPT];
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
   }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
-    const int i = threadIdx.x + u * kQuestThreads;   // < 16 * D: rows past G are unused
+    const int i = threadIdx.x + u * kQuestThreads;   // < 16 * D: rows past GB are unused
     qs[i / D][i - (i / D) * D] = bf16_bits_to_f32(qv[u]);
   }
 #pragma unroll
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     const int lo = max(pos - local_w + 1, 0) / page, hi = pos / page;
     recent = p >= lo && p <= hi;
   }
-  for (int g = threadIdx.x / kQuestPages; g < G; g += kQuestSlots) {
+  for (int g = threadIdx.x / kQuestPages; g < GB; g += kQuestSlots) {
     float acc = 0.f;
 #pragma unroll 8
     for (int d2 = 0; d2 < D / 2; ++d2) {
@@ -140,7 +143,7 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     float v = acc * scale;
     if (!valid) v = kNegInf;
     if (recent) v = __builtin_inff();
-    bound[(int64_t)b * o_sb + (int64_t)(hk * G + g) * o_sh + p] = v;
+    bound[(int64_t)b * o_sb + (int64_t)(hk * G + g0 + g) * o_sh + p] = v;
   }
 }
 
@@ -170,11 +173,10 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
                             int64_t o_sb, int64_t o_sh, float scale, void* stream) {
   if (!q || !kmin || !kmax || !bound || B <= 0 || Hk <= 0 || Hq % Hk != 0 || np <= 0 || page <= 0)
     return (int)hipErrorInvalidValue;
-  const int G = Hq / Hk;
-  if (G > 16) return (int)hipErrorNotSupported;
+  const int G = Hq / Hk, HB = (G + 15) / 16;
   if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
   const int parts = (np + kQuestPages - 1) / kQuestPages;
-  const long grid = (long)B * Hk * parts;
+  const long grid = (long)B * Hk * HB * parts;
   if (grid > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* qq = static_cast<const uint16_t*>(q);
@@ -183,10 +185,10 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
   float* o = static_cast<float*>(bound);
   if (D == 128)
     hipLaunchKernelGGL(quest_score_kernel<128>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
-                       mn, mx, Hk, G, np, page, pos, local_w, scale, o, o_sb, o_sh);
+                       mn, mx, Hk, G, HB, np, page, pos, local_w, scale, o, o_sb, o_sh);
   else
     hipLaunchKernelGGL(quest_score_kernel<64>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
-                       mn, mx, Hk, G, np, page, pos, local_w, scale, o, o_sb, o_sh);
+                       mn, mx, Hk, G, HB, np, page, pos, local_w, scale, o, o_sb, o_sh);
   return (int)hipGetLastError();
 }
 

@@ -481,6 +481,22 @@ def kmeans(X: torch.Tensor, k: int, num_iters: int = 20, generator: Optional[tor
     return cb32[0] if squeeze else cb32
 
 
+def kmeans_pytorch(X: torch.Tensor, k: int, num_iters: int = 20,
+                   generator: Optional[torch.Generator] = None) -> torch.Tensor:
+    """Drop-in for src/quantization.py:102-132: X [N, d_sub] -> centroids
+    [k, d_sub] in X's dtype, fitted on the GPU by `kmeans`.
+
+    d_sub must be 8, the subspace width of the encode kernel and of every PQ
+    caller on the decode path (BASELINE C3, test_correctness.py:33).  N <= k
+    returns the points followed by zero rows, as the reference does.
+    """
+    if X.dim() != 2:
+        raise ValueError(f"X must be [N, d_sub], got {tuple(X.shape)}")
+    if X.shape[1] != D_SUB:
+        raise ValueError(f"d_sub {X.shape[1]} not supported (8)")
+    return kmeans(X, k, num_iters, generator)[0].to(X.dtype)
+
+
 class ProductQuantizer:
     """Drop-in for src/quantization.py:134-226 on the GPU kernels: `fit` runs
     k-means per subspace, `quantize` the bit-exact nearest-codeword encoder

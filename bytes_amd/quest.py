@@ -54,8 +54,8 @@ def quest_page_scores(q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, s
     _, Hk, np_, Dm = kmin.shape
     if one != 1 or Dm != D or tuple(kmax.shape) != tuple(kmin.shape) or kmin.shape[0] != B:
         raise ValueError(f"shape mismatch: q {tuple(q.shape)}, kmin {tuple(kmin.shape)}, kmax {tuple(kmax.shape)}")
-    if Hq % Hk != 0 or Hq // Hk > 16:
-        raise ValueError(f"H_q={Hq}, H_k={Hk}: groups of at most 16 query heads")
+    if Hq % Hk != 0:
+        raise ValueError(f"H_q={Hq} is not a multiple of H_k={Hk}")
     if D not in (64, 128):
         raise ValueError(f"head_dim {D} not supported (64 or 128)")
     kmin, kmax = kmin.contiguous(), kmax.contiguous()
@@ -84,19 +84,11 @@ def quest_select_pages(q, kmin, kmax, S: int, kb: int, page: int, scaling: float
 
 
 def _quest_select(q_blk, k_r, pos, S, kb, page, scaling, local_w=0):
-    """Drop-in for benchmarks/sparse_attention.py:328-364 at decode (one query
-    row).  q_blk [B,H_q,1,D] bf16; k_r [B,H_q,S,D] (GQA-expanded, as the
-    reference passes it) or [B,H_k,S,D]; pos: the query position (int or
-    1-element tensor).  Returns token ids [B,H_q,1,npick*page] int64: every
-    row of the selected pages, clamped to S-1."""
-    if q_blk.shape[2] != 1:
-        raise ValueError("one decode query row per call (Qc == 1)")
-    p = int(pos.reshape(-1)[0].item()) if isinstance(pos, torch.Tensor) else int(pos)
-    kmin, kmax = quest_page_minmax(k_r[:, :, :S], page)
-    pid = quest_select_pages(q_blk, kmin, kmax, S, kb, page, scaling, pos=p, local_w=local_w)
-    off = torch.arange(page, device=pid.device, dtype=torch.int64)
-    tok = (pid.long().unsqueeze(-1) * page + off).reshape(*pid.shape[:-1], -1).clamp(max=S - 1)
-    return tok.unsqueeze(2)
+    """Drop-in for benchmarks/sparse_attention.py:328-364 for Qc >= 1 query
+    rows (see bytes_amd.sparse_attention._quest_select): returns token ids
+    [B,H_q,Qc,npick*page] int64 of the selected pages, clamped to S-1."""
+    from .sparse_attention import _quest_select as qs
+    return qs(q_blk, k_r, pos, S, kb, page, scaling, local_w)
 
 
 def quest_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float, *, page: int = 16,

@@ -214,13 +214,35 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, c
  *   scale * sum_d max(q_d*kmin_d, q_d*kmax_d), d summed in ascending order in fp32
  *   (bit-identical to a sequential evaluation); -inf for pages starting after
  *   `pos`; +inf for pages overlapping (pos - local_w, pos] when local_w > 0.
- *   q [B, Hq, D] bf16; G = Hq/Hk <= 16; D in {64, 128}.
+ *   q [B, Hq, D] bf16; any G = Hq/Hk (head blocks of 16); D in {64, 128}.
  * ------------------------------------------------------------------------- */
 int bytes_quest_page_minmax(const void* k, void* kmin, void* kmax, int B, int Hk, int S, int D, int page,
                             int64_t k_sb, int64_t k_sh, int64_t k_ss, void* stream);
 int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, void* bound, int B, int Hq,
                             int Hk, int np, int D, int page, int pos, int local_w, int64_t q_sb, int64_t q_sh,
                             int64_t o_sb, int64_t o_sh, float scale, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Row steps of the selection functions for query chunks of Qc >= 1 rows
+ * (benchmarks/sparse_attention.py:226-387: select_topk, _quest_select,
+ * attend_topk).  Row r of a [.., Qc, n] array belongs to query row r % Qc,
+ * whose position is pos[r % Qc] (int64 device array of Qc entries).
+ * bytes_select_mask: in place over fp32 scores [rows, n] (row stride
+ *   row_stride): candidate t stands for position t*unit (unit 1: tokens,
+ *   :297-300; unit = page size: pages, :346-355); -inf where t*unit > pos,
+ *   then +inf where local_w > 0 and max(pos-local_w+1, 0)/unit <= t <= pos/unit.
+ * bytes_select_fill: out[r, j] = in[r, j] if j < k_in and 0 <= in[r, j] < S
+ *   and in[r, j] <= pos, else S (the sentinel of :288-293 and the masking rule
+ *   of :376).  in_dtype / out_dtype: 0 int32, 1 int64.
+ * bytes_select_pages: out[r, j] = min(page_ids[r, j / page] * page + j % page,
+ *   S - 1) int64 [rows, npick*page] from int32 page ids [rows, npick] (:358-363).
+ * ------------------------------------------------------------------------- */
+int bytes_select_mask(void* scores, int64_t rows, int n, int64_t row_stride, const void* pos, int Qc, int unit,
+                      int local_w, void* stream);
+int bytes_select_fill(const void* in, int in_dtype, int64_t in_rs, int k_in, void* out, int out_dtype,
+                      int64_t out_rs, int k_out, int64_t rows, const void* pos, int Qc, int64_t S, void* stream);
+int bytes_select_pages(const void* page_ids, int64_t rows, int npick, int page, int64_t S, void* out,
+                       void* stream);
 
 /* ---------------------------------------------------------------------------
  * Product-quantized decode with paged caches, outlier channels and fp8 values.

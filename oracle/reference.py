@@ -249,10 +249,15 @@ def pq_decode(idx: torch.Tensor, centroids: torch.Tensor) -> torch.Tensor:
 def kmeans(X: torch.Tensor, k: int, num_iters: int, generator: torch.Generator) -> torch.Tensor:
     """Codebook fitting (setup only, not on the timed path).
 
-    Restates src/quantization.py:102-132 (`kmeans_pytorch`): random-point
-    init, assign by nearest centroid, mean update, empty clusters re-seeded
-    from a random point.  Values depend on the RNG stream, so codebooks are
-    treated as inputs: parity is measured given identical codebooks.
+    Restates src/quantization.py:102-132 (`kmeans_pytorch`) step for step:
+    - N <= k: the points followed by k - N zero rows (:111-114);
+    - initial centroids: the first k points of one randperm(N) (:117-118);
+    - each iteration assigns every point to argmin of cdist (first index on
+      ties, :122-123), then updates the clusters in index order (:126-130):
+      a non-empty cluster takes the mean of its points, an empty one the point
+      X[randint(0, N, (1,))], drawn in that order from the same generator.
+    The reference draws from torch's global RNG; here the generator is
+    explicit.  Arithmetic is fp32 (X is converted first).
     """
     N, d = X.shape
     X = X.float()
@@ -261,15 +266,13 @@ def kmeans(X: torch.Tensor, k: int, num_iters: int, generator: torch.Generator) 
     perm = torch.randperm(N, generator=generator)
     cent = X[perm[:k]].clone()
     for _ in range(num_iters):
-        dists = torch.cdist(X, cent)
-        labels = torch.argmin(dists, dim=1)
-        sums = torch.zeros(k, d).index_add_(0, labels, X)
-        counts = torch.bincount(labels, minlength=k).float()
-        empty = counts == 0
-        cent = torch.where(empty[:, None], cent, sums / counts.clamp(min=1)[:, None])
-        if empty.any():
-            ridx = torch.randint(0, N, (int(empty.sum()),), generator=generator)
-            cent[empty] = X[ridx]
+        labels = torch.argmin(torch.cdist(X, cent), dim=1)
+        for i in range(k):
+            members = labels == i
+            if bool(members.any()):
+                cent[i] = X[members].mean(dim=0)
+            else:
+                cent[i] = X[torch.randint(0, N, (1,), generator=generator)]
     return cent
 
 
@@ -702,3 +705,127 @@ def quest_select(q, k, budget_tokens: int, page: int = 16, scale: float = 1.0):
     pidx = topk_indices(bound, npick)
     tok = (pidx.unsqueeze(-1) * page + torch.arange(page)).reshape(*pidx.shape[:-1], -1)
     return pidx, tok.clamp(max=S - 1), bound
+
+
+# ---------------------------------------------------------------------------
+# Query chunks of Qc >= 1 rows: select_topk / _quest_select / attend_topk
+# ---------------------------------------------------------------------------
+def _fold_rows(q_blk: torch.Tensor) -> torch.Tensor:
+    """[B,Hq,Qc,D] -> [B,Hq*Qc,1,D]: row (h, qc) becomes query head h*Qc + qc,
+    which reads KV head h // G as every row of query head h does."""
+    B, Hq, Qc, D = q_blk.shape
+    return q_blk.reshape(B, Hq * Qc, 1, D)
+
+
+def selection_mask(s: torch.Tensor, q_pos: torch.Tensor, unit: int = 1, local_w: int = 0) -> torch.Tensor:
+    """Causal mask and forced recent window over candidate t (position t*unit)
+    of query row qc: -inf where t*unit > pos[qc], then +inf where local_w > 0 and
+    max(pos-local_w+1, 0)//unit <= t <= pos//unit.  s [..., Qc, n].
+    Restates benchmarks/sparse_attention.py:248-256 with :298-300 (tokens,
+    unit 1) and :346-355 (pages, unit = page size)."""
+    n = s.shape[-1]
+    pos = q_pos.reshape(-1).long()
+    t = torch.arange(n)
+    valid = (t[None, :] * unit) <= pos[:, None]                           # [Qc, n]
+    out = torch.where(valid, s.float(), torch.full_like(s.float(), NEG_INF))
+    if local_w > 0:
+        lo = (pos - local_w + 1).clamp(min=0) // unit
+        hi = pos // unit
+        rec = (t[None, :] >= lo[:, None]) & (t[None, :] <= hi[:, None])
+        out = torch.where(rec, torch.full_like(out, float("inf")), out)
+    return out
+
+
+def select_topk_from_scores(scores: torch.Tensor, q_pos: torch.Tensor, S: int, kb: int, k_chunk: int,
+                            local_w: int = 0) -> torch.Tensor:
+    """The streaming selection of benchmarks/sparse_attention.py:286-309 over
+    precomputed fp32 scores [..., Qc, max_key] (max_key = max(q_pos) + 1):
+    a running list of kb (score, index) pairs starting as (-inf, S) sentinels
+    (:291-292) is merged with each k_chunk-key tile (causal mask and recent
+    window applied, :297-300) and cut back to kb under the total order (score
+    descending, index ascending).  Keys past a row's position never enter the
+    list (they rank below the sentinels), so every slot a row cannot fill
+    holds the sentinel S - the purpose the reference states at :288-293.
+    Returns int64 [..., Qc, kb] ordered by that order."""
+    max_key = scores.shape[-1]
+    lead = scores.shape[:-1]
+    run_s = torch.full((*lead, kb), NEG_INF)
+    run_i = torch.full((*lead, kb), S, dtype=torch.int64)
+    pos = q_pos.reshape(-1).long()
+    for c0 in range(0, max_key, k_chunk):
+        c1 = min(c0 + k_chunk, max_key)
+        sc = selection_mask(scores[..., c0:c1], pos - c0, 1, 0)           # causal on this tile
+        if local_w > 0:
+            kp = torch.arange(c0, c1)
+            rec = (kp[None, :] > (pos[:, None] - local_w)) & (kp[None, :] <= pos[:, None])
+            sc = torch.where(rec, torch.full_like(sc, float("inf")), sc)
+        kp = torch.arange(c0, c1).expand(*lead, c1 - c0)
+        causal = kp <= pos.reshape(*([1] * (len(lead) - 1)), -1, 1)
+        ci_tile = torch.where(causal, kp, S + 1 + kp)                      # masked keys lose to sentinels
+        cs = torch.cat([run_s, sc], -1)
+        ci = torch.cat([run_i, ci_tile], -1)
+        key = order_key(cs)
+        o = torch.sort(ci, dim=-1, stable=True).indices                    # index ascending
+        o2 = torch.sort(-torch.gather(key, -1, o), dim=-1, stable=True).indices
+        perm = torch.gather(o, -1, o2)[..., :kb]
+        run_s = torch.gather(cs, -1, perm)
+        run_i = torch.gather(ci, -1, perm)
+    return torch.where(run_i > S, torch.full_like(run_i, S), run_i)
+
+
+def select_topk_exact(q_blk, sel_keys, q_pos, S: int, kb: int, k_chunk: int, scaling: float,
+                      local_w: int = 0) -> torch.Tensor:
+    """select_topk(selector="exact"/"approx") of benchmarks/sparse_attention.py:226-325:
+    fp32 scores (q . k) * scaling of every key before max(q_pos) + 1 (:208-210,
+    :294-296), then the streaming selection above.  q_blk [B,Hq,Qc,D];
+    sel_keys [B,Hq,S,D] (GQA-expanded, as the reference passes them) or
+    [B,Hk,S,D].  Returns int64 [B,Hq,Qc,kb]."""
+    B, Hq, Qc, D = q_blk.shape
+    max_key = int(q_pos.max()) + 1
+    s = sparse_score_scalar(_fold_rows(q_blk), sel_keys[:, :, :max_key], scaling)   # [B,Hq*Qc,max_key]
+    return select_topk_from_scores(s.reshape(B, Hq, Qc, max_key), q_pos, S, kb, k_chunk, local_w)
+
+
+def quest_select_rows(q_blk, k_r, q_pos, S: int, kb: int, page: int, scaling: float,
+                      local_w: int = 0) -> torch.Tensor:
+    """_quest_select of benchmarks/sparse_attention.py:328-364 for Qc >= 1 query
+    rows: page metadata, fp32 bounds * scaling, causal page validity and
+    forced recent pages per row, the top ceil(kb/page) pages under the total
+    order, expanded to token ids clamped to S - 1.  Returns int64
+    [B,Hq,Qc,npick*page] (pages in bound-descending order)."""
+    B, Hq, Qc, D = q_blk.shape
+    kmin, kmax = quest_page_minmax(k_r[:, :, :S], page)
+    bound = quest_page_scores(_fold_rows(q_blk), kmin, kmax, scaling).reshape(B, Hq, Qc, -1)
+    bound = selection_mask(bound, q_pos, page, local_w)
+    np_ = bound.shape[-1]
+    npick = min(max(1, (kb + page - 1) // page), np_)
+    pidx = topk_indices(bound, npick)
+    tok = (pidx.unsqueeze(-1) * page + torch.arange(page)).reshape(B, Hq, Qc, npick * page)
+    return tok.clamp(max=S - 1)
+
+
+def attend_topk(q_blk, k_r, v, idx, q_pos, scaling: float) -> torch.Tensor:
+    """Exact attention of each query row over its selected keys.
+
+    Restates benchmarks/sparse_attention.py:367-387: an entry takes part iff
+    it is at or before the row's position and below S (:376; negative entries
+    are masked too, the sentinel rule of sparse_gather_attn); fp32 scores and
+    softmax; the weights are cast to v's dtype and the weighted sum is taken
+    in v's dtype, as the reference does (:386-387).  q_blk [B,Hq,Qc,D];
+    k_r, v [B,Hq,S,D] or [B,Hk,S,D]; idx [B,Hq,Qc,ksel]."""
+    B, Hq, Qc, D = q_blk.shape
+    Hs, S = k_r.shape[1], k_r.shape[2]
+    G = Hq // Hs
+    ksel = idx.shape[-1]
+    pos = q_pos.reshape(-1).long()
+    idx = idx.long()
+    valid = (idx >= 0) & (idx < S) & (idx <= pos[None, None, :, None])
+    gi = idx.clamp(0, S - 1)
+    kr = repeat_kv(k_r, G).float()
+    vr = repeat_kv(v, G)
+    ks = torch.gather(kr.unsqueeze(2).expand(B, Hq, Qc, S, D), 3, gi.unsqueeze(-1).expand(B, Hq, Qc, ksel, D))
+    vs = torch.gather(vr.unsqueeze(2).expand(B, Hq, Qc, S, D), 3, gi.unsqueeze(-1).expand(B, Hq, Qc, ksel, D))
+    sc = (q_blk.float().unsqueeze(3) * ks).sum(-1) * scaling
+    sc = torch.where(valid, sc, torch.full_like(sc, NEG_INF))
+    w = torch.softmax(sc, dim=-1).to(v.dtype)
+    return (w.unsqueeze(-1) * vs).sum(3)

@@ -116,3 +116,55 @@ def test_dense_graph_replays(dev):
         eager = AK.decode_attn_bf16(q, k, v, 0.125)
         assert torch.equal(out, eager), f"replay {it}"
         _check(out, R.decode_attn(y["q"], y["k"], y["v"], scale=0.125), f"replay {it}")
+
+
+def test_workspace_growth_after_capture(dev):
+    """A graph captured with the split-K workspace at one size keeps working
+    after a larger eager call has replaced that workspace: the superseded
+    buffer is never released, so the replay still writes memory nothing else
+    owns and its output equals the eager result."""
+    from bytes_amd import _lib
+    key = (dev.index or 0, "splitk")
+    if key in _lib._ws:                         # start from a fresh workspace, as a new process does
+        _lib._retired.append(_lib._ws.pop(key))
+    x = W.dense(1, 14, 2, 64, 700, seed=41)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    AK.decode_attn_bf16(q, k, v, 0.125)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = AK.decode_attn_bf16(q, k, v, 0.125)
+    torch.cuda.synchronize()
+    before = _lib._ws[key].data_ptr()
+    S = 65536
+    assert _lib.size_query("bytes_decode_attn_bf16_workspace_size", 4, 28, 4, S, 128, 64) > _lib._ws[key].numel()
+    bq = torch.randn((4, 28, 1, 128), device=dev).to(torch.bfloat16)
+    bk = torch.zeros((4, 4, S, 128), dtype=torch.bfloat16, device=dev)
+    filler = [torch.full((1 << 20,), 7, dtype=torch.uint8, device=dev) for _ in range(8)]
+    AK.decode_attn_bf16(bq, bk, bk, 0.1, chunk=64)
+    torch.cuda.synchronize()
+    assert _lib._ws[key].data_ptr() != before
+    for it in range(2):
+        y = W.dense(1, 14, 2, 64, 700, seed=50 + it)
+        q.copy_(y["q"].to(dev)); k.copy_(y["k"].to(dev)); v.copy_(y["v"].to(dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, AK.decode_attn_bf16(q, k, v, 0.125)), f"replay {it}"
+        _check(out, R.decode_attn(y["q"], y["k"], y["v"], scale=0.125), f"grown replay {it}")
+    assert all(int(f[0]) == 7 and int(f[-1]) == 7 for f in filler)
+
+
+def test_workspace_growth_during_capture_raises(dev):
+    """Growing the workspace inside a capture would take the buffer from the
+    graph's pool with its zero fill deferred to replay; the wrapper refuses."""
+    from bytes_amd import _lib
+    key = (dev.index or 0, "splitk")
+    have = _lib.workspace(dev, 1).numel()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="graph capture"):
+        with torch.cuda.graph(g):
+            _lib.workspace(dev, have + 1)
+    torch.cuda.synchronize()
+    assert _lib._ws[key].numel() == have

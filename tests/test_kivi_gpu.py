@@ -128,9 +128,9 @@ def test_decode_eight_wave_workgroups(dev, bits, B, Hq, Hk, D, L, Rw):
 
 
 def test_decode_back_to_back_calls(dev):
-    """The in-kernel split merge leaves its arrival counters at zero: consecutive
-    calls with new data (and a different plan in between) on the shared
-    workspace each match the oracle."""
+    """Consecutive calls with new data, and a different split plan in between,
+    reuse the shared split-K workspace: each call's partials overwrite the
+    previous call's, and every result matches the oracle."""
     for i, (B, Hq, Hk, L, Rw) in enumerate([(2, 8, 2, 4096 + 128, 128), (2, 8, 2, 4096 + 128, 128),
                                             (1, 7, 1, 8192 + 64, 64), (2, 8, 2, 4096 + 128, 128)]):
         _decode_case(dev, 2 + 2 * (i % 2), B, Hq, Hk, 128, L, Rw, seed=50 + i)

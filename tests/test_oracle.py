@@ -394,3 +394,201 @@ def test_paged_rows_follow_the_block_table():
     for b in range(2):
         ref = R.decode_attn_pq_lut_kv(lut[b:b + 1], k_idx[b:b + 1, :, :lens[b]], v_idx[b:b + 1, :, :lens[b]], cb)
         assert torch.equal(out[b:b + 1], ref)
+
+
+# ---------------------------------------------------------------------------
+# k-means (src/quantization.py:102-132), pinned by a brute-force Lloyd replay
+# ---------------------------------------------------------------------------
+def _lloyd_bruteforce(pts, cent, draw):
+    """One Lloyd step over Python lists: squared distances summed coordinate by
+    coordinate, the first centroid on ties, then cluster i (in index order)
+    becomes the mean of its points or, when empty, the point draw() names."""
+    labels = []
+    for p in pts:
+        best, bi = None, 0
+        for i, c in enumerate(cent):
+            dist = sum((a - b) ** 2 for a, b in zip(p, c))
+            if best is None or dist < best:
+                best, bi = dist, i
+        labels.append(bi)
+    new = []
+    for i in range(len(cent)):
+        members = [p for p, l in zip(pts, labels) if l == i]
+        if members:
+            new.append([sum(col) / len(members) for col in zip(*members)])
+        else:
+            new.append(list(pts[draw()]))
+    return new, labels
+
+
+def _sse(pts, cent):
+    return sum(min(sum((a - b) ** 2 for a, b in zip(p, c)) for c in cent) for p in pts)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_kmeans_one_step_bruteforce(seed):
+    g = torch.Generator().manual_seed(100 + seed)
+    X = torch.randn(37, 3, generator=g)
+    pts = X.tolist()
+    k = 5
+    out = R.kmeans(X, k, 1, torch.Generator().manual_seed(seed))
+    rng = torch.Generator().manual_seed(seed)
+    init = [pts[i] for i in torch.randperm(37, generator=rng)[:k].tolist()]
+    want, _ = _lloyd_bruteforce(pts, init, lambda: int(torch.randint(0, 37, (1,), generator=rng)))
+    assert torch.allclose(out, torch.tensor(want), atol=1e-5, rtol=0)
+
+
+def test_kmeans_empty_cluster_takes_drawn_point():
+    # two distinct values: any three initial centroids repeat one, the repeat
+    # loses every tie to the lower index, and its cluster is re-seeded
+    X = torch.tensor([[0.0, 0.0]] * 6 + [[5.0, 5.0]] * 4)
+    pts = X.tolist()
+    for seed in range(6):
+        out = R.kmeans(X, 3, 1, torch.Generator().manual_seed(seed))
+        rng = torch.Generator().manual_seed(seed)
+        init = [pts[i] for i in torch.randperm(10, generator=rng)[:3].tolist()]
+        draws = []
+
+        def draw():
+            draws.append(int(torch.randint(0, 10, (1,), generator=rng)))
+            return draws[-1]
+        want, labels = _lloyd_bruteforce(pts, init, draw)
+        assert len(set(labels)) < 3 and draws, "the data must leave a cluster empty"
+        assert torch.equal(out, torch.tensor(want)), f"seed {seed}"
+
+
+def test_kmeans_sse_does_not_increase():
+    g = torch.Generator().manual_seed(7)
+    centers = torch.randn(4, 2, generator=g) * 6
+    X = (centers.repeat_interleave(30, 0) + torch.randn(120, 2, generator=g))
+    pts = X.tolist()
+    prev = None
+    for it in range(0, 7):
+        cent = R.kmeans(X, 4, it, torch.Generator().manual_seed(3)).tolist()
+        _, labels = _lloyd_bruteforce(pts, cent, lambda: 0)
+        assert len(set(labels)) == 4            # no empty cluster: Lloyd's descent holds
+        sse = _sse(pts, cent)
+        if prev is not None:
+            assert sse <= prev * (1 + 1e-6) + 1e-6, f"iteration {it}: {sse} > {prev}"
+        prev = sse
+
+
+def test_kmeans_pads_when_points_do_not_exceed_k():
+    X = torch.randn(5, 8)
+    out = R.kmeans(X, 8, 10, torch.Generator().manual_seed(0))
+    assert out.shape == (8, 8)
+    assert torch.equal(out[:5], X) and torch.equal(out[5:], torch.zeros(3, 8))
+    same = R.kmeans(X, 5, 10, torch.Generator().manual_seed(0))
+    assert torch.equal(same, X)
+
+
+# ---------------------------------------------------------------------------
+# select_topk / _quest_select / attend_topk over query chunks (Qc >= 1)
+# ---------------------------------------------------------------------------
+def _brute_select(scores, pos, S, kb, local_w):
+    """Per row: the causal keys (t <= pos), recent ones forced to +inf, ranked
+    by Python's sorted() on (-score, t); slots past the causal count hold S."""
+    out = []
+    for row, p in zip(scores, pos):
+        cands = []
+        for t, s in enumerate(row):
+            if t > p:
+                continue
+            if local_w > 0 and p - local_w < t <= p:
+                s = math.inf
+            cands.append((-s, t))
+        picked = [t for _, t in sorted(cands)[:kb]]
+        out.append(picked + [S] * (kb - len(picked)))
+    return out
+
+
+@pytest.mark.parametrize("local_w", [0, 3])
+def test_select_topk_from_scores_bruteforce(local_w):
+    g = torch.Generator().manual_seed(11)
+    Qc, S = 5, 40
+    pos = torch.tensor([2, 9, 17, 31, 39])
+    max_key = int(pos.max()) + 1
+    scores = torch.randint(-3, 4, (2, 3, Qc, max_key), generator=g).float()   # many ties
+    for kb in (1, 4, 8, 12):
+        want = [[_brute_select(scores[b, h].tolist(), pos.tolist(), S, kb, local_w) for h in range(3)]
+                for b in range(2)]
+        for chunk in (1, 5, 16, max_key):
+            got = R.select_topk_from_scores(scores, pos, S, kb, chunk, local_w)
+            assert got.tolist() == want, (kb, chunk)
+
+
+def test_select_topk_exact_integer_keys():
+    """Integer-valued q and keys give exact fp32 scores (and many ties), so the
+    full selection equals the brute-force ranking of Python dot products."""
+    g = torch.Generator().manual_seed(12)
+    B, Hq, Hk, Qc, S, D = 1, 4, 2, 3, 30, 8
+    q = torch.randint(-2, 3, (B, Hq, Qc, D), generator=g).to(torch.bfloat16)
+    k = torch.randint(-2, 3, (B, Hk, S, D), generator=g).to(torch.bfloat16)
+    pos = torch.tensor([5, 20, 29])
+    got = R.select_topk_exact(q, k, pos, S, 9, 7, 0.5)
+    for h in range(Hq):
+        sc = [[sum(float(q[0, h, r, d]) * float(k[0, h // 2, t, d]) for d in range(D)) * 0.5 for t in range(30)]
+              for r in range(Qc)]
+        assert got[0, h].tolist() == _brute_select(sc, pos.tolist(), S, 9, 0), h
+    kr = R.repeat_kv(k, 2)                                   # GQA-expanded keys give the same ids
+    assert torch.equal(R.select_topk_exact(q, kr, pos, S, 9, 7, 0.5), got)
+
+
+@pytest.mark.parametrize("local_w", [0, 20])
+def test_quest_select_rows_bruteforce(local_w):
+    g = torch.Generator().manual_seed(13)
+    B, Hq, Hk, Qc, S, D, page = 1, 4, 2, 3, 70, 8, 16
+    q = torch.randint(-2, 3, (B, Hq, Qc, D), generator=g).to(torch.bfloat16)
+    k = torch.randint(-3, 4, (B, Hk, S, D), generator=g).to(torch.bfloat16)
+    pos = torch.tensor([10, 40, 69])
+    kb = 35                                                  # ceil(35/16) = 3 pages
+    got = R.quest_select_rows(q, k, pos, S, kb, page, 0.25, local_w)
+    np_ = 5
+    for h in range(Hq):
+        for r in range(Qc):
+            p = int(pos[r])
+            cands = []
+            for pg in range(np_):
+                rows = [min(t, S - 1) for t in range(pg * page, pg * page + page)]
+                bnd = sum(max(float(q[0, h, r, d]) * min(float(k[0, h // 2, t, d]) for t in rows),
+                              float(q[0, h, r, d]) * max(float(k[0, h // 2, t, d]) for t in rows))
+                          for d in range(D)) * 0.25
+                if pg * page > p:
+                    bnd = -math.inf
+                if local_w and max(p - local_w + 1, 0) // page <= pg <= p // page:
+                    bnd = math.inf
+                cands.append((-bnd, pg))
+            pages = [pg for _, pg in sorted(cands)[:3]]
+            want = [min(pg * page + o, S - 1) for pg in pages for o in range(page)]
+            assert got[0, h, r].tolist() == want, (h, r)
+    # one row at the last position equals the decode-step selection
+    one = R.quest_select_rows(q[:, :, 2:3], k, pos[2:3], S, kb, page, 0.25)
+    _, tok, _ = R.quest_select(q[:, :, 2:3], k, kb, page, 0.25)
+    assert torch.equal(one.squeeze(2), tok)
+
+
+def test_attend_topk_bruteforce_and_causal_dense():
+    g = torch.Generator().manual_seed(14)
+    B, Hq, Hk, Qc, S, D = 1, 4, 2, 3, 24, 16
+    q = torch.randn(B, Hq, Qc, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hk, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hk, S, D, generator=g).to(torch.float32)
+    pos = torch.tensor([3, 12, 23])
+    idx = torch.randint(-2, S + 3, (B, Hq, Qc, 10), generator=g)
+    idx[..., 0] = 0                                          # every row keeps one valid entry
+    out = R.attend_topk(q, k, v, idx, pos, 0.3)
+    for h in range(Hq):
+        for r in range(Qc):
+            sel = [int(t) for t in idx[0, h, r] if 0 <= int(t) < S and int(t) <= int(pos[r])]
+            sc = [sum(float(q[0, h, r, d]) * float(k[0, h // 2, t, d]) for d in range(D)) * 0.3 for t in sel]
+            m = max(sc)
+            w = [math.exp(s - m) for s in sc]
+            want = [sum(wi * float(v[0, h // 2, t, d]) for wi, t in zip(w, sel)) / sum(w) for d in range(D)]
+            assert torch.allclose(out[0, h, r], torch.tensor(want), atol=1e-5), (h, r)
+    # every position 0..S-1 selected: causal dense attention of each row
+    allidx = torch.arange(S).expand(B, Hq, Qc, S)
+    full = R.attend_topk(q, k, v, allidx, pos, 0.3)
+    for r in range(Qc):
+        p = int(pos[r])
+        dense = R.decode_attn(q[:, :, r:r + 1], k[:, :, :p + 1], v[:, :, :p + 1], scale=0.3)
+        assert torch.allclose(full[:, :, r], dense.squeeze(2).float(), atol=5e-3)   # bf16 output of decode_attn

@@ -186,6 +186,22 @@ def test_kmeans_update_and_determinism(dev):
     assert err(a) < err(init)
 
 
+def test_kmeans_pytorch_drop_in_shapes(dev):
+    """src/quantization.py:102-132 signature: X [N, d_sub] -> [k, d_sub] in X's
+    dtype, padding with zero rows when N <= k; other d_sub raise."""
+    g = torch.Generator().manual_seed(3)
+    X = torch.randn(500, 8, generator=g).to(dev)
+    cb = PQ.kmeans_pytorch(X, 16, 4, generator=torch.Generator().manual_seed(1))
+    assert cb.shape == (16, 8) and cb.dtype == X.dtype
+    assert torch.equal(cb, PQ.kmeans(X, 16, 4, generator=torch.Generator().manual_seed(1))[0])
+    small = torch.randn(5, 8, generator=g).to(dev).to(torch.bfloat16)
+    pad = PQ.kmeans_pytorch(small, 8, 2)
+    assert pad.shape == (8, 8) and pad.dtype == torch.bfloat16
+    assert torch.equal(pad[:5], small) and not pad[5:].any()
+    with pytest.raises(ValueError):
+        PQ.kmeans_pytorch(torch.randn(100, 4, device=dev), 8)
+
+
 def test_product_quantizer_round_trip(dev):
     pq = PQ.ProductQuantizer(64, 8, bits=4, device=dev)
     g = torch.Generator().manual_seed(21)
