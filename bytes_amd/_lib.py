@@ -33,6 +33,10 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64,                          # v strides (b, h, s)
         c_i64, c_i64,                                 # out strides (b, h)
         c_f32, c_int, c_vp, c_sz, c_vp),              # scale, chunk, workspace, bytes, stream
+    "bytes_decode_attn_bf16_noalloc": (
+        c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int,
+        c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+        c_f32, c_int, c_vp),                          # scale, chunk, stream
     "bytes_decode_attn_fp8": (
         c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int,
         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,

@@ -51,6 +51,45 @@ def decode_attn_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     return out.unsqueeze(2)
 
 
+NOALLOC_SCRATCH_BYTES = 16 << 20      # BYTES_NOALLOC_SCRATCH_BYTES of include/bytes_amd.h
+
+
+def decode_attn_bf16_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                             scale: float = 1.0, *, chunk: int = 0) -> torch.Tensor:
+    """decode_attn_bf16 for callers that cannot allocate: writes `out`
+    [B,H_q,1,D] (or [B,H_q,D]) bf16 and allocates nothing, on the device or
+    through torch.  The split-K partials go to a 16 MiB device-resident scratch
+    shared by every call on the device (calls that overlap on one device
+    race).  Inputs must already have unit stride in D and 16-byte-aligned rows
+    (no copy is made).  Raises ValueError when the call's partials exceed the
+    scratch (larger B*H_k*splits); a larger `chunk` needs fewer splits."""
+    C.cuda_tensors(q, k, v, out)
+    C.ndim(q, 4, "q"), C.ndim(k, 4, "k"), C.ndim(v, 4, "v")
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out")):
+        C.dtype_in(t, n, torch.bfloat16)
+    B, Hq, one, D = q.shape
+    _, Hk, S, Dk = k.shape
+    if one != 1 or Dk != D or tuple(v.shape) != tuple(k.shape) or k.shape[0] != B:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if Hq % Hk != 0 or D not in (64, 128) or S == 0:
+        raise ValueError(f"unsupported shape: q {tuple(q.shape)}, k {tuple(k.shape)}")
+    o3 = out.reshape(B, Hq, D) if out.dim() == 4 else out
+    if tuple(o3.shape) != (B, Hq, D):
+        raise ValueError(f"out must be [B,H_q,1,D] or [B,H_q,D]; got {tuple(out.shape)}")
+    qs = q.squeeze(2)
+    for t, n in ((qs, "q"), (k, "k"), (v, "v"), (o3, "out")):
+        if C.rows16(t) is not t:
+            raise ValueError(f"{n} needs unit stride in D and 16-byte-aligned rows (no copy is made)")
+    need = size_query("bytes_decode_attn_bf16_workspace_size", B, Hq, Hk, S, D, int(chunk))
+    if need > NOALLOC_SCRATCH_BYTES:
+        raise ValueError(f"split-K partials need {need} bytes, above the {NOALLOC_SCRATCH_BYTES}-byte scratch")
+    call("bytes_decode_attn_bf16_noalloc", ptr(qs), ptr(k), ptr(v), ptr(o3), B, Hq, Hk, S, D,
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2),
+         v.stride(0), v.stride(1), v.stride(2), o3.stride(0), o3.stride(1),
+         float(scale), int(chunk), stream_of(q))
+    return out
+
+
 def decode_attn_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 1.0,
                     *, chunk: int = 0) -> torch.Tensor:
     """softmax(scale * q.K^T) V with OCP float8_e4m3fn K and V.

@@ -19,6 +19,8 @@
 // The fp8 entry point (src/attention_kernels.py:156-182, `decode_attn_fp8`:
 // OCP e4m3fn K and V, bf16 q, output in q's dtype, no scale) runs the same
 // kernel with K/V rows widened to bf16 (exactly) as they are staged in LDS.
+#include <mutex>
+
 #include "dense_tile.h"
 
 namespace bytes_amd {
@@ -81,6 +83,36 @@ __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(Dense
 
 // Host-side split choice: chunk is a multiple of (waves * tile) tokens; aim
 // for two resident workgroups per CU.
+// Device-resident scratch of the no-allocation entry point: the split-K
+// partials of one call (each device holds its own copy for the life of the
+// process).  Host code never uses the symbol's name as an address: its
+// device address is looked up once per device and kept in g_scratch.
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::once_flag g_scratch_once[kMaxDevices];
+static void* g_scratch[kMaxDevices];
+static int g_scratch_rc[kMaxDevices];
+
+// This device's address of `scratch` (nullptr and a status on failure).
+static void* scratch_address(int* rc) {
+  int dev = 0;
+  *rc = (int)hipGetDevice(&dev);
+  if (*rc) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = (int)hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_rc[dev] = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch[dev] = g_scratch_rc[dev] ? nullptr : p;
+  });
+  *rc = g_scratch_rc[dev];
+  return g_scratch[dev];
+}
+
 static void dense_plan(int S, long units, int chunk_req, int* chunk, int* nsplit) {
   const int step = kDenseWaves * kTile;
   int c;
@@ -163,6 +195,25 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
                            int chunk_req, void* workspace, size_t workspace_bytes, void* stream) {
   return dense_decode(false, q, k, v, out, B, Hq, Hk, S, D, q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb,
                       o_sh, scale, chunk_req, workspace, workspace_bytes, stream);
+}
+
+// The bf16 decode with its split-K partials in this device's `scratch`
+// instead of a caller workspace: no allocation of any kind, so it serves
+// callers that cannot allocate.  Every partial the merge reads is written
+// earlier in the same call, so nothing in the scratch has to start at zero.
+// Calls that overlap on one device share the scratch and race.
+int bytes_decode_attn_bf16_noalloc(const void* q, const void* k, const void* v, void* out, int B, int Hq, int Hk,
+                                   int S, int D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh,
+                                   int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb,
+                                   int64_t o_sh, float scale, int chunk_req, void* stream) {
+  size_t need = 0;
+  int rc = bytes_decode_attn_bf16_workspace_size(B, Hq, Hk, S, D, chunk_req, &need);
+  if (rc) return rc;
+  if (need > kNoAllocScratchBytes) return (int)hipErrorOutOfMemory;
+  void* ws = scratch_address(&rc);
+  if (rc) return rc;
+  return dense_decode(false, q, k, v, out, B, Hq, Hk, S, D, q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb,
+                      o_sh, scale, chunk_req, ws, kNoAllocScratchBytes, stream);
 }
 
 // K/V element strides are in fp8 elements (bytes).

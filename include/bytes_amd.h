@@ -55,6 +55,24 @@ int bytes_decode_attn_bf16(const void* q, const void* k, const void* v, void* ou
                            float scale, int chunk, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* No-allocation variant of bytes_decode_attn_bf16.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * allocation).  Same arguments and results as bytes_decode_attn_bf16 without
+ * the workspace: the split-K partials go to a device-resident scratch array of
+ * BYTES_NOALLOC_SCRATCH_BYTES per device, held until the process ends.
+ * Returns hipErrorOutOfMemory when the call's partials
+ * (bytes_decode_attn_bf16_workspace_size) exceed that size.  Calls that
+ * overlap on one device share the scratch and race; order them on one stream. */
+#define BYTES_NOALLOC_SCRATCH_BYTES (16u << 20)
+int bytes_decode_attn_bf16_noalloc(const void* q, const void* k, const void* v, void* out,
+                                   int B, int Hq, int Hk, int S, int D,
+                                   int64_t q_sb, int64_t q_sh,
+                                   int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                   int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                   int64_t o_sb, int64_t o_sh,
+                                   float scale, int chunk, void* stream);
+
 /* FP8 dense decode: replaces src/attention_kernels.py:156-182 (`decode_attn_fp8`,
  * kernel :98-154).  Same arguments as bytes_decode_attn_bf16 with k, v OCP
  * float8_e4m3fn (strides in elements = bytes), widened to bf16 exactly; out bf16
