@@ -1,18 +1,26 @@
 #!/usr/bin/env python3
 """MI355X decode-attention benchmark (BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--only] [--all] [--no-cpu]
 
-One "step" is one decode-attention call of the named configuration over one
-batch of synthetic inputs already resident in HBM.  W untimed warm-up steps
-run first; then exactly K steps are captured into one hipGraph (each step on
-its own copy of the inputs, rotating through enough copies to exceed 2x the
+One "step" is one decode-attention call of a configuration over one batch of
+synthetic inputs already resident in HBM.  W untimed warm-up steps run
+first; then exactly K steps are captured into one hipGraph (each step on its
+own copy of the inputs, rotating through enough copies to exceed 2x the
 256 MB Infinity Cache, so every step streams from HBM) and the graph replay
 is timed with HIP events on the capture's stream, between two device
-synchronisations.  Rank 0 prints one JSON line.
+synchronisations.  The step's dominant kernel is then timed on its own: K
+more (eager) steps, each with a HIP event pair that the library records on
+the kernel's stream right around that launch.
 
-The cpu_baseline leg times the CPU oracle (test infrastructure, oracle/) on a
-bounded sample of the same workload, only on rank 0 at N=1.
+`value` is the headline config (BASELINE C2, KIVI 2-bit) in us/step;
+`roofline` is its dominant kernel's algorithmic bytes over that kernel's
+average duration (`step_frac` the same over the whole step).  `per_config`
+holds the same figures for every other BASELINE config (C1, C2 4-bit, the
+dense L>=16K point, C3, C4, C5 at k = 256/1024/4096; --all adds more).  Each
+config's cpu_baseline times the CPU oracle (test infrastructure, oracle/) on
+the whole step, or on a stated sample where the whole step would take
+minutes (C5).  Rank 0 prints one JSON line.
 """
 from __future__ import annotations
 
@@ -21,6 +29,7 @@ import json
 import math
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -38,9 +47,14 @@ class Case:
     workload = ""
     dtype = "bf16"
     kernel = ""            # kernel symbol (substring) that dominates the step
+    family = 0             # its family in the library's kernel timing hook (bytes_set_kernel_events)
 
     def bytes_per_step(self) -> int:
         raise NotImplementedError
+
+    def kernel_bytes(self) -> int:
+        """Algorithmic bytes of one launch of the dominant kernel."""
+        return self.bytes_per_step()
 
     def make(self, dev):
         raise NotImplementedError
@@ -49,12 +63,15 @@ class Case:
         raise NotImplementedError
 
     def cpu_sample(self):
-        """-> (description, fn running the oracle on the sample, full/sample work ratio)."""
+        """-> (description, fn running the oracle on the sample, full/sample work ratio);
+        the sample is the whole step (ratio 1) wherever the oracle runs it in
+        seconds."""
         raise NotImplementedError
 
 
 class DenseCase(Case):
     kernel = "dense_decode_kernel"
+    family = 1
 
     def __init__(self, name, B, Hq, Hk, D, L):
         self.name, self.shape = name, (B, Hq, Hk, D, L)
@@ -81,10 +98,14 @@ class DenseCase(Case):
         from bytes_amd import workloads as W
         from oracle import reference as R
         B, Hq, Hk, D, L = self.shape
-        x = W.dense(1, Hq // Hk, 1, D, L, seed=0)          # one (b, kv-head) unit
-        units = B * Hk
-        return (f"one (b, kv-head) unit of {units}: q [1,{Hq // Hk},1,{D}], K/V [1,1,{L},{D}]",
-                lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), units)
+        if B * Hk * L * D > (1 << 28):                     # multi-GiB caches: one (b, kv-head) unit
+            x = W.dense(1, Hq // Hk, 1, D, L, seed=0)
+            units = B * Hk
+            return (f"one (b, kv-head) unit of {units}: q [1,{Hq // Hk},1,{D}], K/V [1,1,{L},{D}]",
+                    lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), units)
+        x = W.dense(*self.shape, seed=0)
+        return (f"the whole step: oracle decode_attn on q [{B},{Hq},1,{D}], K/V [{B},{Hk},{L},{D}]",
+                lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), 1)
 
 
 class DenseFp8Case(DenseCase):
@@ -115,6 +136,7 @@ class DenseFp8Case(DenseCase):
 
 class KiviCase(Case):
     kernel = "kivi_decode_kernel"
+    family = 2
 
     def __init__(self, name, bits, B=4, Hq=28, Hk=4, D=128, L=16384, R=128):
         self.name, self.bits, self.shape = name, bits, (B, Hq, Hk, D, L, R)
@@ -151,13 +173,12 @@ class KiviCase(Case):
         from bytes_amd import workloads as W
         from oracle import reference as R
         B, Hq, Hk, D, L, Rw = self.shape
-        raw = W.kivi_raw(1, Hq // Hk, 1, D, L, Rw, seed=0)
+        raw = W.kivi_raw(B, Hq, Hk, D, L, Rw, seed=0)
         x = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, self.bits)
-        units = B * Hk
         args = [x[n] for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn", "V_residual")]
-        return (f"one (b, kv-head) unit of {units}: oracle kivi_decode_attn on Q [1,{Hq // Hk},1,{D}], "
+        return (f"the whole step: oracle kivi_decode_attn on Q [{B},{Hq},1,{D}], "
                 f"Sq={L - Rw} packed + {Rw} residual",
-                lambda: R.kivi_decode_attn(*args, self.bits, 32), units)
+                lambda: R.kivi_decode_attn(*args, self.bits, 32), 1)
 
 
 class TopkCase(Case):
@@ -165,6 +186,7 @@ class TopkCase(Case):
     deterministic top-k per (b, KV head), gathered bf16 attention for every
     query head of the group.  One step = score + top-k + gather."""
     kernel = "score_kernel"
+    family = 5
 
     def __init__(self, name, kb, B=8, Hq=24, Hk=8, D=128, L=131072, score_bits=16):
         self.name, self.kb, self.shape, self.score_bits = name, kb, (B, Hq, Hk, D, L), score_bits
@@ -216,11 +238,11 @@ class TopkCase(Case):
         from bytes_amd import workloads as W
         from oracle import reference as R
         B, Hq, Hk, D, L = self.shape
-        x = W.dense(1, Hq // Hk, 1, D, L, seed=0)
-        units = B * Hk
-        return (f"one (b, kv-head) unit of {units}: oracle group scores + top-{self.kb} + gather, "
-                f"q [1,{Hq // Hk},1,{D}], K/V [1,1,{L},{D}]",
-                lambda: R.token_topk_decode(x["q"], x["k"], x["v"], self.kb, x["scale"]), units)
+        x = W.dense(1, Hq, Hk, D, L, seed=0)
+        return (f"one batch row of {B} (the oracle's fp32 copies of the whole 4 GiB cache would need "
+                f"tens of GiB): oracle group scores + top-{self.kb} + gather, q [1,{Hq},1,{D}], "
+                f"K/V [1,{Hk},{L},{D}]; x {B} to a full step",
+                lambda: R.token_topk_decode(x["q"], x["k"], x["v"], self.kb, x["scale"]), B)
 
 
 class QuestCase(Case):
@@ -228,6 +250,7 @@ class QuestCase(Case):
     ceil(2048/16) = 128 pages per query head, attention over their rows.  The
     metadata is a property of the cache (built once, outside the step)."""
     kernel = "gather_decode_kernel"
+    family = 4
 
     def __init__(self, name, budget=2048, page=16, B=1, Hq=28, Hk=4, D=128, L=32768):
         self.name, self.budget, self.page, self.shape = name, budget, page, (B, Hq, Hk, D, L)
@@ -241,6 +264,10 @@ class QuestCase(Case):
         bounds = B * Hq * np_ * 4 * 2                      # written, then read by the top-k
         rows = 2 * B * Hq * self.budget * D * 2            # gathered K and V rows (per query head)
         return meta + bounds + rows + 2 * B * Hq * D * 2
+
+    def kernel_bytes(self):
+        B, Hq, Hk, D, L = self.shape
+        return 2 * B * Hq * self.budget * D * 2 + 2 * B * Hq * D * 2
 
     def make(self, dev):
         from bytes_amd import quest as Q
@@ -274,6 +301,7 @@ class PqCase(Case):
     launch (decode_attn_pq_kv_fused, bit-identical to pq_build_lut followed by
     decode_attn_pq_lut_kv); codebook fitting and encoding are setup."""
     kernel = "pq_decode_kernel"
+    family = 3
 
     def __init__(self, name, B=1, Hq=28, Hk=4, D=128, L=32768, K=256):
         self.name, self.shape, self.K = name, (B, Hq, Hk, D, L), K
@@ -301,17 +329,17 @@ class PqCase(Case):
         B, Hq, Hk, D, L = self.shape
         g = torch.Generator().manual_seed(0)
         M = D // 8
-        q = torch.randn(1, Hq // Hk, 1, D, generator=g).to(torch.bfloat16)
-        kcb = torch.randn(1, M, self.K, 8, generator=g).half()
-        vcb = torch.randn(1, M, self.K, 8, generator=g).half()
-        ki = torch.randint(0, self.K, (1, 1, L, M), generator=g).to(torch.uint8)
-        vi = torch.randint(0, self.K, (1, 1, L, M), generator=g).to(torch.uint8)
-        units = B * Hk
+        q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+        kcb = torch.randn(Hk, M, self.K, 8, generator=g).half()
+        vcb = torch.randn(Hk, M, self.K, 8, generator=g).half()
+        ki = torch.randint(0, self.K, (B, Hk, L, M), generator=g).to(torch.uint8)
+        vi = torch.randint(0, self.K, (B, Hk, L, M), generator=g).to(torch.uint8)
 
         def run():
             lut = R.pq_build_lut(q, kcb, 1.0 / D ** 0.5)
             return R.decode_attn_pq_lut_kv(lut, ki, vi, vcb)
-        return (f"one (b, kv-head) unit of {units}: oracle LUT build + pq_lut_kv over L={L}", run, units)
+        return (f"the whole step: oracle LUT build + pq_lut_kv, B{B} Hq{Hq} Hkv{Hk} L{L} (seeded random "
+                f"codes and codebooks of the C3 shape)", run, 1)
 
 
 class CopyCase(Case):
@@ -389,14 +417,10 @@ def clone_inputs(inp, copies):
     return out
 
 
-def time_gpu(case: Case, steps: int, warmup: int, dev) -> dict:
-    base = case.make(dev)
-    nbytes = case.bytes_per_step()
-    copies = max(2, math.ceil(2 * MALL_BYTES / max(nbytes, 1)) + 1)
-    inps = clone_inputs(base, copies)
-    for i in range(warmup):
-        case.step(inps[i % copies])
-    torch.cuda.synchronize()
+def time_step(case: Case, inps, steps: int) -> float:
+    """ms per step: `steps` steps captured in one hipGraph, replay timed with
+    HIP events on the capture's stream between two device synchronisations."""
+    copies = len(inps)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(steps):
@@ -413,35 +437,127 @@ def time_gpu(case: Case, steps: int, warmup: int, dev) -> dict:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     del g
-    return {"ms_per_step": ms, "copies": copies, "bytes_per_step": nbytes}
+    return ms
 
 
-def time_cpu(case: Case, budget_s: float = 20.0) -> dict:
+def time_kernel(case: Case, inps, steps: int) -> float:
+    """Average duration (ms) of the step's dominant kernel over `steps` steps:
+    the library records a HIP event pair on the kernel's own stream right
+    before and after that launch (bytes_set_kernel_events), one pair per step."""
+    from bytes_amd import _lib
+    if case.family == 0:                  # not a library kernel: the step is the kernel
+        return time_step(case, inps, steps)
+    lib = _lib.lib()
+    copies = len(inps)
+    s = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in evs:                # create the events
+        e0.record(s)
+        e1.record(s)
+    torch.cuda.synchronize()
+    try:
+        for i, (e0, e1) in enumerate(evs):
+            _lib.check(lib.bytes_set_kernel_events(case.family, e0.cuda_event, e1.cuda_event),
+                       "bytes_set_kernel_events")
+            case.step(inps[i % copies])
+    finally:
+        lib.bytes_set_kernel_events(0, None, None)
+    torch.cuda.synchronize()
+    return statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def measure(case: Case, steps: int, warmup: int, dev) -> dict:
+    base = case.make(dev)
+    nbytes = case.bytes_per_step()
+    copies = max(2, math.ceil(2 * MALL_BYTES / max(nbytes, 1)) + 1)
+    inps = clone_inputs(base, copies)
+    for i in range(warmup):
+        case.step(inps[i % copies])
+    torch.cuda.synchronize()
+    ms = time_step(case, inps, steps)
+    kms = time_kernel(case, inps, steps)
+    del inps, base
+    torch.cuda.empty_cache()
+    step_bps = nbytes / (ms * 1e-3)
+    kern_bps = case.kernel_bytes() / (kms * 1e-3)
+    return {"ms_per_step": ms, "copies": copies, "bytes_per_step": nbytes, "kernel_ms": kms,
+            "kernel_bytes": case.kernel_bytes(), "step_Bps": step_bps, "kernel_Bps": kern_bps}
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_cpu(case: Case, budget_s: float = 10.0) -> dict:
+    """The CPU oracle (oracle/, test infrastructure) on the same workload:
+    median of at least 5 timed runs (3 when one run takes over a second) after
+    one warm-up, with every host thread torch offers."""
     desc, fn, ratio = case.cpu_sample()
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
+    torch.set_num_threads(os.cpu_count() or 1)
     fn()                                            # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s / 4 and len(times) < 50):
+    while True:
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s:
+        need = 3 if times[0] > 1.0 else 5
+        if len(times) >= need and (time.perf_counter() - t_start > budget_s / 4 or len(times) >= 30):
+            break
+        if time.perf_counter() - t_start > budget_s and len(times) >= 3:
             break
     med = statistics.median(times)
-    return {"value": med * ratio * 1e6, "unit": "us/step", "cores": torch.get_num_threads(),
-            "kind": "port", "sample": f"{desc}; median of {len(times)} runs x {ratio} to a full step"}
+    return {"value": round(med * ratio * 1e6, 1), "unit": "us/step", "cores": torch.get_num_threads(),
+            "host_cpus": os.cpu_count(), "cpu_model": cpu_model(), "kind": "port",
+            "sample": f"{desc}; median of {len(times)} runs" + (f" x {ratio}" if ratio != 1 else "")}
+
+
+# BASELINE.json configs: C1, C2 (2-bit headline and 4-bit), the dense L>=16K
+# point, C3, C4 and C5 at its three budgets.
+DEFAULT_CONFIGS = ["c1_dense", "c2_kivi4", "dense_16k", "c3_pq", "c4_quest", "c5_topk256", "c5_topk1024",
+                   "c5_topk4096"]
+EXTRA_CONFIGS = ["dense_32k", "c2_kivi2_64k", "c2_kivi4_64k", "dense_16k_fp8", "c5_dense", "c5_topk1024_fp8s",
+                 "c5_topk1024_int4s", "c5_topk1024_int2s"]
+
+
+def entry(case: Case, r: dict, cpu) -> dict:
+    e = {"workload": case.workload, "us_per_step": round(r["ms_per_step"] * 1e3, 3),
+         "GBps": round(r["step_Bps"] / 1e9, 1), "hbm_frac": round(r["step_Bps"] / HBM_PEAK, 4),
+         "bytes": r["bytes_per_step"], "kernel": case.kernel, "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+         "kernel_bytes": r["kernel_bytes"], "kernel_GBps": round(r["kernel_Bps"] / 1e9, 1),
+         "kernel_frac": round(r["kernel_Bps"] / HBM_PEAK, 4), "traffic": None}
+    tr = measured_traffic(case.name)
+    if tr is not None:
+        e["traffic"] = tr["traffic_bytes"]
+        e["traffic_source"] = tr["source"]
+    if cpu is not None:
+        e["cpu_baseline"] = cpu
+    return e
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default=HEADLINE)
-    ap.add_argument("--all", action="store_true", help="also time every other config (per_config)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--only", action="store_true", help="time the named config alone (no per_config)")
+    ap.add_argument("--all", action="store_true", help="add the extra configs to per_config")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -459,9 +575,11 @@ def main():
         print(f"unknown config {args.config}; known: {sorted(allc)}", file=sys.stderr)
         sys.exit(2)
     head = allc[args.config]
-    r = time_gpu(head, args.steps, args.warmup, dev)
+    t0 = time.perf_counter()
+    r = measure(head, args.steps, args.warmup, dev)
+    print(f"[bench] {head.name}: {r['ms_per_step'] * 1e3:.3f} us/step, kernel {r['kernel_ms'] * 1e3:.3f} us "
+          f"({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
     us = r["ms_per_step"] * 1e3
-    achieved = r["bytes_per_step"] / (r["ms_per_step"] * 1e-3)
     line = {
         "metric": "decode-attn us/step & % of HBM peak BW (BF16/KIVI/PQ/top-k), 1 MI355X",
         "value": round(us, 3),
@@ -476,27 +594,32 @@ def main():
         "dtype": head.dtype,
         "data": "synthetic (seeded N(0,1), BASELINE.json configs)",
         "config": {"workload": head.workload, "name": head.name, "mall_rotation_copies": r["copies"]},
-        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
-                     "kernel": head.kernel, "algorithmic_bytes": r["bytes_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": round(r["kernel_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(r["kernel_Bps"] / HBM_PEAK, 4), "traffic": None,
+                     "kernel": head.kernel, "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                     "algorithmic_bytes": r["kernel_bytes"],
+                     "step_GBps": round(r["step_Bps"] / 1e9, 1), "step_frac": round(r["step_Bps"] / HBM_PEAK, 4)},
     }
     tr = measured_traffic(head.name)
     if tr is not None:
         line["roofline"]["traffic"] = tr["traffic_bytes"]
         line["roofline"]["traffic_source"] = tr["source"]
-    if args.all:
-        per = {}
-        for name, c in allc.items():
-            if name in (head.name, "copy_calib"):
-                continue
-            rr = time_gpu(c, min(args.steps, 100), args.warmup, dev)
-            a = rr["bytes_per_step"] / (rr["ms_per_step"] * 1e-3)
-            per[name] = {"us_per_step": round(rr["ms_per_step"] * 1e3, 3), "GBps": round(a / 1e9, 1),
-                         "hbm_frac": round(a / HBM_PEAK, 4), "bytes": rr["bytes_per_step"],
-                         "workload": c.workload}
-        line["per_config"] = per
     if not args.no_cpu:
         line["cpu_baseline"] = time_cpu(head)
+    if not args.only:
+        per = {}
+        names = DEFAULT_CONFIGS + (EXTRA_CONFIGS if args.all else [])
+        for name in names:
+            if name == head.name:
+                continue
+            c = allc[name]
+            t1 = time.perf_counter()
+            rr = measure(c, args.steps, args.warmup, dev)
+            cpu = None if args.no_cpu else time_cpu(c)
+            per[name] = entry(c, rr, cpu)
+            print(f"[bench] {name}: {rr['ms_per_step'] * 1e3:.3f} us/step, kernel {rr['kernel_ms'] * 1e3:.3f} us "
+                  f"({time.perf_counter() - t1:.1f} s)", file=sys.stderr, flush=True)
+        line["per_config"] = per
     print(json.dumps(line), flush=True)
 
 

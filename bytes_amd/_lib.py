@@ -24,6 +24,7 @@ c_szp = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES: Dict[str, Tuple] = {
     "bytes_abi_version": (),
     "bytes_error_string": (c_int,),
+    "bytes_set_kernel_events": (c_int, c_vp, c_vp),
     "bytes_decode_attn_bf16_workspace_size": (c_int, c_int, c_int, c_int, c_int, c_int, c_szp),
     "bytes_decode_attn_bf16": (
         c_vp, c_vp, c_vp, c_vp,                       # q, k, v, out

@@ -8,6 +8,7 @@
 //  * softmax runs in the log2 domain: x = score * scale * log2(e), p = 2^(x - m).
 //  * every entry point returns 0 or a hipError_t and never throws.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -92,6 +93,27 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
+
+// Kernel families of the timing hook (bytes_set_kernel_events).
+enum ProfFamily : int { kProfNone = 0, kProfDense = 1, kProfKivi = 2, kProfPq = 3, kProfGather = 4,
+                        kProfScore = 5, kProfQuest = 6, kProfTopk = 7 };
+constexpr int kProfFamilies = 7;
+void prof_begin(int family, hipStream_t st);
+void prof_end(int family, hipStream_t st);
+bool prof_events(int family, hipEvent_t* start, hipEvent_t* stop);
+
+// Launch a family's main kernel.  While the timing hook is set for the
+// family, the launch carries the hook's event pair, which the runtime stamps
+// with the dispatch's own start and end (the kernel's execution time, as a
+// profiler measures it).
+#define BYTES_LAUNCH(FAM, K, G, B, SH, ST, ...)                                  \
+  do {                                                                         \
+    hipEvent_t bytes_e0_, bytes_e1_;                                           \
+    if (prof_events(FAM, &bytes_e0_, &bytes_e1_))                              \
+      hipExtLaunchKernelGGL(K, G, B, SH, ST, bytes_e0_, bytes_e1_, 0, __VA_ARGS__); \
+    else                                                                       \
+      hipLaunchKernelGGL(K, G, B, SH, ST, __VA_ARGS__);                        \
+  } while (0)
 
 // Touch every 8-byte word of a kernel's argument block at entry: the scalar
 // loads of the whole block are then issued together, one scalar-cache round

@@ -177,12 +177,13 @@ static int dense_decode(bool fp8, const void* q, const void* k, const void* v, v
   splitk_carve(workspace, units, ns, a.o);
   dim3 grid((unsigned)(ns * units));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 block(kDenseWaves * 64);
   if (D == 64) {
-    if (fp8) hipLaunchKernelGGL((dense_decode_kernel<64, true>), grid, dim3(kDenseWaves * 64), 0, st, a);
-    else hipLaunchKernelGGL((dense_decode_kernel<64, false>), grid, dim3(kDenseWaves * 64), 0, st, a);
+    if (fp8) BYTES_LAUNCH(kProfDense, (dense_decode_kernel<64, true>), grid, block, 0, st, a);
+    else BYTES_LAUNCH(kProfDense, (dense_decode_kernel<64, false>), grid, block, 0, st, a);
   } else {
-    if (fp8) hipLaunchKernelGGL((dense_decode_kernel<128, true>), grid, dim3(kDenseWaves * 64), 0, st, a);
-    else hipLaunchKernelGGL((dense_decode_kernel<128, false>), grid, dim3(kDenseWaves * 64), 0, st, a);
+    if (fp8) BYTES_LAUNCH(kProfDense, (dense_decode_kernel<128, true>), grid, block, 0, st, a);
+    else BYTES_LAUNCH(kProfDense, (dense_decode_kernel<128, false>), grid, block, 0, st, a);
   }
   int rc = (int)hipGetLastError();
   if (rc) return rc;

@@ -254,11 +254,11 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, c
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((unsigned)(ns * units)), block(kGatherWaves * 64);
   if (D == 128) {
-    if (kv_fp8) hipLaunchKernelGGL((gather_decode_kernel<128, true>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((gather_decode_kernel<128, false>), grid, block, 0, st, a);
+    if (kv_fp8) BYTES_LAUNCH(kProfGather, (gather_decode_kernel<128, true>), grid, block, 0, st, a);
+    else BYTES_LAUNCH(kProfGather, (gather_decode_kernel<128, false>), grid, block, 0, st, a);
   } else {
-    if (kv_fp8) hipLaunchKernelGGL((gather_decode_kernel<64, true>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((gather_decode_kernel<64, false>), grid, block, 0, st, a);
+    if (kv_fp8) BYTES_LAUNCH(kProfGather, (gather_decode_kernel<64, true>), grid, block, 0, st, a);
+    else BYTES_LAUNCH(kProfGather, (gather_decode_kernel<64, false>), grid, block, 0, st, a);
   }
   int rc = (int)hipGetLastError();
   if (rc) return rc;

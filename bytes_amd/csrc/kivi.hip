@@ -825,8 +825,8 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(ns * units)), block(nw * 64);
 #define KIVI_LAUNCH(DD, BB)                                                               \
-  if (nw == 8) hipLaunchKernelGGL((kivi_decode_kernel<DD, BB, 8>), grid, block, 0, st, a); \
-  else hipLaunchKernelGGL((kivi_decode_kernel<DD, BB, 4>), grid, block, 0, st, a);
+  if (nw == 8) BYTES_LAUNCH(kProfKivi, (kivi_decode_kernel<DD, BB, 8>), grid, block, 0, st, a); \
+  else BYTES_LAUNCH(kProfKivi, (kivi_decode_kernel<DD, BB, 4>), grid, block, 0, st, a);
   if (D == 128 && bits == 2) {
     KIVI_LAUNCH(128, 2)
   } else if (D == 128 && bits == 4) {

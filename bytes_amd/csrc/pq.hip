@@ -693,7 +693,7 @@ static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((unsigned)(ns * units)), block(kPqWaves * 64);
   const bool outl = a.C > 0;
-#define PQ_LAUNCH(DD, BL, QQ, F8, OU) hipLaunchKernelGGL((pq_decode_kernel<DD, BL, QQ, F8, OU>), grid, block, 0, st, a)
+#define PQ_LAUNCH(DD, BL, QQ, F8, OU) BYTES_LAUNCH(kProfPq, (pq_decode_kernel<DD, BL, QQ, F8, OU>), grid, block, 0, st, a)
 #define PQ_MODES(DD)                                          \
   if (mode == 0) PQ_LAUNCH(DD, false, true, false, false);    \
   else if (mode == 2) PQ_LAUNCH(DD, true, false, false, false); \

@@ -184,10 +184,10 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
   const uint16_t* mx = static_cast<const uint16_t*>(kmax);
   float* o = static_cast<float*>(bound);
   if (D == 128)
-    hipLaunchKernelGGL(quest_score_kernel<128>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
+    BYTES_LAUNCH(kProfQuest, quest_score_kernel<128>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
                        mn, mx, Hk, G, HB, np, page, pos, local_w, scale, o, o_sb, o_sh);
   else
-    hipLaunchKernelGGL(quest_score_kernel<64>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
+    BYTES_LAUNCH(kProfQuest, quest_score_kernel<64>, dim3((unsigned)grid), dim3(kQuestThreads), 0, st, qq, q_sb, q_sh,
                        mn, mx, Hk, G, HB, np, page, pos, local_w, scale, o, o_sb, o_sh);
   return (int)hipGetLastError();
 }

@@ -481,22 +481,22 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
 template <int D, bool FP8>
 static void launch_dense(const dim3& g, const dim3& blk, hipStream_t st, const ScoreArgs& a) {
   if (a.group_sum)
-    hipLaunchKernelGGL((score_kernel<DenseKeys<D, FP8, true>>), g, blk, 0, st, a);
+    BYTES_LAUNCH(kProfScore, (score_kernel<DenseKeys<D, FP8, true>>), g, blk, 0, st, a);
   else
-    hipLaunchKernelGGL((score_kernel<DenseKeys<D, FP8, false>>), g, blk, 0, st, a);
+    BYTES_LAUNCH(kProfScore, (score_kernel<DenseKeys<D, FP8, false>>), g, blk, 0, st, a);
 }
 
 template <int D, int BITS>
 static void launch_packed(const dim3& g, const dim3& blk, hipStream_t st, const ScoreArgs& a, int nb) {
   if (a.group_sum) {
-    hipLaunchKernelGGL((score_kernel<PackedKeys<D, BITS, 1, true>>), g, blk, 0, st, a);
+    BYTES_LAUNCH(kProfScore, (score_kernel<PackedKeys<D, BITS, 1, true>>), g, blk, 0, st, a);
   } else if constexpr (D == 128) {
-    if (nb == 1) hipLaunchKernelGGL((score_kernel<PackedKeys<128, BITS, 1, false>>), g, blk, 0, st, a);
-    else if (nb == 2) hipLaunchKernelGGL((score_kernel<PackedKeys<128, BITS, 2, false>>), g, blk, 0, st, a);
-    else hipLaunchKernelGGL((score_kernel<PackedKeys<128, BITS, 4, false>>), g, blk, 0, st, a);
+    if (nb == 1) BYTES_LAUNCH(kProfScore, (score_kernel<PackedKeys<128, BITS, 1, false>>), g, blk, 0, st, a);
+    else if (nb == 2) BYTES_LAUNCH(kProfScore, (score_kernel<PackedKeys<128, BITS, 2, false>>), g, blk, 0, st, a);
+    else BYTES_LAUNCH(kProfScore, (score_kernel<PackedKeys<128, BITS, 4, false>>), g, blk, 0, st, a);
   } else {
-    if (nb == 1) hipLaunchKernelGGL((score_kernel<PackedKeys<64, BITS, 1, false>>), g, blk, 0, st, a);
-    else hipLaunchKernelGGL((score_kernel<PackedKeys<64, BITS, 2, false>>), g, blk, 0, st, a);
+    if (nb == 1) BYTES_LAUNCH(kProfScore, (score_kernel<PackedKeys<64, BITS, 1, false>>), g, blk, 0, st, a);
+    else BYTES_LAUNCH(kProfScore, (score_kernel<PackedKeys<64, BITS, 2, false>>), g, blk, 0, st, a);
   }
 }
 

@@ -1033,8 +1033,11 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
   const float* s = static_cast<const float*>(scores);
   int32_t* o = static_cast<int32_t*>(out);
   const int so = sorted ? 1 : 0, hr = hist_ready ? 1 : 0;
-  return vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st)
-             : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st);
+  prof_begin(kProfTopk, st);
+  const int rc = vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st)
+                     : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st);
+  prof_end(kProfTopk, st);
+  return rc;
 }
 
 }  // extern "C"

@@ -34,6 +34,15 @@ int bytes_abi_version(void);
 /* Text of a status code returned by any entry point. */
 const char* bytes_error_string(int code);
 
+/* Kernel timing hook (no counterpart in the reference; for benchmarks): while
+ * set, every entry point of kernel family `family` records the hipEvent_t
+ * `start` on its stream right before launching its main kernel and `stop`
+ * right after it (top-k: around its whole launch sequence).  Families:
+ * 1 dense/fp8 decode, 2 KIVI decode, 3 PQ decode, 4 gather attention,
+ * 5 score pass, 6 Quest page bounds, 7 top-k.  family 0 clears the hook.
+ * Process-wide; not for concurrent use from several threads. */
+int bytes_set_kernel_events(int family, void* start, void* stop);
+
 /* ---------------------------------------------------------------------------
  * Dense bf16 GQA decode attention.
  * Replaces src/attention_kernels.py:65-92 (`decode_attn_bf16`, kernel :8-63).
