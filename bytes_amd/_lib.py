@@ -109,6 +109,12 @@ SIGNATURES: Dict[str, Tuple] = {
     "bytes_pq_encode": (c_vp, c_int, c_int, c_i64, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
     "bytes_pq_decode_vectors": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_vp, c_vp),
     "bytes_pq_kmeans_update": (c_vp, c_int, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp),
+    "bytes_gather_reduce": (c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_int, c_int, c_int, c_int, c_vp),
+    "bytes_packed_stage": (
+        c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64,          # q + strides, packed keys + strides
+        c_vp, c_vp, c_i64, c_i64, c_i64,                        # scale, zero, their strides
+        c_vp, c_i64, c_i64,                                     # out + strides (b, h)
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp),  # B, Hq, Hk, S, D, bits, stage, stream
     "bytes_select_mask": (c_vp, c_i64, c_int, c_i64, c_vp, c_int, c_int, c_int, c_vp),
     "bytes_select_fill": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_i64, c_vp, c_int, c_i64, c_vp),
     "bytes_select_pages": (c_vp, c_i64, c_int, c_int, c_i64, c_vp, c_vp),

@@ -13,6 +13,14 @@ The bytes read (2 * B * H_k * kb * D * 2: the selected K and V rows) are the
 same for every pattern, so GB/s differences come from the pattern alone; the
 peak is MI355X's 8 TB/s (the reference hard-codes 360 GB/s, :22).
 
+It also runs the reference's own probe, the gather-reduce microkernel
+(:25-52, csrc/harness.hip): per (b, KV head) the fp32 sum of the listed fp16
+value rows, over the same budgets and patterns (reads B * H_k * kb * D * 2
+bytes), and the granularity sweep of :136-156: a full gather (every row once,
+so no cache reuse) in random against contiguous order at row widths of
+16 .. 512 bytes (D = 8 .. 256 fp16), which shows where a scatter penalty would
+begin.
+
     python -m bytes_amd.harness.access_pattern [--B 32 --Hk 8 --S 16384]
 """
 from __future__ import annotations
@@ -81,11 +89,59 @@ def main(argv=None):
                              "pct_peak": 100 * gbs / HBM_PEAK_GBS})
             print(f"{tag:>6} {kb:>6} {pat:>13} {ms * 1e3:>9.1f} {gbs:>8.0f} {100 * gbs / HBM_PEAK_GBS:>6.1f}%",
                   flush=True)
+    del q, k
+    # ---- the reference's gather-reduce probe over the same budgets and patterns ----
+    from .kernels import gather_reduce
+    H = a.B * a.Hk
+    vh = v.reshape(H, a.S, a.D).to(torch.float16)
+    del v
+    torch.cuda.empty_cache()
+    probe = []
+    print(f"\ngather-reduce probe H={H} S={a.S} D={a.D} (fp16 rows)")
+    print(f"{'budget':>6} {'kb':>6} {'pattern':>13} {'us':>9} {'GB/s':>8} {'%peak':>7}")
+    for tag, kb in budgets:
+        pats = ["contiguous", "random", "sorted_random", "paged"] if kb < a.S else ["contiguous", "random",
+                                                                                   "sorted_random"]
+        for pat in pats:
+            idx = make_idx(pat, H, a.S, kb, a.page, g, dev)
+            nbytes = H * kb * a.D * 2
+            x = {"v": vh, "i": idx}
+            inps = clones(x, copies_for(nbytes)) if nbytes < (512 << 20) else [x]
+            ms = graph_ms(lambda z: gather_reduce(z["v"], z["i"]), inps, 5, a.runs)
+            del inps
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            probe.append({"budget": tag, "kb": kb, "pattern": pat, "us": ms * 1e3, "gbs": gbs,
+                          "pct_peak": 100 * gbs / HBM_PEAK_GBS})
+            print(f"{tag:>6} {kb:>6} {pat:>13} {ms * 1e3:>9.1f} {gbs:>8.0f} {100 * gbs / HBM_PEAK_GBS:>6.1f}%",
+                  flush=True)
+    del vh
+    torch.cuda.empty_cache()
+    # ---- granularity sweep: full gather, random vs contiguous, by row width ----
+    print(f"\n{'D':>5} {'rowB':>6} {'contig%pk':>10} {'rand%pk':>9} {'rand/contig':>12}")
+    gsweep = []
+    for D in (8, 16, 32, 64, 128, 256):
+        vd = torch.randn(H, a.S, D, generator=g, device=dev, dtype=torch.float16)
+        nbytes = H * a.S * D * 2
+        res = {}
+        for pat in ("contiguous", "random"):
+            idx = make_idx(pat, H, a.S, a.S, a.page, g, dev)
+            x = {"v": vd, "i": idx}
+            inps = clones(x, copies_for(nbytes)) if nbytes < (512 << 20) else [x]
+            ms = graph_ms(lambda z: gather_reduce(z["v"], z["i"]), inps, 5, a.runs)
+            del inps
+            res[pat] = (ms * 1e3, 100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+        gsweep.append({"D": D, "row_bytes": D * 2, "contig_us": res["contiguous"][0], "rand_us": res["random"][0],
+                       "contig_pct": res["contiguous"][1], "rand_pct": res["random"][1],
+                       "ratio": res["random"][1] / res["contiguous"][1]})
+        print(f"{D:>5} {D * 2:>6} {res['contiguous'][1]:>9.1f}% {res['random'][1]:>8.1f}% "
+              f"{res['random'][1] / res['contiguous'][1]:>11.3f}", flush=True)
+        del vd
+        torch.cuda.empty_cache()
     os.makedirs(os.path.dirname(a.output_json) or ".", exist_ok=True)
     with open(a.output_json, "w") as f:
-        json.dump({"schema": "access_pattern_v1", "gpu": torch.cuda.get_device_name(0), "peak_gbs": HBM_PEAK_GBS,
-                   "B": a.B, "H_q": a.Hq, "H_k": a.Hk, "S": a.S, "D": a.D, "page": a.page, "rows": rows_out}, f,
-                  indent=2)
+        json.dump({"schema": "access_pattern_v2", "gpu": torch.cuda.get_device_name(0), "peak_gbs": HBM_PEAK_GBS,
+                   "B": a.B, "H_q": a.Hq, "H_k": a.Hk, "S": a.S, "D": a.D, "page": a.page, "rows": rows_out,
+                   "gather_reduce": probe, "granularity_sweep": gsweep}, f, indent=2)
     print(f"saved {a.output_json}")
 
 

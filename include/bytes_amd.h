@@ -272,6 +272,28 @@ int bytes_select_pages(const void* page_ids, int64_t rows, int npick, int page, 
                        void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Study-harness microkernels.
+ * bytes_gather_reduce: replaces `_gather_reduce_kernel` of
+ *   benchmarks/bench_access_pattern.py:25-52: out[h, d] = sum_k v[h, idx[h, k], d]
+ *   fp32 [H, D] for v fp16 [H, S, D] (strides v_sh, v_ss; D in {8, 16, 32, 64,
+ *   128, 256}) and idx int32 [H, K] (row stride i_sh); entries outside [0, S)
+ *   read the clamped row.  Sums in a fixed order (deterministic).
+ * bytes_packed_stage: replaces `_packed_stage_kernel` of
+ *   benchmarks/bench_unpack_ablation.py:19-53: out[b, hq, t] fp32 (strides o_sb,
+ *   o_sh) over packed keys kp uint8 [B, Hk, S, D*bits/8] (strides k_*) with bf16
+ *   scale/zero [B, Hk, S, D/32] (strides m_*) and q bf16 [B, Hq, D]:
+ *   stage 0 sum of the packed byte of every column, 1 sum of the codes,
+ *   2 sum of code*scale+zero, 3 sum of (code*scale+zero)*q.  D in {64, 128},
+ *   bits in {4, 2}.
+ * ------------------------------------------------------------------------- */
+int bytes_gather_reduce(const void* v, int64_t v_sh, int64_t v_ss, const void* idx, int64_t i_sh, void* out, int H,
+                        int S, int K, int D, void* stream);
+int bytes_packed_stage(const void* q, int64_t q_sb, int64_t q_sh, const void* kp, int64_t k_sb, int64_t k_sh,
+                       int64_t k_ss, const void* scale, const void* zero, int64_t m_sb, int64_t m_sh, int64_t m_ss,
+                       void* out, int64_t o_sb, int64_t o_sh, int B, int Hq, int Hk, int S, int D, int bits,
+                       int stage, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Product-quantized decode with paged caches, outlier channels and fp8 values.
  * Replaces src/attention_kernels.py:
  *   paged_attn_pq_lut_kv    :588-622 (kernel :505-586)   vidx + vcb, block_table

@@ -829,3 +829,45 @@ def attend_topk(q_blk, k_r, v, idx, q_pos, scaling: float) -> torch.Tensor:
     sc = torch.where(valid, sc, torch.full_like(sc, NEG_INF))
     w = torch.softmax(sc, dim=-1).to(v.dtype)
     return (w.unsqueeze(-1) * vs).sum(3)
+
+
+# ---------------------------------------------------------------------------
+# f2/f4 study-harness microkernels
+# ---------------------------------------------------------------------------
+def gather_reduce(v: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """out[h, d] = sum_k v[h, idx[h, k], d] in fp32.
+
+    Restates `_gather_reduce_kernel` / `gather_reduce` of
+    benchmarks/bench_access_pattern.py:25-52 (v [H,S,D] fp16, idx [H,K]).
+    Pinned by: the full contiguous list equals v.sum(1); a permutation of
+    the list gives the same sums; one-hot rows (tests/test_oracle.py)."""
+    H, S, D = v.shape
+    gi = idx.long().unsqueeze(-1).expand(H, idx.shape[1], D)
+    return torch.gather(v.float(), 1, gi).sum(1)
+
+
+def packed_stage(q, packed, scale, zero, bits: int, stage: int) -> torch.Tensor:
+    """The four cumulative stages of benchmarks/bench_unpack_ablation.py:19-53
+    (`_packed_stage_kernel`) per (b, query head) and key row, in fp32:
+    0 sum over columns of each column's packed byte, 1 sum of the codes,
+    2 sum of code*scale+zero, 3 sum of (code*scale+zero)*q.
+    q [B,Hq,1,D]; packed [B,Hk,S,D*bits/8]; scale/zero [B,Hk,S,D/32].
+    Returns [B,Hq,S].  Pinned by: stage 0 = (8/bits) * sum of the bytes,
+    stage 1 = sum of score_keys_unpack, stage 2 = sum of score_keys_dequant,
+    stage 3 = sparse_score_packed at scaling 1 (tests/test_oracle.py)."""
+    B, Hq, _, D = q.shape
+    Hk = packed.shape[1]
+    G = Hq // Hk
+    epb = 8 // bits
+    cols = torch.arange(D)
+    p = packed.long()[..., cols // epb]                                   # [B,Hk,S,D]: the byte of each column
+    if stage == 0:
+        vals = p.float()
+    else:
+        vals = ((p >> ((cols % epb) * bits)) & ((1 << bits) - 1)).float()
+        if stage >= 2:
+            vals = vals * scale.float().repeat_interleave(32, -1) + zero.float().repeat_interleave(32, -1)
+    if stage == 3:
+        vr = repeat_kv(vals, G)                                            # [B,Hq,S,D]
+        return (vr * q.float().reshape(B, Hq, 1, D)).sum(-1)
+    return repeat_kv(vals.sum(-1, keepdim=True), G).squeeze(-1)

@@ -592,3 +592,36 @@ def test_attend_topk_bruteforce_and_causal_dense():
         p = int(pos[r])
         dense = R.decode_attn(q[:, :, r:r + 1], k[:, :, :p + 1], v[:, :, :p + 1], scale=0.3)
         assert torch.allclose(full[:, :, r], dense.squeeze(2).float(), atol=5e-3)   # bf16 output of decode_attn
+
+
+# ---------------------------------------------------------------------------
+# harness microkernels: gather-reduce and the staged packed-score probe
+# ---------------------------------------------------------------------------
+def test_gather_reduce_closed_forms():
+    g = torch.Generator().manual_seed(21)
+    H, S, D = 3, 50, 16
+    v = torch.randn(H, S, D, generator=g).half()
+    full = torch.arange(S).expand(H, S)
+    assert torch.allclose(R.gather_reduce(v, full), v.float().sum(1), atol=1e-4)
+    perm = torch.stack([torch.randperm(S, generator=g) for _ in range(H)])
+    assert torch.allclose(R.gather_reduce(v, perm), v.float().sum(1), atol=1e-4)
+    one = torch.tensor([[7], [0], [S - 1]])
+    assert torch.equal(R.gather_reduce(v, one), torch.stack([v[0, 7], v[1, 0], v[2, S - 1]]).float())
+    twice = torch.tensor([[4, 4, 9]] * H)
+    assert torch.allclose(R.gather_reduce(v, twice), 2 * v[:, 4].float() + v[:, 9].float(), atol=1e-4)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_packed_stage_closed_forms(bits):
+    g = torch.Generator().manual_seed(22)
+    B, Hq, Hk, S, D = 1, 4, 2, 9, 64
+    k = torch.randn(B, Hk, S, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    p, s, z = R.quantize_and_pack_score_keys(k, bits, 32)
+    st = [R.packed_stage(q, p, s, z, bits, i) for i in range(4)]
+    ex = lambda t: R.repeat_kv(t, 2)  # noqa: E731  per-KV-head sums seen by every query head of the group
+    assert torch.equal(st[0], ex((8 // bits) * p.long().sum(-1, keepdim=True).float()).squeeze(-1))
+    assert torch.equal(st[1], ex(R.score_keys_unpack(p, bits).sum(-1, keepdim=True).float()).squeeze(-1))
+    deq = R.score_keys_dequant(p, s, z, bits, 32)
+    assert torch.allclose(st[2], ex(deq.sum(-1, keepdim=True)).squeeze(-1), atol=1e-4)
+    assert torch.allclose(st[3], R.sparse_score_packed(q, p, s, z, 1.0, bits, 32), atol=1e-4)
