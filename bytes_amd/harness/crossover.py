@@ -9,6 +9,12 @@ pass, top-k, gather).  Writes JSON rows {S, frac, lat_ms, stages, winner} and
 prints the int2 / KIVI-4 latency ratio grid of the reference's heatmap.
 
     python -m bytes_amd.harness.crossover [--quick] [--output-json PATH]
+
+--c5 runs BASELINE C5's own sweep instead: at B=8, H_q=24, H_k=8, D=128,
+L=131072, the group-shared token top-k decode (score pass + top-k + gather,
+with bf16, fp8 and packed int2 score keys) at budgets of 1 / 2 / 5 / 10 / 25 /
+50 % of L against dense bf16 and fp8 decode of the same cache, and names the
+budget where each sparse variant stops beating dense bf16.
 """
 from __future__ import annotations
 
@@ -98,9 +104,49 @@ def run_cell(B, Hq, Hk, D, S, frac, seed, runs, dev):
             "dense_bf16_hbm_frac": (2 * kvb / (lat["bf16"] * 1e-3)) / (HBM_PEAK_GBS * 1e9)}
 
 
+C5_FRACS = [0.01, 0.02, 0.05, 0.10, 0.25, 0.50]
+
+
+def c5_sweep(runs, seed, dev, B=8, Hq=24, Hk=8, D=128, L=131072):
+    from .. import attention_kernels as AK
+    from ..sparse import quantize_and_pack_score_keys, token_topk_decode
+    from ..workloads import c5_topk
+    x = c5_topk(seed=seed, device=dev, B=B, Hq=Hq, Hk=Hk, D=D, L=L)
+    q, k, v, sc = x["q"], x["k"], x["v"], x["scale"]
+    kvb = B * Hk * L * D * 2
+    rows = {"dense_bf16": _time(lambda z: AK.decode_attn_bf16(z["q"], z["k"], z["v"], sc), {"q": q, "k": k, "v": v},
+                                2 * kvb, runs)}
+    k8, v8 = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+    rows["dense_fp8"] = _time(lambda z: AK.decode_attn_fp8(z["q"], z["k"], z["v"], sc), {"q": q, "k": k8, "v": v8},
+                              kvb, runs)
+    del v8
+    p2, s2, z2 = quantize_and_pack_score_keys(k, 2, 32)
+    keys = {"bf16": {}, "fp8": {"ks": k8}, "int2": {"ks": p2, "ksc": s2, "kzr": z2, "bits": 2}}
+    sparse = {}
+    for name, extra in keys.items():
+        sparse[name] = []
+        for frac in C5_FRACS:
+            kb = max(1, int(round(frac * L)))
+            inp = {"q": q, "k": k, "v": v, **{n: t for n, t in extra.items() if n != "bits"}}
+            fn = (lambda z, kb=kb, bits=extra.get("bits"):
+                  token_topk_decode(z["q"], z["k"], z["v"], kb, sc, k_score=z.get("ks"), score_scale=z.get("ksc"),
+                                    score_zero=z.get("kzr"), score_bits=bits))
+            ms = graph_ms(fn, [inp], warmup=3, runs=runs)
+            sparse[name].append({"frac": frac, "kb": kb, "ms": ms, "vs_dense_bf16": ms / rows["dense_bf16"]})
+            print(f"C5 {name:5s} score keys, k = {100 * frac:4.1f}% of L ({kb:6d}): {ms * 1e3:8.1f} us "
+                  f"({ms / rows['dense_bf16']:.3f} x dense bf16)", flush=True)
+    cross = {}
+    for name, pts in sparse.items():
+        beaten = [p for p in pts if p["ms"] >= rows["dense_bf16"]]
+        cross[name] = beaten[0]["frac"] if beaten else None
+    return {"shape": {"B": B, "H_q": Hq, "H_k": Hk, "D": D, "L": L}, "dense_ms": rows, "sparse": sparse,
+            "first_budget_not_faster_than_dense_bf16": cross}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--quick", action="store_true", help="3 x 3 grid (S 4K/16K/64K, frac 1%%/5%%/25%%)")
+    ap.add_argument("--c5", action="store_true", help="BASELINE C5's budget sweep against dense at its own shape")
     ap.add_argument("--B", type=int, default=32)
     ap.add_argument("--Hq", type=int, default=64)
     ap.add_argument("--Hk", type=int, default=8)
@@ -109,6 +155,18 @@ def main(argv=None):
     ap.add_argument("--output-json", default="harness_out/sparse_crossover.json")
     a = ap.parse_args(argv)
     dev = torch.device("cuda:0")
+    if a.c5:
+        res = c5_sweep(a.runs, a.seed, dev)
+        print("dense: " + " ".join(f"{n} {ms * 1e3:.1f} us" for n, ms in res["dense_ms"].items()))
+        print("first budget (k/L) not faster than dense bf16: " + ", ".join(
+            f"{n} keys {('%.0f%%' % (100 * f)) if f is not None else 'none (sparse faster at every budget)'}"
+            for n, f in res["first_budget_not_faster_than_dense_bf16"].items()))
+        os.makedirs(os.path.dirname(a.output_json) or ".", exist_ok=True)
+        with open(a.output_json, "w") as f:
+            json.dump({"schema": "c5_crossover_v1", "gpu": torch.cuda.get_device_name(0), "seed": a.seed, **res}, f,
+                      indent=2)
+        print(f"saved {a.output_json}")
+        return
     s_grid = [4096, 16384, 65536] if a.quick else S_GRID
     f_grid = [0.01, 0.05, 0.25] if a.quick else FRAC_GRID
     rows = []

@@ -225,7 +225,7 @@ def test_sparse_decode_scalar_pipeline(dev, frac):
     assert torch.equal(SP.topk_indices(s, kb).cpu().long(), R.topk_indices(s.cpu(), kb))
 
 
-@pytest.mark.parametrize("kb", [256, 1024, 4096])
+@pytest.mark.parametrize("kb", [256, 1024, 4096, 32768])
 def test_token_topk_c5_full(dev, kb):
     """BASELINE C5 at full size: B8 Hq24 Hkv8 D128 L131072."""
     x = W.c5_topk(seed=0, device=dev)
