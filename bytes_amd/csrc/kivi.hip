@@ -446,6 +446,422 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   }
 }
 
+// ============================================================================
+// Streaming decode (caches with an odd number of key groups): phases of 512
+// tokens, one 64-token tile per wave
+// ============================================================================
+// A workgroup of eight waves walks its split's quantized tokens in phases of
+// 512 (one 64-token tile, two key groups, per wave per phase).  The requests
+// of DEPTH phases are in flight at once, held in registers: every thread
+// loads a slice of the phase's key codes and key scales/zeros (staged in a
+// workgroup-shared LDS buffer) and every wave loads its own tile's value codes
+// and value scales/zeros (a wave-private LDS buffer).  When phase p's
+// registers have arrived and every wave is done with phase p-1, they are
+// written to LDS, phase p + DEPTH is requested into the same registers, a
+// barrier publishes the keys, and each wave computes its tile.  Splits are
+// 32-token multiples, so a tile can end after its first key group (the
+// second is then masked).  The bf16 residual window runs on splits of its
+// own.  Caches whose Sq is a multiple of 64 use kivi_decode_kernel, which
+// measured faster on them (the tiles' compute, not HBM, bounds both kernels
+// at two waves per SIMD).
+constexpr int kKsWaves = 8;
+constexpr int kKsPhase = kKsWaves * 64;        // tokens per phase
+constexpr int kKsGroups = kKsPhase / 32;       // key groups per phase
+
+// The decode uses this kernel for caches with an odd number of 32-token key
+// groups (Sq = 32 mod 64), whose key rows are only 8-byte aligned (2-bit) and
+// whose rows of key scales/zeros start on odd halfwords: key codes are read
+// in KPB-byte pieces (8 for 2-bit keys, 16 for 4-bit) and key scales/zeros
+// one halfword at a time, and splits are 32-token multiples.
+template <int D, int BITS, int KPB>
+struct KsCfg {
+  static constexpr int DEPTH = 2;                            // phases in flight
+  static constexpr int NT = kKsWaves * 64;
+  static constexpr int PPC = kKsPhase * BITS / 8 / KPB;      // key pieces per channel per phase
+  static constexpr int KROW = kKsPhase * BITS / 8 + 16;      // LDS bytes per channel row (+16: bank spread)
+  static constexpr int NKP = D * PPC;                        // key pieces per phase
+  static constexpr int KP = (NKP + NT - 1) / NT;             // key pieces per thread per phase
+  // threads past the phase's pieces load a valid piece again and store it
+  // past the channel rows
+  static constexpr int KBYTES = D * KROW + (KP * NT - NKP) * KPB;
+  static constexpr int NKM = 2 * D * kKsGroups;             // key scale/zero halfwords per phase
+  static constexpr int KMPT = (NKM + NT - 1) / NT;
+  static constexpr int KMP = D + 8;                          // fp16 per staged (scale|zero, group) row
+  static constexpr int KMBYTES = 2 * kKsGroups * KMP * 2;
+  static constexpr int VROW = D * BITS / 8;                  // bytes of one token's value codes
+  static constexpr int VBYTES = 64 * VROW;                   // value codes of one wave's tile
+  static constexpr int VDMA = VBYTES / 1024;                 // 16-byte value pieces per lane
+  static constexpr int NGV = D / 32;
+  static constexpr int VMBYTES = 2 * 64 * NGV * 2;           // value scales + zeros of one tile
+  static constexpr int WAVE = VBYTES + VMBYTES;
+  static constexpr int kQuant = KBYTES + KMBYTES + kKsWaves * WAVE;
+  static constexpr int kDense = 4 * DenseCfg<D>::WAVE;       // residual tiles of waves 0-3 (residual splits)
+  static constexpr int kEpi = splitk_smem_floats<D, kKsWaves>() * 4;
+  static constexpr int kSmem0 = kQuant > kDense ? kQuant : kDense;
+  static constexpr int kSmem = kSmem0 > kEpi ? kSmem0 : kEpi;
+  static_assert(kSmem <= 160 * 1024, "fits the LDS of one CU");
+  static_assert(VBYTES >= 1024 && VBYTES % 1024 == 0, "whole 16-byte pieces per lane");
+};
+
+// One phase's requests of one thread.
+template <int D, int BITS, int KPB>
+struct KsRegs {
+  using C = KsCfg<D, BITS, KPB>;
+  using KPiece = typename std::conditional<KPB == 16, u32x4, u32x2>::type;
+  KPiece k[C::KP];                             // key code pieces
+  uint16_t km[C::KMPT];                        // key scales / zeros
+  u32x4 v[C::VDMA];                            // this wave's value codes
+  VMetaReg<D> vm;                              // value scales (lanes 0-31) or zeros (32-63) of two tokens
+};
+
+// One 64-token tile: scores from the staged key phase (kc: this tile's first
+// byte of channel row 0, rows KROW bytes apart; kms: the scale row of its
+// first key group, the second group's row KMP halfwords on, zeros kzo
+// halfwords after the scales), online softmax, value accumulation from the
+// wave's staged value tile.  Scales are folded into the other MFMA operand
+// (see kivi_tile): codes enter the f16 MFMAs as exact integers.
+template <int D, int BITS, int KROW, int KMP>
+__device__ __forceinline__ void kivi_tile64(int lane, const f16x8 (&qh)[D / 32], const char* kc, const _Float16* kms,
+                                            int kzo, const char* vst, const char* vml, bool second, float& m_run,
+                                            float& l_run, f32x4 (&acc)[D / 16], f32x4& zv) {
+  constexpr int KK = D / 32, NGV = D / 32, VROW = D * BITS / 8;
+  const int l16 = lane & 15, lg = lane >> 4;
+  // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
+  // 4-bit: sc[tb][i]       is tile token 16tb + 4lg + i
+  f32x4 sc[4];
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    const _Float16* ks_row = kms + sg * KMP;
+    f16x8 qs[KK];
+    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int off = lg * (D / 4) + kk * 8;
+      const u32x4 ks = *reinterpret_cast<const u32x4*>(ks_row + off);
+      const u32x4 kz = *reinterpret_cast<const u32x4*>(ks_row + kzo + off);
+      qs[kk] = scale8(qh[kk], ks);
+      z = mfma_f16(__builtin_bit_cast(f16x8, kz), qh[kk], z);
+    }
+    sc[sg * 2 + 0] = z;
+    sc[sg * 2 + 1] = z;
+#pragma unroll
+    for (int bb = 0; bb < (BITS == 2 ? 1 : 2); ++bb) {
+      const int blk = BITS == 2 ? sg : sg * 2 + bb;
+#pragma unroll
+      for (int rd = 0; rd < KK / 2; ++rd) {
+        const int ch = lg * (D / 4) + rd * 16 + l16;
+        const u32x2 x = tr4(kc + ch * KROW + blk * 8);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int kk = rd * 2 + half;
+          if (BITS == 2) {
+            const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
+            sc[sg * 2 + 0] = mfma_f16(codes_fp4(e), qs[kk], sc[sg * 2 + 0]);
+            sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
+          } else {
+            const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
+            sc[blk] = mfma_f16(codes_fp8(lo, hi), qs[kk], sc[blk]);
+          }
+        }
+      }
+    }
+  }
+
+  // a tile that ends its split after its first key group: the second
+  // group's tokens (past the split) take no part
+  if (!second) {
+    sc[2] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+    sc[3] = sc[2];
+  }
+  float mx = kNegInf;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[u][i]);
+  mx = fmaxf(mx, shfl_xor_f(mx, 16));
+  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = fast_exp2(m_run - m_new);
+  const bool rescale = __ballot(m_run != kNegInf) != 0;
+  float p[16];
+  float psum = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[u * 4 + i] = fast_exp2(sc[u][i] - m_new);
+      psum += p[u * 4 + i];
+    }
+  l_run = l_run * alpha + psum;
+  m_run = m_new;
+  if (rescale) {
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
+    zv *= alpha;
+  }
+  f16x8 pb[2];
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg)
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int idx = BITS == 2 ? (sg * 2 + (jj & 1)) * 4 + (jj >> 1) : (2 * sg + (jj >> 2)) * 4 + (jj & 3);
+      pb[sg][jj] = (_Float16)p[idx];
+    }
+
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    f16x8 pg[NGV];
+#pragma unroll
+    for (int g = 0; g < NGV; ++g)
+      pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
+    {
+      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, l16 % NGV, sg * 32) * 2 + lg * 16);
+      zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
+    }
+    if (BITS == 2) {
+#pragma unroll
+      for (int rd = 0; rd < D / 64; ++rd) {
+        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+        const int tok = 32 * sg + 8 * lg + r;
+        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
+        const int ca = 2 * rd, cbb = 2 * rd + 1;
+        const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
+        const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
+        acc[ca * 2 + 0] = mfma_f16(codes_fp4(e0), pg[ca], acc[ca * 2 + 0]);
+        acc[cbb * 2 + 0] = mfma_f16(codes_fp4(e1), pg[cbb], acc[cbb * 2 + 0]);
+        acc[ca * 2 + 1] = mfma_f16(codes_fp4(o0), pg[ca], acc[ca * 2 + 1]);
+        acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int rd = 0; rd < D / 32; ++rd) {
+        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+        const int tok = (r & 1) ? 32 * sg + 16 + 4 * lg + (r >> 1) : 32 * sg + 4 * lg + (r >> 1);
+        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
+        const uint32_t lo0 = x[0] & 0x0F0F0F0Fu, hi0 = (x[0] >> 4) & 0x0F0F0F0Fu;
+        const uint32_t lo1 = x[1] & 0x0F0F0F0Fu, hi1 = (x[1] >> 4) & 0x0F0F0F0Fu;
+        acc[2 * rd] = mfma_f16(codes_fp8(lo0, hi0), pg[rd], acc[2 * rd]);
+        acc[2 * rd + 1] = mfma_f16(codes_fp8(lo1, hi1), pg[rd], acc[2 * rd + 1]);
+      }
+    }
+  }
+}
+
+template <int D, int BITS, int KPB>
+__global__ __launch_bounds__(kKsWaves * 64, 1) void kivi_stream_kernel(KiviArgs a) {
+  using C = KsCfg<D, BITS, KPB>;
+  using Regs = KsRegs<D, BITS, KPB>;
+  constexpr int NT = C::NT;
+  constexpr int DEPTH = C::DEPTH;
+  PREFETCH_ARGS(a);
+  __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  int unit, split;
+  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
+  const int b = unit / (a.Hk * a.HB);
+  const int rem = unit - b * a.Hk * a.HB;
+  const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
+  const int hq0 = hk * a.G + hb * 16;
+  const int nh = min(16, a.G - hb * 16);
+  const uint16_t* qrow0 = a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh;
+  const bool qlive = l16 < nh;
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int Sq = a.Sq;
+  const bool quant = split < a.nsq;                // else a split of the residual window
+  const int t_begin = quant ? split * a.chunk : 0;
+  const int t_end = quant ? min(t_begin + a.chunk, Sq) : 0;
+  const int ntok = t_end - t_begin;                // a multiple of 32
+  const int r_begin = quant ? 0 : (split - a.nsq) * kResidPerSplit;
+  const int r_end = quant ? 0 : min(r_begin + kResidPerSplit, a.R);
+  const int rt = r_begin + w * kTile;
+  const bool rtile = !quant && w < 4 && rt < r_end;
+
+  if (quant) {
+    const int nph = (ntok + kKsPhase - 1) / kKsPhase;
+    const int64_t bh = (int64_t)b * a.Hk + hk;
+    const int ngk = Sq >> 5;
+    const int64_t wk = Sq * BITS / 32;             // int32 words per key channel row
+    // zeros are addressed from the scales plus a uniform distance: a per-lane
+    // choice between two argument fields otherwise becomes a vector load of
+    // the argument block, waited on before the first request
+    const int64_t kz_off = a.km - a.ks, vz_off = a.vm - a.vs;
+
+    // Q as the fp16 B operand (scaled by scale*log2e), lane: Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)]
+    u32x4 qraw[D / 32];
+    {
+      const uint16_t* qp = qrow0 + (int64_t)(qlive ? l16 : 0) * a.q_sh + lg * (D / 4);
+#pragma unroll
+      for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = ld16(qp + kk * 8);
+    }
+
+    // Requests of phase ph (clamped into the split: phases and groups past its
+    // end re-read its last valid bytes, which nothing uses).
+    auto issue = [&](int ph, Regs& r) {
+      const int p0 = t_begin + min(ph, nph - 1) * kKsPhase;            // phase's first token
+      const int nvt = min(kKsPhase, t_end - p0);                        // valid tokens of the phase
+      const int npc = max(nvt * BITS / 8 / KPB, 1);                     // valid key pieces per channel
+      const int ngv = max(nvt >> 5, 1);                                 // valid key groups
+      const uint32_t* kqb = a.kq + (bh * D) * wk + p0 * BITS / 32;
+#pragma unroll
+      for (int i = 0; i < C::KP; ++i) {
+        const int pc = min((int)threadIdx.x + NT * i, C::NKP - 1);
+        const int ch = pc / C::PPC, q = pc - (pc / C::PPC) * C::PPC;
+        r.k[i] = *reinterpret_cast<const typename Regs::KPiece*>(kqb + ch * wk + min(q, npc - 1) * (KPB / 4));
+      }
+      const int g0 = p0 >> 5;
+#pragma unroll
+      for (int i = 0; i < C::KMPT; ++i) {
+        const int e = min((int)threadIdx.x + NT * i, C::NKM - 1);
+        const int g = e % kKsGroups, row = e / kKsGroups;               // row = sm * D + ch
+        const int sm = row / D, ch = row - sm * D;
+        const _Float16* src = a.ks + (sm ? kz_off : 0) + (bh * D + ch) * ngk + g0 + min(g, ngv - 1);
+        r.km[i] = *reinterpret_cast<const uint16_t*>(src);
+      }
+      // this wave's tile (waves past the phase's tokens re-read its last
+      // tile); reads stay inside its tv valid tokens (32 or 64)
+      const int wt = p0 + min(w * 64, (nvt - 1) & ~63);
+      const int tv = min(64, t_end - wt);
+      const char* vsrc = reinterpret_cast<const char*>(a.vq + bh * (int64_t)Sq * (D * BITS / 32)) +
+                         (int64_t)wt * C::VROW;
+#pragma unroll
+      for (int i = 0; i < C::VDMA; ++i) r.v[i] = ld16(vsrc + min((lane + 64 * i) * 16, tv * C::VROW - 16));
+      const _Float16* mp =
+          a.vs + (lane < 32 ? 0 : vz_off) + (bh * Sq + wt + min(2 * (lane & 31), tv - 2)) * C::NGV;
+      r.vm = *reinterpret_cast<const VMetaReg<D>*>(mp);
+    };
+    auto stage = [&](const Regs& r) {
+      char* kbuf = smem_raw;
+      _Float16* kml = reinterpret_cast<_Float16*>(smem_raw + C::KBYTES);
+      char* vst = smem_raw + C::KBYTES + C::KMBYTES + w * C::WAVE;
+      char* vml = vst + C::VBYTES;
+#pragma unroll
+      for (int i = 0; i < C::KP; ++i) {
+        const int pc = threadIdx.x + NT * i;
+        const int ch = pc / C::PPC, q = pc - (pc / C::PPC) * C::PPC;
+        const int off = pc < C::NKP ? ch * C::KROW + q * KPB : D * C::KROW + (pc - C::NKP) * KPB;
+        *reinterpret_cast<typename Regs::KPiece*>(kbuf + off) = r.k[i];
+      }
+#pragma unroll
+      for (int i = 0; i < C::KMPT; ++i) {
+        const int e = threadIdx.x + NT * i;
+        if (C::KMPT * NT > C::NKM && e >= C::NKM) continue;
+        const int g = e % kKsGroups, row = e / kKsGroups;
+        const int sm = row / D, ch = row - sm * D;
+        kml[(sm * kKsGroups + g) * C::KMP + kslot_pos<BITS>(ch)] = __builtin_bit_cast(_Float16, r.km[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < C::VDMA; ++i) *reinterpret_cast<u32x4*>(vst + (lane + 64 * i) * 16) = r.v[i];
+      const _Float16* hv = reinterpret_cast<const _Float16*>(&r.vm);
+      _Float16* dst = reinterpret_cast<_Float16*>(vml);
+      const int sm = lane >> 5, tau0 = 2 * (lane & 31);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int g = 0; g < C::NGV; ++g) dst[vmeta_slot<D, BITS>(sm, g, tau0 + u)] = hv[u * C::NGV + g];
+    };
+
+    Regs rg[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      issue(d, rg[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    f16x8 qh[D / 32];
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, qraw[kk]);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
+    }
+    f32x4 zv = {0.f, 0.f, 0.f, 0.f};
+    // Phases run in groups of DEPTH (the last group padded with empty phases,
+    // whose requests re-read the split's last bytes).  Every group but the
+    // last requests the next group's phases, one per staged phase, with no
+    // condition, so the waits before each staging count exactly the
+    // requests that came after its own.  One LDS buffer: the barrier before
+    // the staging waits for every wave to finish the previous phase.
+    // Phase p + DEPTH is requested before phase p is computed, except for
+    // 4-bit keys at D = 128, where it is requested after (its registers would
+    // otherwise not fit beside the tile's).
+    constexpr bool kEarly = !(BITS == 4 && D == 128);
+    auto run_phase = [&](int ph, int d, bool more) {
+      if (ph > 0) __syncthreads();
+      stage(rg[d]);
+      if (more && kEarly) issue(ph + DEPTH, rg[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      const int left = ntok - (ph * kKsPhase + w * 64);                 // tokens of this wave's tile
+      if (left > 0) {
+        const _Float16* kms = reinterpret_cast<const _Float16*>(smem_raw + C::KBYTES) + 2 * w * C::KMP;
+        const char* vst = smem_raw + C::KBYTES + C::KMBYTES + w * C::WAVE;
+        kivi_tile64<D, BITS, C::KROW, C::KMP>(lane, qh, smem_raw + w * 64 * BITS / 8, kms, kKsGroups * C::KMP, vst,
+                                              vst + C::VBYTES, left > 32, m_run, l_run, acc, zv);
+      }
+      if (more && !kEarly) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue(ph + DEPTH, rg[d]);
+      }
+    };
+    const int ngroups = (nph + DEPTH - 1) / DEPTH;
+    int p0 = 0;
+    for (int gi = 0; gi + 1 < ngroups; ++gi, p0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) run_phase(p0 + d, d, true);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      if (p0 + d < nph) run_phase(p0 + d, d, false);
+    }
+#pragma unroll
+    for (int g = 0; g < C::NGV; ++g) {
+      const float zg = __shfl(zv[g], l16, 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * g][i] += zg;
+        acc[2 * g + 1][i] += zg;
+      }
+    }
+  } else if (rtile) {
+    // A split of the bf16 residual window: one 32-token dense tile per wave of
+    // waves 0-3.  Its K and V rows go straight from HBM to the wave's LDS tile
+    // buffers (global_load_lds) in the buffers' swizzled layout: LDS chunk c
+    // of row r holds column chunk c ^ swz(r).
+    using DC = DenseCfg<D>;
+    const uint16_t* rkbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
+    const uint16_t* rvbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
+    char* kst = smem_raw + w * DC::WAVE;
+    char* rvst = kst + DC::VT;
+#pragma unroll
+    for (int i = 0; i < DC::VT / 1024; ++i) {
+      const int p = lane + 64 * i;
+      const int rr = p / DC::CPR, cc = p - rr * DC::CPR;
+      const int row = min(rt + rr, a.R - 1);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(rkbase + (int64_t)row * a.kr_ss + kswz<D>(rr, cc) * 8),
+          (__attribute__((address_space(3))) void*)(kst + i * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(rvbase + (int64_t)row * a.vr_ss + vswz<D>(rr, cc) * 8),
+          (__attribute__((address_space(3))) void*)(rvst + i * 1024), 16, 0, 0);
+    }
+    bf16x8 qb[D / 32];
+    load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
+    // the compiler does not track LDS written by global_load_lds: wait for
+    // every request (the tile's and Q's) before the tile is read
+    __builtin_amdgcn_s_waitcnt(0);
+    wave_lds_sync();
+    dense_compute<D>(range_mask(rt, r_end), a.scale_log2, lane, qb, kst, rvst, m_run, l_run, acc);
+  }
+  splitk_epilogue<D, kKsWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0, nh,
+                               (BITS == 2 && quant) ? kDmapKivi2 : kDmapDense);
+}
+
 template <int D, int BITS, int NW>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a) {
   using C = KiviCfg<D, BITS, NW>;
@@ -731,6 +1147,42 @@ static void kivi_plan(int Sq, int R, long units, int chunk_req, int* nw, int* ch
   *rchunk = rc;
 }
 
+// Plan of the streaming kernel: one eight-wave workgroup per CU at a time.
+// The bf16 residual window gets splits of its own (128 tokens, one 32-token
+// tile per wave of waves 0-3), and the quantized tokens of each unit are cut
+// into the splits left on the CUs (about CUs/units - residual splits), in
+// `gran`-token multiples (64 for 2-bit keys read in 16-byte pieces, else 32).
+static void kivi_stream_plan(int Sq, int R, long units, int chunk_req, int gran, int* chunk, int* nsq, int* rsplit,
+                             int* rchunk) {
+  const long cus = device_cu_count();
+  const int nr = (R + kResidPerSplit - 1) / kResidPerSplit;
+  int c;
+  if (chunk_req > 0) {
+    c = chunk_req;
+  } else {
+    long ns = cus / units - nr;
+    if (ns < 1) ns = 1;
+    c = (int)((Sq + ns - 1) / ns);
+  }
+  c = (c + gran - 1) / gran * gran;
+  if (c < gran) c = gran;
+  int n = Sq > 0 ? (Sq + c - 1) / c : 0;
+  if (n + nr > 1024) {                            // the merge takes up to 1024 splits
+    c = ((Sq + 1023 - nr) / (1024 - nr) + gran - 1) / gran * gran;
+    n = (Sq + c - 1) / c;
+  }
+  *chunk = c;
+  *nsq = n;
+  *rsplit = nr;
+  *rchunk = 0;
+}
+
+// Key piece width (bytes) and split granularity (tokens) of the streaming kernel.
+static void kivi_stream_shape(int bits, int* kpb, int* gran) {
+  *kpb = bits == 2 ? 8 : 16;
+  *gran = 32;
+}
+
 }  // namespace bytes_amd
 
 using namespace bytes_amd;
@@ -774,14 +1226,21 @@ int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D
   if ((D != 64 && D != 128) || (bits != 2 && bits != 4)) return (int)hipErrorInvalidValue;
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
-  int nw, chunk, nsq, rsplit, rchunk;
-  kivi_plan(Sq, R, units, chunk_req, &nw, &chunk, &nsq, &rsplit, &rchunk);
+  int chunk, nsq, rsplit, rchunk;
+  if (Sq % kKiviTile == 0) {
+    int nw;
+    kivi_plan(Sq, R, units, chunk_req, &nw, &chunk, &nsq, &rsplit, &rchunk);
+  } else {
+    int kpb, gran;
+    kivi_stream_shape(bits, &kpb, &gran);
+    kivi_stream_plan(Sq, R, units, chunk_req, gran, &chunk, &nsq, &rsplit, &rchunk);
+  }
   *bytes = splitk_workspace_bytes(units, nsq + rsplit, D);
   return 0;
 }
 
-// Kq/K_scale/K_mn/Vq/V_scale/V_mn contiguous in the layouts above; Sq % 64 == 0
-// (Sq == 0 allowed); group size 32.  hipErrorNotSupported for other shapes.
+// Kq/K_scale/K_mn/Vq/V_scale/V_mn contiguous in the layouts above; Sq % 32 == 0
+// (Sq == 0 allowed); group size 32.
 int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, const void* k_mn, const void* k_res,
                            const void* vq, const void* v_scale, const void* v_mn, const void* v_res, void* out,
                            int B, int Hq, int Hk, int Sq, int R, int D, int bits, int64_t q_sb, int64_t q_sh,
@@ -793,7 +1252,7 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   if ((D != 64 && D != 128) || (bits != 2 && bits != 4)) return (int)hipErrorInvalidValue;
   if (Sq > 0 && (!kq || !k_scale || !k_mn || !vq || !v_scale || !v_mn)) return (int)hipErrorInvalidValue;
   if (R > 0 && (!k_res || !v_res)) return (int)hipErrorInvalidValue;
-  if (Sq % kKiviTile != 0) return (int)hipErrorNotSupported;
+  if (Sq % 32 != 0) return (int)hipErrorInvalidValue;     // key groups of 32 tokens
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
   if (units > 65535) return (int)hipErrorInvalidConfiguration;
@@ -812,8 +1271,17 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.vr_sb = vr_sb; a.vr_sh = vr_sh; a.vr_ss = vr_ss;
   a.Hk = Hk; a.G = G; a.HB = HB; a.Sq = Sq; a.R = R;
   a.scale_log2 = scale * kLog2e;
-  int nw;
-  kivi_plan(Sq, R, units, chunk_req, &nw, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
+  // Sq a multiple of 64: the two-half kernel; else (an odd number of 32-token
+  // key groups) the streaming kernel, whose loads and tiles take 32-token
+  // granularity
+  const bool halves = Sq % kKiviTile == 0;
+  int nw = 8, kpb = 16, gran = 32;
+  if (halves) {
+    kivi_plan(Sq, R, units, chunk_req, &nw, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
+  } else {
+    kivi_stream_shape(bits, &kpb, &gran);
+    kivi_stream_plan(Sq, R, units, chunk_req, gran, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
+  }
   const int ns = a.nsq + a.rsplit;                       // quantized chunks, then the residual's own splits
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
@@ -823,18 +1291,36 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   a.o.Hk = Hk; a.o.HB = HB; a.o.G = G;
   splitk_carve(workspace, units, ns, a.o);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)(ns * units)), block(nw * 64);
-#define KIVI_LAUNCH(DD, BB)                                                               \
-  if (nw == 8) BYTES_LAUNCH(kProfKivi, (kivi_decode_kernel<DD, BB, 8>), grid, block, 0, st, a); \
+  const dim3 grid((unsigned)(ns * units));
+  if (halves) {
+    const dim3 block(nw * 64);
+#define KIVI_HALVES(DD, BB)                                                                         \
+  if (nw == 8) BYTES_LAUNCH(kProfKivi, (kivi_decode_kernel<DD, BB, 8>), grid, block, 0, st, a);     \
   else BYTES_LAUNCH(kProfKivi, (kivi_decode_kernel<DD, BB, 4>), grid, block, 0, st, a);
+    if (D == 128 && bits == 2) {
+      KIVI_HALVES(128, 2)
+    } else if (D == 128 && bits == 4) {
+      KIVI_HALVES(128, 4)
+    } else if (D == 64 && bits == 2) {
+      KIVI_HALVES(64, 2)
+    } else {
+      KIVI_HALVES(64, 4)
+    }
+#undef KIVI_HALVES
+    int rc = (int)hipGetLastError();
+    if (rc) return rc;
+    return splitk_combine(a.o, units, D, st);
+  }
+  const dim3 block(kKsWaves * 64);
+#define KIVI_LAUNCH(DD, BB, KP) BYTES_LAUNCH(kProfKivi, (kivi_stream_kernel<DD, BB, KP>), grid, block, 0, st, a)
   if (D == 128 && bits == 2) {
-    KIVI_LAUNCH(128, 2)
+    KIVI_LAUNCH(128, 2, 8);
   } else if (D == 128 && bits == 4) {
-    KIVI_LAUNCH(128, 4)
+    KIVI_LAUNCH(128, 4, 16);
   } else if (D == 64 && bits == 2) {
-    KIVI_LAUNCH(64, 2)
+    KIVI_LAUNCH(64, 2, 8);
   } else {
-    KIVI_LAUNCH(64, 4)
+    KIVI_LAUNCH(64, 4, 16);
   }
 #undef KIVI_LAUNCH
   int rc = (int)hipGetLastError();

@@ -120,14 +120,8 @@ def kivi_decode_attn(Q, Kq, K_scale, K_mn, K_residual, Vq, V_scale, V_mn, V_resi
     if Sq + R == 0:
         raise ValueError("empty KV cache")
     sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    if Sq % 64 != 0:
-        # Shapes the fused kernel does not tile (Sq not a multiple of 64): dequantize
-        # the packed part to bf16 on the GPU and run the dense kernel over the
-        # concatenated cache.
-        from .attention_kernels import decode_attn_bf16
-        kd = _dequant_last_dim(Kq, K_scale, K_mn, group_size, bits, torch.bfloat16, False).transpose(2, 3)
-        vd = _dequant_last_dim(Vq, V_scale, V_mn, group_size, bits, torch.bfloat16, False)
-        return decode_attn_bf16(Q, torch.cat([kd, K_residual], 2), torch.cat([vd, V_residual], 2), sc)
+    if Sq % 32 != 0:
+        raise ValueError(f"quantized length {Sq} is not a whole number of 32-token key groups")
     q3 = C.rows16(Q.squeeze(2))
     kr, vr = C.rows16(K_residual), C.rows16(V_residual)
     t = [x.contiguous() if x is not None else None for x in (Kq, K_scale, K_mn, Vq, V_scale, V_mn)]

@@ -73,20 +73,55 @@ def _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=0, chunk=0):
     (1, 4, 2, 128, 300, 300),           # residual only, three 128-token residual splits, ragged end
     (1, 7, 1, 128, 1024 + 200, 200),    # residual pieces of 64 tokens (two tiles) on the last splits
     (2, 8, 2, 128, 256 + 384, 384),     # more residual than four 128-token pieces hold: own splits
+    (1, 7, 1, 128, 2080 + 128, 128),    # Sq = 2080, an odd number of key groups: the streaming kernel
+    (2, 4, 4, 64, 1056 + 32, 32),       # the same at D = 64, G = 1
 ])
 def test_decode_small(dev, bits, B, Hq, Hk, D, L, Rw):
     _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-def test_decode_fallback_shape(dev, bits):
-    # Sq = 96 is not a multiple of the 64-token tile: GPU dequant + dense kernel path
+def test_decode_odd_group_count(dev, bits):
+    # Sq = 96: three 32-token key groups (2-bit key rows are 24 bytes: 8-byte key pieces)
     _decode_case(dev, bits, 1, 4, 2, 128, 96 + 16, 16, seed=3)
 
 
-@pytest.mark.parametrize("chunk", [256, 512])
-def test_decode_split_counts(dev, chunk):
-    _decode_case(dev, 2, 1, 7, 1, 128, 4096 + 128, 128, seed=4, chunk=chunk)
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("extra", [0, 32])
+@pytest.mark.parametrize("chunk", [64, 256, 512, 1280, 2304])
+def test_decode_split_counts(dev, bits, extra, chunk):
+    """Forced split lengths on both kernels: Sq = 4096 (an even number of key
+    groups: the two-half kernel) and Sq = 4128 (odd: the streaming kernel,
+    whose splits of 1280 and 2304 tokens run five and five phases, the second
+    phase group padded with an empty phase, and whose 4128-token cache ends
+    in a half tile)."""
+    _decode_case(dev, bits, 1, 7, 1, 128, 4096 + extra + 128, 128, seed=4, chunk=chunk)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_c2_odd_group_count_runs_fused(dev, bits):
+    """C2 with 32 more packed tokens (Sq = 16288, an odd number of key groups)
+    runs in the fused decode kernel (its launch is seen by the kernel timing
+    hook) and matches the oracle."""
+    from bytes_amd import _lib
+    raw = W.kivi_raw(L=16288 + 128, seed=9)
+    cpu = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, bits)
+    g = _to(cpu, dev)
+    names = ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn", "V_residual")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    e1.record()
+    torch.cuda.synchronize()
+    t_before = e0.elapsed_time(e1)
+    lib = _lib.lib()
+    assert lib.bytes_set_kernel_events(2, e0.cuda_event, e1.cuda_event) == 0
+    try:
+        out = K.kivi_decode_attn(*[g[n] for n in names], bits)
+    finally:
+        lib.bytes_set_kernel_events(0, None, None)
+    torch.cuda.synchronize()
+    assert e0.elapsed_time(e1) != t_before and e0.elapsed_time(e1) > 0, "the fused KIVI kernel did not launch"
+    _check(out, R.kivi_decode_attn(*[cpu[n] for n in names], bits), f"C2+32 kivi{bits}")
 
 
 @pytest.mark.parametrize("bits", [2, 4])
@@ -114,16 +149,13 @@ def test_decode_c2_full(dev, bits):
 
 @pytest.mark.parametrize("bits", [2, 4])
 @pytest.mark.parametrize("B,Hq,Hk,D,L,Rw", [
-    (2, 8, 4, 64, 16256 + 128, 128),      # 8-wave workgroups, residual on a split of its own
-    (1, 14, 2, 128, 65536 + 64, 64),      # 8-wave workgroups, residual pieces on the last splits
-    (2, 8, 2, 128, 65536 + 200, 200),     # 64-token pieces: two residual tiles per split (4-bit: both
-                                          # right after the waves' own tiles; 2-bit: after the chunk)
+    (2, 8, 4, 64, 16256 + 128, 128),      # two-half kernel, eight-wave workgroups
+    (1, 14, 2, 128, 65536 + 64, 64),      # two-half kernel, residual pieces on the last splits
+    (2, 8, 2, 128, 65536 + 200, 200),     # two-half kernel, two residual tiles per piece
+    (2, 8, 4, 64, 16288 + 128, 128),      # streaming kernel, D = 64
+    (1, 14, 2, 128, 65568 + 64, 64),      # streaming kernel: about 19 phases per split (phase-group loop)
 ])
-def test_decode_eight_wave_workgroups(dev, bits, B, Hq, Hk, D, L, Rw):
-    """Shapes whose 1024-token grid fills half to all of the CUs take the
-    eight-wave, 1024-token-chunk kernel (on a 256-CU device).  Residual tiles
-    that fit in the first half's key block run without waiting for the other
-    waves; larger pieces wait for the whole chunk."""
+def test_decode_long_contexts(dev, bits, B, Hq, Hk, D, L, Rw):
     _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
 
 
