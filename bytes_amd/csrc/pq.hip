@@ -96,6 +96,101 @@ __device__ __forceinline__ int pq_len(const PqArgs& a, int b) {
   return a.btab ? max(0, min(a.clens[b], a.S)) : a.S;
 }
 
+// ---- LUT entries on MFMA ----
+// Every kernel that builds LUT entries (pq_lut_kernel and the decodes that
+// build their own) computes
+//   lut[h][j][c] = (lut_scale * 2^k_h) * dot(q_h[8j .. 8j+7] * 2^-k_h, cb[j][c])
+// where k_h = max(0, e_h - 15) for the head's largest |q| = 1.x * 2^e_h (the
+// scaled row then fits fp16), and dot comes from v_mfma_f32_16x16x16_f16 on
+// a block-diagonal pair of subspaces (j even, j + 1): rows 0-7 are heads
+// against subspace j in k-slots 0-7, rows 8-15 the same heads against
+// subspace j + 1 in slots 8-15, columns are 16 consecutive codewords, so each
+// codeword byte is read once.  The A operand is hi = fp16(q'); a second MFMA
+// accumulates lo = fp16(q' - hi) where any lane of the wave has a nonzero lo
+// part (it adds exact zeros otherwise, so skipping it changes nothing).
+// Every product is exact (fp16 x fp16), q' = hi + lo exactly for
+// |q'| >= 2^-17, and an entry depends only on its own head's q row and the
+// slot its subspace takes: any grouping of heads gives the same bits.
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lut_shift(float amax) {
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127;
+  return (e >= 16 && e < 128) ? e - 15 : 0;
+}
+
+// hi and lo A operands of lane (m, g) for subspace pair (j, j + 1): x = the
+// scaled q values of dims (g & 1) * 4 .. +3 of subspace j + (g >> 1) of head
+// m % 8, taken where the lane's row block matches its slot block (m / 8 ==
+// g / 2) and zero elsewhere (the caller passes zeros for such lanes).
+__device__ __forceinline__ void lut_a_operands(f32x4 x, f16x4& hi, f16x4& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const _Float16 h = (_Float16)x[i];
+    hi[i] = h;
+    lo[i] = (_Float16)(x[i] - (float)h);
+  }
+}
+
+// B operand of codewords c0 .. c0+15 for subspace pair (j, j + 1): lane
+// (n = lane % 16, g = lane / 16) holds dims (g & 1) * 4 .. +3 of codeword
+// c0 + n of subspace j + (g >> 1) (codewords past K repeat codeword K - 1).
+__device__ __forceinline__ f16x4 lut_b_operand(const _Float16* cb, int K, int j, int c0, int lane) {
+  const int c = min(c0 + (lane & 15), K - 1);
+  const int jj = j + (lane >> 5);
+  return *reinterpret_cast<const f16x4*>(cb + ((int64_t)jj * K + c) * 8 + ((lane >> 4) & 1) * 4);
+}
+
+// Entries of one subspace pair and 16 codewords: lane (n, g) receives heads
+// (g & 1) * 4 .. +3 of codeword c0 + n, subspace j + (g >> 1).
+__device__ __forceinline__ f32x4 lut_mfma(f16x4 hi, f16x4 lo, bool use_lo, f16x4 b) {
+  f32x4 e = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  if (use_lo) e = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, b, e, 0, 0, 0);
+  return e;
+}
+
+// True where any lane of the wave holds a nonzero lo part (wave-uniform).
+__device__ __forceinline__ bool lut_need_lo(f16x4 lo) {
+  const bool nz = (float)lo[0] != 0.f || (float)lo[1] != 0.f || (float)lo[2] != 0.f || (float)lo[3] != 0.f;
+  return __ballot(nz) != 0;
+}
+
+// Scaled rows q' = q * 2^-k_h (fp32, qs[h][D]) and entry multipliers
+// lut_scale * 2^k_h (mul[h]) of a workgroup's heads, in LDS: wave w takes
+// row h = w.  The row is loaded first (lut_load_q, issued before any other
+// request so that it heads the queue) and stored later (lut_store_q); rows at
+// or past nh are zero with multiplier zero.  q0 points at head 0's row.
+template <int D>
+struct LutQ {
+  float x[D / 64];
+};
+
+template <int D>
+__device__ __forceinline__ LutQ<D> lut_load_q(const uint16_t* q0, int64_t q_sh, int h, int nh) {
+  constexpr int PL = D / 64;
+  const int lane = threadIdx.x & 63;
+  const uint16_t* row = q0 + (int64_t)min(h, nh - 1) * q_sh + lane * PL;
+  LutQ<D> r;
+#pragma unroll
+  for (int p = 0; p < PL; ++p) r.x[p] = h < nh ? bf16_bits_to_f32(row[p]) : 0.f;
+  return r;
+}
+
+template <int D>
+__device__ __forceinline__ void lut_store_q(const LutQ<D>& r, int h, int nh, float lut_scale, float* qs,
+                                            float* mul) {
+  constexpr int PL = D / 64;
+  const int lane = threadIdx.x & 63;
+  float amax = 0.f;
+#pragma unroll
+  for (int p = 0; p < PL; ++p) amax = fmaxf(amax, fabsf(r.x[p]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, shfl_xor_f(amax, o));
+  const int k = lut_shift(amax);
+#pragma unroll
+  for (int p = 0; p < PL; ++p) qs[h * D + lane * PL + p] = ldexpf(r.x[p], -k);
+  if (lane == 0) mul[h] = h < nh ? ldexpf(lut_scale, k) : 0.f;
+}
+
 template <int D, bool QV>
 struct PqCfg {
   static constexpr int M = D / 8;
@@ -319,6 +414,8 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   // The first tile's codes are requested before the LUTs are staged, so they
   // arrive meanwhile.  Every later request is unconditional (rows clamped to
   // len - 1 past the end), so each wait counts the same requests.
+  LutQ<D> qrow;
+  if (BUILD_LUT && w < kPqHeads) qrow = lut_load_q<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, w, nh);
   Regs r;
   if (any) pq_issue<D, QV, VF8, OUT>(a, b, kih, vih, vh, koh, len, t, lane, r);
 
@@ -336,53 +433,37 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
 
   // ---- stage the group's LUTs ----
   if (BUILD_LUT) {
-    // LUT[h][j][c] = lut_scale * sum_e q[h][8j+e] * kcb[j][c][e], e ascending,
-    // fp32.  The unit's q rows go to LDS as fp32 (in the tile buffers, unused
-    // until the tile loop).  Thread t scores codewords c = t % TPJ + TPJ*i of
-    // subspace j = t / TPJ against every head, so it reads its heads' q rows
-    // once; all of its codewords are requested at once (codewords past K
-    // repeat codeword K - 1 and land in LUT entries no code reads).
-    static_assert(kPqWaves * C::TILE >= kPqHeads * D * 4, "q rows fit in the tile buffers");
-    constexpr int NT = kPqWaves * 64, TPJ = NT / M, CPT = kPqKMax / TPJ;
-    static_assert(TPJ * M == NT && CPT * TPJ == kPqKMax, "threads per subspace");
+    // the unit's LUT entries on MFMA (see lut_a_operands): wave w builds
+    // subspace pair 2w, 2w + 1 (waves past M/2 idle); its codeword operands
+    // are requested before the scaled q rows are staged (in the tile buffers,
+    // unused until the tile loop)
+    static_assert(kPqWaves * C::TILE >= kPqHeads * D * 4 + kPqHeads * 4, "q rows fit in the tile buffers");
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
-    const int j = threadIdx.x / TPJ, c0 = threadIdx.x - j * TPJ;
-    u32x4 craw[CPT];
+    const int jp = min(2 * w, M - 2);
+    f16x4 bop[kPqKMax / 16];
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) craw[i] = ld16(cb + ((int64_t)j * K + min(c0 + TPJ * i, K - 1)) * 8);
+    for (int c16 = 0; c16 < kPqKMax / 16; ++c16) bop[c16] = lut_b_operand(cb, K, jp, c16 * 16, lane);
     float* qs = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB);
-    if (threadIdx.x < kPqHeads * M) {
-      const int h = threadIdx.x / M, jq = threadIdx.x - (threadIdx.x / M) * M;
-      const u32x4 qraw = ld16(a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + min(h, nh - 1)) * a.q_sh + jq * 8);
-      const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
-#pragma unroll
-      for (int x = 0; x < 8; ++x) qs[(h * M + jq) * 8 + x] = bf16_bits_to_f32(qh[x]);
-    }
+    float* mul = qs + kPqHeads * D;
+    if (w < kPqHeads) lut_store_q<D>(qrow, w, nh, a.lut_scale, qs, mul);
     __syncthreads();
-    f32x4 qv[kPqHeads][2];
+    if (2 * w < M) {
+      const int m = lane & 15, g = lane >> 4, hm = m & 7;
+      const bool on = (m >> 3) == (g >> 1) && hm < kPqHeads;
+      const f32x4 x = on ? *reinterpret_cast<const f32x4*>(qs + hm * D + 8 * (jp + (g >> 1)) + (g & 1) * 4)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+      f16x4 hi, lo;
+      lut_a_operands(x, hi, lo);
+      const bool use_lo = lut_need_lo(lo);
+      const float mul4[4] = {mul[0], mul[1], mul[2], mul[3]};
 #pragma unroll
-    for (int h = 0; h < kPqHeads; ++h) {
-      qv[h][0] = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8);
-      qv[h][1] = *reinterpret_cast<const f32x4*>(qs + (h * M + j) * 8 + 4);
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const _Float16* ch = reinterpret_cast<const _Float16*>(&craw[i]);
-      f32x4 e4;
-#pragma unroll
-      for (int h = 0; h < kPqHeads; ++h) {
-        float sum = 0.f;
-        sum += qv[h][0][0] * (float)ch[0];
-        sum += qv[h][0][1] * (float)ch[1];
-        sum += qv[h][0][2] * (float)ch[2];
-        sum += qv[h][0][3] * (float)ch[3];
-        sum += qv[h][1][0] * (float)ch[4];
-        sum += qv[h][1][1] * (float)ch[5];
-        sum += qv[h][1][2] * (float)ch[6];
-        sum += qv[h][1][3] * (float)ch[7];
-        e4[h] = sum * a.lut_scale;
+      for (int c16 = 0; c16 < kPqKMax / 16; ++c16) {
+        const f32x4 e = lut_mfma(hi, lo, use_lo, bop[c16]);
+        // lanes with g = 0 / 2 hold heads 0..3 of codeword c16 * 16 + m, subspace jp / jp + 1
+        if ((g & 1) == 0)
+          *reinterpret_cast<f32x4*>(lut + ((jp + (g >> 1)) * kPqKMax + c16 * 16 + m) * kPqHeads) =
+              f32x4{mul4[0] * e[0], mul4[1] * e[1], mul4[2] * e[2], mul4[3] * e[3]};
       }
-      *reinterpret_cast<f32x4*>(lut + (j * kPqKMax + c0 + TPJ * i) * kPqHeads) = e4;
     }
   } else {
     // the caller's LUTs, transposed so the heads of one (subspace, code) are
@@ -443,6 +524,301 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   }
   splitk_epilogue<D, kPqWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem_raw), a.o, unit, split, b, hq0, nh,
                                kDmapDense);
+}
+
+// ============================================================================
+// Grouped decode for quantized values (modes 0 and 3, G <= 8): a unit is
+// (b, kv head) with all G of its query heads, so every token's codes are read
+// once and its per-token work is shared by the whole group.  A workgroup takes
+// a chunk of <= kPqgChunk tokens; phases A and B reuse one LDS region:
+//   A. the unit's LUTs (fp32, [head quad][subspace][code][4 heads]: a code's
+//      entries for four heads are one 16-byte read, and a wave's reads of
+//      random codes spread over all 16 16-byte bank slots; built on MFMA from
+//      q and the key codebook, or the caller's LUT transposed) are resident;
+//      thread i scores token i of the chunk for every head, summing the M
+//      entries in subspace order, and stores the scores and the token's value
+//      codes;
+//   B. the value codebook replaces the LUTs.  The chunk's per-head maximum is
+//      known, so each wave turns its 32-token tiles straight into fp16
+//      probabilities (no running rescale), stored in MFMA operand order; then
+//      each wave accumulates two 16-column blocks of the output over a group
+//      of tiles (O^T += V^T P^T, the V operand read from the codebook by
+//      transposed LDS reads), the tile groups are added in group order, and
+//      each column block is written to the split's partial (or the output).
+// ============================================================================
+constexpr int kPqgThreads = kPqWaves * 64;
+constexpr int kPqgChunk = kPqgThreads;    // tokens per workgroup: one per thread in phase A
+
+template <int D, int HP>
+struct PqgCfg {
+  static constexpr int M = D / 8;
+  static constexpr int NT = kPqgChunk / kTile;                 // tiles per chunk
+  static constexpr int LUT = M * kPqKMax * HP * 4;             // A: fp32 LUTs [HP/4][M][256][4]
+  static constexpr int VCB = M * kPqKMax * 8 * 2;              // B: fp16 value codebook
+  static constexpr int PS = NT * 64 * 16;                      // B: fp16 probabilities, [tile][lane] x 8
+  static constexpr int A2 = (kPqWaves - D / 32) * 2 * 64 * 16;  // B: accumulators of tile groups past 0
+  static constexpr int X = LUT > VCB + PS + A2 ? LUT : VCB + PS + A2;
+  static constexpr int SC = HP * kPqgChunk * 4;                // scores [HP][chunk]
+  static constexpr int VC = kPqgChunk * M;                     // value codes [chunk][M]
+  static constexpr int HS = 16 * 4;                            // per-head multipliers, then maxima
+  static constexpr int LS = kPqWaves * 16 * 4;                 // per-wave probability sums
+  static constexpr int kSmem = X + SC + VC + HS + LS;
+  static_assert(HP * D * 4 <= SC, "q rows fit in the score area");
+};
+
+// M code bytes of one row (16 or 8 bytes, aligned).
+template <int M>
+__device__ __forceinline__ u32x4 ld_codes(const uint8_t* p) {
+  if constexpr (M == 16) {
+    return ld16(p);
+  } else {
+    const u32x2 h = *reinterpret_cast<const u32x2*>(p);
+    return u32x4{h[0], h[1], 0u, 0u};
+  }
+}
+
+template <int D, bool BUILD_LUT, int HP>
+__global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
+  using C = PqgCfg<D, HP>;
+  constexpr int M = D / 8;
+  __shared__ __attribute__((aligned(16))) char smem[C::kSmem];
+  float* lut = reinterpret_cast<float*>(smem);
+  char* vcb = smem;
+  f16x8* ps = reinterpret_cast<f16x8*>(smem + C::VCB);
+  float* sc = reinterpret_cast<float*>(smem + C::X);
+  uint8_t* vc = reinterpret_cast<uint8_t*>(smem + C::X + C::SC);
+  float* hsm = reinterpret_cast<float*>(smem + C::X + C::SC + C::VC);
+  float* lsum = hsm + 16;
+  f32x4* acc2 = reinterpret_cast<f32x4*>(smem + C::VCB + C::PS);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int unit, split;
+  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
+  const int b = unit / a.Hk, hk = unit - (unit / a.Hk) * a.Hk;
+  const int G = a.G, hq0 = hk * G, K = a.K;
+  const int len = pq_len(a, b);
+  const int t_begin = split * a.chunk;
+  const int n = max(0, min(a.chunk, len - t_begin));   // tokens of this chunk
+
+  // wave w's q row heads the queue; then this thread's token (clamped into
+  // the chunk), whose codes arrive while the LUTs are built or staged
+  LutQ<D> qrow;
+  if (BUILD_LUT && w < HP) qrow = lut_load_q<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, w, G);
+  u32x4 kc, vcd;
+  {
+    int blk, row;
+    pq_locate(a, b, t_begin + min(tid, max(n - 1, 0)), blk, row);
+    kc = ld_codes<M>(a.kidx + (int64_t)hk * a.ki_sh + (int64_t)blk * a.ki_sb + (int64_t)row * a.ki_ss);
+    vcd = ld_codes<M>(a.vidx + (int64_t)hk * a.vi_sh + (int64_t)blk * a.vi_sb + (int64_t)row * a.vi_ss);
+  }
+
+  // ---- phase A: the LUTs ----
+  if constexpr (BUILD_LUT) {
+    // LUT entries on MFMA (see lut_a_operands): wave w builds subspace pair
+    // 2w, 2w + 1 (waves past M/2 idle) for all HP heads (rows past G are
+    // zero); the scaled q rows are staged in the score area
+    const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
+    const int jp = min(2 * w, M - 2);
+    f16x4 bop[kPqKMax / 16];
+#pragma unroll
+    for (int c16 = 0; c16 < kPqKMax / 16; ++c16) bop[c16] = lut_b_operand(cb, K, jp, c16 * 16, lane);
+    float* qs = sc;
+    float* mul = hsm;
+    if (w < HP) lut_store_q<D>(qrow, w, G, a.lut_scale, qs, mul);
+    __syncthreads();
+    if (2 * w < M) {
+      const int m = lane & 15, g = lane >> 4, hm = m & 7;
+      const bool on = (m >> 3) == (g >> 1) && hm < HP;
+      const f32x4 x = on ? *reinterpret_cast<const f32x4*>(qs + hm * D + 8 * (jp + (g >> 1)) + (g & 1) * 4)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+      f16x4 hi, lo;
+      lut_a_operands(x, hi, lo);
+      const bool use_lo = lut_need_lo(lo);
+      const int quad = g & 1;
+      float mg[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mg[i] = mul[min(4 * quad + i, HP - 1)];
+#pragma unroll
+      for (int c16 = 0; c16 < kPqKMax / 16; ++c16) {
+        const f32x4 e = lut_mfma(hi, lo, use_lo, bop[c16]);
+        // lane (n, g) holds heads 4 * quad .. +3 of codeword c16 * 16 + n, subspace jp + g / 2
+        if (quad < HP / 4)
+          *reinterpret_cast<f32x4*>(lut + ((quad * M + jp + (g >> 1)) * kPqKMax + c16 * 16 + m) * 4) =
+              f32x4{mg[0] * e[0], mg[1] * e[1], mg[2] * e[2], mg[3] * e[3]};
+      }
+    }
+  } else {
+    // the caller's LUTs [B, Hq, M, K]: slot s = (j, c) of 256 per subspace,
+    // consecutive codes across lanes (each load instruction reads 256
+    // contiguous bytes of one head's row), all HP x M*256/threads loads in
+    // flight; codes past K repeat code K - 1, heads past G repeat head G - 1
+    constexpr int SPT = M * kPqKMax / kPqgThreads;
+    const float* lb = a.lut + (int64_t)b * a.l_sb + (int64_t)hq0 * a.l_sh;
+    float v[SPT][HP];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int sl = tid + kPqgThreads * i;
+      const int off = (sl >> 8) * K + min(sl & 255, K - 1);
+#pragma unroll
+      for (int h = 0; h < HP; ++h) v[i][h] = lb[(int64_t)min(h, G - 1) * a.l_sh + off];
+    }
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int sl = tid + kPqgThreads * i;
+#pragma unroll
+      for (int h4 = 0; h4 < HP / 4; ++h4)
+        *reinterpret_cast<f32x4*>(lut + ((h4 * M + (sl >> 8)) * kPqKMax + (sl & 255)) * 4) =
+            f32x4{v[i][4 * h4], v[i][4 * h4 + 1], v[i][4 * h4 + 2], v[i][4 * h4 + 3]};
+    }
+  }
+  // the value codebook, held in registers until phase B (requested after the
+  // LUT operands so it arrives during phase A): slot s = (j, c) of 256 per
+  // subspace (codewords past K repeat codeword K - 1; no code reads them)
+  constexpr int VPT = M * kPqKMax / kPqgThreads;
+  static_assert(VPT * kPqgThreads == M * kPqKMax, "codebook slots per thread");
+  const _Float16* vcbh = a.vcb + (int64_t)hk * a.vcb_sh;
+  u32x4 vraw[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int sl = tid + kPqgThreads * i;
+    vraw[i] = ld16(vcbh + (int64_t)((sl >> 8) * K + min(sl & 255, K - 1)) * 8);
+  }
+  __syncthreads();
+
+  // ---- phase A: scores of token tid, subspaces in order ----
+  {
+    float s[HP];
+#pragma unroll
+    for (int h = 0; h < HP; ++h) s[h] = 0.f;
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      const uint32_t code = (kc[j >> 2] >> ((j & 3) * 8)) & 0xFFu;
+#pragma unroll
+      for (int h4 = 0; h4 < HP / 4; ++h4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(lut + ((h4 * M + j) * kPqKMax + (int)code) * 4);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) s[4 * h4 + x] += v[x];
+      }
+    }
+    const bool live = tid < n;
+#pragma unroll
+    for (int h = 0; h < HP; ++h) sc[h * kPqgChunk + tid] = live ? s[h] : kNegInf;
+    if constexpr (M == 16) {
+      *reinterpret_cast<u32x4*>(vc + tid * M) = vcd;
+    } else {
+      *reinterpret_cast<u32x2*>(vc + tid * M) = u32x2{vcd[0], vcd[1]};
+    }
+  }
+  __syncthreads();
+
+  // ---- phase B: the value codebook over the LUTs; per-head chunk maxima ----
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) *reinterpret_cast<u32x4*>(vcb + (tid + kPqgThreads * i) * 16) = vraw[i];
+  if (w < HP) {
+    float m = kNegInf;
+#pragma unroll
+    for (int i = 0; i < kPqgChunk / 64; ++i) m = fmaxf(m, sc[w * kPqgChunk + lane + 64 * i] * a.scale_log2);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, shfl_xor_f(m, o));
+    if (lane == 0) hsm[w] = m;
+  }
+  __syncthreads();
+
+  // B0: fp16 probabilities of tiles w, w + 8 in P^T operand order (head l16,
+  // tokens t0 + blk*16 + lg*4 + i at position blk*4 + i); tokens past n have
+  // score -inf and so probability zero
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int hh = l16 < HP ? l16 : 0;
+  const bool col = l16 < G;
+  const float m_run = hsm[hh];
+  const float m_use = m_run == kNegInf ? 0.f : m_run;
+  constexpr int NT = C::NT;
+  {
+    float l_part = 0.f;
+#pragma unroll
+    for (int tile = w; tile < NT; tile += kPqWaves) {
+      f16x8 ph;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc + hh * kPqgChunk + tile * kTile + blk * 16 + lg * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = col ? fast_exp2(s4[i] * a.scale_log2 - m_use) : 0.f;
+          l_part += p;
+          ph[blk * 4 + i] = (_Float16)p;
+        }
+      }
+      ps[tile * 64 + lane] = ph;
+    }
+    l_part += shfl_xor_f(l_part, 16);
+    l_part += shfl_xor_f(l_part, 32);
+    if (lg == 0) lsum[w * 16 + l16] = l_part;
+  }
+  __syncthreads();
+
+  // B1: wave w accumulates output column blocks db = 2*dp, 2*dp + 1
+  // (dp = w % DP) over tiles tq, tq + TS, .. (tq = w / DP); for block db
+  // the lane supplies V rows of codeword subspace 2*db + (l16 & 3) / 2 to the
+  // transposed reads (columns db*16 + (l16 & 3)*4 .. +3); both subspaces'
+  // codes sit in byte 2*e + (l16 & 3) / 2 of value-code word dp
+  constexpr int DP = D / 32, TS = kPqWaves / DP;
+  const int dp = w % DP, tq = w / DP;
+  const int sub = (l16 & 3) >> 1;
+  const char* vb0 = vcb + ((4 * dp + sub) * kPqKMax * 8 + (l16 & 1) * 4) * 2;
+  const char* vb1 = vb0 + 2 * kPqKMax * 8 * 2;
+  const uint8_t* vcw = vc + dp * 4;
+  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int k = 0; k < NT / TS; ++k) {
+    const int tile = tq + k * TS;
+    const f16x8 ph = ps[tile * 64 + lane];
+    u32x2 hv[2][2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = tile * kTile + hf * 16 + lg * 4 + (l16 >> 2);
+      const uint32_t word = *reinterpret_cast<const uint32_t*>(vcw + row * M);
+      hv[0][hf] = tr16(vb0 + ((word >> (8 * sub)) & 0xFFu) * 16);
+      hv[1][hf] = tr16(vb1 + ((word >> (8 * (2 + sub))) & 0xFFu) * 16);
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const u32x4 raw = {hv[e][0][0], hv[e][0][1], hv[e][1][0], hv[e][1][1]};
+      acc[e] = mfma_f16(__builtin_bit_cast(f16x8, raw), ph, acc[e]);
+    }
+  }
+  // the tile groups' sums join group 0's, in group order
+  if (tq > 0) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) acc2[(((tq - 1) * DP + dp) * 2 + e) * 64 + lane] = acc[e];
+  }
+  __syncthreads();
+
+  // B2: acc[e][i] = O^T[d = (2*dp + e)*16 + lg*4 + i][head l16]; the head's
+  // sum over the waves' probability sums, in wave order
+  if (tq == 0 && col) {
+#pragma unroll
+    for (int t2 = 1; t2 < TS; ++t2)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) acc[e] += acc2[(((t2 - 1) * DP + dp) * 2 + e) * 64 + lane];
+    float L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kPqWaves; ++ww) L += lsum[ww * 16 + l16];
+    const SplitKOut& o = a.o;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int d0 = (2 * dp + e) * 16 + lg * 4;
+      if (o.nsplit <= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out(o, b, hq0 + l16, d0 + i, acc[e][i] / L);
+      } else {
+        const size_t r = ((size_t)unit * 16 + l16) * o.nsplit + split;
+        *reinterpret_cast<f32x4*>(o.part_acc + r * D + d0) = acc[e];
+        if (dp == 0 && e == 0 && lg == 0) {
+          o.part_ml[r * 2 + 0] = m_run;
+          o.part_ml[r * 2 + 1] = L;
+        }
+      }
+    }
+  }
 }
 
 // ============================================================================
@@ -529,26 +905,85 @@ static void pq_plan(int S, long units, int chunk_req, int* chunk, int* ns) {
   *ns = (S + c - 1) / c;
 }
 
+// Plan of the grouped kernel (units = B * Hk): chunks of <= kPqgChunk tokens,
+// a multiple of the 32-token tile, sized to fill the CUs once; false where it
+// does not apply (G > 8, a requested chunk above kPqgChunk, too many splits).
+static bool pq_group_plan(int G, int S, long units, int chunk_req, int* chunk, int* ns) {
+  if (G > 8) return false;
+  long c;
+  if (chunk_req > 0) {
+    if (chunk_req > kPqgChunk) return false;
+    c = chunk_req;
+  } else {
+    const long target = device_cu_count();
+    c = ((long)S * units + target - 1) / target;
+  }
+  c = (c + kTile - 1) / kTile * kTile;
+  if (c > kPqgChunk) c = kPqgChunk;
+  *chunk = (int)c;
+  *ns = (int)((S + c - 1) / c);
+  return *ns <= 1024;
+}
+
 // ============================================================================
-// LUT build: lut[b, h, j, c] = scale * sum_e q[b, h, 8j+e] * cb[h/G][j][c][e]
+// LUT build: lut[b, h, j, c] = scale * q[b, h, 8j..8j+7] . cb[h/G][j][c], the
+// entries of the MFMA contract above.  One wave per (b, kv head, block of 8
+// query heads of its group, subspace pair): lane l finds the largest |q| of
+// head l % 8 over an eighth of its row, then one MFMA (two where a lo part is
+// nonzero) per 16 codewords.
 // ============================================================================
-__global__ void pq_lut_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh, const _Float16* cb, int64_t cb_sh,
-                              int Hq, int G, int M, int K, float scale, float* lut) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t per_b = (int64_t)Hq * M * K;
-  const int b = blockIdx.y;
-  if (gid >= per_b) return;
-  const int h = (int)(gid / (M * K));
-  const int r = (int)(gid - (int64_t)h * M * K);
-  const int j = r / K, c = r - (r / K) * K;
-  const u32x4 qraw = ld16(q + (int64_t)b * q_sb + (int64_t)h * q_sh + j * 8);
-  const u32x4 craw = ld16(cb + (int64_t)(h / G) * cb_sh + ((int64_t)j * K + c) * 8);
-  const uint16_t* qh = reinterpret_cast<const uint16_t*>(&qraw);
-  const _Float16* ch = reinterpret_cast<const _Float16*>(&craw);
-  float sum = 0.f;
+__global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh, const _Float16* cb,
+                                                    int64_t cb_sh, int Hk, int G, int HB, int M, int K, float scale,
+                                                    float* lut) {
+  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
+  const int MP = (M + 1) / 2;
+  int r = blockIdx.x;
+  const int jp = 2 * (r % MP);
+  r /= MP;
+  const int hb = r % HB;
+  r /= HB;
+  const int hk = r % Hk, b = r / Hk;
+  const int D = M * 8;
+  const int h0 = hb * 8, nh = min(8, G - h0);
+  const uint16_t* qb = q + (int64_t)b * q_sb + (int64_t)(hk * G + h0) * q_sh;
+  // head l % 8 (clamped to the block): the largest |q| over dims (l / 8) * D/8 .. +D/8
+  const int ha = min(lane & 7, nh - 1);
+  float amax = 0.f;
+  for (int d = (lane >> 3) * M; d < ((lane >> 3) + 1) * M; ++d)
+    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(qb[(int64_t)ha * q_sh + d])));
+  amax = fmaxf(amax, shfl_xor_f(amax, 8));
+  amax = fmaxf(amax, shfl_xor_f(amax, 16));
+  amax = fmaxf(amax, shfl_xor_f(amax, 32));
+  const int k_own = lut_shift(amax);                     // of head l % 8
+  const float mul_own = (lane & 7) < nh ? ldexpf(scale, k_own) : 0.f;
+  // A operand: row m is head m % 8 against subspace jp + m / 8
+  const int hm = m & 7, jj = jp + (g >> 1);
+  const int k_m = __shfl(k_own, hm, 64);
+  const bool on = (m >> 3) == (g >> 1) && hm < nh && jj < M;
+  f32x4 x;
 #pragma unroll
-  for (int x = 0; x < 8; ++x) sum += bf16_bits_to_f32(qh[x]) * (float)ch[x];
-  lut[(int64_t)b * per_b + gid] = sum * scale;
+  for (int i = 0; i < 4; ++i)
+    x[i] = on ? ldexpf(bf16_bits_to_f32(qb[(int64_t)hm * q_sh + 8 * jj + (g & 1) * 4 + i]), -k_m) : 0.f;
+  f16x4 hi, lo;
+  lut_a_operands(x, hi, lo);
+  const bool use_lo = lut_need_lo(lo);
+  float mg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) mg[i] = __shfl(mul_own, (g & 1) * 4 + i, 64);
+  // subspace jp + 1 past M (odd M) reads subspace M - 1; its entries are not stored
+  const _Float16* cbh = cb + (int64_t)hk * cb_sh - (jp + 1 < M ? 0 : (int64_t)K * 8 * (lane >> 5));
+  const int64_t Hq = (int64_t)Hk * G;
+  float* lb = lut + ((int64_t)b * Hq + hk * G + h0) * M * K + (int64_t)jj * K;
+  const int ncb = (K + 15) / 16;
+  for (int c16 = 0; c16 < ncb; ++c16) {
+    const f32x4 e = lut_mfma(hi, lo, use_lo, lut_b_operand(cbh, K, jp, c16 * 16, lane));
+    const int c = c16 * 16 + m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = (g & 1) * 4 + i;
+      if (h < nh && jj < M && c < K) lb[(int64_t)h * M * K + c] = mg[i] * e[i];
+    }
+  }
 }
 
 // ============================================================================
@@ -667,6 +1102,11 @@ int bytes_pq_decode_workspace_size(int B, int Hq, int Hk, int S, int D, int chun
   int chunk, ns;
   pq_plan(S, units, chunk_req, &chunk, &ns);
   *bytes = splitk_workspace_bytes(units, ns, D);
+  // the grouped kernel's plan (quantized-value modes) may need more
+  if (pq_group_plan(G, S, (long)B * Hk, chunk_req, &chunk, &ns)) {
+    const size_t g = splitk_workspace_bytes((long)B * Hk, ns, D);
+    if (g > *bytes) *bytes = g;
+  }
   return 0;
 }
 
@@ -678,19 +1118,45 @@ static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S
                      size_t workspace_bytes, void* stream) {
   a.Hk = Hk; a.G = Hq / Hk; a.HG = (a.G + kPqHeads - 1) / kPqHeads; a.S = S; a.K = K;
   a.scale_log2 = scale * kLog2e;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  a.o.out = out;
+  a.o.out_dtype = out_dtype;
+  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
+  {
+    // quantized values and G <= 8: one unit per (b, kv head)
+    const long gunits = (long)B * Hk;
+    int gns;
+    if ((mode == 0 || mode == 3) && a.C == 0 && gunits <= kMaxUnits &&
+        pq_group_plan(a.G, S, gunits, chunk_req, &a.chunk, &gns)) {
+      if (!workspace || workspace_bytes < splitk_workspace_bytes(gunits, gns, D)) return (int)hipErrorInvalidValue;
+      a.o.Hk = Hk; a.o.HB = 1; a.o.G = a.G; a.o.hbs = a.G;
+      splitk_carve(workspace, gunits, gns, a.o);
+      const dim3 grid((unsigned)(gns * gunits)), block(kPqgThreads);
+#define PQG_LAUNCH(DD, BL, HP) BYTES_LAUNCH(kProfPq, (pq_group_kernel<DD, BL, HP>), grid, block, 0, st, a)
+#define PQG_HP(DD, BL)            \
+  if (a.G <= 4) PQG_LAUNCH(DD, BL, 4); \
+  else PQG_LAUNCH(DD, BL, 8);
+      if (D == 128) {
+        if (mode == 3) { PQG_HP(128, true) } else { PQG_HP(128, false) }
+      } else {
+        if (mode == 3) { PQG_HP(64, true) } else { PQG_HP(64, false) }
+      }
+#undef PQG_HP
+#undef PQG_LAUNCH
+      const int rc = (int)hipGetLastError();
+      if (rc) return rc;
+      return splitk_combine(a.o, gunits, D, st);
+    }
+  }
   const long units = (long)B * Hk * a.HG;
   if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
   int ns;
   pq_plan(S, units, chunk_req, &a.chunk, &ns);
   if (ns > 1024) return (int)hipErrorInvalidConfiguration;
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
-  a.o.out = out;
-  a.o.out_dtype = out_dtype;
-  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
   // the merge kernel maps unit -> (b, hk, head group of kPqHeads)
   a.o.Hk = Hk; a.o.HB = a.HG; a.o.G = a.G; a.o.hbs = kPqHeads;
   splitk_carve(workspace, units, ns, a.o);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((unsigned)(ns * units)), block(kPqWaves * 64);
   const bool outl = a.C > 0;
 #define PQ_LAUNCH(DD, BL, QQ, F8, OU) BYTES_LAUNCH(kProfPq, (pq_decode_kernel<DD, BL, QQ, F8, OU>), grid, block, 0, st, a)
@@ -853,14 +1319,12 @@ int bytes_pq_build_lut(const void* q, const void* cb, void* lut, int B, int Hq, 
                        int64_t q_sh, int64_t cb_sh, float scale, void* stream) {
   if (!q || !cb || !lut || B <= 0 || Hk <= 0 || Hq % Hk != 0 || D % 8 != 0 || K <= 0 || K > kPqKMax)
     return (int)hipErrorInvalidValue;
-  if (B > 65535) return (int)hipErrorInvalidConfiguration;
-  const int M = D / 8;
-  const int64_t per_b = (int64_t)Hq * M * K;
-  const int th = 256;
-  dim3 grid((unsigned)((per_b + th - 1) / th), (unsigned)B);
-  hipLaunchKernelGGL(pq_lut_kernel, grid, dim3(th), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(q), q_sb, q_sh, static_cast<const _Float16*>(cb), cb_sh, Hq,
-                     Hq / Hk, M, K, scale, static_cast<float*>(lut));
+  const int M = D / 8, G = Hq / Hk, HB = (G + 7) / 8;
+  const int64_t waves = (int64_t)B * Hk * HB * ((M + 1) / 2);
+  if (waves > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(pq_lut_kernel, dim3((unsigned)waves), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(q), q_sb, q_sh, static_cast<const _Float16*>(cb), cb_sh, Hk, G, HB,
+                     M, K, scale, static_cast<float*>(lut));
   return (int)hipGetLastError();
 }
 

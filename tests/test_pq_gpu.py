@@ -113,6 +113,31 @@ def test_lut_kv_split_counts(dev, chunk):
     _check(out, R.decode_attn_pq_lut_kv(lut, k_idx, v_idx, vcb), f"lut_kv chunk {chunk}")
 
 
+@pytest.mark.parametrize("G,S,D,chunk", [(1, 777, 128, 0), (2, 2049, 64, 0), (3, 100, 128, 0), (5, 4100, 128, 64),
+                                         (8, 1500, 128, 0), (7, 5000, 128, 512), (7, 5000, 128, 544),
+                                         (9, 1200, 128, 0), (16, 640, 64, 0)])
+def test_lut_kv_group_sizes(dev, G, S, D, chunk):
+    """Query groups of 1..16 heads per KV head, quantized values: all G heads
+    in one workgroup (G <= 8, chunks of <= 512 tokens) or groups of four
+    (G > 8, or a longer chunk), against the oracle; the LUT built inside the
+    kernel gives the caller-LUT result bit for bit."""
+    B, Hk, K = 2, 2, 256
+    M = D // 8
+    g = torch.Generator().manual_seed(G * 1000 + S)
+    q = torch.randn(B, Hk * G, 1, D, generator=g).to(torch.bfloat16)
+    kcb, vcb = _rand_cb((Hk, M, K, 8), S + 5), _rand_cb((Hk, M, K, 8), S + 6)
+    k_idx = torch.randint(0, K, (B, Hk, S, M), generator=g).to(torch.uint8)
+    v_idx = torch.randint(0, K, (B, Hk, S, M), generator=g).to(torch.uint8)
+    d = {n: t.to(dev) for n, t in dict(q=q, kcb=kcb, vcb=vcb, k_idx=k_idx, v_idx=v_idx).items()}
+    scale = D ** -0.5
+    lut = PQ.pq_build_lut(d["q"], d["kcb"], scale)
+    two = PQ.decode_attn_pq_lut_kv(lut, d["k_idx"], d["v_idx"], d["vcb"], chunk=chunk)
+    fused = PQ.decode_attn_pq_kv_fused(d["q"], d["kcb"], d["k_idx"], d["v_idx"], d["vcb"], scale, chunk=chunk)
+    assert torch.equal(fused, two)
+    _check(two, R.decode_attn_pq_lut_kv(R.pq_build_lut(q, kcb, scale), k_idx, v_idx, vcb),
+           f"lut_kv G{G} S{S} D{D} chunk {chunk}")
+
+
 def test_c3_full(dev):
     """BASELINE C3: B1 Hq28 Hkv4 D128 L32768, 16 x 8-dim subspaces, 256 fp16 codewords per head."""
     x = W.c3_pq(seed=0, device=dev)
