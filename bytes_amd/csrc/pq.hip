@@ -101,56 +101,70 @@ __device__ __forceinline__ int pq_len(const PqArgs& a, int b) {
 // build their own) computes
 //   lut[h][j][c] = (lut_scale * 2^k_h) * dot(q_h[8j .. 8j+7] * 2^-k_h, cb[j][c])
 // where k_h = max(0, e_h - 15) for the head's largest |q| = 1.x * 2^e_h (the
-// scaled row then fits fp16), and dot comes from v_mfma_f32_16x16x16_f16 on
-// a block-diagonal pair of subspaces (j even, j + 1): rows 0-7 are heads
-// against subspace j in k-slots 0-7, rows 8-15 the same heads against
-// subspace j + 1 in slots 8-15, columns are 16 consecutive codewords, so each
-// codeword byte is read once.  The A operand is hi = fp16(q'); a second MFMA
-// accumulates lo = fp16(q' - hi) where any lane of the wave has a nonzero lo
-// part (it adds exact zeros otherwise, so skipping it changes nothing).
-// Every product is exact (fp16 x fp16), q' = hi + lo exactly for
-// |q'| >= 2^-17, and an entry depends only on its own head's q row and the
-// slot its subspace takes: any grouping of heads gives the same bits.
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+// scaled row then fits fp16), and dot comes from v_mfma_f32_32x32x16_f16 on
+// a block-diagonal pair of subspaces (j even, j + 1): rows 0-7 are up to 8
+// heads against subspace j in k-slots 0-7, rows 16-23 the same heads against
+// subspace j + 1 in slots 8-15 (other rows zero), and columns are 32
+// consecutive codewords, so each lane reads one whole 16-byte codeword.  The
+// A operand is hi = fp16(q'); a second MFMA accumulates lo = fp16(q' - hi)
+// where any lane of the wave has a nonzero lo part (it adds exact zeros
+// otherwise, so skipping it changes nothing).  Every product is exact
+// (fp16 x fp16), q' = hi + lo exactly for |q'| >= 2^-17, and an entry depends
+// only on its own head's q row and the slots its subspace takes: any grouping
+// of heads gives the same bits.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int lut_shift(float amax) {
   const int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127;
   return (e >= 16 && e < 128) ? e - 15 : 0;
 }
 
-// hi and lo A operands of lane (m, g) for subspace pair (j, j + 1): x = the
-// scaled q values of dims (g & 1) * 4 .. +3 of subspace j + (g >> 1) of head
-// m % 8, taken where the lane's row block matches its slot block (m / 8 ==
-// g / 2) and zero elsewhere (the caller passes zeros for such lanes).
-__device__ __forceinline__ void lut_a_operands(f32x4 x, f16x4& hi, f16x4& lo) {
+// Row and slot block of lane l's A operand: row m = l % 32 (head m % 16 of
+// subspace j + m / 16 when m % 16 < 8), slots 8 * (l / 32) .. +7.  The lane
+// holds values only where its row block matches its slot block.
+__device__ __forceinline__ bool lut_a_live(int lane, int* head, int* sub) {
+  const int m = lane & 31;
+  *head = m & 15;
+  *sub = m >> 4;
+  return (m & 15) < 8 && (m >> 4) == (lane >> 5);
+}
+
+// hi and lo parts of eight scaled q values (zero where !live).
+__device__ __forceinline__ void lut_a_operands(const float* x, bool live, f16x8& hi, f16x8& lo) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const _Float16 h = (_Float16)x[i];
+  for (int i = 0; i < 8; ++i) {
+    const float v = live ? x[i] : 0.f;
+    const _Float16 h = (_Float16)v;
     hi[i] = h;
-    lo[i] = (_Float16)(x[i] - (float)h);
+    lo[i] = (_Float16)(v - (float)h);
   }
 }
 
-// B operand of codewords c0 .. c0+15 for subspace pair (j, j + 1): lane
-// (n = lane % 16, g = lane / 16) holds dims (g & 1) * 4 .. +3 of codeword
-// c0 + n of subspace j + (g >> 1) (codewords past K repeat codeword K - 1).
-__device__ __forceinline__ f16x4 lut_b_operand(const _Float16* cb, int K, int j, int c0, int lane) {
-  const int c = min(c0 + (lane & 15), K - 1);
-  const int jj = j + (lane >> 5);
-  return *reinterpret_cast<const f16x4*>(cb + ((int64_t)jj * K + c) * 8 + ((lane >> 4) & 1) * 4);
+// B operand of codewords c0 .. c0+31 for subspace pair (j, j + 1): lane l
+// holds codeword c0 + l % 32 of subspace j + l / 32 (codewords past K repeat
+// codeword K - 1).
+__device__ __forceinline__ f16x8 lut_b_operand(const _Float16* cb, int K, int j, int c0, int lane) {
+  const int c = min(c0 + (lane & 31), K - 1);
+  return __builtin_bit_cast(f16x8, ld16(cb + ((int64_t)(j + (lane >> 5)) * K + c) * 8));
 }
 
-// Entries of one subspace pair and 16 codewords: lane (n, g) receives heads
-// (g & 1) * 4 .. +3 of codeword c0 + n, subspace j + (g >> 1).
-__device__ __forceinline__ f32x4 lut_mfma(f16x4 hi, f16x4 lo, bool use_lo, f16x4 b) {
-  f32x4 e = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-  if (use_lo) e = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, b, e, 0, 0, 0);
+// Entries of one subspace pair and 32 codewords: lane l receives heads
+// 4 * (l / 32) + i of codeword c0 + l % 32 in e[i] (subspace j) and e[8 + i]
+// (subspace j + 1), i = 0..3.
+__device__ __forceinline__ f32x16 lut_mfma(f16x8 hi, f16x8 lo, bool use_lo, f16x8 b) {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  f32x16 e = __builtin_amdgcn_mfma_f32_32x32x16_f16(hi, b, z, 0, 0, 0);
+  if (use_lo) e = __builtin_amdgcn_mfma_f32_32x32x16_f16(lo, b, e, 0, 0, 0);
   return e;
 }
 
 // True where any lane of the wave holds a nonzero lo part (wave-uniform).
-__device__ __forceinline__ bool lut_need_lo(f16x4 lo) {
-  const bool nz = (float)lo[0] != 0.f || (float)lo[1] != 0.f || (float)lo[2] != 0.f || (float)lo[3] != 0.f;
+__device__ __forceinline__ bool lut_need_lo(const f16x8& lo) {
+  bool nz = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) nz = nz || (float)lo[i] != 0.f;
   return __ballot(nz) != 0;
 }
 
@@ -433,36 +447,38 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
 
   // ---- stage the group's LUTs ----
   if (BUILD_LUT) {
-    // the unit's LUT entries on MFMA (see lut_a_operands): wave w builds
+    // the unit's LUT entries on MFMA (see lut_a_live): wave w builds
     // subspace pair 2w, 2w + 1 (waves past M/2 idle); its codeword operands
     // are requested before the scaled q rows are staged (in the tile buffers,
     // unused until the tile loop)
     static_assert(kPqWaves * C::TILE >= kPqHeads * D * 4 + kPqHeads * 4, "q rows fit in the tile buffers");
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
     const int jp = min(2 * w, M - 2);
-    f16x4 bop[kPqKMax / 16];
+    f16x8 bop[kPqKMax / 32];
 #pragma unroll
-    for (int c16 = 0; c16 < kPqKMax / 16; ++c16) bop[c16] = lut_b_operand(cb, K, jp, c16 * 16, lane);
+    for (int c32 = 0; c32 < kPqKMax / 32; ++c32) bop[c32] = lut_b_operand(cb, K, jp, c32 * 32, lane);
     float* qs = reinterpret_cast<float*>(smem_raw + C::LUT + C::VCB);
     float* mul = qs + kPqHeads * D;
     if (w < kPqHeads) lut_store_q<D>(qrow, w, nh, a.lut_scale, qs, mul);
     __syncthreads();
     if (2 * w < M) {
-      const int m = lane & 15, g = lane >> 4, hm = m & 7;
-      const bool on = (m >> 3) == (g >> 1) && hm < kPqHeads;
-      const f32x4 x = on ? *reinterpret_cast<const f32x4*>(qs + hm * D + 8 * (jp + (g >> 1)) + (g & 1) * 4)
-                         : f32x4{0.f, 0.f, 0.f, 0.f};
-      f16x4 hi, lo;
-      lut_a_operands(x, hi, lo);
+      int hm, sub;
+      const bool live = lut_a_live(lane, &hm, &sub) && hm < kPqHeads;
+      f16x8 hi, lo;
+      lut_a_operands(qs + min(hm, kPqHeads - 1) * D + 8 * (jp + sub), live, hi, lo);
       const bool use_lo = lut_need_lo(lo);
       const float mul4[4] = {mul[0], mul[1], mul[2], mul[3]};
+      const int n = lane & 31;
 #pragma unroll
-      for (int c16 = 0; c16 < kPqKMax / 16; ++c16) {
-        const f32x4 e = lut_mfma(hi, lo, use_lo, bop[c16]);
-        // lanes with g = 0 / 2 hold heads 0..3 of codeword c16 * 16 + m, subspace jp / jp + 1
-        if ((g & 1) == 0)
-          *reinterpret_cast<f32x4*>(lut + ((jp + (g >> 1)) * kPqKMax + c16 * 16 + m) * kPqHeads) =
-              f32x4{mul4[0] * e[0], mul4[1] * e[1], mul4[2] * e[2], mul4[3] * e[3]};
+      for (int c32 = 0; c32 < kPqKMax / 32; ++c32) {
+        const f32x16 e = lut_mfma(hi, lo, use_lo, bop[c32]);
+        // lanes 0..31 hold heads 0..3 of codeword c32 * 32 + n for subspaces jp, jp + 1
+        if (lane < 32) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2)
+            *reinterpret_cast<f32x4*>(lut + ((jp + s2) * kPqKMax + c32 * 32 + n) * kPqHeads) =
+                f32x4{mul4[0] * e[8 * s2], mul4[1] * e[8 * s2 + 1], mul4[2] * e[8 * s2 + 2], mul4[3] * e[8 * s2 + 3]};
+        }
       }
     }
   } else {
@@ -613,37 +629,38 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
 
   // ---- phase A: the LUTs ----
   if constexpr (BUILD_LUT) {
-    // LUT entries on MFMA (see lut_a_operands): wave w builds subspace pair
+    // LUT entries on MFMA (see lut_a_live): wave w builds subspace pair
     // 2w, 2w + 1 (waves past M/2 idle) for all HP heads (rows past G are
     // zero); the scaled q rows are staged in the score area
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
     const int jp = min(2 * w, M - 2);
-    f16x4 bop[kPqKMax / 16];
+    f16x8 bop[kPqKMax / 32];
 #pragma unroll
-    for (int c16 = 0; c16 < kPqKMax / 16; ++c16) bop[c16] = lut_b_operand(cb, K, jp, c16 * 16, lane);
+    for (int c32 = 0; c32 < kPqKMax / 32; ++c32) bop[c32] = lut_b_operand(cb, K, jp, c32 * 32, lane);
     float* qs = sc;
     float* mul = hsm;
     if (w < HP) lut_store_q<D>(qrow, w, G, a.lut_scale, qs, mul);
     __syncthreads();
     if (2 * w < M) {
-      const int m = lane & 15, g = lane >> 4, hm = m & 7;
-      const bool on = (m >> 3) == (g >> 1) && hm < HP;
-      const f32x4 x = on ? *reinterpret_cast<const f32x4*>(qs + hm * D + 8 * (jp + (g >> 1)) + (g & 1) * 4)
-                         : f32x4{0.f, 0.f, 0.f, 0.f};
-      f16x4 hi, lo;
-      lut_a_operands(x, hi, lo);
+      int hm, sub;
+      const bool live = lut_a_live(lane, &hm, &sub) && hm < HP;
+      f16x8 hi, lo;
+      lut_a_operands(qs + min(hm, HP - 1) * D + 8 * (jp + sub), live, hi, lo);
       const bool use_lo = lut_need_lo(lo);
-      const int quad = g & 1;
+      const int quad = lane >> 5, n = lane & 31;
       float mg[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) mg[i] = mul[min(4 * quad + i, HP - 1)];
 #pragma unroll
-      for (int c16 = 0; c16 < kPqKMax / 16; ++c16) {
-        const f32x4 e = lut_mfma(hi, lo, use_lo, bop[c16]);
-        // lane (n, g) holds heads 4 * quad .. +3 of codeword c16 * 16 + n, subspace jp + g / 2
-        if (quad < HP / 4)
-          *reinterpret_cast<f32x4*>(lut + ((quad * M + jp + (g >> 1)) * kPqKMax + c16 * 16 + m) * 4) =
-              f32x4{mg[0] * e[0], mg[1] * e[1], mg[2] * e[2], mg[3] * e[3]};
+      for (int c32 = 0; c32 < kPqKMax / 32; ++c32) {
+        const f32x16 e = lut_mfma(hi, lo, use_lo, bop[c32]);
+        // lane l holds heads 4 * quad .. +3 of codeword c32 * 32 + n for subspaces jp, jp + 1
+        if (quad < HP / 4) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2)
+            *reinterpret_cast<f32x4*>(lut + ((quad * M + jp + s2) * kPqKMax + c32 * 32 + n) * 4) =
+                f32x4{mg[0] * e[8 * s2], mg[1] * e[8 * s2 + 1], mg[2] * e[8 * s2 + 2], mg[3] * e[8 * s2 + 3]};
+        }
       }
     }
   } else {
@@ -930,12 +947,12 @@ static bool pq_group_plan(int G, int S, long units, int chunk_req, int* chunk, i
 // entries of the MFMA contract above.  One wave per (b, kv head, block of 8
 // query heads of its group, subspace pair): lane l finds the largest |q| of
 // head l % 8 over an eighth of its row, then one MFMA (two where a lo part is
-// nonzero) per 16 codewords.
+// nonzero) per 32 codewords.
 // ============================================================================
 __global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh, const _Float16* cb,
                                                     int64_t cb_sh, int Hk, int G, int HB, int M, int K, float scale,
                                                     float* lut) {
-  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x;
   const int MP = (M + 1) / 2;
   int r = blockIdx.x;
   const int jp = 2 * (r % MP);
@@ -943,10 +960,9 @@ __global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* q, int64_t q
   const int hb = r % HB;
   r /= HB;
   const int hk = r % Hk, b = r / Hk;
-  const int D = M * 8;
   const int h0 = hb * 8, nh = min(8, G - h0);
   const uint16_t* qb = q + (int64_t)b * q_sb + (int64_t)(hk * G + h0) * q_sh;
-  // head l % 8 (clamped to the block): the largest |q| over dims (l / 8) * D/8 .. +D/8
+  // head l % 8 (clamped to the block): the largest |q| over dims (l / 8) * M .. +M
   const int ha = min(lane & 7, nh - 1);
   float amax = 0.f;
   for (int d = (lane >> 3) * M; d < ((lane >> 3) + 1) * M; ++d)
@@ -956,33 +972,35 @@ __global__ __launch_bounds__(64) void pq_lut_kernel(const uint16_t* q, int64_t q
   amax = fmaxf(amax, shfl_xor_f(amax, 32));
   const int k_own = lut_shift(amax);                     // of head l % 8
   const float mul_own = (lane & 7) < nh ? ldexpf(scale, k_own) : 0.f;
-  // A operand: row m is head m % 8 against subspace jp + m / 8
-  const int hm = m & 7, jj = jp + (g >> 1);
-  const int k_m = __shfl(k_own, hm, 64);
-  const bool on = (m >> 3) == (g >> 1) && hm < nh && jj < M;
-  f32x4 x;
+  int hm, sub;
+  const bool live = lut_a_live(lane, &hm, &sub) && hm < nh && jp + sub < M;
+  const int k_m = __shfl(k_own, hm & 7, 64);
+  float x[8];
+  const uint16_t* qr = qb + (int64_t)min(hm, nh - 1) * q_sh + 8 * min(jp + sub, M - 1);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    x[i] = on ? ldexpf(bf16_bits_to_f32(qb[(int64_t)hm * q_sh + 8 * jj + (g & 1) * 4 + i]), -k_m) : 0.f;
-  f16x4 hi, lo;
-  lut_a_operands(x, hi, lo);
+  for (int i = 0; i < 8; ++i) x[i] = ldexpf(bf16_bits_to_f32(qr[i]), -k_m);
+  f16x8 hi, lo;
+  lut_a_operands(x, live, hi, lo);
   const bool use_lo = lut_need_lo(lo);
+  const int quad = lane >> 5, n = lane & 31;
   float mg[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) mg[i] = __shfl(mul_own, (g & 1) * 4 + i, 64);
+  for (int i = 0; i < 4; ++i) mg[i] = __shfl(mul_own, 4 * quad + i, 64);
   // subspace jp + 1 past M (odd M) reads subspace M - 1; its entries are not stored
   const _Float16* cbh = cb + (int64_t)hk * cb_sh - (jp + 1 < M ? 0 : (int64_t)K * 8 * (lane >> 5));
   const int64_t Hq = (int64_t)Hk * G;
-  float* lb = lut + ((int64_t)b * Hq + hk * G + h0) * M * K + (int64_t)jj * K;
-  const int ncb = (K + 15) / 16;
-  for (int c16 = 0; c16 < ncb; ++c16) {
-    const f32x4 e = lut_mfma(hi, lo, use_lo, lut_b_operand(cbh, K, jp, c16 * 16, lane));
-    const int c = c16 * 16 + m;
+  float* lb = lut + ((int64_t)b * Hq + hk * G + h0) * M * K;
+  const int ncb = (K + 31) / 32;
+  for (int c32 = 0; c32 < ncb; ++c32) {
+    const f32x16 e = lut_mfma(hi, lo, use_lo, lut_b_operand(cbh, K, jp, c32 * 32, lane));
+    const int c = c32 * 32 + n;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = (g & 1) * 4 + i;
-      if (h < nh && jj < M && c < K) lb[(int64_t)h * M * K + c] = mg[i] * e[i];
-    }
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * quad + i, j = jp + s2;
+        if (h < nh && j < M && c < K) lb[((int64_t)h * M + j) * K + c] = mg[i] * e[8 * s2 + i];
+      }
   }
 }
 
