@@ -73,6 +73,14 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64,                                 # idx strides (b, h)
         c_i64, c_i64,                                 # out strides
         c_f32, c_int, c_vp, c_sz, c_vp),              # scaling, chunk, workspace, bytes, stream
+    "bytes_quest_gather_attn": (
+        c_vp, c_vp, c_vp, c_int, c_vp, c_i64, c_i64,  # q, k, v, k/v are fp8, bound, bound strides (b, h)
+        c_int, c_int, c_vp,                           # np, npick, out
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int,   # B, Hq, Hk, S, D, page, limit
+        c_i64, c_i64,                                 # q strides
+        c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,     # k, v strides (b, h, s)
+        c_i64, c_i64,                                 # out strides
+        c_f32, c_int, c_vp, c_sz, c_vp),              # scaling, chunk, workspace, bytes, stream
     "bytes_quest_page_minmax": (c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp),
     "bytes_quest_page_scores": (
         c_vp, c_vp, c_vp, c_vp,                       # q, kmin, kmax, bound

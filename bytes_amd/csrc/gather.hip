@@ -19,7 +19,15 @@
 // its chunk's row numbers in LDS, then its waves run the dense bf16 tile loop
 // with rows fetched through that list (prefetching the next tile's rows while
 // the current tile is computed).
+// Quest selection in the prologue (bytes_quest_gather_attn): instead of a
+// page list, each workgroup receives its query head's row of page bounds and
+// selects the top npick pages itself (exact: bound descending, lowest
+// page first among equal bounds, the order of bytes_topk; a radix select by
+// the whole workgroup), listing them in ascending page order as the unfused
+// top-k does; the page top-k launch of benchmarks/sparse_attention.py:356-358
+// then disappears from the step.
 #include "dense_tile.h"
+#include "wave_select.h"
 
 namespace bytes_amd {
 
@@ -35,6 +43,9 @@ struct GatherArgs {
   int Hk, G, HB, S, kb, chunk, per_head;
   int page;                  // 0: idx holds rows; > 0: idx holds page ids of `page` rows each
   int limit;                 // rows >= limit take no part
+  const float* bound;        // Quest selection: page bounds [B, Hq, np] (row strides b_sb, b_sh)
+  int64_t b_sb, b_sh;
+  int np;
   float scale_log2;
   SplitKOut o;
 };
@@ -42,9 +53,14 @@ struct GatherArgs {
 constexpr int kGatherWaves = 4;
 constexpr int kGatherChunkMax = 1024;   // index-list entries per workgroup
 
+constexpr int kGatherSelMax = 4096;     // pages per bound row selected in the prologue
+
 template <int D>
 struct GatherCfg {
   static constexpr int kRows = kGatherChunkMax * 4;
+  static constexpr int kSel = kBins * 4 + kGatherSelMax * 4 + block_select_words<kGatherWaves * 64>() * 4;
+  // histogram, bound row / page list, scan words
+  static_assert(kSel <= DenseCfg<D>::kSmem, "the selection fits in the tile buffers");
   static constexpr int kSmem = DenseCfg<D>::kSmem + kRows;
 };
 
@@ -84,7 +100,8 @@ __device__ __forceinline__ void gather_issue_fp8(const uint8_t* kbase, const uin
   }
 }
 
-template <int D, bool FP8>
+// SEL > 0: Quest selection in the prologue, SEL bounds per thread.
+template <int D, bool FP8, int SEL>
 __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(GatherArgs a) {
   using C = DenseCfg<D>;
   __shared__ __attribute__((aligned(16))) char smem_raw[GatherCfg<D>::kSmem];
@@ -117,6 +134,36 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
   bf16x8 qb[C::KK];
   load_q_bf16<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, nh, lane, qb);
 
+  // Quest selection: the head's bound row is staged in LDS (coalesced), then
+  // the workgroup selects the top kb / page pages (thread t ranking bounds
+  // SEL*t .. +SEL) and lists them, ascending, over the staged row
+  int32_t* pids = reinterpret_cast<int32_t*>(smem_raw + kBins * 4);
+  if constexpr (SEL > 0) {
+    constexpr int NT = kGatherWaves * 64;
+    float* brow = reinterpret_cast<float*>(pids);
+    uint32_t* red = reinterpret_cast<uint32_t*>(smem_raw + kBins * 4 + kGatherSelMax * 4);
+    const float* bsrc = a.bound + (int64_t)b * a.b_sb + (int64_t)hq0 * a.b_sh;
+    // all of a thread's loads in flight together (indices clamped to the row)
+    float bv[SEL];
+#pragma unroll
+    for (int u = 0; u < SEL; ++u) bv[u] = bsrc[min((int)threadIdx.x + NT * u, a.np - 1)];
+#pragma unroll
+    for (int u = 0; u < SEL; ++u) brow[threadIdx.x + NT * u] = bv[u];
+    __syncthreads();
+    uint32_t key[SEL];
+#pragma unroll
+    for (int q4 = 0; q4 < SEL / 4; ++q4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(brow + SEL * threadIdx.x + 4 * q4);   // past np: unused
+#pragma unroll
+      for (int e = 0; e < 4; ++e) key[4 * q4 + e] = score_order_key(v[e]);
+    }
+    uint32_t T, need;
+    block_select_threshold<NT, SEL>(key, a.np, a.kb / a.page, reinterpret_cast<uint32_t*>(smem_raw), red, T, need);
+    // every thread's reads of the staged row precede the first list write
+    block_select_compact<NT, SEL>(key, a.np, T, need, red, [&](uint32_t pos, int idx, uint32_t) { pids[pos] = idx; });
+    __syncthreads();
+  }
+
   const int p_begin = split * a.chunk;
   const int n = min(a.chunk, a.kb - p_begin);
   for (int i = threadIdx.x; i < n; i += kGatherWaves * 64) {
@@ -124,7 +171,7 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
     int64_t r;
     bool ok;
     if (a.page > 0) {
-      const int pid = irow[j / a.page];
+      const int pid = SEL > 0 ? pids[j / a.page] : irow[j / a.page];
       r = (int64_t)pid * a.page + j % a.page;
       r = r < a.S - 1 ? r : a.S - 1;
       ok = pid >= 0;
@@ -190,6 +237,22 @@ static void gather_plan(int kb, long units, int chunk_req, int* chunk, int* ns) 
   *ns = (kb + c - 1) / c;
 }
 
+static void gather_launch(const GatherArgs& a, int D, int kv_fp8, dim3 grid, dim3 block, hipStream_t st) {
+#define GL(DD, F8, SL) BYTES_LAUNCH(kProfGather, (gather_decode_kernel<DD, F8, SL>), grid, block, 0, st, a)
+#define GL_SEL(DD, F8)                  \
+  if (!a.bound) GL(DD, F8, 0);          \
+  else if (a.np <= 1024) GL(DD, F8, 4); \
+  else if (a.np <= 2048) GL(DD, F8, 8); \
+  else GL(DD, F8, 16);
+  if (D == 128) {
+    if (kv_fp8) { GL_SEL(128, true) } else { GL_SEL(128, false) }
+  } else {
+    if (kv_fp8) { GL_SEL(64, true) } else { GL_SEL(64, false) }
+  }
+#undef GL_SEL
+#undef GL
+}
+
 static long gather_units(int B, int Hq, int Hk, int per_head) {
   const int G = Hq / Hk, HB = (G + 15) / 16;
   return per_head ? (long)B * Hq : (long)B * Hk * HB;
@@ -226,6 +289,9 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, c
   GatherArgs a;
   a.page = page;
   a.limit = limit;
+  a.bound = nullptr;
+  a.b_sb = a.b_sh = 0;
+  a.np = 0;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
   a.k = k;
@@ -253,13 +319,58 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, c
   splitk_carve(workspace, units, ns, a.o);
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((unsigned)(ns * units)), block(kGatherWaves * 64);
-  if (D == 128) {
-    if (kv_fp8) BYTES_LAUNCH(kProfGather, (gather_decode_kernel<128, true>), grid, block, 0, st, a);
-    else BYTES_LAUNCH(kProfGather, (gather_decode_kernel<128, false>), grid, block, 0, st, a);
-  } else {
-    if (kv_fp8) BYTES_LAUNCH(kProfGather, (gather_decode_kernel<64, true>), grid, block, 0, st, a);
-    else BYTES_LAUNCH(kProfGather, (gather_decode_kernel<64, false>), grid, block, 0, st, a);
-  }
+  gather_launch(a, D, kv_fp8, grid, block, st);
+  int rc = (int)hipGetLastError();
+  if (rc) return rc;
+  return splitk_combine(a.o, units, D, st);
+}
+
+// Quest decode after the page bounds: per query head, the top npick pages of
+// bound[b, hq, :np] (exact; bound descending, lowest page first on equal
+// bounds) are selected inside the gather kernel and attended over, rows
+// p*page + o clamped to S-1, rows >= limit masked.  Same workspace as
+// bytes_gather_attn with per_head = 1 and kb = npick * page.
+int bytes_quest_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, const void* bound, int64_t b_sb,
+                            int64_t b_sh, int np, int npick, void* out, int B, int Hq, int Hk, int S, int D, int page,
+                            int limit, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                            int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scaling,
+                            int chunk_req, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !k || !v || !bound || !out || B <= 0 || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || S <= 0)
+    return (int)hipErrorInvalidValue;
+  if (D != 64 && D != 128) return (int)hipErrorInvalidValue;
+  if (page <= 0 || np <= 0 || npick <= 0 || npick > np || limit < 0 || limit > S) return (int)hipErrorInvalidValue;
+  if (np > kGatherSelMax) return (int)hipErrorNotSupported;
+  const long units = gather_units(B, Hq, Hk, 1);
+  if (units > kMaxUnits) return (int)hipErrorInvalidConfiguration;
+  const int kb = npick * page;
+  GatherArgs a;
+  a.page = page;
+  a.limit = limit;
+  a.bound = static_cast<const float*>(bound);
+  a.b_sb = b_sb; a.b_sh = b_sh;
+  a.np = np;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_sb; a.q_sh = q_sh;
+  a.k = k;
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
+  a.v = v;
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.idx = nullptr;
+  a.i_sb = a.i_sh = 0;
+  a.Hk = Hk; a.G = Hq / Hk; a.HB = (a.G + 15) / 16; a.S = S; a.kb = kb;
+  a.per_head = 1;
+  a.scale_log2 = scaling * kLog2e;
+  int ns;
+  gather_plan(kb, units, chunk_req, &a.chunk, &ns);
+  if (ns > 1024) return (int)hipErrorInvalidConfiguration;
+  if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
+  a.o.out = out;
+  a.o.out_dtype = kOutBF16;
+  a.o.o_sb = o_sb; a.o.o_sh = o_sh;
+  a.o.Hk = Hq; a.o.HB = 1; a.o.G = 1;
+  splitk_carve(workspace, units, ns, a.o);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  gather_launch(a, D, kv_fp8, dim3((unsigned)(ns * units)), dim3(kGatherWaves * 64), st);
   int rc = (int)hipGetLastError();
   if (rc) return rc;
   return splitk_combine(a.o, units, D, st);

@@ -10,7 +10,8 @@
 //    `local_w` tokens (:349-355).
 // The products of bf16 values are exact in fp32 and every thread sums its
 // page's terms in ascending d, so the bounds are bit-identical to a
-// sequential fp32 evaluation; the page top-k that follows is then bit-exact.
+// sequential fp32 evaluation (up to the sign of an all-zero bound, which
+// ranks the same); the page top-k that follows is then bit-exact.
 #include "common.h"
 
 namespace bytes_amd {
@@ -59,20 +60,26 @@ constexpr int kQuestThreads = 256;
 constexpr int kQuestPages = 32;                    // pages per workgroup
 constexpr int kQuestSlots = kQuestThreads / kQuestPages;   // head slots per round
 
-// One workgroup per (b, kv head, 32 pages); thread (page, head slot).  The
-// pages' min/max rows are staged in LDS (rows padded to an odd number of
-// dwords, so the 32 pages a wave reads at one d sit in distinct banks) and
-// each (page, head) bound is summed over d in order.
+// One workgroup per (b, kv head, head block of 16, 32 pages); thread (page
+// t % 32, head slot t / 32).  The pages' min/max rows are widened to fp32 in
+// LDS (rows padded by 16 bytes, so the 16 pages a 16-lane group reads at one d
+// sit in distinct banks) and q is split into q+ = q (q >= 0 or NaN, else 0)
+// and q- = q (q < 0, else 0).  Each term is then fma(q-_d, kmin_d, q+_d *
+// kmax_d): one of the two products is an exact zero, so the term is the
+// rounded product max(q_d*kmin_d, q_d*kmax_d) picks (kmax >= kmin), NaN
+// propagating as that max does when the min/max rows carry it at the same d
+// (as every page with a NaN key does).  Terms are summed in ascending d.
 template <int D>
 __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                                                     const uint16_t* kmin, const uint16_t* kmax,
                                                                     int Hk, int G, int HB, int np, int page,
                                                                     int pos, int local_w, float scale,
                                                                     float* bound, int64_t o_sb, int64_t o_sh) {
-  constexpr int RW = D / 2 + 1;                    // dwords per padded row
-  __shared__ uint32_t mn_s[kQuestPages * RW];
-  __shared__ uint32_t mx_s[kQuestPages * RW];
-  __shared__ float qs[16][D];
+  constexpr int PITCH = D + 4;                     // floats per padded row
+  __shared__ __attribute__((aligned(16))) float mn_s[kQuestPages * PITCH];
+  __shared__ __attribute__((aligned(16))) float mx_s[kQuestPages * PITCH];
+  __shared__ __attribute__((aligned(16))) float qp_s[16 * D];
+  __shared__ __attribute__((aligned(16))) float qm_s[16 * D];
   const int parts = (np + kQuestPages - 1) / kQuestPages;
   const int bhb = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
   const int bh = bhb / HB, hb = bhb - (bhb / HB) * HB;
@@ -82,15 +89,16 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
   const int g0 = hb * 16, GB = min(16, G - g0);
   // Every load is issued before any LDS store that consumes one (indices
   // clamped, so no load sits under a lane mask): one memory round trip.
-  constexpr int QPT = 16 * D / kQuestThreads;      // query elements per thread (G <= 16)
   constexpr int CH = D / 8;                        // 16-byte chunks per row
+  constexpr int QPT = (16 * CH + kQuestThreads - 1) / kQuestThreads;   // q chunks per thread (16 heads)
   constexpr int MPT = kQuestPages * CH / kQuestThreads;   // min/max chunks per thread
-  uint16_t qv[QPT];
+  static_assert(QPT >= 1 && MPT >= 1, "chunks per thread");
+  u32x4 qv[QPT];
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
-    const int i = min((int)threadIdx.x + u * kQuestThreads, GB * D - 1);
-    const int g = i / D, d = i - (i / D) * D;
-    qv[u] = q[(int64_t)b * q_sb + (int64_t)(hk * G + g0 + g) * q_sh + d];
+    const int e = min((int)threadIdx.x + u * kQuestThreads, 16 * CH - 1);
+    const int g = min(e / CH, GB - 1), c = e - (e / CH) * CH;
+    qv[u] = ld16(q + (int64_t)b * q_sb + (int64_t)(hk * G + g0 + g) * q_sh + c * 8);
   }
   const int64_t row0 = ((int64_t)b * Hk + hk) * np;
   u32x4 av[MPT], zv[MPT];
@@ -102,20 +110,45 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     av[u] = ld16(kmin + r * D + c * 8);
     zv[u] = ld16(kmax + r * D + c * 8);
   }
+  auto widen = [](const u32x4& raw, f32x4& lo4, f32x4& hi4) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      lo4[2 * j] = __uint_as_float(raw[j] << 16);
+      lo4[2 * j + 1] = __uint_as_float(raw[j] & 0xFFFF0000u);
+      hi4[2 * j] = __uint_as_float(raw[2 + j] << 16);
+      hi4[2 * j + 1] = __uint_as_float(raw[2 + j] & 0xFFFF0000u);
+    }
+  };
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
-    const int i = threadIdx.x + u * kQuestThreads;   // < 16 * D: rows past GB are unused
-    qs[i / D][i - (i / D) * D] = bf16_bits_to_f32(qv[u]);
+    const int e = min((int)threadIdx.x + u * kQuestThreads, 16 * CH - 1);   // rows past GB are unused
+    const int g = e / CH, c = e - (e / CH) * CH;
+    f32x4 x0, x1;
+    widen(qv[u], x0, x1);
+    f32x4 p0v, p1v, m0v, m1v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p0v[j] = (x0[j] >= 0.f || x0[j] != x0[j]) ? x0[j] : 0.f;
+      p1v[j] = (x1[j] >= 0.f || x1[j] != x1[j]) ? x1[j] : 0.f;
+      m0v[j] = x0[j] < 0.f ? x0[j] : 0.f;
+      m1v[j] = x1[j] < 0.f ? x1[j] : 0.f;
+    }
+    *reinterpret_cast<f32x4*>(qp_s + g * D + c * 8) = p0v;
+    *reinterpret_cast<f32x4*>(qp_s + g * D + c * 8 + 4) = p1v;
+    *reinterpret_cast<f32x4*>(qm_s + g * D + c * 8) = m0v;
+    *reinterpret_cast<f32x4*>(qm_s + g * D + c * 8 + 4) = m1v;
   }
 #pragma unroll
   for (int u = 0; u < MPT; ++u) {
     const int e = threadIdx.x + u * kQuestThreads;
     const int pp = e / CH, c = e - (e / CH) * CH;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mn_s[pp * RW + c * 4 + j] = av[u][j];
-      mx_s[pp * RW + c * 4 + j] = zv[u][j];
-    }
+    f32x4 a0, a1, z0, z1;
+    widen(av[u], a0, a1);
+    widen(zv[u], z0, z1);
+    *reinterpret_cast<f32x4*>(mn_s + pp * PITCH + c * 8) = a0;
+    *reinterpret_cast<f32x4*>(mn_s + pp * PITCH + c * 8 + 4) = a1;
+    *reinterpret_cast<f32x4*>(mx_s + pp * PITCH + c * 8) = z0;
+    *reinterpret_cast<f32x4*>(mx_s + pp * PITCH + c * 8 + 4) = z1;
   }
   __syncthreads();
   const int pp = threadIdx.x % kQuestPages;
@@ -128,17 +161,27 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     const int lo = max(pos - local_w + 1, 0) / page, hi = pos / page;
     recent = p >= lo && p <= hi;
   }
+  const float* mnr = mn_s + pp * PITCH;
+  const float* mxr = mx_s + pp * PITCH;
   for (int g = threadIdx.x / kQuestPages; g < GB; g += kQuestSlots) {
+    const float* qpr = qp_s + g * D;
+    const float* qmr = qm_s + g * D;
     float acc = 0.f;
-#pragma unroll 8
-    for (int d2 = 0; d2 < D / 2; ++d2) {
-      const uint32_t a = mn_s[pp * RW + d2], z = mx_s[pp * RW + d2];
-      const float lo0 = __uint_as_float(a << 16), lo1 = __uint_as_float(a & 0xFFFF0000u);
-      const float hi0 = __uint_as_float(z << 16), hi1 = __uint_as_float(z & 0xFFFF0000u);
-      const float q0 = qs[g][2 * d2], q1 = qs[g][2 * d2 + 1];
-      const float t0 = nmax(q0 * lo0, q0 * hi0);
-      acc = d2 == 0 ? t0 : acc + t0;
-      acc = acc + nmax(q1 * lo1, q1 * hi1);
+    {
+#pragma clang fp contract(off)
+#pragma unroll 4
+      for (int d4 = 0; d4 < D / 4; ++d4) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(mnr + 4 * d4);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(mxr + 4 * d4);
+        const f32x4 qp = *reinterpret_cast<const f32x4*>(qpr + 4 * d4);
+        const f32x4 qm = *reinterpret_cast<const f32x4*>(qmr + 4 * d4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float hp = qp[e] * hi[e];
+          const float t = __builtin_fmaf(qm[e], lo[e], hp);
+          acc = (d4 == 0 && e == 0) ? t : acc + t;
+        }
+      }
     }
     float v = acc * scale;
     if (!valid) v = kNegInf;

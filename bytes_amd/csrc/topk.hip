@@ -23,7 +23,7 @@
 // Step 3 also clears the histogram and list counters, which are zero between
 // calls.  Short rows, and unsorted selections larger than the lists hold
 // (k > 8192), run step 3's exact path alone.
-#include "common.h"
+#include "wave_select.h"
 
 namespace bytes_amd {
 
@@ -31,7 +31,6 @@ constexpr int kTopkThreads = 1024;     // select kernel
 constexpr int kPassThreads = 512;      // histogram and filter kernels (four 16-byte loads per thread)
 constexpr int kSlice = 8192;           // row elements per histogram / filter workgroup
 constexpr int kTopkMaxK = 8192;
-constexpr int kBins = 2048;            // digit = top 11 bits of the order key
 constexpr int kCandCap = 8192;         // candidate list capacity per row
 constexpr int kSortMax = 16384;        // LDS sort capacity (above list + candidates)
 constexpr int kShortRow = 16384;       // rows up to this length take the single-kernel exact path
@@ -609,15 +608,6 @@ constexpr int kWaveRow = 4096;
 constexpr int kWaveK = 256;
 constexpr int kWaveRowsPerWG = 4;
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(v, off, 64);
-    if (lane >= off) v += y;
-  }
-  return v;
-}
-
 template <bool VEC, int PER>
 __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const float* scores, int64_t row_stride,
                                                                         int64_t rows, int n, int k, int32_t* out,
@@ -645,107 +635,18 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
   }
-  auto valid = [&](int q) { return i0 + q < n; };
-
-  // the digit passes start at the highest bit in which the row's keys differ
-  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-#pragma unroll
-  for (int q = 0; q < PER; ++q)
-    if (valid(q)) {
-      kmin = min(kmin, key[q]);
-      kmax = max(kmax, key[q]);
-    }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off, 64));
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
-  }
-  const uint32_t diff = kmin ^ kmax;
-  const int hb = diff ? 31 - __builtin_clz(diff) : -1;
-  uint32_t pmask = hb < 0 ? 0xFFFFFFFFu : ~(uint32_t)((2ull << hb) - 1ull);
-  uint32_t prefix = kmin & pmask, kr = (uint32_t)k;
-#pragma unroll 1
-  for (int hi = hb; hi >= 0; hi -= 11) {
-    const int shift = hi >= 10 ? hi - 10 : 0;
-    const uint32_t dmask = (1u << (hi - shift + 1)) - 1u;
-    u32x4* h4 = reinterpret_cast<u32x4*>(hist) + lane * 8;      // this lane's 32 bins
-#pragma unroll
-    for (int q = 0; q < 8; ++q) h4[q] = u32x4{0u, 0u, 0u, 0u};
-    wave_lds_sync();
-#pragma unroll
-    for (int q = 0; q < PER; ++q)
-      if (valid(q) && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> shift) & dmask], 1u);
-    wave_lds_sync();
-    uint32_t c[32];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const u32x4 v = h4[q];
-      c[4 * q] = v[0]; c[4 * q + 1] = v[1]; c[4 * q + 2] = v[2]; c[4 * q + 3] = v[3];
-    }
-    uint32_t s = 0;
-#pragma unroll
-    for (int b = 0; b < 32; ++b) s += c[b];
-    // inclusive suffix sum over lanes (bins above this lane's range included)
-    uint32_t suf = s;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = __shfl_down(suf, off, 64);
-      if (lane + off < 64) suf += y;
-    }
-    const uint32_t above_lane = suf - s;         // keys in digits above this lane's bins
-    // digit d: count(digits > d) < kr <= count(digits >= d)
-    const bool mine = above_lane < kr && kr <= suf;
-    uint32_t acc = above_lane, d = 0u, above = 0u;
-    bool got = false;
-#pragma unroll
-    for (int b = 31; b >= 0; --b) {
-      if (!got && acc + c[b] >= kr) {
-        got = true;
-        d = 32u * lane + b;
-        above = acc;
-      }
-      acc += c[b];
-    }
-    const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
-    d = __shfl(d, src, 64);
-    above = __shfl(above, src, 64);
-    kr -= above;
-    prefix |= d << shift;
-    pmask |= dmask << shift;
-    wave_lds_sync();
-  }
-  const uint32_t T = prefix, need = kr;          // keys equal to T to take (>= 1)
+  uint32_t T, need;
+  wave_select_threshold<PER>(key, n, k, hist, T, need);
   if (ghist) {                                   // a histogram the caller built: leave it at zero
     u32x4* gh = reinterpret_cast<u32x4*>(ghist + row * kBins) + lane * 8;
 #pragma unroll
     for (int q = 0; q < 8; ++q) gh[q] = u32x4{0u, 0u, 0u, 0u};
   }
-
   // compaction in index order (lane, q): slot = selected keys before this one
-  uint32_t ne = 0u, ng = 0u;
-#pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    ne += (valid(q) && key[q] == T) ? 1u : 0u;
-    ng += (valid(q) && key[q] > T) ? 1u : 0u;
-  }
-  uint32_t rank = wave_incl_scan(ne, lane) - ne;          // keys equal to T before this lane
-  const uint32_t take_eq = rank >= need ? 0u : (need - rank < ne ? need - rank : ne);
-  const uint32_t nt = ng + take_eq;
-  uint32_t pos = wave_incl_scan(nt, lane) - nt;
-#pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    const bool v = valid(q);
-    bool take = v && key[q] > T;
-    if (v && key[q] == T) {
-      take = rank < need;
-      ++rank;
-    }
-    if (take) {
-      if (sorted) sb[pos] = sort_val(key[q], i0 + q);
-      else o[pos] = i0 + q;
-      ++pos;
-    }
-  }
+  wave_select_compact<PER>(key, n, T, need, [&](uint32_t pos, int idx, uint32_t kk) {
+    if (sorted) sb[pos] = sort_val(kk, idx);
+    else o[pos] = idx;
+  });
   if (!sorted) return;
 
   // in-wave bitonic sort of sb[0, P) into descending order (padding zeros sort last)
@@ -794,8 +695,7 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
   static_assert(PER % 4 == 0 && NT * PER <= kSmallRow && BPT % 4 == 0, "keys and bins per thread");
   __shared__ __attribute__((aligned(16))) uint32_t hist[kBins];
   __shared__ uint64_t sb[kSmallSortK];
-  __shared__ uint32_t wa[NW], wb[NW], wc[NW], wd[NW];
-  __shared__ uint32_t sel[2];
+  __shared__ uint32_t red[block_select_words<NT>()];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t row = blockIdx.x;
   const float* x = scores + row * row_stride;
@@ -812,121 +712,18 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
   }
-  auto valid = [&](int q) { return i0 + q < n; };
-
-  // key range of the row
-  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-#pragma unroll
-  for (int q = 0; q < PER; ++q)
-    if (valid(q)) {
-      kmin = min(kmin, key[q]);
-      kmax = max(kmax, key[q]);
-    }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off, 64));
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
-  }
-  if (lane == 0) {
-    wa[w] = kmin;
-    wb[w] = kmax;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int v = 0; v < NW; ++v) {
-    kmin = min(kmin, wa[v]);
-    kmax = max(kmax, wb[v]);
-  }
-  const uint32_t diff = kmin ^ kmax;
-  const int hb = diff ? 31 - __builtin_clz(diff) : -1;        // highest differing bit
-  uint32_t pmask = hb < 0 ? 0xFFFFFFFFu : ~(uint32_t)((2ull << hb) - 1ull);
-  uint32_t prefix = kmin & pmask, kr = (uint32_t)k;
-
-  u32x4* h4 = reinterpret_cast<u32x4*>(hist) + tid * (BPT / 4);   // this thread's bins
-#pragma unroll 1
-  for (int hi = hb; hi >= 0; hi -= 11) {
-    const int lo = hi >= 10 ? hi - 10 : 0;
-    const uint32_t dmask = (1u << (hi - lo + 1)) - 1u;
-#pragma unroll
-    for (int q = 0; q < BPT / 4; ++q) h4[q] = u32x4{0u, 0u, 0u, 0u};
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < PER; ++q)
-      if (valid(q) && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> lo) & dmask], 1u);
-    __syncthreads();
-    uint32_t c[BPT];
-#pragma unroll
-    for (int q = 0; q < BPT / 4; ++q) {
-      const u32x4 v = h4[q];
-      c[4 * q] = v[0]; c[4 * q + 1] = v[1]; c[4 * q + 2] = v[2]; c[4 * q + 3] = v[3];
-    }
-    uint32_t s = 0u;
-#pragma unroll
-    for (int b = 0; b < BPT; ++b) s += c[b];
-    // inclusive suffix sum over the wave's lanes, then the waves above
-    uint32_t suf = s;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = (uint32_t)__shfl_down((int)suf, off, 64);
-      if (lane + off < 64) suf += y;
-    }
-    if (lane == 0) wc[w] = suf;
-    __syncthreads();
-    uint32_t acc = suf - s;                      // keys in the bins above this thread's
-#pragma unroll
-    for (int v = 0; v < NW; ++v) acc += v > w ? wc[v] : 0u;
-    // digit d: count(digits > d) < kr <= count(digits >= d); exactly one
-    // thread and bin see the crossing
-#pragma unroll
-    for (int b = BPT - 1; b >= 0; --b) {
-      if (acc < kr && acc + c[b] >= kr) {
-        sel[0] = (uint32_t)(BPT * tid + b);
-        sel[1] = acc;
-      }
-      acc += c[b];
-    }
-    __syncthreads();
-    kr -= sel[1];
-    prefix |= sel[0] << lo;
-    pmask |= dmask << lo;
-  }
-  const uint32_t T = prefix, need = kr;          // keys equal to T to take (>= 1), lowest indices first
+  uint32_t T, need;
+  block_select_threshold<NT, PER>(key, n, k, hist, red, T, need);
   if (ghist) {                                   // a histogram the caller built: leave it at zero
     u32x4* gh = reinterpret_cast<u32x4*>(ghist + row * kBins) + tid * (BPT / 4);
 #pragma unroll
     for (int q = 0; q < BPT / 4; ++q) gh[q] = u32x4{0u, 0u, 0u, 0u};
   }
-
-  // placement in index order: one scan of (equal << 16 | greater), both < 2^16
-  uint32_t ne = 0u, ng = 0u;
-#pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    ne += (valid(q) && key[q] == T) ? 1u : 0u;
-    ng += (valid(q) && key[q] > T) ? 1u : 0u;
-  }
-  const uint32_t packed = (ne << 16) | ng;
-  const uint32_t incl = wave_incl_scan(packed, lane);
-  if (lane == 63) wd[w] = incl;
-  __syncthreads();
-  uint32_t before = incl - packed;
-#pragma unroll
-  for (int v = 0; v < NW; ++v) before += v < w ? wd[v] : 0u;
-  uint32_t rank = before >> 16;                  // keys equal to T before this thread
-  uint32_t pos = (before & 0xFFFFu) + (rank < need ? rank : need);
-#pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    const bool v = valid(q);
-    bool take = v && key[q] > T;
-    if (v && key[q] == T) {
-      take = rank < need;
-      ++rank;
-    }
-    if (take) {
-      if (sorted) sb[pos] = sort_val(key[q], i0 + q);
-      else o[pos] = i0 + q;
-      ++pos;
-    }
-  }
+  // placement in index order
+  block_select_compact<NT, PER>(key, n, T, need, red, [&](uint32_t pos, int idx, uint32_t kk) {
+    if (sorted) sb[pos] = sort_val(kk, idx);
+    else o[pos] = idx;
+  });
   if (!sorted) return;
   int P = 64;
   while (P < k) P <<= 1;

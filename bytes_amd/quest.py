@@ -14,8 +14,8 @@ from typing import Optional, Tuple
 import torch
 
 from . import _checks as C
-from ._lib import call, ptr, stream_of
-from .sparse import sparse_gather_attn, topk_indices
+from ._lib import call, ptr, size_query, stream_of, workspace
+from .sparse import _qk_shapes, sparse_gather_attn, topk_indices
 
 
 def quest_page_minmax(k: torch.Tensor, page: int = 16) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -91,6 +91,46 @@ def _quest_select(q_blk, k_r, pos, S, kb, page, scaling, local_w=0):
     return qs(q_blk, k_r, pos, S, kb, page, scaling, local_w)
 
 
+_SELECT_IN_GATHER_MAX = 4096        # page-bound rows the gather kernel selects from itself
+
+
+def quest_gather_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bound: torch.Tensor, npick: int,
+                      scaling: float, *, page: int = 16, limit: Optional[int] = None, chunk: int = 0) -> torch.Tensor:
+    """The top `npick` pages of each query head's bound row (bound [B,H_q,np]
+    fp32; exact: bound descending, lowest page first on equal bounds), attended
+    over in one gather launch that selects the pages itself: equal bit for bit
+    to topk_indices(bound, npick, sorted=False) followed by
+    sparse_gather_attn(..., page=page, limit=limit)
+    (benchmarks/sparse_attention.py:356-387).  np <= 4096."""
+    B, Hq, Hk, S, D = _qk_shapes(q, k)
+    C.cuda_tensors(q, v, bound)
+    C.dtype_in(k, "k", torch.bfloat16, torch.float8_e4m3fn)
+    C.dtype_in(v, "v", k.dtype)
+    C.dtype_in(bound, "bound", torch.float32)
+    if tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"shape mismatch: k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if bound.dim() != 3 or tuple(bound.shape[:2]) != (B, Hq):
+        raise ValueError(f"bound must be [B, H_q, np]; got {tuple(bound.shape)}")
+    np_ = bound.shape[-1]
+    if not 0 < npick <= np_ or np_ > _SELECT_IN_GATHER_MAX or page < 1:
+        raise ValueError(f"npick={npick}, np={np_}, page={page} (need 0 < npick <= np <= {_SELECT_IN_GATHER_MAX})")
+    lim = S if limit is None else int(limit)
+    if not 0 <= lim <= S:
+        raise ValueError(f"limit={limit} outside [0, S]")
+    if bound.stride(-1) != 1:
+        bound = bound.contiguous()
+    qs = C.rows16(q.squeeze(2))
+    k, v = C.rows16(k), C.rows16(v)
+    out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=q.device)
+    kb = npick * page
+    ws = workspace(q.device, size_query("bytes_gather_attn_workspace_size", B, Hq, Hk, kb, D, 1, int(chunk)))
+    call("bytes_quest_gather_attn", ptr(qs), ptr(k), ptr(v), int(k.dtype == torch.float8_e4m3fn), ptr(bound),
+         bound.stride(0), bound.stride(1), np_, int(npick), ptr(out), B, Hq, Hk, S, D, int(page), lim,
+         qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
+         out.stride(0), out.stride(1), float(scaling), int(chunk), ptr(ws), ws.numel(), stream_of(q))
+    return out.unsqueeze(2)
+
+
 def quest_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, scaling: float, *, page: int = 16,
                  meta: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, pos: Optional[int] = None,
                  local_w: int = 0, return_pages: bool = False):
@@ -98,11 +138,18 @@ def quest_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kb: int, sca
     when `meta` is None), the top ceil(kb/page) pages per query head, exact
     attention over their rows (rows past `pos` masked, as attend_topk,
     benchmarks/sparse_attention.py:367-387).  q [B,H_q,1,D]; k, v [B,H_k,S,D]
-    bf16.  Returns out [B,H_q,1,D] bf16 (and the page ids if return_pages)."""
+    bf16.  Returns out [B,H_q,1,D] bf16 (and the page ids, ordered by bound
+    descending, if return_pages).  Up to 4096 pages, the gather kernel selects
+    the pages itself (two launches and the split merge); return_pages and
+    longer caches run the page top-k as a launch of its own."""
     S = k.shape[2]
     if meta is None:
         meta = quest_page_minmax(k, page)
     p = S - 1 if pos is None else int(pos)
+    if not return_pages and meta[0].shape[2] <= _SELECT_IN_GATHER_MAX:
+        bound = quest_page_scores(q, meta[0], meta[1], scaling, page=page, pos=p, local_w=local_w)
+        return quest_gather_attn(q, k, v, bound, _npick(kb, page, bound.shape[-1]), scaling, page=page,
+                                 limit=p + 1)
     pid = quest_select_pages(q, meta[0], meta[1], S, kb, page, scaling, pos=p, local_w=local_w,
                              sorted=return_pages)
     out = sparse_gather_attn(q, k, v, pid, scaling, page=page, limit=p + 1)

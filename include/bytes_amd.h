@@ -249,6 +249,25 @@ int bytes_quest_page_scores(const void* q, const void* kmin, const void* kmax, v
                             int Hk, int np, int D, int page, int pos, int local_w, int64_t q_sb, int64_t q_sh,
                             int64_t o_sb, int64_t o_sh, float scale, void* stream);
 
+/* Quest decode after the page bounds, in one kernel (plus the split merge):
+ * replaces the page top-k and the attention of benchmarks/sparse_attention.py
+ * :356-387 (`_quest_select`'s topk over page bounds, then `attend_topk`).
+ * For every query head, the top npick pages of bound[b, hq, 0..np) (the
+ * exact top-k of bytes_topk: bound descending, lowest page first on equal
+ * bounds) are selected inside the gather kernel and attended over in
+ * ascending page order, rows min(p*page + o, S-1), rows >= limit masked; the
+ * result equals bytes_topk (unsorted) followed by bytes_gather_attn
+ * (per_head = 1) bit for bit.  bound strides b_sb, b_sh (unit stride along
+ * pages); np <= 4096 (hipErrorNotSupported above); other arguments as
+ * bytes_gather_attn, whose workspace size (per_head = 1, kb = npick * page)
+ * this call needs.
+ */
+int bytes_quest_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, const void* bound, int64_t b_sb,
+                            int64_t b_sh, int np, int npick, void* out, int B, int Hq, int Hk, int S, int D, int page,
+                            int limit, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                            int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, float scaling,
+                            int chunk, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Row steps of the selection functions for query chunks of Qc >= 1 rows
  * (benchmarks/sparse_attention.py:226-387: select_topk, _quest_select,

@@ -100,3 +100,45 @@ def test_quest_decode_causal_position(dev):
     tok = (pidx.unsqueeze(-1) * 16 + torch.arange(16)).reshape(1, 8, -1).clamp(max=1999)
     tok = torch.where(tok <= pos, tok, torch.full_like(tok, -1))
     _check(out, R.sparse_gather_attn(x["q"], x["k"], x["v"], tok, 0.09), "quest pos 1234")
+
+
+@pytest.mark.parametrize("B,Hq,Hk,np_,npick,page,S,lim", [
+    (1, 8, 2, 64, 8, 16, 1000, 1000),        # np = one wave's 64 lanes
+    (2, 6, 3, 777, 100, 8, 6200, 5000),      # ragged np, rows past limit masked
+    (1, 4, 1, 2048, 128, 16, 32768, 32768),  # the C4 page count
+    (1, 4, 4, 3000, 1, 16, 48000, 47000),    # np above 2048 (64 bounds per lane), one page
+    (1, 2, 1, 4096, 4096, 4, 16384, 16384),  # every page
+])
+def test_quest_gather_selects_like_topk_then_gather(dev, B, Hq, Hk, np_, npick, page, S, lim):
+    """The in-kernel page selection equals bytes_topk (unsorted) + gather bit for
+    bit, on integer-valued bounds (many ties) with -inf and +inf entries."""
+    from bytes_amd.sparse import sparse_gather_attn, topk_indices
+    g = torch.Generator().manual_seed(np_ + npick)
+    x = W.dense(B, Hq, Hk, 128, S, seed=np_)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    bound = torch.randint(-20, 20, (B, Hq, np_), generator=g).float()
+    bound[..., 5::17] = float("-inf")
+    bound[..., 3::29] = float("inf")
+    bound = bound.to(dev)
+    got = Q.quest_gather_attn(q, k, v, bound, npick, 0.09, page=page, limit=lim)
+    pid = topk_indices(bound, npick, sorted=False)
+    assert torch.equal(pid.cpu().long(), R.topk_indices(bound.cpu(), npick).sort(-1).values)
+    want = sparse_gather_attn(q, k, v, pid, 0.09, page=page, limit=lim)
+    assert got.shape == want.shape and torch.equal(got, want)
+
+
+def test_quest_decode_fused_path_c4(dev):
+    """BASELINE C4 through the default (fused) path: the same output as the
+    unfused pipeline with ascending page ids, bit for bit, and the oracle's
+    within tolerance."""
+    from bytes_amd.sparse import sparse_gather_attn
+    x = W.c4_quest(seed=0)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    sc = x["scale"]
+    meta = Q.quest_page_minmax(k, 16)
+    out = Q.quest_decode(q, k, v, 2048, sc, meta=meta)
+    pid = Q.quest_select_pages(q, meta[0], meta[1], 32768, 2048, 16, sc, sorted=False)
+    assert torch.equal(out, sparse_gather_attn(q, k, v, pid, sc, page=16))
+    rpid, rtok, _ = R.quest_select(x["q"], x["k"], 2048, 16, sc)
+    assert torch.equal(pid.cpu().long(), rpid.sort(-1).values)
+    _check(out, R.sparse_gather_attn(x["q"], x["k"], x["v"], rtok, sc), "C4 quest decode (fused)")
