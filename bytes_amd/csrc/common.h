@@ -66,6 +66,27 @@ __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(
 // which does not change a softmax numerator or denominator at fp32 precision.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- wave-wide reductions and scans on DPP (no LDS round trip) ----
+// dpp_u32<CTRL, ROWS>: lane i reads the lane CTRL names; lanes whose source
+// lies outside their row of 16, or whose row is not in ROWS, read 0.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xF, true);
+}
+
+// Inclusive prefix sum over the 64 lanes: shifts of 1, 2, 4, 8 within each
+// row of 16, then each row adds the totals of the rows before it (row
+// broadcasts of lanes 15 and 31).
+__device__ __forceinline__ uint32_t wave_prefix_sum(uint32_t x) {
+  x += dpp_u32<0x111>(x);         // row_shr:1
+  x += dpp_u32<0x112>(x);         // row_shr:2
+  x += dpp_u32<0x114>(x);         // row_shr:4
+  x += dpp_u32<0x118>(x);         // row_shr:8
+  x += dpp_u32<0x142, 0xA>(x);    // row_bcast:15 into rows 1 and 3
+  x += dpp_u32<0x143, 0xC>(x);    // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
 // Wave-scope ordering point for wave-private LDS buffers: keeps the compiler
 // from moving LDS accesses across it and orders them at wavefront scope.
 __device__ __forceinline__ void wave_lds_sync() {

@@ -46,6 +46,7 @@ struct GatherArgs {
   const float* bound;        // Quest selection: page bounds [B, Hq, np] (row strides b_sb, b_sh)
   int64_t b_sb, b_sh;
   int np;
+  int b_vec;                 // every bound row starts 16-byte aligned and np % 4 == 0
   float scale_log2;
   SplitKOut o;
 };
@@ -143,12 +144,21 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
     float* brow = reinterpret_cast<float*>(pids);
     uint32_t* red = reinterpret_cast<uint32_t*>(smem_raw + kBins * 4 + kGatherSelMax * 4);
     const float* bsrc = a.bound + (int64_t)b * a.b_sb + (int64_t)hq0 * a.b_sh;
-    // all of a thread's loads in flight together (indices clamped to the row)
-    float bv[SEL];
+    // all of a thread's loads in flight together (indices clamped to the row):
+    // 16-byte chunks where the row allows, else single floats
+    if (a.b_vec) {
+      u32x4 bv[SEL / 4];
 #pragma unroll
-    for (int u = 0; u < SEL; ++u) bv[u] = bsrc[min((int)threadIdx.x + NT * u, a.np - 1)];
+      for (int u = 0; u < SEL / 4; ++u) bv[u] = ld16(bsrc + 4 * min((int)threadIdx.x + NT * u, a.np / 4 - 1));
 #pragma unroll
-    for (int u = 0; u < SEL; ++u) brow[threadIdx.x + NT * u] = bv[u];
+      for (int u = 0; u < SEL / 4; ++u) *reinterpret_cast<u32x4*>(brow + 4 * (threadIdx.x + NT * u)) = bv[u];
+    } else {
+      float bv[SEL];
+#pragma unroll
+      for (int u = 0; u < SEL; ++u) bv[u] = bsrc[min((int)threadIdx.x + NT * u, a.np - 1)];
+#pragma unroll
+      for (int u = 0; u < SEL; ++u) brow[threadIdx.x + NT * u] = bv[u];
+    }
     __syncthreads();
     uint32_t key[SEL];
 #pragma unroll
@@ -292,6 +302,7 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, c
   a.bound = nullptr;
   a.b_sb = a.b_sh = 0;
   a.np = 0;
+  a.b_vec = 0;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
   a.k = k;
@@ -349,6 +360,7 @@ int bytes_quest_gather_attn(const void* q, const void* k, const void* v, int kv_
   a.bound = static_cast<const float*>(bound);
   a.b_sb = b_sb; a.b_sh = b_sh;
   a.np = np;
+  a.b_vec = (reinterpret_cast<uintptr_t>(bound) % 16 == 0 && b_sb % 4 == 0 && b_sh % 4 == 0 && np % 4 == 0) ? 1 : 0;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh;
   a.k = k;

@@ -23,13 +23,12 @@ namespace bytes_amd {
 
 constexpr int kBins = 2048;            // digit = 11 bits of the order key
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(v, off, 64);
-    if (lane >= off) v += y;
-  }
-  return v;
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) { return wave_prefix_sum(v); }
+
+// Inclusive suffix sum over the 64 lanes (lane i: sum over lanes >= i).
+__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
+  const uint32_t incl = wave_prefix_sum(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) - incl + v;
 }
 
 template <int PER>
@@ -76,12 +75,7 @@ __device__ __forceinline__ void wave_select_threshold(const uint32_t (&key)[PER]
 #pragma unroll
     for (int b = 0; b < 32; ++b) s += c[b];
     // inclusive suffix sum over lanes (bins above this lane's range included)
-    uint32_t suf = s;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = __shfl_down(suf, off, 64);
-      if (lane + off < 64) suf += y;
-    }
+    const uint32_t suf = wave_suffix_sum(s);
     const uint32_t above_lane = suf - s;         // keys in digits above this lane's bins
     // digit d: count(digits > d) < kr <= count(digits >= d)
     const bool mine = above_lane < kr && kr <= suf;
@@ -97,8 +91,8 @@ __device__ __forceinline__ void wave_select_threshold(const uint32_t (&key)[PER]
       acc += c[b];
     }
     const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
-    d = __shfl(d, src, 64);
-    above = __shfl(above, src, 64);
+    d = (uint32_t)__builtin_amdgcn_readlane((int)d, src);
+    above = (uint32_t)__builtin_amdgcn_readlane((int)above, src);
     kr -= above;
     prefix |= d << shift;
     pmask |= dmask << shift;
@@ -142,8 +136,9 @@ __device__ __forceinline__ void wave_select_compact(const uint32_t (&key)[PER], 
 }
 
 // LDS words block_select_* need beside the kBins histogram.
+constexpr int kSelCand = 64;           // crossing-bin keys ranked directly by one wave
 template <int NT>
-constexpr int block_select_words() { return 4 * (NT / 64) + 2; }
+constexpr int block_select_words() { return 4 * (NT / 64) + 4 + kSelCand; }
 
 template <int NT, int PER>
 __device__ void block_select_threshold(const uint32_t (&key)[PER], int n, int k, uint32_t* hist, uint32_t* red,
@@ -154,7 +149,8 @@ __device__ void block_select_threshold(const uint32_t (&key)[PER], int n, int k,
   uint32_t* wa = red;
   uint32_t* wb = red + NW;
   uint32_t* wc = red + 2 * NW;
-  uint32_t* sel = red + 4 * NW;
+  uint32_t* sel = red + 4 * NW;                  // [4]: digit, count above, candidate count, result
+  uint32_t* cand = red + 4 * NW + 4;             // [kSelCand]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int i0 = PER * tid;
   auto valid = [&](int q) { return i0 + q < n; };
@@ -207,12 +203,7 @@ __device__ void block_select_threshold(const uint32_t (&key)[PER], int n, int k,
 #pragma unroll
     for (int b = 0; b < BPT; ++b) s += c[b];
     // inclusive suffix sum over the wave's lanes, then the waves above
-    uint32_t suf = s;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = (uint32_t)__shfl_down((int)suf, off, 64);
-      if (lane + off < 64) suf += y;
-    }
+    const uint32_t suf = wave_suffix_sum(s);
     if (lane == 0) wc[w] = suf;
     __syncthreads();
     uint32_t acc = suf - s;                      // keys in the bins above this thread's
@@ -225,13 +216,42 @@ __device__ void block_select_threshold(const uint32_t (&key)[PER], int n, int k,
       if (acc < kr && acc + c[b] >= kr) {
         sel[0] = (uint32_t)(BPT * tid + b);
         sel[1] = acc;
+        sel[2] = c[b];
       }
       acc += c[b];
     }
+    if (tid == 0) sel[3] = 0u;                   // candidate slots taken (the picked bin is not this thread's)
     __syncthreads();
     kr -= sel[1];
     prefix |= sel[0] << lo;
     pmask |= dmask << lo;
+    const uint32_t nc = sel[2];
+    if (lo > 0 && nc <= (uint32_t)kSelCand) {
+      // few keys in the crossing bin: list them, then one wave finds the kr-th
+      // largest by counting, for each candidate, the candidates above it
+#pragma unroll
+      for (int q = 0; q < PER; ++q)
+        if (valid(q) && (key[q] & pmask) == prefix) cand[atomicAdd(&sel[3], 1u)] = key[q];
+      __syncthreads();
+      if (w == 0) {
+        const uint32_t mine = lane < (int)nc ? cand[lane] : 0u;
+        uint32_t gt = 0u, ge = 0u;
+        for (uint32_t j = 0; j < nc; ++j) {
+          const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)mine, (int)j);
+          gt += o > mine ? 1u : 0u;
+          ge += o >= mine ? 1u : 0u;
+        }
+        if (lane < (int)nc && gt < kr && kr <= ge) {   // lanes holding the threshold agree
+          sel[0] = mine;
+          sel[1] = kr - gt;
+        }
+      }
+      __syncthreads();
+      T = sel[0];
+      need = sel[1];
+      __syncthreads();                           // sel is reused by the caller's next select
+      return;
+    }
   }
   T = prefix;
   need = kr;                                     // keys equal to T to take (>= 1), lowest indices first

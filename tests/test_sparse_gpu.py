@@ -112,6 +112,19 @@ def test_topk_small_rows(dev, rows, n, k):
                        R.topk_indices(s, k, sorted_by_score=False))
 
 
+@pytest.mark.parametrize("rows,n,k,shift", [(16, 3000, 150, 0.0), (16, 3000, 750, 0.0), (28, 2048, 128, 0.0),
+                                            (4, 1000, 999, 0.0), (28, 2048, 128, 40.0), (8, 4096, 1, 0.0)])
+def test_topk_small_rows_continuous(dev, rows, n, k, shift):
+    """Rows of distinct continuous scores (and the same shifted far from zero,
+    as page bounds sit): the digit pass that reaches a crossing bin of a few
+    keys ranks those keys directly; the result must equal the oracle's."""
+    g = torch.Generator().manual_seed(rows * n + k)
+    s = torch.randn(rows, n, generator=g) + shift
+    for so in (True, False):
+        got = SP.topk_indices(s.to(dev), k, sorted=so).cpu()
+        assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=so)), so
+
+
 @pytest.mark.parametrize("rows,n,k", [(300, 2048, 128), (28, 2048, 128), (280, 4096, 600), (5, 1000, 17)])
 def test_topk_narrow_range_rows(dev, rows, n, k):
     """Scores in a narrow range (every key shares its top bits; the digit
