@@ -300,7 +300,7 @@ class PqCase(Case):
     (q against the key codebooks) is part of the step, fused into the decode
     launch (decode_attn_pq_kv_fused, bit-identical to pq_build_lut followed by
     decode_attn_pq_lut_kv); codebook fitting and encoding are setup."""
-    kernel = "pq_decode_kernel"
+    kernel = "pq_group_kernel"
     family = 3
 
     def __init__(self, name, B=1, Hq=28, Hk=4, D=128, L=32768, K=256):

@@ -11,6 +11,13 @@
 // chunk of the rows it visits and keeps two batches of eight rows in flight;
 // the chunk sums are reduced through LDS in a fixed order.
 //
+// stream_read_kernel / empty_kernel: the floor probes the decode kernels are
+// measured against.  G workgroups each read their own contiguous slice of a
+// buffer in 16-byte loads, NL per thread in flight at a time, fold the words
+// and write one float per thread; empty_kernel is a launch that does nothing.
+// Together they give the fixed cost of a launch, the first HBM round trip and
+// the streaming-read ceiling at a given grid.
+//
 // packed_stage_kernel: the staged packed-score probe of
 // benchmarks/bench_unpack_ablation.py:19-53 (`_packed_stage_kernel`): per
 // (b, query head) and key row t of packed 4/2-bit keys (the layout of
@@ -87,6 +94,27 @@ __global__ __launch_bounds__(kGrThreads) void gather_reduce_kernel(const uint16_
     if (cc * 8 + i < D) out[(int64_t)h * D + cc * 8 + i] = s;
   }
 }
+
+constexpr int kSrThreads = 256;
+constexpr int kSrLoads = 8;         // 16-byte loads per thread in flight
+
+__global__ __launch_bounds__(kSrThreads) void stream_read_kernel(const u32x4* src, int64_t vec_per_wg, float* out) {
+  const u32x4* p = src + (int64_t)blockIdx.x * vec_per_wg;
+  uint32_t acc = 0;
+  for (int64_t base = 0; base < vec_per_wg; base += (int64_t)kSrThreads * kSrLoads) {
+    u32x4 r[kSrLoads];
+#pragma unroll
+    for (int i = 0; i < kSrLoads; ++i) {
+      const int64_t e = base + threadIdx.x + (int64_t)i * kSrThreads;
+      r[i] = ld16(p + (e < vec_per_wg ? e : vec_per_wg - 1));
+    }
+#pragma unroll
+    for (int i = 0; i < kSrLoads; ++i) acc ^= r[i][0] ^ r[i][1] ^ r[i][2] ^ r[i][3];
+  }
+  out[(int64_t)blockIdx.x * kSrThreads + threadIdx.x] = (float)acc;
+}
+
+__global__ __launch_bounds__(kSrThreads) void empty_kernel() {}
 
 constexpr int kPsThreads = 256;
 constexpr int kPsRowsPerThread = 4;
@@ -222,6 +250,23 @@ int bytes_packed_stage(const void* q, int64_t q_sb, int64_t q_sh, const void* kp
   }
 #undef PS_STAGES
 #undef PS
+  return (int)hipGetLastError();
+}
+
+
+// Floor probes (see stream_read_kernel): `wgs` workgroups of 256 threads read
+// bytes / wgs each from src (bytes a multiple of 16 * wgs; src 16-byte
+// aligned); out holds wgs * 256 floats.
+int bytes_stream_read(const void* src, int64_t bytes, int wgs, void* out, void* stream) {
+  if (!src || !out || wgs <= 0 || bytes <= 0 || bytes % (16LL * wgs) != 0) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)wgs), dim3(kSrThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src), bytes / 16 / wgs, static_cast<float*>(out));
+  return (int)hipGetLastError();
+}
+
+int bytes_empty_launch(int wgs, void* stream) {
+  if (wgs <= 0) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(empty_kernel, dim3((unsigned)wgs), dim3(kSrThreads), 0, static_cast<hipStream_t>(stream));
   return (int)hipGetLastError();
 }
 

@@ -58,3 +58,24 @@ def stage_score(q: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, zero
          packed.stride(2), ptr(scale), ptr(zero), scale.stride(0), scale.stride(1), scale.stride(2), ptr(out),
          out.stride(0), out.stride(1), B, Hq, Hk, S, D, bits, stage, stream_of(q))
     return out
+
+
+def stream_read(src: torch.Tensor, wgs: int, out: torch.Tensor = None) -> torch.Tensor:
+    """Floor probe: `wgs` workgroups of 256 threads read src (a contiguous
+    device tensor whose byte size is a multiple of 16 * wgs) in 16-byte loads,
+    one contiguous slice each; returns the fp32 fold [wgs * 256]."""
+    C.cuda_tensors(src)
+    if not src.is_contiguous():
+        raise ValueError("src must be contiguous")
+    nbytes = src.numel() * src.element_size()
+    if wgs <= 0 or nbytes % (16 * wgs) != 0 or src.data_ptr() % 16 != 0:
+        raise ValueError(f"{nbytes} bytes do not split into {wgs} slices of 16-byte words")
+    if out is None:
+        out = torch.empty(wgs * 256, dtype=torch.float32, device=src.device)
+    call("bytes_stream_read", ptr(src), nbytes, int(wgs), ptr(out), stream_of(src))
+    return out
+
+
+def empty_launch(wgs: int, device: torch.device) -> None:
+    """Floor probe: a launch of `wgs` workgroups of 256 threads that do nothing."""
+    call("bytes_empty_launch", int(wgs), torch.cuda.current_stream(device).cuda_stream)

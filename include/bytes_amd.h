@@ -312,6 +312,16 @@ int bytes_packed_stage(const void* q, int64_t q_sb, int64_t q_sh, const void* kp
                        void* out, int64_t o_sb, int64_t o_sh, int B, int Hq, int Hk, int S, int D, int bits,
                        int stage, void* stream);
 
+/* Floor probes: the fixed cost of a launch, the first HBM round trip and the
+ * streaming-read ceiling the decode kernels are measured against (no
+ * counterpart in the reference; they bound what its decode paths can reach
+ * on MI355X).  bytes_stream_read: `wgs` workgroups of 256 threads each read
+ * bytes / wgs contiguous bytes of src in 16-byte loads (bytes a multiple of
+ * 16 * wgs, src 16-byte aligned), out [wgs * 256] fp32 (a fold of the words
+ * read).  bytes_empty_launch: `wgs` workgroups that do nothing. */
+int bytes_stream_read(const void* src, int64_t bytes, int wgs, void* out, void* stream);
+int bytes_empty_launch(int wgs, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Product-quantized decode with paged caches, outlier channels and fp8 values.
  * Replaces src/attention_kernels.py:

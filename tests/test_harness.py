@@ -3,7 +3,7 @@ counts exactly the bytes of the tensors the reference's capacity study
 allocates (benchmarks/bench_sparse_capacity.py:46-83)."""
 import torch
 
-from bytes_amd.harness import access_pattern, capacity, crossover, kernels, score_ablation, timing, unpack_ablation  # noqa: F401,E501
+from bytes_amd.harness import access_pattern, capacity, crossover, floor, kernels, score_ablation, timing, unpack_ablation  # noqa: F401,E501
 
 
 def _nbytes(*shapes_dtypes):
