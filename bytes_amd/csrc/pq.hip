@@ -17,15 +17,18 @@
 //   codes [B, Hk, S, M] uint8 (unit stride along M)
 //   codebooks fp16 [Hk or 1, M, K, 8] contiguous (per-KV-head or shared)
 //
-// Decode: a unit is (b, kv head, group of up to 4 query heads); its token axis
-// is cut into split-K chunks.  A workgroup stages the group's LUTs in LDS (for
-// dequant mode it builds them there from q and the key codebook: one 8-term
-// dot per entry, so q.k_hat is evaluated subspace by subspace) and, for
-// quantized values, the head's value codebook.  Per 32-token tile a wave sums
-// 16 LUT entries per (token, head) into the score-MFMA layout, runs the fp32
-// online softmax, rebuilds the V tile in LDS (16-byte codebook rows selected by
-// the value codes, or the bf16 V rows themselves), and accumulates O^T += V^T P^T
-// on MFMA, as the dense kernel does.
+// Decode, general kernel (pq_decode_kernel: every mode, paged caches,
+// outliers, any G): a unit is (b, kv head, group of up to 4 query heads); its
+// token axis is cut into split-K chunks.  A workgroup stages the group's LUTs
+// in LDS (for the q + codebook modes it builds them there on MFMA, entry for
+// entry as pq_lut_kernel) and, for quantized values, the head's value
+// codebook.  Per 32-token tile a wave sums M LUT entries per (token, head) into
+// the score-MFMA layout, runs the fp32 online softmax and accumulates
+// O^T += V^T P^T on MFMA, as the dense kernel does.  Quantized V is never
+// materialised: the transposed PV reads address the codebook row of each
+// lane's token directly; dense (bf16 / fp8) V rows are staged per tile.
+// Modes 0 and 3 with G <= 8 and no outliers or paging run the grouped kernel
+// (pq_group_kernel, below) instead.
 //
 // Paged caches (block_table [B, max_blocks] int32, context_lens [B] int32):
 // token t of sequence b is row t % bs of block block_table[b][t / bs]; the
@@ -321,8 +324,9 @@ __device__ __forceinline__ void pq_stage_dense_v(int lane, const PqRegs<D, QV, V
 // half l/32 of the subspaces for the four heads at once (LUTs are kept
 // [subspace][code][head], one 16-byte read per subspace), the halves are
 // added, the wave passes the scores through its tile buffer into the
-// score-MFMA layout (head l%16, rows blk*16 + lg*4 + i), then the V tile is
-// built in the same buffer and the softmax/PV step runs.
+// score-MFMA layout (head l%16, rows blk*16 + lg*4 + i) and the softmax/PV
+// step runs: quantized V straight from the codebook in LDS, dense V staged in
+// the same buffer first.
 template <int D, bool QV, bool VF8, bool OUT>
 __device__ __forceinline__ void pq_tile(const PqArgs& a, const PqRegs<D, QV, VF8, OUT>& r, uint32_t vmask, int lane,
                                         int nh, const float* lut, const char* vcb, const float* qo, char* vst,
