@@ -51,6 +51,28 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// Division by a run-time constant d >= 1, for numerators n in [0, 2^31):
+// floor(n / d) = (mulhi(m, n) + n) >> l with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1 (the round-up method of Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994).
+// The host sets it up once per launch; on the device a quotient costs two
+// scalar instructions instead of a reciprocal-and-correct sequence.
+struct FastDiv {
+  uint32_t m = 1, l = 0, d = 1;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d < 1 ? 1 : d;
+  uint32_t l = 0;
+  while ((1ull << l) < f.d) ++l;
+  f.l = l;
+  f.m = (uint32_t)((((1ull << l) - f.d) << 32) / f.d + 1);
+  return f;
+}
+__device__ __forceinline__ int fast_div(int n, const FastDiv& f) {
+  return (int)((__umulhi(f.m, (uint32_t)n) + (uint32_t)n) >> f.l);
+}
+
 // fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

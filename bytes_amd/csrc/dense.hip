@@ -45,11 +45,8 @@ __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(Dense
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  int unit, split;
-  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
-  const int b = unit / (a.Hk * a.HB);
-  const int rem = unit - b * a.Hk * a.HB;
-  const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
+  const UnitLoc loc = splitk_locate(a.o);
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk, hb = loc.hb;
   const int hq0 = hk * a.G + hb * 16;
   const int nh = min(16, a.G - hb * 16);
 

@@ -48,6 +48,7 @@ struct GatherArgs {
   int np;
   int b_vec;                 // every bound row starts 16-byte aligned and np % 4 == 0
   float scale_log2;
+  FastDiv dG;                // division by G
   SplitKOut o;
 };
 
@@ -108,24 +109,22 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
   __shared__ __attribute__((aligned(16))) char smem_raw[GatherCfg<D>::kSmem];
   int32_t* rows = reinterpret_cast<int32_t*>(smem_raw + C::kSmem);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int unit, split;
-  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
+  // per-head units are (b, query head): the split grid's "kv heads" are the
+  // query heads (o.Hk = Hq, o.HB = 1) and the kv head is hq / G
+  const UnitLoc loc = splitk_locate(a.o);
+  const int unit = loc.unit, split = loc.split;
 
-  int b, hk, hq0, nh;
+  int b = loc.b, hk, hq0, nh;
   const int32_t* irow;
   if (a.per_head) {
-    const int Hq = a.Hk * a.G;
-    b = unit / Hq;
-    const int hq = unit - b * Hq;
-    hk = hq / a.G;
+    const int hq = loc.hk;
+    hk = fast_div(hq, a.dG);
     hq0 = hq;
     nh = 1;
     irow = a.idx + (int64_t)b * a.i_sb + (int64_t)hq * a.i_sh;
   } else {
-    b = unit / (a.Hk * a.HB);
-    const int rem = unit - b * a.Hk * a.HB;
-    hk = rem / a.HB;
-    const int hb = rem - hk * a.HB;
+    hk = loc.hk;
+    const int hb = loc.hb;
     hq0 = hk * a.G + hb * 16;
     nh = min(16, a.G - hb * 16);
     irow = a.idx + (int64_t)b * a.i_sb + (int64_t)hk * a.i_sh;
@@ -313,6 +312,7 @@ int bytes_gather_attn(const void* q, const void* k, const void* v, int kv_fp8, c
   a.i_sb = i_sb; a.i_sh = i_sh;
   a.Hk = Hk; a.G = Hq / Hk; a.HB = (a.G + 15) / 16; a.S = S; a.kb = kb;
   a.per_head = per_head ? 1 : 0;
+  a.dG = make_fastdiv((uint32_t)a.G);
   a.scale_log2 = scaling * kLog2e;
   int ns;
   gather_plan(kb, units, chunk_req, &a.chunk, &ns);
@@ -371,6 +371,7 @@ int bytes_quest_gather_attn(const void* q, const void* k, const void* v, int kv_
   a.i_sb = a.i_sh = 0;
   a.Hk = Hk; a.G = Hq / Hk; a.HB = (a.G + 15) / 16; a.S = S; a.kb = kb;
   a.per_head = 1;
+  a.dG = make_fastdiv((uint32_t)a.G);
   a.scale_log2 = scaling * kLog2e;
   int ns;
   gather_plan(kb, units, chunk_req, &a.chunk, &ns);

@@ -158,7 +158,12 @@ struct KiviCfg {
   static constexpr int NGV = D / 32;                        // value groups per token
   static constexpr int VMBYTES = 2 * kKiviTile * NGV * 2;   // value scale + zero of one tile
   static constexpr int WAVE_BYTES = VBYTES + VMBYTES;
-  static constexpr int kQuant = KCBYTES + KMETA + NW * WAVE_BYTES;
+  // Q of the unit's 16 head columns as the fp16 B operand (scaled, k-slot
+  // order within each 8-channel chunk), staged once per workgroup: row pitch
+  // D*2 + 16 bytes so the 16 head rows a 16-lane group reads sit in distinct banks
+  static constexpr int QP = D * 2 + 16;
+  static constexpr int QOFF = KCBYTES + KMETA + NW * WAVE_BYTES;
+  static constexpr int kQuant = QOFF + 16 * QP;
   static constexpr int kDense = DenseCfg<D>::kSmem;        // residual tiles of waves 0-3 (and their merge)
   static constexpr int kEpi = splitk_smem_floats<D, NW>() * 4;
   static constexpr int kSmem0 = kQuant > kDense ? kQuant : kDense;
@@ -253,25 +258,33 @@ using VMetaReg = typename std::conditional<(D >= 128), u32x4, u32x2>::type;
 template <int D, int BITS>
 struct KiviRegs {
   u32x4 v[KiviCfg<D, BITS>::VDMA];
-  VMetaReg<D> vm;
+  VMetaReg<D> vm;         // value scales (lanes 0-31) / zeros (32-63) of two tokens
 };
 
-// Issue the value loads of the tile at o into registers (a dummy when !live:
-// same instructions, every lane reading the first bytes), so control flow
-// stays uniform and the compiler waits for exactly the registers it uses.
-// Value codes and value scales/zeros of a tile are contiguous in HBM.
+// Buffer resources over one unit's quantized cache.  A split without
+// quantized tokens gets zero-sized resources: its requests are issued like
+// any other (every wait counts the same requests on every path) and read
+// zeros without touching memory.  Offsets are 32-bit (a unit's cache is far
+// below 4 GiB), so every request is a buffer load with a per-lane offset
+// computed once and a uniform offset in a scalar register.
+struct KiviRsrc {
+  __amdgpu_buffer_rsrc_t kq, ks, kz, vq;
+  const char* vs;          // the unit's value scales and zeros (a readable dummy when
+  const char* vz;          // the split has no quantized tokens)
+};
+
+// Issue the value loads of the tile at token o into registers.  Value codes
+// and value scales/zeros of a tile are contiguous in HBM; lanes 0-31 take the
+// scales and lanes 32-63 the zeros of tokens o + 2(l % 32), +1.
 template <int D, int BITS>
-__device__ __forceinline__ void kivi_issue(const uint32_t* vqb, const _Float16* vsb, const _Float16* vmb, int o,
-                                           bool live, int lane, KiviRegs<D, BITS>& r) {
+__device__ __forceinline__ void kivi_issue(const KiviRsrc& rs, bool quant, int o, int lane, KiviRegs<D, BITS>& r) {
   using C = KiviCfg<D, BITS>;
-  const char* vsrc = reinterpret_cast<const char*>(vqb) + (int64_t)o * C::VROW;
+  const int vo = o * C::VROW;
 #pragma unroll
-  for (int i = 0; i < C::VDMA; ++i) {
-    const char* src = live ? vsrc + (lane + 64 * i) * 16 : reinterpret_cast<const char*>(vqb);
-    r.v[i] = ld16(src);
-  }
-  const _Float16* mp = (lane < 32 ? vsb : vmb) + (int64_t)(o + 2 * (lane & 31)) * C::NGV;
-  r.vm = *reinterpret_cast<const VMetaReg<D>*>(live ? mp : vsb);
+  for (int i = 0; i < C::VDMA; ++i)
+    r.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vq, lane * 16 + i * 1024, vo, 0));
+  const char* mb = lane < 32 ? rs.vs : rs.vz;
+  r.vm = *reinterpret_cast<const VMetaReg<D>*>(mb + (quant ? (uint32_t)(o + 2 * (lane & 31)) * C::NGV * 2 : 0u));
 }
 
 // Write one tile's prefetched value codes and scales/zeros to the wave's LDS buffers.
@@ -657,11 +670,8 @@ __global__ __launch_bounds__(kKsWaves * 64, 1) void kivi_stream_kernel(KiviArgs 
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  int unit, split;
-  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
-  const int b = unit / (a.Hk * a.HB);
-  const int rem = unit - b * a.Hk * a.HB;
-  const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
+  const UnitLoc loc = splitk_locate(a.o);
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk, hb = loc.hb;
   const int hq0 = hk * a.G + hb * 16;
   const int nh = min(16, a.G - hb * 16);
   const uint16_t* qrow0 = a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh;
@@ -867,13 +877,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   using C = KiviCfg<D, BITS, NW>;
   PREFETCH_ARGS(a);
   __shared__ __attribute__((aligned(16))) char smem_raw[C::kSmem];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int l16 = lane & 15, lg = lane >> 4;
-  int unit, split;
-  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
-  const int b = unit / (a.Hk * a.HB);
-  const int rem = unit - b * a.Hk * a.HB;
-  const int hk = rem / a.HB, hb = rem - (rem / a.HB) * a.HB;
+  const UnitLoc loc = splitk_locate(a.o);
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk, hb = loc.hb;
   const int hq0 = hk * a.G + hb * 16;
   const int nh = min(16, a.G - hb * 16);
   const uint16_t* qrow0 = a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh;
@@ -897,8 +904,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   const int r_end = min(r_begin + (resid_only ? kResidPerSplit : a.rchunk), a.R);
   const bool resid_first = a.rsplit == 0 && a.R > 0 && r_begin < r_end;
   const bool resid = resid_only || resid_first;
-  const uint16_t* rkbase = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
-  const uint16_t* rvbase = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
   static_assert(kResidPerSplit == 4 * kTile && NW >= 4, "one residual tile per wave of waves 0-3");
   const int rt = r_begin + w * kTile;
   // Lanes of head columns past nh load head hq0's query instead of zeros:
@@ -909,8 +914,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   u32x4 qbraw[D / 32];
   const bool qlive = l16 < nh;
   const bool rtile = resid && rt < r_end;         // this wave has a residual tile
+  // residual rows (the bases are computed where the residual is used)
+  auto resid_k = [&]() { return a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh; };
+  auto resid_v = [&]() { return a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh; };
   auto issue_resid = [&]() {
-    dense_issue<D>(rkbase, rvbase, a.kr_ss, a.vr_ss, a.R, rt, r_end, lane, rr);
+    dense_issue<D>(resid_k(), resid_v(), a.kr_ss, a.vr_ss, a.R, rt, r_end, lane, rr);
     const uint16_t* qp = qrow0 + (int64_t)(qlive ? l16 : 0) * a.q_sh + lg * 8;
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk) qbraw[kk] = ld16(qp + kk * 32);
@@ -922,7 +930,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   const bool quant = t_begin < t_end;
   const int g_lo = t_begin >> 5;
   const int ngs = (t_end - t_begin) >> 5;        // even: splits are multiples of 64 tokens
-  const int64_t bh = (int64_t)b * a.Hk + hk;
+  const uint32_t bh = (uint32_t)(b * a.Hk + hk);
   const int ngk = Sq >> 5;
 
   char* kchunk = smem_raw;
@@ -934,15 +942,31 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   // same requests whatever the path (the counts of a wait after paths that
   // issued different requests are those of the shortest).  A split without
   // quantized tokens (a residual-only split, or Sq == 0 with no quantized
-  // cache at all) requests 16 bytes at its own query row instead.
-  const void* dummy = qrow0;
-  const uint32_t* vqb = quant ? a.vq + bh * (int64_t)Sq * (D * BITS / 32) : static_cast<const uint32_t*>(dummy);
-  const _Float16* vsb = quant ? a.vs + bh * (int64_t)Sq * C::NGV : static_cast<const _Float16*>(dummy);
-  const _Float16* vmb = quant ? a.vm + bh * (int64_t)Sq * C::NGV : static_cast<const _Float16*>(dummy);
+  // cache at all) requests through zero-sized resources and reads zeros.
+  const uint32_t wkb = (uint32_t)Sq * BITS / 8;    // bytes per key channel row
+  const uint32_t mrb = (uint32_t)ngk * 2;          // bytes per key scale/zero row
+  // a unit's part of each tensor: unit bytes (32-bit) times the unit index
+  auto at = [&](const void* p, uint32_t unit_bytes) {
+    return static_cast<const char*>(p) + (uint64_t)bh * unit_bytes;
+  };
+  const uint32_t kq_u = D * wkb, km_u = D * mrb, vq_u = (uint32_t)Sq * C::VROW, vm_u = (uint32_t)Sq * C::NGV * 2;
+  KiviRsrc rs;
+  rs.kq = buf_rsrc(at(a.kq, kq_u), quant ? kq_u : 0u);
+  rs.ks = buf_rsrc(at(a.ks, km_u), quant ? km_u : 0u);
+  rs.kz = buf_rsrc(at(a.km, km_u), quant ? km_u : 0u);
+  rs.vq = buf_rsrc(at(a.vq, vq_u), quant ? vq_u : 0u);
+  rs.vs = quant ? at(a.vs, vm_u) : reinterpret_cast<const char*>(qrow0);
+  rs.vz = quant ? at(a.vm, vm_u) : reinterpret_cast<const char*>(qrow0);
 
   // Q as the fp16 B operand (scaled by scale*log2e):
-  //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)].
-  u32x4 qraw[D / 32];
+  //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)],
+  // read from the workgroup's staged copy: thread t < 16 * D/8 loads chunk
+  // t % (D/8) of head column t / (D/8) (columns past nh take head hq0's row;
+  // their results are never stored).
+  constexpr int QT = 16 * (D / 8);
+  const int qt = min((int)threadIdx.x, QT - 1);
+  const int qh_col = qt / (D / 8), qc = qt % (D / 8);
+  u32x4 qraw1;
 
   // The chunk is staged in two halves of C::CHUNK/2 tokens, each the
   // first (ph = 0) or second (ph = 1) tile of every wave.
@@ -956,43 +980,46 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   constexpr int PERH = D * HP / NT;                // key pieces per thread per half
   constexpr int WRH = C::KMG / 4;                  // meta words per (scale|zero, channel) per half
   constexpr int PERMH = 2 * D * WRH / NT;
+  static_assert(NT % HP == 0 && NT / WRH == 64 && D % 64 == 0, "row blocks of the staging loops");
   const int pieces = quant ? (t_end - t_begin) * BITS / 128 : 1;
   const int nwr = quant ? ngs >> 1 : 1;
-  const uint32_t* kqb =
-      quant ? a.kq + (bh * D) * (int64_t)(Sq * BITS / 32) + t_begin * BITS / 32 : static_cast<const uint32_t*>(dummy);
-  const int64_t wk = quant ? Sq * BITS / 32 : 0;
-  const int64_t mrow = quant ? ngk : 0;           // key scale/zero row stride (0: dummy)
-  const _Float16* ksb = quant ? a.ks + g_lo : static_cast<const _Float16*>(dummy);
-  const _Float16* kmb = quant ? a.km + g_lo : static_cast<const _Float16*>(dummy);
+  // per-thread parts of the offsets: thread t takes piece t % HP of key
+  // channel row t / HP (+ NT / HP rows per step i) and word t % WRH of meta
+  // row t / WRH (+ 64 rows per step, scales then zeros)
+  const int tid = threadIdx.x;
+  const uint32_t krow = (uint32_t)(tid / HP) * wkb, kpc = tid % HP;
+  const uint32_t mrow = (uint32_t)(tid / WRH) * mrb, mwd = tid % WRH;
+  const uint32_t ksplit = (uint32_t)t_begin * BITS / 8, msplit = (uint32_t)g_lo * 2;
   const int tw = t_begin + w * kKiviTile;
   u32x4 kv[NTW][PERH];
   uint32_t mv[NTW][PERMH];
   KiviRegs<D, BITS> rg[NTW];
+  // A half's requests: this wave's value tile first, then the workgroup's key
+  // codes and scales/zeros, so that the value tile has arrived by the time
+  // the barrier after the key staging lets the wave go on to its tile.
   auto issue = [&](auto phc) {
     constexpr int ph = decltype(phc)::value;
+    const int t = tw + ph * STEP;
+    kivi_issue<D, BITS>(rs, quant, t < t_end ? t : t_begin, lane, rg[ph]);
+    __builtin_amdgcn_sched_barrier(0);
+    const int ko = krow + min(ph * HP + (int)kpc, pieces - 1) * 16;
 #pragma unroll
-    for (int i = 0; i < PERH; ++i) {
-      const int pc = threadIdx.x + NT * i;
-      const int ch = pc / HP, q = ph * HP + (pc - (pc / HP) * HP);
-      kv[ph][i] = ld16(kqb + ch * wk + min(q, pieces - 1) * 4);
-    }
+    for (int i = 0; i < PERH; ++i)
+      kv[ph][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kq, ko, (int)(ksplit + i * (NT / HP) * wkb), 0));
+    const int mo = mrow + min(ph * WRH + (int)mwd, nwr - 1) * 4;
 #pragma unroll
     for (int i = 0; i < PERMH; ++i) {
-      const int pc = threadIdx.x + NT * i;
-      const int row = pc / WRH, wi = ph * WRH + (pc - (pc / WRH) * WRH);
-      const int sm = row / D, ch = row - sm * D;
-      const uint32_t* src = reinterpret_cast<const uint32_t*>((sm ? kmb : ksb) + (bh * D + ch) * mrow);
-      mv[ph][i] = src[min(wi, nwr - 1)];
+      const int r0 = (i * 64) % D;                 // first channel of this step's rows
+      const uint32_t so = msplit + (uint32_t)r0 * mrb;
+      mv[ph][i] = (i * 64) / D ? __builtin_amdgcn_raw_buffer_load_b32(rs.kz, mo, (int)so, 0)
+                               : __builtin_amdgcn_raw_buffer_load_b32(rs.ks, mo, (int)so, 0);
     }
-    const int t = tw + ph * STEP;
-    kivi_issue<D, BITS>(vqb, vsb, vmb, t < t_end ? t : 0, t < t_end, lane, rg[ph]);
     // keep the compiler from moving requests across this point
     __builtin_amdgcn_sched_barrier(0);
   };
   auto issue_first = [&]() {
-    const uint16_t* qp = qrow0 + (int64_t)(qlive ? l16 : 0) * a.q_sh + lg * (D / 4);
-#pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) qraw[kk] = ld16(qp + kk * 8);
+    qraw1 = ld16(qrow0 + (int64_t)(qh_col < nh ? qh_col : 0) * a.q_sh + qc * 8);
     issue(std::integral_constant<int, 0>());
   };
   issue_first();
@@ -1000,13 +1027,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
 
 
   if (quant) {
-    f16x8 qh[D / 32];
+    char* qlds = smem_raw + C::QOFF;
+    {
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, qraw1);
+      f16x8 qo;
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) {
-      const bf16x8 qv = __builtin_bit_cast(bf16x8, qraw[kk]);
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
+      for (int jj = 0; jj < 8; ++jj) qo[jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
+      if ((int)threadIdx.x < QT) *reinterpret_cast<f16x8*>(qlds + qh_col * C::QP + qc * 16) = qo;
     }
+    f16x8 qh[D / 32];
 
     _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
     f32x4 zv = {0.f, 0.f, 0.f, 0.f};   // value zero term: row g = value group, column = head
@@ -1032,6 +1061,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
         dst[C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
       }
       __syncthreads();
+      if (ph == 0) {
+#pragma unroll
+        for (int kk = 0; kk < D / 32; ++kk)
+          qh[kk] = *reinterpret_cast<const f16x8*>(qlds + l16 * C::QP + (lg * (D / 32) + kk) * 16);
+      }
       // The second half is requested only once the first has arrived: every
       // workgroup's first half then reaches the head of the memory queues
       // before any second half, and the second half streams in while the

@@ -407,11 +407,8 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
   float* lut = reinterpret_cast<float*>(smem_raw);
   char* vcb = smem_raw + C::LUT;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int unit, split;
-  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
-  const int b = unit / (a.Hk * a.HG);
-  const int rem = unit - b * a.Hk * a.HG;
-  const int hk = rem / a.HG, hg = rem - (rem / a.HG) * a.HG;
+  const UnitLoc loc = splitk_locate(a.o);     // head blocks of kPqHeads: o.HB = HG
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk, hg = loc.hb;
   const int hq0 = hk * a.G + hg * kPqHeads;
   const int nh = min(kPqHeads, a.G - hg * kPqHeads);
 
@@ -611,9 +608,8 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
   float* lsum = hsm + 16;
   f32x4* acc2 = reinterpret_cast<f32x4*>(smem + C::VCB + C::PS);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  int unit, split;
-  xcd_unit_split(a.o.nsplit, a.o.nwg, unit, split);
-  const int b = unit / a.Hk, hk = unit - (unit / a.Hk) * a.Hk;
+  const UnitLoc loc = splitk_locate(a.o);     // o.HB = 1: unit = b * Hk + hk
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk;
   const int G = a.G, hq0 = hk * G, K = a.K;
   const int len = pq_len(a, b);
   const int t_begin = split * a.chunk;

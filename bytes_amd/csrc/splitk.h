@@ -27,6 +27,7 @@ struct SplitKOut {
   int Hk, HB, G;        // unit u -> b = u / (Hk*HB), hk, hb; query head = hk*G + hb*hbs + h
   int hbs = 16;         // query heads per head block
   int nwg = 0;          // workgroups of the split grid (units * nsplit)
+  FastDiv dsplit, dunit, dhb;   // division by nsplit, Hk * HB and HB (set by splitk_carve)
 };
 
 constexpr long kMaxUnits = 65535;         // grid.y limit
@@ -46,6 +47,9 @@ inline void splitk_carve(void* ws, long units, long nsplit, SplitKOut& o) {
   o.part_acc = reinterpret_cast<float*>(p + ml);
   o.nsplit = (int)nsplit;
   o.nwg = (int)(units * nsplit);
+  o.dsplit = make_fastdiv((uint32_t)nsplit);
+  o.dunit = make_fastdiv((uint32_t)(o.Hk * o.HB));
+  o.dhb = make_fastdiv((uint32_t)o.HB);
 }
 
 // Workgroups of a 1-D grid are dealt round-robin over the XCDs (8 on MI355X),
@@ -61,6 +65,26 @@ __device__ __forceinline__ void xcd_unit_split(int nsplit, int N, int& unit, int
   const int idx = x * q + min(x, r) + k;
   unit = idx / nsplit;
   split = idx - unit * nsplit;
+}
+
+// The same mapping with the divisions set up on the host, and the unit's
+// (b, hk, hb): unit = (b * Hk + hk) * HB + hb.
+struct UnitLoc {
+  int unit, split, b, hk, hb;
+};
+__device__ __forceinline__ UnitLoc splitk_locate(const SplitKOut& o) {
+  const int L = blockIdx.x;
+  const int x = L % kXcds, k = L / kXcds;
+  const int q = o.nwg / kXcds, r = o.nwg % kXcds;
+  const int idx = x * q + min(x, r) + k;
+  UnitLoc u;
+  u.unit = fast_div(idx, o.dsplit);
+  u.split = idx - u.unit * o.nsplit;
+  u.b = fast_div(u.unit, o.dunit);
+  const int rem = u.unit - u.b * (int)o.dunit.d;
+  u.hk = fast_div(rem, o.dhb);
+  u.hb = rem - u.hk * (int)o.dhb.d;
+  return u;
 }
 
 

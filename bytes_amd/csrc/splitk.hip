@@ -50,9 +50,9 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o, XcdUnit
   if (unit >= xm.first[x + 1]) return;
   const int rw = kk - uk * wu;
   const int h = rw / NSL, slice = rw - h * NSL;
-  const int b = unit / (o.Hk * o.HB);
+  const int b = fast_div(unit, o.dunit);
   const int rem = unit - b * o.Hk * o.HB;
-  const int hk = rem / o.HB, hb = rem - (rem / o.HB) * o.HB;
+  const int hk = fast_div(rem, o.dhb), hb = rem - hk * o.HB;
   const int nh = min(o.hbs, o.G - hb * o.hbs);
   if (h >= nh) return;
   const int lane = threadIdx.x, item = lane % kCombItems, g = lane / kCombItems;
