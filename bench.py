@@ -296,10 +296,11 @@ class QuestCase(Case):
 
 
 class PqCase(Case):
-    """BASELINE C3: PQ-LUT decode with quantized keys and values.  The LUT build
-    (q against the key codebooks) is part of the step, fused into the decode
-    launch (decode_attn_pq_kv_fused, bit-identical to pq_build_lut followed by
-    decode_attn_pq_lut_kv); codebook fitting and encoding are setup."""
+    """BASELINE C3: PQ-LUT decode with quantized keys and values.  Scoring q
+    against the key codebooks is part of the step, fused into the decode launch
+    (decode_attn_pq_kv_fused: q . k_hat on MFMA from the codebook rows, within
+    the attention tolerance of pq_build_lut followed by decode_attn_pq_lut_kv);
+    codebook fitting and encoding are setup."""
     kernel = "pq_group_kernel"
     family = 3
 

@@ -27,8 +27,8 @@
 // O^T += V^T P^T on MFMA, as the dense kernel does.  Quantized V is never
 // materialised: the transposed PV reads address the codebook row of each
 // lane's token directly; dense (bf16 / fp8) V rows are staged per tile.
-// Modes 0 and 3 with G <= 8 and no outliers or paging run the grouped kernel
-// (pq_group_kernel, below) instead.
+// Modes 0 and 3 with G <= 8 and no outliers (contiguous or paged caches) run
+// the grouped kernel (pq_group_kernel, below) instead.
 //
 // Paged caches (block_table [B, max_blocks] int32, context_lens [B] int32):
 // token t of sequence b is row t % bs of block block_table[b][t / bs]; the
@@ -178,7 +178,7 @@ __device__ __forceinline__ bool lut_need_lo(const f16x8& lo) {
 // or past nh are zero with multiplier zero.  q0 points at head 0's row.
 template <int D>
 struct LutQ {
-  float x[D / 64];
+  uint32_t x[D / 64];      // raw bf16 bits, one value per word (rows past nh are zeroed where they are stored)
 };
 
 template <int D>
@@ -188,7 +188,7 @@ __device__ __forceinline__ LutQ<D> lut_load_q(const uint16_t* q0, int64_t q_sh, 
   const uint16_t* row = q0 + (int64_t)min(h, nh - 1) * q_sh + lane * PL;
   LutQ<D> r;
 #pragma unroll
-  for (int p = 0; p < PL; ++p) r.x[p] = h < nh ? bf16_bits_to_f32(row[p]) : 0.f;
+  for (int p = 0; p < PL; ++p) r.x[p] = row[p];
   return r;
 }
 
@@ -197,14 +197,17 @@ __device__ __forceinline__ void lut_store_q(const LutQ<D>& r, int h, int nh, flo
                                             float* mul) {
   constexpr int PL = D / 64;
   const int lane = threadIdx.x & 63;
+  float x[PL];
+#pragma unroll
+  for (int p = 0; p < PL; ++p) x[p] = h < nh ? __uint_as_float(r.x[p] << 16) : 0.f;
   float amax = 0.f;
 #pragma unroll
-  for (int p = 0; p < PL; ++p) amax = fmaxf(amax, fabsf(r.x[p]));
+  for (int p = 0; p < PL; ++p) amax = fmaxf(amax, fabsf(x[p]));
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, shfl_xor_f(amax, o));
   const int k = lut_shift(amax);
 #pragma unroll
-  for (int p = 0; p < PL; ++p) qs[h * D + lane * PL + p] = ldexpf(r.x[p], -k);
+  for (int p = 0; p < PL; ++p) qs[h * D + lane * PL + p] = ldexpf(x[p], -k);
   if (lane == 0) mul[h] = h < nh ? ldexpf(lut_scale, k) : 0.f;
 }
 
@@ -548,13 +551,19 @@ __global__ __launch_bounds__(kPqWaves * 64, 1) void pq_decode_kernel(PqArgs a) {
 // (b, kv head) with all G of its query heads, so every token's codes are read
 // once and its per-token work is shared by the whole group.  A workgroup takes
 // a chunk of <= kPqgChunk tokens; phases A and B reuse one LDS region:
-//   A. the unit's LUTs (fp32, [head quad][subspace][code][4 heads]: a code's
-//      entries for four heads are one 16-byte read, and a wave's reads of
-//      random codes spread over all 16 16-byte bank slots; built on MFMA from
-//      q and the key codebook, or the caller's LUT transposed) are resident;
-//      thread i scores token i of the chunk for every head, summing the M
-//      entries in subspace order, and stores the scores and the token's value
-//      codes;
+//   A. scores of every (token, head) of the chunk, by one of two routes:
+//      SRC 0 (the caller's LUT): the unit's LUTs (fp32, [head quad][subspace]
+//      [code][4 heads]: a code's entries for four heads are one 16-byte read,
+//      and a wave's reads of random codes spread over all 16 16-byte bank
+//      slots) are resident; thread i scores token i for every head, summing
+//      the M entries in subspace order;
+//      SRC 2 (q and the key codebook): the key codebook is resident and the
+//      scores are q . k_hat on v_mfma_f32_16x16x32_f16, whose A operand (a
+//      token's 8 channels of one subspace) is exactly the codeword its code
+//      selects: each lane reads that 16-byte codebook row, no LUT is formed;
+//      q enters as the B operand in the LUT's scaled hi/lo form, so every
+//      product is exact and the sums run in fp32;
+//      the scores and the tokens' value codes are stored;
 //   B. the value codebook replaces the LUTs.  The chunk's per-head maximum is
 //      known, so each wave turns its 32-token tiles straight into fp16
 //      probabilities (no running rescale), stored in MFMA operand order; then
@@ -575,6 +584,9 @@ struct PqgCfg {
   static constexpr int PS = NT * 64 * 16;                      // B: fp16 probabilities, [tile][lane] x 8
   static constexpr int A2 = (kPqWaves - D / 32) * 2 * 64 * 16;  // B: accumulators of tile groups past 0
   static constexpr int X = LUT > VCB + PS + A2 ? LUT : VCB + PS + A2;
+  static constexpr int KCB = M * kPqKMax * 8 * 2;              // A (SRC 2): fp16 key codebook
+  static_assert(KCB <= LUT, "the key codebook fits the LUT area");
+  static_assert(kPqgChunk * 16 + HP * D * 4 <= PS, "SRC 2 staging: key codes and q rows fit the probability area");
   static constexpr int SC = HP * kPqgChunk * 4;                // scores [HP][chunk]
   static constexpr int VC = kPqgChunk * M;                     // value codes [chunk][M]
   static constexpr int HS = 16 * 4;                            // per-head multipliers, then maxima
@@ -594,8 +606,9 @@ __device__ __forceinline__ u32x4 ld_codes(const uint8_t* p) {
   }
 }
 
-template <int D, bool BUILD_LUT, int HP>
+template <int D, int SRC, int HP, bool PAGED>
 __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
+  static_assert(SRC == 0 || SRC == 2, "scores from the caller's LUT or from q and the key codebook");
   using C = PqgCfg<D, HP>;
   constexpr int M = D / 8;
   __shared__ __attribute__((aligned(16))) char smem[C::kSmem];
@@ -611,58 +624,46 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
   const UnitLoc loc = splitk_locate(a.o);     // o.HB = 1: unit = b * Hk + hk
   const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk;
   const int G = a.G, hq0 = hk * G, K = a.K;
-  const int len = pq_len(a, b);
+  const int len = PAGED ? pq_len(a, b) : a.S;       // a contiguous cache needs no length load
   const int t_begin = split * a.chunk;
   const int n = max(0, min(a.chunk, len - t_begin));   // tokens of this chunk
 
   // wave w's q row heads the queue; then this thread's token (clamped into
   // the chunk), whose codes arrive while the LUTs are built or staged
   LutQ<D> qrow;
-  if (BUILD_LUT && w < HP) qrow = lut_load_q<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, w, G);
+  if constexpr (SRC == 2) qrow = lut_load_q<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, min(w, HP - 1), G);
   u32x4 kc, vcd;
   {
     int blk, row;
-    pq_locate(a, b, t_begin + min(tid, max(n - 1, 0)), blk, row);
+    if constexpr (PAGED) {
+      pq_locate(a, b, t_begin + min(tid, max(n - 1, 0)), blk, row);
+    } else {
+      blk = b;
+      row = t_begin + min(tid, max(n - 1, 0));
+    }
     kc = ld_codes<M>(a.kidx + (int64_t)hk * a.ki_sh + (int64_t)blk * a.ki_sb + (int64_t)row * a.ki_ss);
     vcd = ld_codes<M>(a.vidx + (int64_t)hk * a.vi_sh + (int64_t)blk * a.vi_sb + (int64_t)row * a.vi_ss);
   }
 
-  // ---- phase A: the LUTs ----
-  if constexpr (BUILD_LUT) {
-    // LUT entries on MFMA (see lut_a_live): wave w builds subspace pair
-    // 2w, 2w + 1 (waves past M/2 idle) for all HP heads (rows past G are
-    // zero); the scaled q rows are staged in the score area
+  // ---- phase A: the key codebook (SRC 2) or the LUTs (SRC 0) ----
+  char* kcbl = smem;                                          // SRC 2: key codebook [M][256][8] fp16
+  uint8_t* kcl = reinterpret_cast<uint8_t*>(smem + C::VCB);   // SRC 2: key codes [chunk][16]
+  float* qs = reinterpret_cast<float*>(smem + C::VCB + kPqgChunk * 16);   // SRC 2: scaled q rows [HP][D]
+  if constexpr (SRC == 2) {
+    // codebook slot s = (j, c) of 256 per subspace (codewords past K repeat
+    // codeword K - 1; no code reads them), all loads in flight at once
+    constexpr int KPT = M * kPqKMax / kPqgThreads;
     const _Float16* cb = a.kcb + (int64_t)hk * a.kcb_sh;
-    const int jp = min(2 * w, M - 2);
-    f16x8 bop[kPqKMax / 32];
+    u32x4 kraw[KPT];
 #pragma unroll
-    for (int c32 = 0; c32 < kPqKMax / 32; ++c32) bop[c32] = lut_b_operand(cb, K, jp, c32 * 32, lane);
-    float* qs = sc;
-    float* mul = hsm;
-    if (w < HP) lut_store_q<D>(qrow, w, G, a.lut_scale, qs, mul);
-    __syncthreads();
-    if (2 * w < M) {
-      int hm, sub;
-      const bool live = lut_a_live(lane, &hm, &sub) && hm < HP;
-      f16x8 hi, lo;
-      lut_a_operands(qs + min(hm, HP - 1) * D + 8 * (jp + sub), live, hi, lo);
-      const bool use_lo = lut_need_lo(lo);
-      const int quad = lane >> 5, n = lane & 31;
-      float mg[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mg[i] = mul[min(4 * quad + i, HP - 1)];
-#pragma unroll
-      for (int c32 = 0; c32 < kPqKMax / 32; ++c32) {
-        const f32x16 e = lut_mfma(hi, lo, use_lo, bop[c32]);
-        // lane l holds heads 4 * quad .. +3 of codeword c32 * 32 + n for subspaces jp, jp + 1
-        if (quad < HP / 4) {
-#pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2)
-            *reinterpret_cast<f32x4*>(lut + ((quad * M + jp + s2) * kPqKMax + c32 * 32 + n) * 4) =
-                f32x4{mg[0] * e[8 * s2], mg[1] * e[8 * s2 + 1], mg[2] * e[8 * s2 + 2], mg[3] * e[8 * s2 + 3]};
-        }
-      }
+    for (int i = 0; i < KPT; ++i) {
+      const int sl = tid + kPqgThreads * i;
+      kraw[i] = ld16(cb + (int64_t)((sl >> 8) * K + min(sl & 255, K - 1)) * 8);
     }
+    if (w < HP) lut_store_q<D>(qrow, w, G, a.lut_scale, qs, hsm);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) *reinterpret_cast<u32x4*>(kcbl + (tid + kPqgThreads * i) * 16) = kraw[i];
+    *reinterpret_cast<u32x4*>(kcl + tid * 16) = kc;
   } else {
     // the caller's LUTs [B, Hq, M, K]: slot s = (j, c) of 256 per subspace,
     // consecutive codes across lanes (each load instruction reads 256
@@ -687,6 +688,7 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
             f32x4{v[i][4 * h4], v[i][4 * h4 + 1], v[i][4 * h4 + 2], v[i][4 * h4 + 3]};
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
   // the value codebook, held in registers until phase B (requested after the
   // LUT operands so it arrives during phase A): slot s = (j, c) of 256 per
   // subspace (codewords past K repeat codeword K - 1; no code reads them)
@@ -701,8 +703,80 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
   }
   __syncthreads();
 
-  // ---- phase A: scores of token tid, subspaces in order ----
-  {
+  // ---- phase A: scores ----
+  if constexpr (SRC == 2) {
+    // wave w scores 16-token blocks w, w + 8, ..: lane (l16, lg) supplies the
+    // codeword of subspace 4*kk + lg of token 16*blk + l16 (A) and q of head
+    // l16 at channels 32*kk + 8*lg .. +7 (B); the MFMA leaves head l16's
+    // scores of tokens 16*blk + 4*lg + i in lane (l16, lg).  Every LDS read
+    // of the wave's blocks is issued before the first MFMA.
+    const int l16 = lane & 15, lg = lane >> 4;
+    constexpr int KS = M / 4;                                   // MFMA k-steps
+    constexpr int NB = kPqgChunk / 16 / kPqWaves;               // blocks per wave
+    const bool hlive = l16 < HP;
+    const float* qrow = qs + min(l16, HP - 1) * D + lg * 8;
+    f16x8 qhi[KS], qlo[KS];
+    bool nzl = false;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(qrow + kk * 32);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(qrow + kk * 32 + 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = hlive ? (i < 4 ? x0[i] : x1[i - 4]) : 0.f;
+        const _Float16 hv = (_Float16)v;
+        qhi[kk][i] = hv;
+        qlo[kk][i] = (_Float16)(v - (float)hv);
+        nzl = nzl || (float)qlo[kk][i] != 0.f;
+      }
+    }
+    const bool nz = __ballot(nzl) != 0;
+    const float mul = hsm[min(l16, HP - 1)];
+    u32x4 cw[NB];
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi)
+      cw[bi] = *reinterpret_cast<const u32x4*>(kcl + ((w + kPqWaves * bi) * 16 + l16) * 16);   // the token's codes
+    f16x8 cwd[NB][KS];
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi)
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const uint32_t code = (cw[bi][kk] >> (8 * lg)) & 0xFFu;       // subspace 4*kk + lg
+        cwd[bi][kk] = *reinterpret_cast<const f16x8*>(kcbl + ((4 * kk + lg) * kPqKMax + (int)code) * 16);
+      }
+    f32x4 acc[NB];
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi) acc[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nz) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi)
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          acc[bi] = mfma_f16(cwd[bi][kk], qhi[kk], acc[bi]);
+          acc[bi] = mfma_f16(cwd[bi][kk], qlo[kk], acc[bi]);
+        }
+    } else {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi)
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) acc[bi] = mfma_f16(cwd[bi][kk], qhi[kk], acc[bi]);
+    }
+    if (hlive) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+        const int t0 = (w + kPqWaves * bi) * 16 + lg * 4;
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = t0 + i < n ? mul * acc[bi][i] : kNegInf;
+        *reinterpret_cast<f32x4*>(sc + l16 * kPqgChunk + t0) = o;
+      }
+    }
+    if constexpr (M == 16) {
+      *reinterpret_cast<u32x4*>(vc + tid * M) = vcd;
+    } else {
+      *reinterpret_cast<u32x2*>(vc + tid * M) = u32x2{vcd[0], vcd[1]};
+    }
+  } else {
     float s[HP];
 #pragma unroll
     for (int h = 0; h < HP; ++h) s[h] = 0.f;
@@ -1150,14 +1224,16 @@ static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S
       a.o.Hk = Hk; a.o.HB = 1; a.o.G = a.G; a.o.hbs = a.G;
       splitk_carve(workspace, gunits, gns, a.o);
       const dim3 grid((unsigned)(gns * gunits)), block(kPqgThreads);
-#define PQG_LAUNCH(DD, BL, HP) BYTES_LAUNCH(kProfPq, (pq_group_kernel<DD, BL, HP>), grid, block, 0, st, a)
+#define PQG_LAUNCH(DD, BL, HP)                                                                   \
+  if (a.btab) BYTES_LAUNCH(kProfPq, (pq_group_kernel<DD, BL, HP, true>), grid, block, 0, st, a);  \
+  else BYTES_LAUNCH(kProfPq, (pq_group_kernel<DD, BL, HP, false>), grid, block, 0, st, a);
 #define PQG_HP(DD, BL)            \
-  if (a.G <= 4) PQG_LAUNCH(DD, BL, 4); \
-  else PQG_LAUNCH(DD, BL, 8);
+  if (a.G <= 4) { PQG_LAUNCH(DD, BL, 4) } \
+  else { PQG_LAUNCH(DD, BL, 8) }
       if (D == 128) {
-        if (mode == 3) { PQG_HP(128, true) } else { PQG_HP(128, false) }
+        if (mode == 3) { PQG_HP(128, 2) } else { PQG_HP(128, 0) }
       } else {
-        if (mode == 3) { PQG_HP(64, true) } else { PQG_HP(64, false) }
+        if (mode == 3) { PQG_HP(64, 2) } else { PQG_HP(64, 0) }
       }
 #undef PQG_HP
 #undef PQG_LAUNCH

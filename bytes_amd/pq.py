@@ -116,14 +116,16 @@ def decode_attn_pq_lut_kv(lut: torch.Tensor, k_idx: torch.Tensor, v_idx: torch.T
 def decode_attn_pq_kv_fused(q: torch.Tensor, k_centroids: torch.Tensor, k_idx: torch.Tensor, v_idx: torch.Tensor,
                             v_centroids: torch.Tensor, scale: float = 1.0, d_sub_v: int = 8, *,
                             chunk: int = 0) -> torch.Tensor:
-    """pq_build_lut(q, k_centroids, scale) followed by decode_attn_pq_lut_kv, in
-    one launch: every workgroup builds its heads' LUTs in LDS from q and the key
-    codebook, entry for entry as pq_build_lut writes them
-    (benchmarks/test_correctness.py:272-273), then runs the decode of
-    src/attention_kernels.py:471-500.  The result is bit-identical to the two
-    calls.  q [B,H_q,1,D] bf16; k_centroids, v_centroids [M,K,8] or
-    [H_k,M,K,8]; k_idx, v_idx [B,H_k,S,M].  Returns [B,H_q,1,D] in v_centroids'
-    dtype."""
+    """pq_build_lut(q, k_centroids, scale) followed by decode_attn_pq_lut_kv
+    (benchmarks/test_correctness.py:272-273, then src/attention_kernels.py:
+    471-500), in one launch that forms no LUT in HBM.  With at most 8 query
+    heads per KV head the scores are scale * (q . k_hat) on MFMA, k_hat the
+    codebook rows the key codes select (exact products, fp32 sums); with more,
+    each workgroup builds its heads' LUTs in LDS entry for entry as
+    pq_build_lut and the result is bit-identical to the two calls.  Either way
+    it agrees with the two calls within the attention tolerance.  q
+    [B,H_q,1,D] bf16; k_centroids, v_centroids [M,K,8] or [H_k,M,K,8]; k_idx,
+    v_idx [B,H_k,S,M].  Returns [B,H_q,1,D] in v_centroids' dtype."""
     if d_sub_v != D_SUB:
         raise ValueError(f"d_sub_v={d_sub_v} not supported (8)")
     C.cuda_tensors(q, k_centroids, k_idx, v_idx, v_centroids)

@@ -377,9 +377,12 @@ int bytes_pq_lut_scores(const void* lut, int64_t l_sb, int64_t l_sh, const void*
  *   mode 2  decode_attn_dequant    :267-296 (kernel :187-265): scores q . k_hat with
  *           k_hat = concat_j kcb[j, kidx[t,j]] (no scale), dense bf16 v
  *   mode 3  mode 0 with the LUT precompute fused (benchmarks/test_correctness.py:272-273
- *           followed by :471-500): each workgroup builds lut = scale * (q . kcb) in LDS,
- *           entry for entry as bytes_pq_build_lut, so the output is bit-identical to
- *           bytes_pq_build_lut + mode 0; q, kcb, vidx, vcb required, lut unused
+ *           followed by :471-500), no LUT in HBM: for G <= 8 the scores are
+ *           scale * (q . k_hat) on MFMA from the codebook rows the codes select
+ *           (exact products, fp32 sums; within the attention tolerance of
+ *           bytes_pq_build_lut + mode 0); for G > 8 each workgroup builds
+ *           lut = scale * (q . kcb) in LDS entry for entry as bytes_pq_build_lut
+ *           (bit-identical to the two calls); q, kcb, vidx, vcb required, lut unused
  *   lut [B, Hq, M, K] fp32 (one head contiguous); q [B, Hq, D] bf16;
  *   out [B, Hq, D] of out_dtype (0 bf16, 1 f16, 2 f32).  `scale` multiplies the
  *   scores in modes 0-2 (the reference has none: pass 1.0) and the LUT entries in

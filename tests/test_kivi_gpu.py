@@ -159,6 +159,20 @@ def test_decode_long_contexts(dev, bits, B, Hq, Hk, D, L, Rw):
     _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
 
 
+@pytest.mark.parametrize("Rw", [40, 64, 100, 128])
+def test_decode_residual_lengths_eight_wave_grid(dev, Rw):
+    """Eight-wave grid with 512-token splits (B=2, Hk=4, Sq=16256, 2-bit): the
+    residual window, whole and ragged, rides in pieces on the last splits."""
+    _decode_case(dev, 2, 2, 8, 4, 128, 16256 + Rw, Rw, seed=70 + Rw)
+
+
+@pytest.mark.parametrize("Rw", [72, 128])
+def test_decode_residual_lengths_c2_grid(dev, Rw):
+    """The C2 grid (16 units of 1024-token splits, the last holding 896 tokens)
+    with G = 2 and a whole or ragged residual window."""
+    _decode_case(dev, 2, 2, 16, 8, 128, 16256 + Rw, Rw, seed=90 + Rw)
+
+
 def test_decode_back_to_back_calls(dev):
     """Consecutive calls with new data, and a different split plan in between,
     reuse the shared split-K workspace: each call's partials overwrite the

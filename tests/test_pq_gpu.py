@@ -119,8 +119,10 @@ def test_lut_kv_split_counts(dev, chunk):
 def test_lut_kv_group_sizes(dev, G, S, D, chunk):
     """Query groups of 1..16 heads per KV head, quantized values: all G heads
     in one workgroup (G <= 8, chunks of <= 512 tokens) or groups of four
-    (G > 8, or a longer chunk), against the oracle; the LUT built inside the
-    kernel gives the caller-LUT result bit for bit."""
+    (G > 8, or a longer chunk), against the oracle.  The fused call scores
+    from q and the key codebook (on MFMA in the grouped kernel, through an
+    in-kernel LUT in the general one): within the attention tolerance of the
+    caller-LUT call, and bit for bit where the general kernel runs."""
     B, Hk, K = 2, 2, 256
     M = D // 8
     g = torch.Generator().manual_seed(G * 1000 + S)
@@ -133,9 +135,14 @@ def test_lut_kv_group_sizes(dev, G, S, D, chunk):
     lut = PQ.pq_build_lut(d["q"], d["kcb"], scale)
     two = PQ.decode_attn_pq_lut_kv(lut, d["k_idx"], d["v_idx"], d["vcb"], chunk=chunk)
     fused = PQ.decode_attn_pq_kv_fused(d["q"], d["kcb"], d["k_idx"], d["v_idx"], d["vcb"], scale, chunk=chunk)
-    assert torch.equal(fused, two)
-    _check(two, R.decode_attn_pq_lut_kv(R.pq_build_lut(q, kcb, scale), k_idx, v_idx, vcb),
-           f"lut_kv G{G} S{S} D{D} chunk {chunk}")
+    grouped = G <= 8 and chunk <= 512
+    if grouped:
+        _check(fused, two.cpu(), f"fused vs two calls G{G} S{S} D{D} chunk {chunk}")
+    else:
+        assert torch.equal(fused, two)
+    ref = R.decode_attn_pq_lut_kv(R.pq_build_lut(q, kcb, scale), k_idx, v_idx, vcb)
+    _check(two, ref, f"lut_kv G{G} S{S} D{D} chunk {chunk}")
+    _check(fused, ref, f"fused G{G} S{S} D{D} chunk {chunk}")
 
 
 def test_c3_full(dev):
@@ -160,9 +167,11 @@ def test_c3_full(dev):
                                                    (1, 7, 1, 1000, 128, 256, True),
                                                    (2, 8, 2, 333, 64, 16, False),
                                                    (2, 12, 2, 5000, 128, 64, True)])
-def test_fused_lut_build_matches_two_calls(dev, B, Hq, Hk, S, D, K, per_head):
-    """decode_attn_pq_kv_fused == pq_build_lut + decode_attn_pq_lut_kv, bit for
-    bit (same LUT entries, same decode), and within tolerance of the oracle."""
+def test_fused_matches_two_calls(dev, B, Hq, Hk, S, D, K, per_head):
+    """decode_attn_pq_kv_fused against pq_build_lut + decode_attn_pq_lut_kv and
+    the oracle: within the attention tolerance (scores q . k_hat on MFMA from
+    the codebook rows, exact products summed in fp32, instead of summed LUT
+    entries), deterministic from call to call."""
     g = torch.Generator().manual_seed(S + K)
     M = D // 8
     q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
@@ -176,7 +185,9 @@ def test_fused_lut_build_matches_two_calls(dev, B, Hq, Hk, S, D, K, per_head):
     two = PQ.decode_attn_pq_lut_kv(lut, d["k_idx"], d["v_idx"], d["vcb"])
     fused = PQ.decode_attn_pq_kv_fused(d["q"], d["kcb"], d["k_idx"], d["v_idx"], d["vcb"], scale)
     assert fused.shape == two.shape and fused.dtype == two.dtype
-    assert torch.equal(fused, two)
+    again = PQ.decode_attn_pq_kv_fused(d["q"], d["kcb"], d["k_idx"], d["v_idx"], d["vcb"], scale)
+    assert torch.equal(fused, again)
+    _check(fused, two.cpu(), f"fused vs two calls B{B} Hq{Hq} Hk{Hk} S{S} D{D} K{K}")
     ref = R.decode_attn_pq_lut_kv(R.pq_build_lut(q, kcb, scale), k_idx, v_idx, vcb)
     _check(fused, ref, f"fused B{B} Hq{Hq} Hk{Hk} S{S} D{D} K{K}")
 
