@@ -9,13 +9,13 @@ first; then exactly K steps are captured into one hipGraph (each step on its
 own copy of the inputs, rotating through enough copies to exceed 2x the
 256 MB Infinity Cache, so every step streams from HBM) and the graph replay
 is timed with HIP events on the capture's stream, between two device
-synchronisations.  The step's dominant kernel is then timed on its own: K
-more (eager) steps, each with a HIP event pair that the library records on
-the kernel's stream right around that launch.
+synchronisations.  The step's dominant kernel is then timed on its own: at
+least 60 more (eager) steps, each with a HIP event pair that the library
+records on the kernel's stream right around that launch, and the median pair.
 
 `value` is the headline config (BASELINE C2, KIVI 2-bit) in us/step;
 `roofline` is its dominant kernel's algorithmic bytes over that kernel's
-average duration (`step_frac` the same over the whole step).  `per_config`
+median duration (`step_frac` the same over the whole step).  `per_config`
 holds the same figures for every other BASELINE config (C1, C2 4-bit, the
 dense L>=16K point, C3, C4, C5 at k = 256/1024/4096; --all adds more).  Each
 config's cpu_baseline times the CPU oracle (test infrastructure, oracle/) on
@@ -442,12 +442,15 @@ def time_step(case: Case, inps, steps: int) -> float:
 
 
 def time_kernel(case: Case, inps, steps: int) -> float:
-    """Average duration (ms) of the step's dominant kernel over `steps` steps:
-    the library records a HIP event pair on the kernel's own stream right
-    before and after that launch (bytes_set_kernel_events), one pair per step."""
+    """Duration (ms) of the step's dominant kernel: the library records a HIP
+    event pair on the kernel's own stream right before and after that launch
+    (bytes_set_kernel_events), one pair per step, over at least 60 steps; the
+    median of the pairs (a single pair is perturbed now and then by the host's
+    launch timing)."""
     from bytes_amd import _lib
     if case.family == 0:                  # not a library kernel: the step is the kernel
         return time_step(case, inps, steps)
+    steps = max(steps, 60)
     lib = _lib.lib()
     copies = len(inps)
     s = torch.cuda.current_stream()
@@ -464,7 +467,7 @@ def time_kernel(case: Case, inps, steps: int) -> float:
     finally:
         lib.bytes_set_kernel_events(0, None, None)
     torch.cuda.synchronize()
-    return statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
 
 
 def measure(case: Case, steps: int, warmup: int, dev) -> dict:
