@@ -83,6 +83,25 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// Reductions over the four lanes l % 16 + 16 j (j = 0..3) of a wave, the lanes
+// that hold one column of an MFMA output: gfx950 row swaps (v_permlane16_swap
+// exchanges 16-lane rows 2i and 2i+1, v_permlane32_swap the two 32-lane
+// halves; with both operands equal, each lane then holds its own value and its
+// partner's) instead of LDS permutes.  Every lane receives the result, the
+// same on all four lanes; the maximum is IEEE maximum (no NaN quieting).
+__device__ __forceinline__ float col_max4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // 2^x on the hardware exp unit (v_exp_f32).  Used for softmax weights, whose
 // arguments are <= 0: results below the normal range flush towards zero,
 // which does not change a softmax numerator or denominator at fp32 precision.

@@ -127,10 +127,9 @@ __device__ __forceinline__ void tile_softmax_pv_at(const f32x4 (&s)[2], uint32_t
       const int j = blk * 16 + lg * 4 + i;
       const float xv = ((vmask >> j) & 1u) ? s[blk][i] * scale_log2 : kNegInf;
       x[blk * 4 + i] = xv;
-      mx = fmaxf(mx, xv);
+      mx = __builtin_elementwise_maximum(mx, xv);
     }
-  mx = fmaxf(mx, shfl_xor_f(mx, 16));
-  mx = fmaxf(mx, shfl_xor_f(mx, 32));
+  mx = col_max4(mx);
   const float m_new = fmaxf(m_run, mx);
   const float m_use = (m_new == kNegInf) ? 0.f : m_new;
   const float alpha = fast_exp2(m_run - m_use);

@@ -134,6 +134,7 @@ struct KiviArgs {
 // halves of one 64-token tile per wave.
 constexpr int kKiviTile = 64;
 constexpr int kResidPerSplit = 128;  // residual tokens per split at most (one 32-token tile per wave)
+constexpr int kKiviOnes = 128;       // LDS bytes of f16 ones after a wave's value scales/zeros (the softmax row sums)
 
 template <int D, int BITS, int NW = 4>
 struct KiviCfg {
@@ -157,7 +158,7 @@ struct KiviCfg {
   static constexpr int VDMA = VBYTES / 1024;               // 16-byte value chunks per lane per tile
   static constexpr int NGV = D / 32;                        // value groups per token
   static constexpr int VMBYTES = 2 * kKiviTile * NGV * 2;   // value scale + zero of one tile
-  static constexpr int WAVE_BYTES = VBYTES + VMBYTES;
+  static constexpr int WAVE_BYTES = VBYTES + VMBYTES + kKiviOnes;
   // Q of the unit's 16 head columns as the fp16 B operand (scaled, k-slot
   // order within each 8-channel chunk), staged once per workgroup: row pitch
   // D*2 + 16 bytes so the 16 head rows a 16-lane group reads sit in distinct banks
@@ -253,6 +254,72 @@ __device__ __forceinline__ f16x8 scale8(f16x8 x, u32x4 s) { return x * __builtin
 template <int D>
 using VMetaReg = typename std::conditional<(D >= 128), u32x4, u32x2>::type;
 
+// Online softmax of one 64-token tile with a lazy running maximum.
+//
+// On entry sc[u][i] holds s - m_ref for its (token, head), where the
+// reference m_ref is the running maximum m_run (0 before the wave's first
+// tile, when m_run = -inf): the zero-term chain of the scores starts from
+// negm = -m_ref.  The reference moves only when some head's tile maximum
+// exceeds it by more than kKiviLazy (log2 units) - always on the first tile -
+// so probabilities stay below 2^kKiviLazy and the rescale of the accumulators
+// (and its exp) is skipped on most tiles.  The softmax denominators are not
+// summed here: the value zero-term MFMA has rows of ones (rows >= NGV of its A
+// operand) and accumulates sum_t p[h][t] in zv row kKiviOnesRow, rescaled with
+// the accumulators.  p receives exp2(s - m_run) in sc's order.
+constexpr float kKiviLazy = 8.f;
+constexpr int kKiviOnesRow = 12;     // zv row read back as the denominator (lanes 48-63, element 0)
+template <int D>
+__device__ __forceinline__ void kivi_softmax(f32x4 (&sc)[4], float& m_run, f32x4& negm, f32x4 (&acc)[D / 16],
+                                             f32x4& zv, float (&p)[16]) {
+  float mx = kNegInf;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = __builtin_elementwise_maximum(mx, sc[u][i]);
+  mx = col_max4(mx);
+  const bool first = m_run == kNegInf;            // the same on every lane of the wave
+  if (__ballot(first || mx > kKiviLazy) != 0) {
+    const float m_new = first ? mx : fmaxf(m_run, m_run + mx);
+    const float shift = first ? mx : m_new - m_run;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[u][i] -= shift;
+    if (__ballot(!first) != 0) {
+      const float alpha = fast_exp2(m_run - m_new);
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
+      zv *= alpha;
+    }
+    m_run = m_new;
+    negm = f32x4{-m_new, -m_new, -m_new, -m_new};
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[u * 4 + i] = fast_exp2(sc[u][i]);
+}
+
+// After a wave's last quantized tile: the value zero term added to the
+// accumulators (acc[db][i] holds a channel of value group db / 2 in both
+// layouts; group g's term is held by lane l16 of row group 0 at element g)
+// and the lane's share of the denominator (the ones row, on lanes 48-63).
+template <int D>
+__device__ __forceinline__ void kivi_finish(int lane, const f32x4& zv, f32x4 (&acc)[D / 16], float& l_run) {
+  const int l16 = lane & 15;
+#pragma unroll
+  for (int g = 0; g < D / 32; ++g) {
+    const float zg = __shfl(zv[g], l16, 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * g][i] += zg;
+      acc[2 * g + 1][i] += zg;
+    }
+  }
+  static_assert(kKiviOnesRow % 4 == 0, "the ones row is element 0 of its lane group");
+  l_run = (lane >> 4) == kKiviOnesRow / 4 ? zv[0] : 0.f;
+}
+
 // One tile's prefetched value codes and value scales/zeros (written to the
 // wave's LDS buffers when the tile runs).
 template <int D, int BITS>
@@ -317,7 +384,7 @@ __device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[D / 32], const char* kc,
                                           const char* vst, const char* vmeta_lds, const char* kmeta, float& m_run,
-                                          float& l_run, f32x4 (&acc)[D / 16], f32x4& zv) {
+                                          f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
   using C = KiviCfg<D, BITS, NW>;
   const int l16 = lane & 15, lg = lane >> 4;
   constexpr int KMG = C::KMG;
@@ -336,7 +403,7 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
     // group's channel scales, and the zero term as the initial scores
     const int grp = grp0 + sg;
     f16x8 qs[C::KK];
-    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 z = negm;
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) {
       const int off = (grp * C::KMP + lg * (D / 4) + kk * 8) * 2;
@@ -373,34 +440,8 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
   }
 
   // ---------------- online softmax (Q carries scale*log2(e); tiles are full) ----------------
-  float mx = kNegInf;
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[u][i]);
-  mx = fmaxf(mx, shfl_xor_f(mx, 16));
-  mx = fmaxf(mx, shfl_xor_f(mx, 32));
-  const float m_new = fmaxf(m_run, mx);
-  const float alpha = fast_exp2(m_run - m_new);
-  // before a workgroup's first tile every lane's state is empty (m = -inf,
-  // acc = 0): the rescale is skipped on that wave-uniform condition
-  const bool rescale = __ballot(m_run != kNegInf) != 0;
   float p[16];
-  float psum = 0.f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[u * 4 + i] = fast_exp2(sc[u][i] - m_new);
-      psum += p[u * 4 + i];
-    }
-  l_run = l_run * alpha + psum;
-  m_run = m_new;
-  if (rescale) {
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
-    zv *= alpha;
-  }
+  kivi_softmax<D>(sc, m_run, negm, acc, zv, p);
 
   // P^T as the B operand, k-slot jj of sub-tile sg:
   //   2-bit: token 32sg + 8lg + jj  -> p[(sg*2 + jj%2)*4 + jj/2]
@@ -419,13 +460,14 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
     // P^T scaled by each value group's token scales; the zero term on MFMA
-    // rows = groups (lane row l16 reads group l16 % NGV, rows >= NGV unused)
+    // rows = groups (lane row l16 reads group l16), rows >= NGV read the
+    // wave's ones rows and sum P^T (the denominator)
     f16x8 pg[C::NGV];
 #pragma unroll
     for (int g = 0; g < C::NGV; ++g)
       pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
     {
-      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, l16 % C::NGV, sg * 32) * 2 + lg * 16);
+      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, C::NGV), sg * 32) * 2 + lg * 16);
       zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
     }
     if (BITS == 2) {
@@ -506,7 +548,7 @@ struct KsCfg {
   static constexpr int VDMA = VBYTES / 1024;                 // 16-byte value pieces per lane
   static constexpr int NGV = D / 32;
   static constexpr int VMBYTES = 2 * 64 * NGV * 2;           // value scales + zeros of one tile
-  static constexpr int WAVE = VBYTES + VMBYTES;
+  static constexpr int WAVE = VBYTES + VMBYTES + kKiviOnes;
   static constexpr int kQuant = KBYTES + KMBYTES + kKsWaves * WAVE;
   static constexpr int kDense = 4 * DenseCfg<D>::WAVE;       // residual tiles of waves 0-3 (residual splits)
   static constexpr int kEpi = splitk_smem_floats<D, kKsWaves>() * 4;
@@ -536,7 +578,7 @@ struct KsRegs {
 template <int D, int BITS, int KROW, int KMP>
 __device__ __forceinline__ void kivi_tile64(int lane, const f16x8 (&qh)[D / 32], const char* kc, const _Float16* kms,
                                             int kzo, const char* vst, const char* vml, bool second, float& m_run,
-                                            float& l_run, f32x4 (&acc)[D / 16], f32x4& zv) {
+                                            f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
   constexpr int KK = D / 32, NGV = D / 32, VROW = D * BITS / 8;
   const int l16 = lane & 15, lg = lane >> 4;
   // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
@@ -546,7 +588,7 @@ __device__ __forceinline__ void kivi_tile64(int lane, const f16x8 (&qh)[D / 32],
   for (int sg = 0; sg < 2; ++sg) {
     const _Float16* ks_row = kms + sg * KMP;
     f16x8 qs[KK];
-    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 z = negm;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const int off = lg * (D / 4) + kk * 8;
@@ -586,32 +628,8 @@ __device__ __forceinline__ void kivi_tile64(int lane, const f16x8 (&qh)[D / 32],
     sc[2] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
     sc[3] = sc[2];
   }
-  float mx = kNegInf;
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[u][i]);
-  mx = fmaxf(mx, shfl_xor_f(mx, 16));
-  mx = fmaxf(mx, shfl_xor_f(mx, 32));
-  const float m_new = fmaxf(m_run, mx);
-  const float alpha = fast_exp2(m_run - m_new);
-  const bool rescale = __ballot(m_run != kNegInf) != 0;
   float p[16];
-  float psum = 0.f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[u * 4 + i] = fast_exp2(sc[u][i] - m_new);
-      psum += p[u * 4 + i];
-    }
-  l_run = l_run * alpha + psum;
-  m_run = m_new;
-  if (rescale) {
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) acc[db] *= alpha;
-    zv *= alpha;
-  }
+  kivi_softmax<D>(sc, m_run, negm, acc, zv, p);
   f16x8 pb[2];
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg)
@@ -628,7 +646,7 @@ __device__ __forceinline__ void kivi_tile64(int lane, const f16x8 (&qh)[D / 32],
     for (int g = 0; g < NGV; ++g)
       pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
     {
-      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, l16 % NGV, sg * 32) * 2 + lg * 16);
+      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, NGV), sg * 32) * 2 + lg * 16);
       zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
     }
     if (BITS == 2) {
@@ -790,7 +808,11 @@ __global__ __launch_bounds__(kKsWaves * 64, 1) void kivi_stream_kernel(KiviArgs 
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
     }
-    f32x4 zv = {0.f, 0.f, 0.f, 0.f};
+    f32x4 zv = {0.f, 0.f, 0.f, 0.f}, negm = {0.f, 0.f, 0.f, 0.f};
+    // this wave's ones rows (read by the value zero-term MFMA), published by
+    // the first phase's barrier
+    reinterpret_cast<uint16_t*>(smem_raw + C::KBYTES + C::KMBYTES + w * C::WAVE + C::VBYTES + C::VMBYTES)[lane] =
+        0x3C00u;
     // Phases run in groups of DEPTH (the last group padded with empty phases,
     // whose requests re-read the split's last bytes).  Every group but the
     // last requests the next group's phases, one per staged phase, with no
@@ -812,7 +834,7 @@ __global__ __launch_bounds__(kKsWaves * 64, 1) void kivi_stream_kernel(KiviArgs 
         const _Float16* kms = reinterpret_cast<const _Float16*>(smem_raw + C::KBYTES) + 2 * w * C::KMP;
         const char* vst = smem_raw + C::KBYTES + C::KMBYTES + w * C::WAVE;
         kivi_tile64<D, BITS, C::KROW, C::KMP>(lane, qh, smem_raw + w * 64 * BITS / 8, kms, kKsGroups * C::KMP, vst,
-                                              vst + C::VBYTES, left > 32, m_run, l_run, acc, zv);
+                                              vst + C::VBYTES, left > 32, m_run, negm, acc, zv);
       }
       if (more && !kEarly) {
         __builtin_amdgcn_sched_barrier(0);
@@ -829,15 +851,7 @@ __global__ __launch_bounds__(kKsWaves * 64, 1) void kivi_stream_kernel(KiviArgs 
     for (int d = 0; d < DEPTH; ++d) {
       if (p0 + d < nph) run_phase(p0 + d, d, false);
     }
-#pragma unroll
-    for (int g = 0; g < C::NGV; ++g) {
-      const float zg = __shfl(zv[g], l16, 64);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * g][i] += zg;
-        acc[2 * g + 1][i] += zg;
-      }
-    }
+    kivi_finish<D>(lane, zv, acc, l_run);
   } else if (rtile) {
     // A split of the bf16 residual window: one 32-token dense tile per wave of
     // waves 0-3.  Its K and V rows go straight from HBM to the wave's LDS tile
@@ -1038,7 +1052,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
     f16x8 qh[D / 32];
 
     _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
-    f32x4 zv = {0.f, 0.f, 0.f, 0.f};   // value zero term: row g = value group, column = head
+    // value zero term: row g = value group, column = head; rows >= NGV: the
+    // denominators (from this wave's ones rows, published by the first barrier)
+    f32x4 zv = {0.f, 0.f, 0.f, 0.f}, negm = {0.f, 0.f, 0.f, 0.f};
+    reinterpret_cast<uint16_t*>(vml + C::VMBYTES)[lane] = 0x3C00u;
 #pragma unroll
     for (int ph = 0; ph < NTW; ++ph) {
       // this half's key codes and scales/zeros into LDS, stored unconditionally
@@ -1079,21 +1096,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
       if (t < t_end) {
         const int off = t - t_begin;
         kivi_tile<D, BITS, NW>((t >> 5) - g_lo, lane, qh, kchunk + ph * C::KHALF + (off - ph * STEP) * BITS / 8, vst, vml,
-                               kmeta, m_run, l_run, acc,
-                           zv);
+                               kmeta, m_run, negm, acc, zv);
       }
     }
-    // acc[db][i] holds a channel of value group db / 2 (both layouts): add
-    // that group's zero term, held by lane l16 of row group 0 at element g
-#pragma unroll
-    for (int g = 0; g < C::NGV; ++g) {
-      const float zg = __shfl(zv[g], l16, 64);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * g][i] += zg;
-        acc[2 * g + 1][i] += zg;
-      }
-    }
+    kivi_finish<D>(lane, zv, acc, l_run);
   }
 
   if (resid) {

@@ -142,8 +142,7 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
   constexpr int NT = NW * 64;
   constexpr int P = acc_pitch<D>();
   constexpr int D4 = D / 4;
-  l_run += shfl_xor_f(l_run, 16);
-  l_run += shfl_xor_f(l_run, 32);
+  l_run = col_sum4(l_run);
   float* wm = smem;
   float* wl = wm + NW * 16;
   float* wacc = wl + NW * 16;
