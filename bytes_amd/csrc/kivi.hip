@@ -1077,17 +1077,24 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
         dst[0] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] & 0xFFFFu));
         dst[C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(mv[ph][i] >> 16));
       }
-      __syncthreads();
+      // The second half is requested only once the first has arrived: first
+      // halves then reach the head of the memory queues before second
+      // halves, and the second half streams in while the first tiles run.
+      // One workgroup per CU (NW = 8): once the whole workgroup's first half
+      // has arrived (measured faster there); several rounds of 4-wave
+      // workgroups: by each wave once its own share has arrived (the stores
+      // above waited for it; the barrier then orders LDS only, so those
+      // requests stay in flight), which keeps more bytes in flight.
+      constexpr bool kWaveIssue = NW == 4;
+      if (kWaveIssue && ph == 0) issue(std::integral_constant<int, 1>());
+      if (kWaveIssue) lds_barrier();
+      else __syncthreads();
       if (ph == 0) {
 #pragma unroll
         for (int kk = 0; kk < D / 32; ++kk)
           qh[kk] = *reinterpret_cast<const f16x8*>(qlds + l16 * C::QP + (lg * (D / 32) + kk) * 16);
       }
-      // The second half is requested only once the first has arrived: every
-      // workgroup's first half then reaches the head of the memory queues
-      // before any second half, and the second half streams in while the
-      // first tiles run.
-      if (ph == 0) issue(std::integral_constant<int, 1>());
+      if (!kWaveIssue && ph == 0) issue(std::integral_constant<int, 1>());
       const int t = tw + ph * STEP;
       wave_lds_sync();
       kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
