@@ -808,8 +808,7 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
     float m = kNegInf;
 #pragma unroll
     for (int i = 0; i < kPqgChunk / 64; ++i) m = fmaxf(m, sc[w * kPqgChunk + lane + 64 * i] * a.scale_log2);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, shfl_xor_f(m, o));
+    m = wave_max_f32(m);
     if (lane == 0) hsm[w] = m;
   }
   __syncthreads();
@@ -840,8 +839,7 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
       }
       ps[tile * 64 + lane] = ph;
     }
-    l_part += shfl_xor_f(l_part, 16);
-    l_part += shfl_xor_f(l_part, 32);
+    l_part = col_sum4(l_part);
     if (lg == 0) lsum[w * 16 + l16] = l_part;
   }
   __syncthreads();
@@ -858,24 +856,35 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
   const char* vb1 = vb0 + 2 * kPqKMax * 8 * 2;
   const uint8_t* vcw = vc + dp * 4;
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  // every tile's code words and probabilities are read, then every codeword
+  // row, then the MFMAs run: two LDS round trips for the wave's tiles
+  // instead of two per tile
+  constexpr int KT = NT / TS;
+  uint32_t word[KT][2];
+  f16x8 ph[KT];
 #pragma unroll
-  for (int k = 0; k < NT / TS; ++k) {
+  for (int k = 0; k < KT; ++k) {
     const int tile = tq + k * TS;
-    const f16x8 ph = ps[tile * 64 + lane];
-    u32x2 hv[2][2];
+    ph[k] = ps[tile * 64 + lane];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+      word[k][hf] = *reinterpret_cast<const uint32_t*>(vcw + (tile * kTile + hf * 16 + lg * 4 + (l16 >> 2)) * M);
+  }
+  u32x2 hv[KT][2][2];
+#pragma unroll
+  for (int k = 0; k < KT; ++k)
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const int row = tile * kTile + hf * 16 + lg * 4 + (l16 >> 2);
-      const uint32_t word = *reinterpret_cast<const uint32_t*>(vcw + row * M);
-      hv[0][hf] = tr16(vb0 + ((word >> (8 * sub)) & 0xFFu) * 16);
-      hv[1][hf] = tr16(vb1 + ((word >> (8 * (2 + sub))) & 0xFFu) * 16);
+      hv[k][0][hf] = tr16(vb0 + ((word[k][hf] >> (8 * sub)) & 0xFFu) * 16);
+      hv[k][1][hf] = tr16(vb1 + ((word[k][hf] >> (8 * (2 + sub))) & 0xFFu) * 16);
     }
 #pragma unroll
+  for (int k = 0; k < KT; ++k)
+#pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const u32x4 raw = {hv[e][0][0], hv[e][0][1], hv[e][1][0], hv[e][1][1]};
-      acc[e] = mfma_f16(__builtin_bit_cast(f16x8, raw), ph, acc[e]);
+      const u32x4 raw = {hv[k][e][0][0], hv[k][e][0][1], hv[k][e][1][0], hv[k][e][1][1]};
+      acc[e] = mfma_f16(__builtin_bit_cast(f16x8, raw), ph[k], acc[e]);
     }
-  }
   // the tile groups' sums join group 0's, in group order
   if (tq > 0) {
 #pragma unroll
