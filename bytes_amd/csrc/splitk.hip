@@ -10,8 +10,9 @@
 // 64 lanes are 16 float4 items of the slice x 4 split groups; lane (g, item)
 // takes splits g, g+4, ... of each block of up to 128 splits, and all of a block's
 // loads (the acc rows and every split's (m, l)) are issued before any is
-// used, so a block costs one memory round trip.  Split groups are folded by
-// a fixed butterfly, so the result is bit-reproducible run to run.
+// used, so a block costs one memory round trip.  Lanes are folded by fixed
+// DPP rotations and row swaps (no LDS round trips), so the result is
+// bit-reproducible run to run.
 #include "splitk.h"
 
 namespace bytes_amd {
@@ -84,8 +85,7 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o, XcdUnit
       for (int k = 0; k < 4; ++k) M = fmaxf(M, m4[k]);
     }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f(M, off));
+  M = wave_max_f32(M);
   if (M == kNegInf) M = 0.f;
 
   float L = 0.f;
@@ -111,12 +111,9 @@ __global__ __launch_bounds__(64) void splitk_combine_kernel(SplitKOut o, XcdUnit
       A.x += w * pv[u].x; A.y += w * pv[u].y; A.z += w * pv[u].z; A.w += w * pv[u].w;
     }
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) L += shfl_xor_f(L, off);
-#pragma unroll
-  for (int off = kCombItems; off < 64; off <<= 1) {
-    A.x += shfl_xor_f(A.x, off); A.y += shfl_xor_f(A.y, off); A.z += shfl_xor_f(A.z, off); A.w += shfl_xor_f(A.w, off);
-  }
+  L = wave_sum_f32(L);
+  static_assert(kCombItems == 16, "split groups are the four lanes l % 16 + 16 j");
+  A.x = col_sum4(A.x); A.y = col_sum4(A.y); A.z = col_sum4(A.z); A.w = col_sum4(A.w);
   if (g == 0) {
     const float il = 1.f / L;
     const int hq = hk * o.G + hb * o.hbs + h, d = (slice * kCombItems + item) * 4;
