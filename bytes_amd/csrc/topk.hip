@@ -49,28 +49,21 @@ template <int NT>
 __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  // the wave's scan on DPP (every lane active), then each thread adds the
+  // totals of the waves before its own
+  const uint32_t x = wave_prefix_sum(v);
   if (lane == 63) wsum[w] = x;
   __syncthreads();
-  if (w == 0) {
-    uint32_t s = lane < NW ? wsum[lane] : 0u;
+  uint32_t before = 0u, tot = 0u;
 #pragma unroll
-    for (int off = 1; off < NW; off <<= 1) {
-      const uint32_t y = __shfl_up(s, off, 64);
-      if (lane >= off) s += y;
-    }
-    if (lane < NW) wsum[lane] = s;
+  for (int u = 0; u < NW; ++u) {
+    const uint32_t t = wsum[u];
+    before += u < w ? t : 0u;
+    tot += t;
   }
-  __syncthreads();
-  total = wsum[NW - 1];
-  const uint32_t r = x + (w > 0 ? wsum[w - 1] : 0u);
+  total = tot;
   __syncthreads();   // wsum is reused by the next scan
-  return r;
+  return x + before;
 }
 
 // Buffer resource over the n floats of a row: reads past the row return zero.
@@ -277,9 +270,12 @@ __global__ __launch_bounds__(kPassThreads) void topk_filter_kernel(const float* 
       na += d > d0 ? 1u : 0u;
       nc += d == d0 ? 1u : 0u;
     }
-  uint32_t ta, tc;
-  uint32_t oa = block_incl_scan<kPassThreads>(na, wsum, ta) - na;
-  uint32_t oc = block_incl_scan<kPassThreads>(nc, wsum, tc) - nc;
+  // one scan of (candidates << 16 | above): both stay below 2^16 per workgroup
+  static_assert(kSlice < 65536, "packed counts");
+  uint32_t tp;
+  const uint32_t op = block_incl_scan<kPassThreads>((nc << 16) | na, wsum, tp) - ((nc << 16) | na);
+  uint32_t oa = op & 0xFFFFu, oc = op >> 16;
+  const uint32_t ta = tp & 0xFFFFu, tc = tp >> 16;
   if (threadIdx.x == 0) {
     sel[2] = ta ? atomicAdd(ws.cnt + row * kCntStride + 0, ta) : 0u;
     sel[3] = tc ? atomicAdd(ws.cnt + row * kCntStride + 1, tc) : 0u;
