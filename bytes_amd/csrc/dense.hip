@@ -78,8 +78,6 @@ __global__ __launch_bounds__(kDenseWaves * 64, 2) void dense_decode_kernel(Dense
                                   hq0, nh);
 }
 
-// Host-side split choice: chunk is a multiple of (waves * tile) tokens; aim
-// for two resident workgroups per CU.
 // Device-resident scratch of the no-allocation entry point: the split-K
 // partials of one call (each device holds its own copy for the life of the
 // process).  Host code never uses the symbol's name as an address: its
@@ -110,13 +108,19 @@ static void* scratch_address(int* rc) {
   return g_scratch[dev];
 }
 
-static void dense_plan(int S, long units, int chunk_req, int* chunk, int* nsplit) {
+// Host-side split choice: chunk is a multiple of (waves * tile) tokens; aim
+// for per_cu workgroups per CU: one for bf16 K/V (measured faster than two at
+// L = 16K and 32K: half the partials to merge, longer pipelines per wave),
+// two for fp8 (whose rows are widened to bf16 as they are staged).  More
+// workgroups per CU never means fewer splits, so the workspace query plans
+// for two.
+static void dense_plan(int S, long units, int chunk_req, int per_cu, int* chunk, int* nsplit) {
   const int step = kDenseWaves * kTile;
   int c;
   if (chunk_req > 0) {
     c = (chunk_req + step - 1) / step * step;
   } else {
-    const long target = 2L * device_cu_count();
+    const long target = (long)per_cu * device_cu_count();
     long per = ((long)S * units + target - 1) / target;
     c = (int)((per + step - 1) / step * step);
     if (c < step) c = step;
@@ -141,7 +145,7 @@ int bytes_decode_attn_bf16_workspace_size(int B, int Hq, int Hk, int S, int D, i
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
   int chunk, ns;
-  dense_plan(S, units, chunk_req, &chunk, &ns);
+  dense_plan(S, units, chunk_req, 2, &chunk, &ns);
   *bytes = splitk_workspace_bytes(units, ns, D);
   return 0;
 }
@@ -165,7 +169,7 @@ static int dense_decode(bool fp8, const void* q, const void* k, const void* v, v
   a.Hk = Hk; a.G = G; a.S = S; a.HB = HB;
   a.scale_log2 = scale * kLog2e;
   int ns;
-  dense_plan(S, units, chunk_req, &a.chunk, &ns);
+  dense_plan(S, units, chunk_req, fp8 ? 2 : 1, &a.chunk, &ns);
   if (!workspace || workspace_bytes < splitk_workspace_bytes(units, ns, D)) return (int)hipErrorInvalidValue;
   a.o.out = out;
   a.o.out_dtype = kOutBF16;
