@@ -261,12 +261,13 @@ using VMetaReg = typename std::conditional<(D >= 128), u32x4, u32x2>::type;
 // tile, when m_run = -inf): the zero-term chain of the scores starts from
 // negm = -m_ref.  The reference moves only when some head's tile maximum
 // exceeds it by more than kKiviLazy (log2 units) - always on the first tile -
-// so probabilities stay below 2^kKiviLazy and the rescale of the accumulators
+// so probabilities stay below 2^kKiviLazy = 16 (their fp16 products with the
+// value scales stay finite for scales below 4096) and the rescale of the accumulators
 // (and its exp) is skipped on most tiles.  The softmax denominators are not
 // summed here: the value zero-term MFMA has rows of ones (rows >= NGV of its A
 // operand) and accumulates sum_t p[h][t] in zv row kKiviOnesRow, rescaled with
 // the accumulators.  p receives exp2(s - m_run) in sc's order.
-constexpr float kKiviLazy = 8.f;
+constexpr float kKiviLazy = 4.f;
 constexpr int kKiviOnesRow = 12;     // zv row read back as the denominator (lanes 48-63, element 0)
 template <int D>
 __device__ __forceinline__ void kivi_softmax(f32x4 (&sc)[4], float& m_run, f32x4& negm, f32x4 (&acc)[D / 16],

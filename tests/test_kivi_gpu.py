@@ -185,3 +185,36 @@ def test_decode_back_to_back_calls(dev):
 def test_decode_many_splits_use_the_merge_kernel(dev):
     # chunk 256 over 69120 packed tokens: 270 splits, several blocks of the merge kernel
     _decode_case(dev, 2, 1, 7, 1, 128, 69120 + 32, 32, seed=6, chunk=256)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("Sq,chunk,amp", [(16256, 512, 1800.0), (16288, 4096, 900.0)])
+def test_decode_rising_scores_large_values(dev, bits, Sq, chunk, amp):
+    """Scores that climb by many octaves along the cache up to its middle (a
+    bump along head 0's query in every key) and values of magnitude ~1000
+    (value scales up to a few thousand), on splits long enough that each wave
+    runs several tiles: the two-half kernel (Sq = 16256, 512-token splits: a
+    wave's two tiles 256 tokens, ~7.7 octaves, apart) and the streaming kernel
+    (Sq = 16288, 4096-token splits: eight phases per wave, 512 tokens and
+    ~7.7 octaves apart).  The running maximum moves on many tiles, and
+    probabilities times value scales must stay finite in fp16.  Error bound
+    relative to the output's magnitude."""
+    B, Hq, Hk, D, Rw = 1, 7, 1, 128, 64
+    raw = W.kivi_raw(B, Hq, Hk, D, Sq + Rw, Rw, seed=Sq + bits)
+    q = raw["q"].float()
+    t = torch.arange(Sq + Rw, dtype=torch.float32)
+    bump = (1.0 - (t - Sq / 2).abs() / (Sq / 2)).clamp(min=0.0)
+    qdir = q[0, 0, 0] / q[0, 0, 0].pow(2).sum()
+    k = raw["k"].float() + (bump[:, None] * amp) * qdir
+    raw["k"] = k.to(torch.bfloat16)
+    raw["v"] = (raw["v"].float() * 1000.0).to(torch.bfloat16)
+    cpu = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, bits)
+    gpu = _to(cpu, dev)
+    names = ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn", "V_residual")
+    out = K.kivi_decode_attn(*[gpu[n] for n in names], bits, 32, chunk=chunk)
+    ref = R.kivi_decode_attn(*[cpu[n] for n in names], bits, 32)
+    assert torch.isfinite(out.float()).all()
+    d = (out.float().cpu() - ref.float()).abs()
+    mag = ref.float().abs().max()
+    print(f"kivi{bits} Sq{Sq} chunk{chunk} rising: max-abs {d.max():.3e} of |ref| max {mag:.3e}", flush=True)
+    assert d.max() <= 2e-2 * mag and d.mean() <= 2e-3 * mag
