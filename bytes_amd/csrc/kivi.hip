@@ -378,10 +378,13 @@ __device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg
 // exact fp16 integers:
 //   keys   s[t][h] = sum_c (q[h][c] sc[c][g]) code[t][c] + sum_c q[h][c] zero[c][g]
 //          (g = key group of t; the second sum is one MFMA chain on the zeros,
-//          whose A rows are all equal, and initialises the score tile);
+//          whose A rows are all equal, started from -m_run, and initialises
+//          the score tile, so the scores come out shifted by the running
+//          maximum; see kivi_softmax);
 //   values o[c][h] += sum_t code[t][c] (p[h][t] vs[t][g]) + sum_t p[h][t] vm[t][g]
 //          (g = value group of channel c; the second sum accumulates in zv,
-//          rows = groups, and is added to acc once after the last tile).
+//          rows = groups, and is added to acc once after the last tile; rows
+//          of ones in the same MFMA sum p, the softmax denominator).
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[D / 32], const char* kc,
                                           const char* vst, const char* vmeta_lds, const char* kmeta, float& m_run,
