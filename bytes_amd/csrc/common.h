@@ -37,6 +37,15 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// 16-byte global load with the non-temporal hint, for data streamed once in
+// whole cache lines per instruction (consecutive lanes, consecutive 16-byte
+// chunks): measured ~7.0 TB/s against ~6.1 for plain loads on MI355X.  (A
+// pattern that reads half of each line per instruction refetches the other
+// half and gets slower with it.)
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
 // 16-byte load issued by every lane (p must be readable for all of them),
 // zeroed afterwards where !live.  A load under a lane mask makes the compiler
 // merge its result with the masked-off value right after the load, which waits
@@ -80,6 +89,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
 }
+
+// Cache-policy operand of a buffer load with the non-temporal hint (nt), for
+// the same streamed, whole-line reads as ld16_nt.
+constexpr int kNonTemporal = 2;
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 

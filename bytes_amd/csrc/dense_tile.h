@@ -74,8 +74,8 @@ __device__ __forceinline__ void dense_issue(const uint16_t* kbase, const uint16_
     const int rr = p / C::CPR, pos = p - rr * C::CPR;
     const int row = live ? min(t0 + rr, S - 1) : S - 1;
     const int col = live ? pos * 8 : 0;
-    r.k[i] = ld16(kbase + (int64_t)row * k_ss + col);
-    r.v[i] = ld16(vbase + (int64_t)row * v_ss + col);
+    r.k[i] = ld16_nt(kbase + (int64_t)row * k_ss + col);
+    r.v[i] = ld16_nt(vbase + (int64_t)row * v_ss + col);
   }
 }
 
@@ -259,8 +259,8 @@ __device__ __forceinline__ void dense_issue_fp8(const uint8_t* kbase, const uint
     const int rr = p / R::CPR8, pos = p - rr * R::CPR8;
     const int row = live ? min(t0 + rr, S - 1) : S - 1;
     const int col = live ? pos * 16 : 0;
-    r.k[i] = ld16(kbase + (int64_t)row * k_ss + col);
-    r.v[i] = ld16(vbase + (int64_t)row * v_ss + col);
+    r.k[i] = ld16_nt(kbase + (int64_t)row * k_ss + col);
+    r.v[i] = ld16_nt(vbase + (int64_t)row * v_ss + col);
   }
 }
 

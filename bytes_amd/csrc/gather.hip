@@ -80,8 +80,8 @@ __device__ __forceinline__ void gather_issue(const uint16_t* kbase, const uint16
     const int j = j0 + rr;
     int row = j < n ? rows[j] : 0;
     row = row < 0 ? 0 : row;
-    r.k[i] = ld16(kbase + (int64_t)row * k_ss + pos * 8);
-    r.v[i] = ld16(vbase + (int64_t)row * v_ss + pos * 8);
+    r.k[i] = ld16_nt(kbase + (int64_t)row * k_ss + pos * 8);
+    r.v[i] = ld16_nt(vbase + (int64_t)row * v_ss + pos * 8);
   }
 }
 
@@ -97,8 +97,8 @@ __device__ __forceinline__ void gather_issue_fp8(const uint8_t* kbase, const uin
     const int j = j0 + rr;
     int row = j < n ? rows[j] : 0;
     row = row < 0 ? 0 : row;
-    r.k[i] = ld16(kbase + (int64_t)row * k_ss + pos * 16);
-    r.v[i] = ld16(vbase + (int64_t)row * v_ss + pos * 16);
+    r.k[i] = ld16_nt(kbase + (int64_t)row * k_ss + pos * 16);
+    r.v[i] = ld16_nt(vbase + (int64_t)row * v_ss + pos * 16);
   }
 }
 

@@ -350,9 +350,9 @@ __device__ __forceinline__ void kivi_issue(const KiviRsrc& rs, bool quant, int o
   const int vo = o * C::VROW;
 #pragma unroll
   for (int i = 0; i < C::VDMA; ++i)
-    r.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vq, lane * 16 + i * 1024, vo, 0));
+    r.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vq, lane * 16 + i * 1024, vo, kNonTemporal));
   const char* mb = lane < 32 ? rs.vs : rs.vz;
-  r.vm = *reinterpret_cast<const VMetaReg<D>*>(mb + (quant ? (uint32_t)(o + 2 * (lane & 31)) * C::NGV * 2 : 0u));
+  r.vm = __builtin_nontemporal_load(reinterpret_cast<const VMetaReg<D>*>(mb + (quant ? (uint32_t)(o + 2 * (lane & 31)) * C::NGV * 2 : 0u)));
 }
 
 // Write one tile's prefetched value codes and scales/zeros to the wave's LDS buffers.
@@ -762,7 +762,7 @@ __global__ __launch_bounds__(kKsWaves * 64, 1) void kivi_stream_kernel(KiviArgs 
       const char* vsrc = reinterpret_cast<const char*>(a.vq + bh * (int64_t)Sq * (D * BITS / 32)) +
                          (int64_t)wt * C::VROW;
 #pragma unroll
-      for (int i = 0; i < C::VDMA; ++i) r.v[i] = ld16(vsrc + min((lane + 64 * i) * 16, tv * C::VROW - 16));
+      for (int i = 0; i < C::VDMA; ++i) r.v[i] = ld16_nt(vsrc + min((lane + 64 * i) * 16, tv * C::VROW - 16));
       const _Float16* mp =
           a.vs + (lane < 32 ? 0 : vz_off) + (bh * Sq + wt + min(2 * (lane & 31), tv - 2)) * C::NGV;
       r.vm = *reinterpret_cast<const VMetaReg<D>*>(mp);
@@ -1021,10 +1021,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
     kivi_issue<D, BITS>(rs, quant, t < t_end ? t : t_begin, lane, rg[ph]);
     __builtin_amdgcn_sched_barrier(0);
     const int ko = krow + min(ph * HP + (int)kpc, pieces - 1) * 16;
+    // non-temporal when a half's pieces of a channel row fill whole 128-byte
+    // lines (else the other half of each line is fetched again later)
+    constexpr int KPOL = HP * 16 >= 128 ? kNonTemporal : 0;
 #pragma unroll
     for (int i = 0; i < PERH; ++i)
       kv[ph][i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kq, ko, (int)(ksplit + i * (NT / HP) * wkb), 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kq, ko, (int)(ksplit + i * (NT / HP) * wkb), KPOL));
     const int mo = mrow + min(ph * WRH + (int)mwd, nwr - 1) * 4;
 #pragma unroll
     for (int i = 0; i < PERMH; ++i) {

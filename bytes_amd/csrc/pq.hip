@@ -595,13 +595,14 @@ struct PqgCfg {
   static_assert(HP * D * 4 <= SC, "q rows fit in the score area");
 };
 
-// M code bytes of one row (16 or 8 bytes, aligned).
+// M code bytes of one row (16 or 8 bytes, aligned), streamed non-temporally
+// (consecutive threads read consecutive rows).
 template <int M>
 __device__ __forceinline__ u32x4 ld_codes(const uint8_t* p) {
   if constexpr (M == 16) {
-    return ld16(p);
+    return ld16_nt(p);
   } else {
-    const u32x2 h = *reinterpret_cast<const u32x2*>(p);
+    const u32x2 h = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
     return u32x4{h[0], h[1], 0u, 0u};
   }
 }

@@ -107,8 +107,8 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     const int e = threadIdx.x + u * kQuestThreads;
     const int pp = e / CH, c = e - (e / CH) * CH;
     const int64_t r = row0 + min(p0 + pp, np - 1);  // pages past np: copies nothing reads
-    av[u] = ld16(kmin + r * D + c * 8);
-    zv[u] = ld16(kmax + r * D + c * 8);
+    av[u] = ld16_nt(kmin + r * D + c * 8);
+    zv[u] = ld16_nt(kmax + r * D + c * 8);
   }
   auto widen = [](const u32x4& raw, f32x4& lo4, f32x4& hi4) {
 #pragma unroll
