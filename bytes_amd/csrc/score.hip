@@ -63,13 +63,15 @@ constexpr int kScoreWaves = 4;
 // resource (the store is dropped).  The store instruction is then issued on
 // every path, with no branch around it, so the waits for the next rows'
 // loads count the same requests in every iteration.  (The host keeps each
-// unit's output span below 2^31 bytes.)
+// unit's output span below 2^31 bytes.)  The stores carry the non-temporal
+// hint: the scores are read back only by the next pass, and plain stores
+// interleaved with the streaming key reads cost ~4% of the pass at C5.
 __device__ __forceinline__ void score_store(const ScoreArgs& a, int b, int row0, int rows, int r, int tok, bool ok,
                                             float v) {
   float* base = a.out + (int64_t)b * a.o_sb + (int64_t)row0 * a.o_sh;
   const uint32_t span = (uint32_t)(((int64_t)(rows - 1) * a.o_sh + a.S) * 4);
   const uint32_t off = ok ? (uint32_t)(((int64_t)r * a.o_sh + tok) * 4) : 0x80000000u;
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), buf_rsrc(base, span), (int)off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), buf_rsrc(base, span), (int)off, 0, kNonTemporal);
 }
 
 __device__ __forceinline__ void score_emit_sum(const ScoreArgs& a, float tot, int tok, int b, int hk, int lg,
@@ -79,26 +81,44 @@ __device__ __forceinline__ void score_emit_sum(const ScoreArgs& a, float tot, in
   if (hlds && ok) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
 }
 
+// Group-summed scores of 64 consecutive tokens, one per lane (lane l holds
+// token tok = t + l): one store instruction of whole lines.  (Stores of 16
+// lanes per column tile cost ~15% of the score pass's time at C5.)
+__device__ __forceinline__ void score_emit_sum64(const ScoreArgs& a, float tot, int tok, int b, int hk,
+                                                 uint32_t* hlds) {
+  const bool ok = tok < a.S;
+  score_store(a, b, hk, 1, 0, tok, ok, tot);
+  if (hlds && ok) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
+}
+
 // ---- bf16 / fp8 keys ------------------------------------------------------
 
 template <int D, bool FP8, bool GS>
 struct DenseKeys {
   static constexpr int CT = 4;                 // 16-token column tiles per wave iteration
-  typedef typename std::conditional<FP8, u32x2, u32x4>::type T;
-  struct Regs {
-    T k[4][D / 32];          // [column tile][k-step]
-  };
   static constexpr int ES = FP8 ? 1 : 2;       // bytes per key element
-  __amdgpu_buffer_rsrc_t rk;   // the unit's key rows (rows at or past S read zero)
-  uint32_t koff, row_bytes;    // this lane's byte offset in a tile row block; bytes per token row
+  static constexpr int CPR = D * ES / 16;      // 16-byte chunks per key row
+  // One iteration's 64 key rows are read whole-line (consecutive lanes,
+  // consecutive 16-byte chunks of a row; non-temporal) and staged in the
+  // wave's LDS block, chunk c of row r at slot c ^ (r % CPR), where the MFMA
+  // B operands are read from: the 16 rows one operand read touches sit in
+  // distinct slots.  (Reading the operands straight from memory splits each
+  // row's 128-byte lines over several instructions, which the non-temporal
+  // hint turns into refetches.)
+  static constexpr int kWaveLds = 64 * D * ES;
+  static constexpr int kLds = kScoreWaves * kWaveLds;
+  struct Regs {
+    u32x4 k[CPR];            // chunk lane + 64 i: row (lane + 64 i) / CPR, chunk (lane + 64 i) % CPR
+  };
+  const uint8_t* kbase;         // the unit's key rows
+  uint32_t row_bytes;          // bytes per token row
+  char* kst;                   // this wave's LDS block
   bf16x8 qa[D / 32];
 
   __device__ __forceinline__ void init(const ScoreArgs& a, int b, int hk, int hq0, int nh, int lane) {
     const int l16 = lane & 15, lg = lane >> 4;
     row_bytes = (uint32_t)(a.k_ss * ES);
-    rk = buf_rsrc(static_cast<const uint8_t*>(a.k) + ((int64_t)b * a.k_sb + (int64_t)hk * a.k_sh) * ES,
-                  (uint32_t)((int64_t)a.S * a.k_ss * ES));
-    koff = (uint32_t)l16 * row_bytes + lg * 8 * ES;
+    kbase = static_cast<const uint8_t*>(a.k) + ((int64_t)b * a.k_sb + (int64_t)hk * a.k_sh) * ES;
     // Q as the A operand: lane holds Q[h = l16][dims (kk*4 + lg)*8 .. +8]
     const bool live = l16 < nh;
     const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + (live ? l16 : 0)) * a.q_sh + lg * 8;
@@ -107,20 +127,18 @@ struct DenseKeys {
       qa[kk] = __builtin_bit_cast(bf16x8, ld16_live(qp + kk * 32, live));
   }
 
-  // K rows t .. t+63 of one iteration as B operands: buffer loads with the
-  // iteration's row offset in the scalar offset (rows past S read zero).
+  // K rows t .. t+63 of one iteration, whole rows per load instruction,
+  // through a buffer resource that starts at row t (wave-uniform) and ends at
+  // row S, so rows past S read zero and the per-lane offsets are the same in
+  // every iteration.
   __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lane, Regs& r) const {
+    const auto rk = buf_rsrc(kbase + (uint64_t)(uint32_t)t * row_bytes,
+                             (uint32_t)(t < a.S ? a.S - t : 0) * row_bytes);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      // row block in the (scalar) offset, k-step in the instruction's immediate
-      const uint32_t soff = (uint32_t)(t + c * 16) * row_bytes;
-#pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) {
-        if constexpr (FP8)
-          r.k[c][kk] = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)(koff + kk * 32 * ES), (int)soff, 0);
-        else
-          r.k[c][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(koff + kk * 32 * ES), (int)soff, 0);
-      }
+    for (int i = 0; i < CPR; ++i) {
+      const int p = lane + 64 * i;
+      const uint32_t off = (uint32_t)(p / CPR) * row_bytes + (uint32_t)(p % CPR) * 16;
+      r.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)off, 0, kNonTemporal));
     }
   }
 
@@ -134,26 +152,43 @@ struct DenseKeys {
   __device__ __forceinline__ void tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
                                        int nh, uint32_t* hlds) const {
     const int l16 = lane & 15, lg = lane >> 4;
+    wave_lds_sync();                             // the previous iteration's operand reads are done
+#pragma unroll
+    for (int i = 0; i < CPR; ++i) {
+      const int p = lane + 64 * i;
+      const int row = p / CPR, ch = p % CPR;
+      *reinterpret_cast<u32x4*>(kst + (row * CPR + (ch ^ (row % CPR))) * 16) = r.k[i];
+    }
+    wave_lds_sync();
+    float keep = 0.f;                            // group sum: lane group lg keeps column tile lg's
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      const int row = c * 16 + l16;
+      const char* rp = kst + row * CPR * 16;
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < D / 32; ++kk) s = mfma_bf16(qa[kk], operand(r.k[c][kk]), s);
+      for (int kk = 0; kk < D / 32; ++kk) {
+        if constexpr (FP8) {
+          // dims (kk*4 + lg)*8 .. +8: 8 bytes, half lg & 1 of chunk kk*2 + lg/2
+          const int ch = kk * 2 + (lg >> 1);
+          const u32x2 w = *reinterpret_cast<const u32x2*>(rp + (ch ^ (row % CPR)) * 16 + (lg & 1) * 8);
+          s = mfma_bf16(qa[kk], operand(w), s);
+        } else {
+          const int ch = kk * 4 + lg;
+          const u32x4 w = *reinterpret_cast<const u32x4*>(rp + (ch ^ (row % CPR)) * 16);
+          s = mfma_bf16(qa[kk], operand(w), s);
+        }
+      }
       const int tok = t + c * 16 + l16;
       if constexpr (GS) {
-        // heads lg*4 + i; group sum in head order, lane groups added in order
+        // heads lg*4 + i summed in head order per lane, then the four lane
+        // groups of the column folded by row swaps
         float part = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (lg * 4 + i < nh) part += s[i] * a.scaling;
-        const float p1 = __shfl(part, l16 + 16, 64);
-        const float p2 = __shfl(part, l16 + 32, 64);
-        const float p3 = __shfl(part, l16 + 48, 64);
-        float tot = part;
-        if (nh > 4) tot += p1;
-        if (nh > 8) tot += p2;
-        if (nh > 12) tot += p3;
-        score_emit_sum(a, tot, tok, b, hk, lg, hlds);
+        const float tot = col_sum4(part);
+        keep = lg == c ? tot : keep;
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -162,6 +197,7 @@ struct DenseKeys {
         }
       }
     }
+    if constexpr (GS) score_emit_sum64(a, keep, t + lane, b, hk, hlds);
   }
 };
 
@@ -190,6 +226,8 @@ struct PackedKeys {
     T k[CT];                                   // [column tile]
     SR srow, mrow;                             // scale / min row (NG bf16) of token t + lane
   };
+  static constexpr int kLds = 16;              // operands come straight from registers
+  char* kst;
   // Buffer resources over one KV head's codes and scale/min rows: every load
   // is a 32-bit lane offset plus a uniform row offset, and rows at or past S
   // read as zero (their scores are not stored).
@@ -432,6 +470,8 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   const int nh = min(a.HPU, a.G - hb * a.HPU);
   P pol;
   pol.init(a, b, hk, hq0, nh, lane);
+  __shared__ __attribute__((aligned(16))) char kst_mem[P::kLds];
+  pol.kst = kst_mem + w * (P::kLds / kScoreWaves);
 
   const int t_begin = part * a.tok_per_wg;
   const int t_end = min(t_begin + a.tok_per_wg, a.S);
@@ -560,8 +600,8 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
     return (int)hipErrorNotSupported;
   a.scaling = scaling;
   const long units = (long)B * Hk * a.HB;
-  // about 8 workgroups per CU in total, each a multiple of one iteration of all waves
-  const long target = 8L * device_cu_count();
+  // about 4 workgroups per CU in total (two rounds of two), each a multiple of one iteration of all waves
+  const long target = 4L * device_cu_count();
   const int step = kScoreWaves * 64;
   long per = ((long)S * units + target - 1) / target;
   per = (per + step - 1) / step * step;
