@@ -81,7 +81,7 @@ SIGNATURES: Dict[str, Tuple] = {
         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,     # k, v strides (b, h, s)
         c_i64, c_i64,                                 # out strides
         c_f32, c_int, c_vp, c_sz, c_vp),              # scaling, chunk, workspace, bytes, stream
-    "bytes_stream_read": (c_vp, c_i64, c_int, c_vp, c_vp),
+    "bytes_stream_read": (c_vp, c_i64, c_int, c_int, c_vp, c_vp),
     "bytes_empty_launch": (c_int, c_vp),
     "bytes_quest_page_minmax": (c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp),
     "bytes_quest_page_scores": (

@@ -98,6 +98,7 @@ __global__ __launch_bounds__(kGrThreads) void gather_reduce_kernel(const uint16_
 constexpr int kSrThreads = 256;
 constexpr int kSrLoads = 8;         // 16-byte loads per thread in flight
 
+template <bool NT>
 __global__ __launch_bounds__(kSrThreads) void stream_read_kernel(const u32x4* src, int64_t vec_per_wg, float* out) {
   const u32x4* p = src + (int64_t)blockIdx.x * vec_per_wg;
   uint32_t acc = 0;
@@ -106,7 +107,8 @@ __global__ __launch_bounds__(kSrThreads) void stream_read_kernel(const u32x4* sr
 #pragma unroll
     for (int i = 0; i < kSrLoads; ++i) {
       const int64_t e = base + threadIdx.x + (int64_t)i * kSrThreads;
-      r[i] = ld16(p + (e < vec_per_wg ? e : vec_per_wg - 1));
+      const u32x4* a = p + (e < vec_per_wg ? e : vec_per_wg - 1);
+      r[i] = NT ? ld16_nt(a) : ld16(a);
     }
 #pragma unroll
     for (int i = 0; i < kSrLoads; ++i) acc ^= r[i][0] ^ r[i][1] ^ r[i][2] ^ r[i][3];
@@ -256,11 +258,13 @@ int bytes_packed_stage(const void* q, int64_t q_sb, int64_t q_sh, const void* kp
 
 // Floor probes (see stream_read_kernel): `wgs` workgroups of 256 threads read
 // bytes / wgs each from src (bytes a multiple of 16 * wgs; src 16-byte
-// aligned); out holds wgs * 256 floats.
-int bytes_stream_read(const void* src, int64_t bytes, int wgs, void* out, void* stream) {
+// aligned); out holds wgs * 256 floats.  nontemporal != 0 issues the loads
+// with the non-temporal hint, as the decode kernels stream K/V rows.
+int bytes_stream_read(const void* src, int64_t bytes, int wgs, int nontemporal, void* out, void* stream) {
   if (!src || !out || wgs <= 0 || bytes <= 0 || bytes % (16LL * wgs) != 0) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)wgs), dim3(kSrThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const u32x4*>(src), bytes / 16 / wgs, static_cast<float*>(out));
+  hipLaunchKernelGGL(nontemporal ? stream_read_kernel<true> : stream_read_kernel<false>, dim3((unsigned)wgs),
+                     dim3(kSrThreads), 0, static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
+                     bytes / 16 / wgs, static_cast<float*>(out));
   return (int)hipGetLastError();
 }
 

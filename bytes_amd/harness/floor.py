@@ -10,6 +10,8 @@ bench.py (csrc/harness.hip: stream_read_kernel, empty_kernel):
              dependent HBM round trip after launch)
   stream     W workgroups reading N bytes in total, contiguous slices, eight
              16-byte loads per thread in flight
+  stream_nt  the same reads with the non-temporal hint (the decode kernels
+             stream their K/V rows so)
 for W in {256, 512, 1024, 2048} and N from 4 MB to 1 GB.
 
     python -m bytes_amd.harness.floor
@@ -51,10 +53,12 @@ def main(argv=None):
         del bufs
     for nbytes in (4 << 20, 32 << 20, 128 << 20, 512 << 20, 1 << 30):
         bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(copies_for(nbytes))]
-        for wgs in (256, 512, 1024, 2048):
-            outs = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
-            emit("stream", wgs, nbytes, graph_ms(lambda x, w=wgs: stream_read(x, w, outs), bufs,
-                                                 runs=max(5, a.runs // (1 + nbytes // (128 << 20)))))
+        for nt in (False, True):
+            for wgs in (256, 512, 1024, 2048):
+                outs = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+                emit("stream_nt" if nt else "stream", wgs, nbytes,
+                     graph_ms(lambda x, w=wgs, n=nt: stream_read(x, w, outs, nontemporal=n), bufs,
+                              runs=max(5, a.runs // (1 + nbytes // (128 << 20)))))
         del bufs
         torch.cuda.empty_cache()
     os.makedirs(os.path.dirname(a.output_json) or ".", exist_ok=True)

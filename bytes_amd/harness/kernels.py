@@ -60,10 +60,11 @@ def stage_score(q: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, zero
     return out
 
 
-def stream_read(src: torch.Tensor, wgs: int, out: torch.Tensor = None) -> torch.Tensor:
+def stream_read(src: torch.Tensor, wgs: int, out: torch.Tensor = None, nontemporal: bool = False) -> torch.Tensor:
     """Floor probe: `wgs` workgroups of 256 threads read src (a contiguous
     device tensor whose byte size is a multiple of 16 * wgs) in 16-byte loads,
-    one contiguous slice each; returns the fp32 fold [wgs * 256]."""
+    one contiguous slice each (with the non-temporal hint if `nontemporal`);
+    returns the fp32 fold [wgs * 256]."""
     C.cuda_tensors(src)
     if not src.is_contiguous():
         raise ValueError("src must be contiguous")
@@ -72,7 +73,7 @@ def stream_read(src: torch.Tensor, wgs: int, out: torch.Tensor = None) -> torch.
         raise ValueError(f"{nbytes} bytes do not split into {wgs} slices of 16-byte words")
     if out is None:
         out = torch.empty(wgs * 256, dtype=torch.float32, device=src.device)
-    call("bytes_stream_read", ptr(src), nbytes, int(wgs), ptr(out), stream_of(src))
+    call("bytes_stream_read", ptr(src), nbytes, int(wgs), int(bool(nontemporal)), ptr(out), stream_of(src))
     return out
 
 

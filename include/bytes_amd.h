@@ -318,8 +318,10 @@ int bytes_packed_stage(const void* q, int64_t q_sb, int64_t q_sh, const void* kp
  * on MI355X).  bytes_stream_read: `wgs` workgroups of 256 threads each read
  * bytes / wgs contiguous bytes of src in 16-byte loads (bytes a multiple of
  * 16 * wgs, src 16-byte aligned), out [wgs * 256] fp32 (a fold of the words
- * read).  bytes_empty_launch: `wgs` workgroups that do nothing. */
-int bytes_stream_read(const void* src, int64_t bytes, int wgs, void* out, void* stream);
+ * read); nontemporal != 0 issues the loads with the non-temporal hint (as
+ * the decode kernels read K/V rows).  bytes_empty_launch: `wgs` workgroups
+ * that do nothing. */
+int bytes_stream_read(const void* src, int64_t bytes, int wgs, int nontemporal, void* out, void* stream);
 int bytes_empty_launch(int wgs, void* stream);
 
 /* ---------------------------------------------------------------------------

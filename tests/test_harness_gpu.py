@@ -57,15 +57,16 @@ def test_packed_stages_match_oracle(dev, bits, D):
             assert torch.allclose(out, ref, rtol=1e-4, atol=1e-3), (stage, (out - ref).abs().max())
 
 
-def test_stream_read_folds_every_word(dev):
+@pytest.mark.parametrize("nontemporal", [False, True])
+def test_stream_read_folds_every_word(dev, nontemporal):
     """The floor probe reads each 16-byte word of its slice exactly once:
     thread t of workgroup g folds (XOR) the words of vectors t + 256*i of
-    each 2048-vector block of slice g."""
+    each 2048-vector block of slice g (plain and non-temporal loads alike)."""
     import numpy as np
     wgs, vec_per_wg = 4, 4096
     g = torch.Generator().manual_seed(7)
     words = torch.randint(0, 2**31 - 1, (wgs * vec_per_wg * 4,), generator=g, dtype=torch.int64).to(torch.int32)
-    out = HK.stream_read(words.to(dev), wgs).cpu()
+    out = HK.stream_read(words.to(dev), wgs, nontemporal=nontemporal).cpu()
     w = words.numpy().view(np.uint32).reshape(wgs, vec_per_wg // 2048, 8, 256, 4)
     want = np.bitwise_xor.reduce(w, axis=(1, 2, 4)).reshape(-1).astype(np.float32)
     assert np.array_equal(out.numpy(), want)
