@@ -11,10 +11,10 @@
 // A = Q (heads as rows) and B = K^T (tokens as columns).  Both operands use
 // the same permutation of the contraction index: at k-step kk, lane l holds
 // dims (kk*4 + l/16)*8 .. +8 of its row, so a lane's four k-steps cover 64
-// contiguous bytes of one key row and each key row is read by 16-byte loads
-// straight from HBM into the MFMA operand registers (no LDS round trip).  The
-// output tile lands with head (l/16)*4 + i and token l%16 in lane l, so the
-// group sum of up to four heads is a sum inside one lane.
+// contiguous bytes of one key row.  Key rows arrive whole-line (non-temporal
+// loads) and are staged in the wave's LDS block, from which the B operands are
+// read.  The output tile lands with head (l/16)*4 + i and token l%16 in lane
+// l, so the group sum of up to four heads is a sum inside one lane.
 //
 // fp8 (OCP e4m3fn) keys (`score_bits=8`, :1113) load 8 bytes per operand and
 // are widened to bf16 exactly in registers.
@@ -57,6 +57,8 @@ struct ScoreArgs {
 };
 
 constexpr int kScoreWaves = 4;
+constexpr int kStoreBatch = 4;   // wave iterations whose group sums are stored together
+constexpr int kWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): every vector memory request done
 
 // Score stores go through a buffer resource over the unit's output rows
 // [row0, row0 + rows), and a lane that must not store gets an offset past the
@@ -129,11 +131,11 @@ struct DenseKeys {
 
   // K rows t .. t+63 of one iteration, whole rows per load instruction,
   // through a buffer resource that starts at row t (wave-uniform) and ends at
-  // row S, so rows past S read zero and the per-lane offsets are the same in
-  // every iteration.
-  __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lane, Regs& r) const {
+  // row lim (<= S), so rows at or past lim read zero without a memory access
+  // and the per-lane offsets are the same in every iteration.
+  __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lim, int lane, Regs& r) const {
     const auto rk = buf_rsrc(kbase + (uint64_t)(uint32_t)t * row_bytes,
-                             (uint32_t)(t < a.S ? a.S - t : 0) * row_bytes);
+                             (uint32_t)(t < lim ? lim - t : 0) * row_bytes);
 #pragma unroll
     for (int i = 0; i < CPR; ++i) {
       const int p = lane + 64 * i;
@@ -149,8 +151,12 @@ struct DenseKeys {
     return __builtin_bit_cast(bf16x8, b);
   }
 
-  __device__ __forceinline__ void tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
-                                       int nh, uint32_t* hlds) const {
+  // Group sums are returned (token t + lane per lane) for the driver to
+  // store; per-head scores are stored here.
+  static constexpr bool kDeferStore = GS;
+
+  __device__ __forceinline__ float tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
+                                        int nh, uint32_t* hlds) const {
     const int l16 = lane & 15, lg = lane >> 4;
     wave_lds_sync();                             // the previous iteration's operand reads are done
 #pragma unroll
@@ -197,7 +203,7 @@ struct DenseKeys {
         }
       }
     }
-    if constexpr (GS) score_emit_sum64(a, keep, t + lane, b, hk, hlds);
+    return keep;
   }
 };
 
@@ -227,6 +233,7 @@ struct PackedKeys {
     SR srow, mrow;                             // scale / min row (NG bf16) of token t + lane
   };
   static constexpr int kLds = 16;              // operands come straight from registers
+  static constexpr bool kDeferStore = false;   // scores are stored by tile()
   char* kst;
   // Buffer resources over one KV head's codes and scale/min rows: every load
   // is a 32-bit lane offset plus a uniform row offset, and rows at or past S
@@ -314,7 +321,8 @@ struct PackedKeys {
     }
   }
 
-  __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lane, Regs& r) const {
+  // (lim is not used: the resources end at S)
+  __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lim, int lane, Regs& r) const {
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
       const uint32_t row = (uint32_t)(t + c * 16);                  // wave-uniform
@@ -494,16 +502,68 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     // the tile's first use of the current rows, so only one batch is ever in
     // flight).
     typename P::Regs r0, r1;
-    pol.issue(a, t, lane, r0);
-    while (true) {
+    pol.issue(a, t, t_end, lane, r0);
+    if constexpr (P::kDeferStore) {
+      // Group sums of kStoreBatch iterations are stored together: each store
+      // sits in the in-order memory counter between two batches of key
+      // loads, so one store per iteration would hold up every wait for the
+      // next rows until the write is acknowledged.
+      static_assert(kStoreBatch % 2 == 0, "the register sets alternate within a batch");
+      // one iteration: the next rows are requested (past the range the
+      // resource has zero length, so the last step's requests read nothing
+      // and return at once), the current rows scored; false at the range end
+      auto step = [&](float& sc, typename P::Regs& cur, typename P::Regs& nxt) {
+        const bool more = t + STEP < t_end;
+        pol.issue(a, t + STEP, t_end, lane, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        sc = pol.tile(a, cur, t, lane, b, hk, hq0, nh, hlds);
+        // finished here: left alone, the compiler sinks each tile's group sums
+        // down to the stores, past the next batch's loads, and then needs
+        // registers that those loads are still filling
+        asm volatile("" : "+v"(sc));
+        t += STEP;
+        return more;
+      };
+      // Each exit waits for its last (empty) requests in a block of its own:
+      // the compiler's wait placement does not tell paths apart, so requests
+      // still in flight where an exit joins the full-batch stores would make
+      // those stores wait for the next batch's rows.
+      while (true) {
+        float sc[kStoreBatch];
+        const int t0 = t;
+        int n = 0;
+#pragma unroll
+        for (int j = 0; j < kStoreBatch; j += 2) {
+          if (!step(sc[j], r0, r1)) {
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            n = j + 1;
+            break;
+          }
+          if (!step(sc[j + 1], r1, r0)) {
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            n = j + 2;
+            break;
+          }
+        }
+        if (n == 0) {
+#pragma unroll
+          for (int j = 0; j < kStoreBatch; ++j) score_emit_sum64(a, sc[j], t0 + j * STEP + lane, b, hk, hlds);
+          continue;
+        }
+#pragma unroll
+        for (int j = 0; j < kStoreBatch; ++j)
+          if (j < n) score_emit_sum64(a, sc[j], t0 + j * STEP + lane, b, hk, hlds);
+        break;
+      }
+    } else while (true) {
       const bool more1 = t + STEP < t_end;
-      pol.issue(a, more1 ? t + STEP : t, lane, r1);
+      pol.issue(a, more1 ? t + STEP : t, a.S, lane, r1);
       __builtin_amdgcn_sched_barrier(0);
       pol.tile(a, r0, t, lane, b, hk, hq0, nh, hlds);
       t += STEP;
       if (!more1) break;
       const bool more0 = t + STEP < t_end;
-      pol.issue(a, more0 ? t + STEP : t, lane, r0);
+      pol.issue(a, more0 ? t + STEP : t, a.S, lane, r0);
       __builtin_amdgcn_sched_barrier(0);
       pol.tile(a, r1, t, lane, b, hk, hq0, nh, hlds);
       t += STEP;
