@@ -660,8 +660,10 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
     return (int)hipErrorNotSupported;
   a.scaling = scaling;
   const long units = (long)B * Hk * a.HB;
-  // about 4 workgroups per CU in total (two rounds of two), each a multiple of one iteration of all waves
-  const long target = 4L * device_cu_count();
+  // about 8 workgroups per CU in total (four rounds of two resident), each a
+  // multiple of one iteration of all waves: finer than two rounds, so the
+  // last round's uneven finish costs less
+  const long target = 8L * device_cu_count();
   const int step = kScoreWaves * 64;
   long per = ((long)S * units + target - 1) / target;
   per = (per + step - 1) / step * step;
