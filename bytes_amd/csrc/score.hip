@@ -109,6 +109,11 @@ struct DenseKeys {
   // hint turns into refetches.)
   static constexpr int kWaveLds = 64 * D * ES;
   static constexpr int kLds = kScoreWaves * kWaveLds;
+  // LDS reserved per workgroup.  With 256-byte rows two resident workgroups
+  // would keep 256 KB of key rows in flight per CU; one (128 KB) streams
+  // faster (C5: 336 against 347 us per score pass), so the reservation
+  // leaves room for only one.  Narrower rows keep two (128 KB in flight).
+  static constexpr int kLdsReserve = D * ES >= 256 ? 2 * kLds : kLds;
   struct Regs {
     u32x4 k[CPR];            // chunk lane + 64 i: row (lane + 64 i) / CPR, chunk (lane + 64 i) % CPR
   };
@@ -233,6 +238,7 @@ struct PackedKeys {
     SR srow, mrow;                             // scale / min row (NG bf16) of token t + lane
   };
   static constexpr int kLds = 16;              // operands come straight from registers
+  static constexpr int kLdsReserve = kLds;
   static constexpr bool kDeferStore = false;   // scores are stored by tile()
   char* kst;
   // Buffer resources over one KV head's codes and scale/min rows: every load
@@ -478,7 +484,7 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   const int nh = min(a.HPU, a.G - hb * a.HPU);
   P pol;
   pol.init(a, b, hk, hq0, nh, lane);
-  __shared__ __attribute__((aligned(16))) char kst_mem[P::kLds];
+  __shared__ __attribute__((aligned(16))) char kst_mem[P::kLdsReserve];
   pol.kst = kst_mem + w * (P::kLds / kScoreWaves);
 
   const int t_begin = part * a.tok_per_wg;
@@ -660,9 +666,10 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
     return (int)hipErrorNotSupported;
   a.scaling = scaling;
   const long units = (long)B * Hk * a.HB;
-  // about 8 workgroups per CU in total (four rounds of two resident), each a
-  // multiple of one iteration of all waves: finer than two rounds, so the
-  // last round's uneven finish costs less
+  // about 8 workgroups per CU in total (eight rounds of one resident with
+  // 256-byte key rows, four of two otherwise), each a multiple of one
+  // iteration of all waves: fine enough that the last round's uneven finish
+  // costs little
   const long target = 8L * device_cu_count();
   const int step = kScoreWaves * 64;
   long per = ((long)S * units + target - 1) / target;
