@@ -43,6 +43,22 @@ def test_group_scores(dev, B, Hq, Hk, S):
     assert (s.cpu() - ref).abs().max() <= SCORE_TOL
 
 
+def test_group_scores_long_ragged(dev):
+    """A cache long enough that each wave of the score pass runs several
+    iterations and stores whole batches of group sums, with a ragged last
+    range (S = 200003), plain and with the fused selection histogram of the
+    top-k pipeline: scores against the oracle, the pipeline's selection
+    bit-exact against the oracle's top-k on the same scores."""
+    B, Hq, Hk, S = 2, 24, 8, 200003
+    x = W.dense(B, Hq, Hk, 128, S, seed=5)
+    q, k, v = (x[n].to(dev) for n in ("q", "k", "v"))
+    s = SP.group_scores(q, k, 0.088)
+    ref = R.group_scores(x["q"], x["k"], 0.088)
+    assert (s.cpu() - ref).abs().max() <= SCORE_TOL
+    _, idx = SP.token_topk_decode(q, k, v, 1024, 0.088)
+    assert torch.equal(idx.cpu().long(), R.topk_indices(s.cpu(), 1024, sorted_by_score=False))
+
+
 def _tie_heavy(rows, n, seed):
     g = torch.Generator().manual_seed(seed)
     s = torch.randint(-8, 8, (rows, n), generator=g).float() * 0.25      # many exact ties
