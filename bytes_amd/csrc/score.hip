@@ -114,6 +114,7 @@ struct DenseKeys {
   // faster (C5: 336 against 347 us per score pass), so the reservation
   // leaves room for only one.  Narrower rows keep two (128 KB in flight).
   static constexpr int kLdsReserve = D * ES >= 256 ? 2 * kLds : kLds;
+  static_assert(kLdsReserve + 2048 * 4 <= 160 * 1024, "the reservation and the histogram fit a CU's LDS");
   struct Regs {
     u32x4 k[CPR];            // chunk lane + 64 i: row (lane + 64 i) / CPR, chunk (lane + 64 i) % CPR
   };
