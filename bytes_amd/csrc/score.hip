@@ -473,6 +473,11 @@ struct PackedKeys {
 
 // ---- driver ---------------------------------------------------------------
 
+// The register budget is that of two workgroups per CU; policies whose LDS
+// reservation holds a CU to one workgroup make the compiler report the
+// missed occupancy target, which is intended there.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <class P>
 __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a) {
   PREFETCH_ARGS(a);
@@ -584,6 +589,8 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
       if (hlds_mem[i]) atomicAdd(hr + i, hlds_mem[i]);
   }
 }
+
+#pragma clang diagnostic pop
 
 template <int D, bool FP8>
 static void launch_dense(const dim3& g, const dim3& blk, hipStream_t st, const ScoreArgs& a) {
