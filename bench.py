@@ -556,8 +556,10 @@ def entry(case: Case, r: dict, cpu) -> dict:
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # defaults: at least 200 timed steps after 20 warm-up steps, as the
+    # baseline's measurement rules ask
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default=HEADLINE)
     ap.add_argument("--only", action="store_true", help="time the named config alone (no per_config)")
     ap.add_argument("--all", action="store_true", help="add the extra configs to per_config")
