@@ -13,14 +13,19 @@ synchronisations.  The step's dominant kernel is then timed on its own: at
 least 60 more (eager) steps, each with a HIP event pair that the library
 records on the kernel's stream right around that launch, and the median pair.
 
+Before a config is timed, one step on its own inputs is checked against the
+CPU oracle (test infrastructure, oracle/, used only as the checker): outside
+the attention tolerance (max-abs 2e-2, mean-abs 2e-3) the run stops and no
+JSON line is printed; each config's `gate` records the differences.
+
 `value` is the headline config (BASELINE C2, KIVI 2-bit) in us/step;
 `roofline` is its dominant kernel's algorithmic bytes over that kernel's
 median duration (`step_frac` the same over the whole step).  `per_config`
 holds the same figures for every other BASELINE config (C1, C2 4-bit, the
-dense L>=16K point, C3, C4, C5 at k = 256/1024/4096; --all adds more).  Each
-config's cpu_baseline times the CPU oracle (test infrastructure, oracle/) on
-the whole step, or on a stated sample where the whole step would take
-minutes (C5).  Rank 0 prints one JSON line.
+dense and KIVI L>=16K points, C3, C4, C5 at k = 256/1024/4096; --all adds
+more).  Each config's cpu_baseline times the CPU oracle on the whole step,
+or on a stated sample where the whole step would take minutes (C5).  Rank 0
+prints one JSON line.
 """
 from __future__ import annotations
 
@@ -68,6 +73,13 @@ class Case:
         seconds."""
         raise NotImplementedError
 
+    def reference(self, inp, out):
+        """Parity gate: (GPU output, oracle output) on the CPU for the step's
+        own inputs `inp` and output `out`; where the oracle's fp32 copies of
+        the whole cache would not fit host memory, batch row 0 of both.  None:
+        no gate (not a decode step)."""
+        raise NotImplementedError
+
 
 class DenseCase(Case):
     kernel = "dense_decode_kernel"
@@ -106,6 +118,13 @@ class DenseCase(Case):
         x = W.dense(*self.shape, seed=0)
         return (f"the whole step: oracle decode_attn on q [{B},{Hq},1,{D}], K/V [{B},{Hk},{L},{D}]",
                 lambda: R.decode_attn(x["q"], x["k"], x["v"], scale=x["scale"]), 1)
+
+    def reference(self, inp, out):
+        from oracle import reference as R
+        B, Hq, Hk, D, L = self.shape
+        rows = slice(0, 1) if B * Hk * L * D > (1 << 28) else slice(0, B)
+        q, k, v = (inp[n][rows].cpu() for n in ("q", "k", "v"))
+        return out[rows].cpu(), R.decode_attn(q, k, v, scale=inp["scale"])
 
 
 class DenseFp8Case(DenseCase):
@@ -180,6 +199,12 @@ class KiviCase(Case):
                 f"Sq={L - Rw} packed + {Rw} residual",
                 lambda: R.kivi_decode_attn(*args, self.bits, 32), 1)
 
+    def reference(self, inp, out):
+        from oracle import reference as R
+        args = [inp[n].cpu() for n in ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn",
+                                       "V_residual")]
+        return out.cpu(), R.kivi_decode_attn(*args, self.bits, 32)
+
 
 class TopkCase(Case):
     """BASELINE C5: group-summed fp32 scores per KV head over the whole cache,
@@ -244,6 +269,20 @@ class TopkCase(Case):
                 f"K/V [1,{Hk},{L},{D}]; x {B} to a full step",
                 lambda: R.token_topk_decode(x["q"], x["k"], x["v"], self.kb, x["scale"]), B)
 
+    def reference(self, inp, out):
+        from oracle import reference as R
+        q, k, v = (inp[n][0:1].cpu() for n in ("q", "k", "v"))
+        if self.score_bits == 16:
+            ks = k
+        elif self.score_bits == 8:
+            ks = inp["ks"][0:1].cpu().float()
+        else:
+            ks = R.score_keys_dequant(inp["ks"][0:1].cpu(), inp["ksc"][0:1].cpu(), inp["kzr"][0:1].cpu(),
+                                      self.score_bits, 32)
+        idx = R.topk_indices(R.group_scores(q, ks, inp["scale"]), self.kb)
+        o = out[0] if isinstance(out, tuple) else out              # (output, selected indices)
+        return o[0:1].cpu(), R.sparse_gather_attn(q, k, v, idx, inp["scale"])
+
 
 class QuestCase(Case):
     """BASELINE C4: Quest page bounds from the per-page min/max metadata, top
@@ -294,6 +333,12 @@ class QuestCase(Case):
         return (f"the whole step: oracle page metadata + bounds + page top-k + gather "
                 f"(B{B} Hq{Hq} L{L})", run, 1)
 
+    def reference(self, inp, out):
+        from oracle import reference as R
+        q, k, v = (inp[n].cpu() for n in ("q", "k", "v"))
+        _, tok, _ = R.quest_select(q, k, self.budget, self.page, inp["scale"])
+        return out.cpu(), R.sparse_gather_attn(q, k, v, tok, inp["scale"])
+
 
 class PqCase(Case):
     """BASELINE C3: PQ-LUT decode with quantized keys and values.  Scoring q
@@ -342,6 +387,12 @@ class PqCase(Case):
         return (f"the whole step: oracle LUT build + pq_lut_kv, B{B} Hq{Hq} Hkv{Hk} L{L} (seeded random "
                 f"codes and codebooks of the C3 shape)", run, 1)
 
+    def reference(self, inp, out):
+        from oracle import reference as R
+        x = {n: inp[n].cpu() for n in ("q", "k_cb", "v_cb", "k_idx", "v_idx")}
+        lut = R.pq_build_lut(x["q"], x["k_cb"], inp["scale"])
+        return out.cpu(), R.decode_attn_pq_lut_kv(lut, x["k_idx"], x["v_idx"], x["v_cb"])
+
 
 class CopyCase(Case):
     """Plain device copy of known size: the calibration point for HBM byte counters
@@ -367,6 +418,9 @@ class CopyCase(Case):
         src = torch.randint(0, 255, (self.nbytes // 16,), dtype=torch.uint8)
         dst = torch.empty_like(src)
         return f"copy of {self.nbytes // 16} bytes", lambda: dst.copy_(src), 16
+
+    def reference(self, inp, out):
+        return None
 
 
 def cases():
@@ -470,8 +524,36 @@ def time_kernel(case: Case, inps, steps: int) -> float:
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
 
 
-def measure(case: Case, steps: int, warmup: int, dev) -> dict:
+GATE_MAX_ABS, GATE_MEAN_ABS = 2e-2, 2e-3      # north_star attention tolerance
+
+
+class GateFailure(RuntimeError):
+    pass
+
+
+def parity_gate(case: Case, base, dev):
+    """One step on the config's own inputs checked against the CPU oracle
+    (the checker, as in the tests) before anything is timed; a step outside
+    the attention tolerance raises GateFailure, so no figure is reported
+    for it."""
+    out = case.step(base)
+    torch.cuda.synchronize()
+    pair = case.reference(base, out)
+    if pair is None:
+        return None
+    got, ref = pair
+    d = (got.float() - ref.float()).abs()
+    g = {"max_abs": float(d.max()), "mean_abs": float(d.mean()), "tolerance": [GATE_MAX_ABS, GATE_MEAN_ABS],
+         "checked": list(got.shape)}
+    if not (torch.isfinite(got.float()).all() and g["max_abs"] <= GATE_MAX_ABS and g["mean_abs"] <= GATE_MEAN_ABS):
+        raise GateFailure(f"{case.name}: step output differs from the oracle (max-abs {g['max_abs']:.3e}, "
+                          f"mean-abs {g['mean_abs']:.3e}); not timed")
+    return {k: (round(v, 7) if isinstance(v, float) else v) for k, v in g.items()}
+
+
+def measure(case: Case, steps: int, warmup: int, dev, gate: bool = True) -> dict:
     base = case.make(dev)
+    gate_r = parity_gate(case, base, dev) if gate else None
     nbytes = case.bytes_per_step()
     copies = max(2, math.ceil(2 * MALL_BYTES / max(nbytes, 1)) + 1)
     inps = clone_inputs(base, copies)
@@ -485,7 +567,7 @@ def measure(case: Case, steps: int, warmup: int, dev) -> dict:
     step_bps = nbytes / (ms * 1e-3)
     kern_bps = case.kernel_bytes() / (kms * 1e-3)
     return {"ms_per_step": ms, "copies": copies, "bytes_per_step": nbytes, "kernel_ms": kms,
-            "kernel_bytes": case.kernel_bytes(), "step_Bps": step_bps, "kernel_Bps": kern_bps}
+            "kernel_bytes": case.kernel_bytes(), "step_Bps": step_bps, "kernel_Bps": kern_bps, "gate": gate_r}
 
 
 def cpu_model() -> str:
@@ -530,12 +612,12 @@ def time_cpu(case: Case, budget_s: float = 10.0) -> dict:
             "sample": f"{desc}; median of {len(times)} runs" + (f" x {ratio}" if ratio != 1 else "")}
 
 
-# C1, C2 (2-bit headline and 4-bit), the dense L>=16K
-# point, C3, C4 and C5 at its three budgets.
-DEFAULT_CONFIGS = ["c1_dense", "c2_kivi4", "dense_16k", "c3_pq", "c4_quest", "c5_topk256", "c5_topk1024",
-                   "c5_topk4096"]
-EXTRA_CONFIGS = ["dense_32k", "c2_kivi2_64k", "c2_kivi4_64k", "dense_16k_fp8", "c5_dense", "c5_topk1024_fp8s",
-                 "c5_topk1024_int4s", "c5_topk1024_int2s"]
+# C1, C2 (2-bit headline and 4-bit), the dense and
+# KIVI L>=16K points the north_star bar is judged at (dense B4 L16K and L32K,
+# KIVI-2/-4 at L64K), C3, C4 and C5 at its three budgets.
+DEFAULT_CONFIGS = ["c1_dense", "c2_kivi4", "dense_16k", "dense_32k", "c2_kivi2_64k", "c2_kivi4_64k", "c3_pq",
+                   "c4_quest", "c5_topk256", "c5_topk1024", "c5_topk4096"]
+EXTRA_CONFIGS = ["dense_16k_fp8", "c5_dense", "c5_topk1024_fp8s", "c5_topk1024_int4s", "c5_topk1024_int2s"]
 
 
 def entry(case: Case, r: dict, cpu) -> dict:
@@ -543,7 +625,7 @@ def entry(case: Case, r: dict, cpu) -> dict:
          "GBps": round(r["step_Bps"] / 1e9, 1), "hbm_frac": round(r["step_Bps"] / HBM_PEAK, 4),
          "bytes": r["bytes_per_step"], "kernel": case.kernel, "kernel_us": round(r["kernel_ms"] * 1e3, 3),
          "kernel_bytes": r["kernel_bytes"], "kernel_GBps": round(r["kernel_Bps"] / 1e9, 1),
-         "kernel_frac": round(r["kernel_Bps"] / HBM_PEAK, 4), "traffic": None}
+         "kernel_frac": round(r["kernel_Bps"] / HBM_PEAK, 4), "traffic": None, "gate": r["gate"]}
     tr = measured_traffic(case.name)
     if tr is not None:
         e["traffic"] = tr["traffic_bytes"]
@@ -564,6 +646,7 @@ def main():
     ap.add_argument("--only", action="store_true", help="time the named config alone (no per_config)")
     ap.add_argument("--all", action="store_true", help="add the extra configs to per_config")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
+    ap.add_argument("--no-gate", action="store_true", help="skip the parity gate against the CPU oracle")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -582,7 +665,11 @@ def main():
         sys.exit(2)
     head = allc[args.config]
     t0 = time.perf_counter()
-    r = measure(head, args.steps, args.warmup, dev)
+    try:
+        r = measure(head, args.steps, args.warmup, dev, gate=not args.no_gate)
+    except GateFailure as ex:
+        print(f"bench.py: parity gate failed: {ex}", file=sys.stderr)
+        sys.exit(1)
     print(f"[bench] {head.name}: {r['ms_per_step'] * 1e3:.3f} us/step, kernel {r['kernel_ms'] * 1e3:.3f} us "
           f"({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
     us = r["ms_per_step"] * 1e3
@@ -600,6 +687,7 @@ def main():
         "dtype": head.dtype,
         "data": "synthetic (seeded N(0,1), BASELINE.json configs)",
         "config": {"workload": head.workload, "name": head.name, "mall_rotation_copies": r["copies"]},
+        "gate": r["gate"],
         "roofline": {"bound": "hbm", "achieved": round(r["kernel_Bps"] / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(r["kernel_Bps"] / HBM_PEAK, 4), "traffic": None,
                      "kernel": head.kernel, "kernel_us": round(r["kernel_ms"] * 1e3, 3),
@@ -620,7 +708,11 @@ def main():
                 continue
             c = allc[name]
             t1 = time.perf_counter()
-            rr = measure(c, args.steps, args.warmup, dev)
+            try:
+                rr = measure(c, args.steps, args.warmup, dev, gate=not args.no_gate)
+            except GateFailure as ex:
+                print(f"bench.py: parity gate failed: {ex}", file=sys.stderr)
+                sys.exit(1)
             cpu = None if args.no_cpu else time_cpu(c)
             per[name] = entry(c, rr, cpu)
             print(f"[bench] {name}: {rr['ms_per_step'] * 1e3:.3f} us/step, kernel {rr['kernel_ms'] * 1e3:.3f} us "

@@ -128,6 +128,10 @@ SIGNATURES: Dict[str, Tuple] = {
     "bytes_select_mask": (c_vp, c_i64, c_int, c_i64, c_vp, c_int, c_int, c_int, c_vp),
     "bytes_select_fill": (c_vp, c_int, c_i64, c_int, c_vp, c_int, c_i64, c_int, c_i64, c_vp, c_int, c_i64, c_vp),
     "bytes_select_pages": (c_vp, c_i64, c_int, c_int, c_i64, c_vp, c_vp),
+    "bytes_select_mask_at": (c_vp, c_i64, c_int, c_i64, c_i64, c_vp, c_int, c_int, c_int, c_vp),
+    "bytes_select_merge": (c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_int, c_i64, c_vp,
+                           c_i64, c_int, c_vp, c_i64, c_int, c_vp),
+    "bytes_select_recent": (c_vp, c_int, c_i64, c_int, c_vp, c_vp),
 }
 _RESTYPES = {"bytes_error_string": ctypes.c_char_p}
 

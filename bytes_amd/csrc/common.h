@@ -121,8 +121,10 @@ __device__ __forceinline__ float wave_max_f32(float x) {
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-// Sum over all 64 lanes in a fixed order (bit-reproducible), every lane
-// receiving it; the same rotations and swaps as wave_max_f32.
+// Sum over all 64 lanes, every lane receiving the same value; the same
+// rotations and swaps as wave_max_f32.  The rotations add in a different
+// order on each lane, so the lanes' sums can differ in the last bits: the
+// result is lane 0's sum, broadcast (bit-reproducible run to run).
 __device__ __forceinline__ float wave_sum_f32(float x) {
   x += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x128, 0xF, 0xF, false));
   x += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x124, 0xF, 0xF, false));
@@ -131,7 +133,8 @@ __device__ __forceinline__ float wave_sum_f32(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  x = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
 }
 __device__ __forceinline__ float col_sum4(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -256,17 +256,20 @@ using VMetaReg = typename std::conditional<(D >= 128), u32x4, u32x2>::type;
 
 // Online softmax of one 64-token tile with a lazy running maximum.
 //
-// On entry sc[u][i] holds s - m_ref for its (token, head), where the
-// reference m_ref is the running maximum m_run (0 before the wave's first
-// tile, when m_run = -inf): the zero-term chain of the scores starts from
-// negm = -m_ref.  The reference moves only when some head's tile maximum
-// exceeds it by more than kKiviLazy (log2 units) - always on the first tile -
-// so probabilities stay below 2^kKiviLazy = 16 (their fp16 products with the
-// value scales stay finite for scales below 4096) and the rescale of the accumulators
-// (and its exp) is skipped on most tiles.  The softmax denominators are not
-// summed here: the value zero-term MFMA has rows of ones (rows >= NGV of its A
-// operand) and accumulates sum_t p[h][t] in zv row kKiviOnesRow, rescaled with
-// the accumulators.  p receives exp2(s - m_run) in sc's order.
+// On entry sc[u][i] holds s - m_run for its (token, head), where m_run is the
+// head's frame (0 before the wave's first tile, when m_run = -inf): the
+// zero-term chain of the scores starts from negm = -m_run.  The frame moves
+// only when some score of the head's tile exceeds it - always on the first
+// tile - and then to the tile maximum plus kKiviLazy (log2 units), so the
+// tiles after it whose scores climb by up to kKiviLazy skip the rescale of the
+// accumulators (and its exp).  Every probability p = exp2(s - m_run) is at
+// most 1, so its fp16 products with the value scales are at most the scale
+// itself and stay finite for every finite fp16 scale.  The softmax
+// denominators are not summed here: the value zero-term MFMA has rows of ones
+// (rows >= NGV of its A operand) and accumulates sum_t p[h][t] in zv row
+// kKiviOnesRow, rescaled with the accumulators.  The accumulators, the
+// denominator and m_run handed to the residual tiles and the split merge are
+// all in the frame.  p receives exp2(s - m_run) in sc's order.
 constexpr float kKiviLazy = 4.f;
 constexpr int kKiviOnesRow = 12;     // zv row read back as the denominator (lanes 48-63, element 0)
 template <int D>
@@ -279,9 +282,9 @@ __device__ __forceinline__ void kivi_softmax(f32x4 (&sc)[4], float& m_run, f32x4
     for (int i = 0; i < 4; ++i) mx = __builtin_elementwise_maximum(mx, sc[u][i]);
   mx = col_max4(mx);
   const bool first = m_run == kNegInf;            // the same on every lane of the wave
-  if (__ballot(first || mx > kKiviLazy) != 0) {
-    const float m_new = first ? mx : fmaxf(m_run, m_run + mx);
-    const float shift = first ? mx : m_new - m_run;
+  if (__ballot(first || mx > 0.f) != 0) {
+    const float m_new = first ? mx + kKiviLazy : (mx > 0.f ? m_run + mx + kKiviLazy : m_run);
+    const float shift = first ? m_new : m_new - m_run;
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll

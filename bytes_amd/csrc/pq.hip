@@ -28,7 +28,9 @@
 // materialised: the transposed PV reads address the codebook row of each
 // lane's token directly; dense (bf16 / fp8) V rows are staged per tile.
 // Modes 0 and 3 with G <= 8 and no outliers (contiguous or paged caches) run
-// the grouped kernel (pq_group_kernel, below) instead.
+// the grouped kernel (pq_group_kernel, below) instead; its mode 3 scores
+// q . k_hat on MFMA from the staged key codebook rows rather than from LUT
+// entries (within the attention tolerance, not bit-identical to the LUT path).
 //
 // Paged caches (block_table [B, max_blocks] int32, context_lens [B] int32):
 // token t of sequence b is row t % bs of block block_table[b][t / bs]; the
@@ -1293,9 +1295,13 @@ static PqArgs pq_args_zero() {
 // mode 0: LUT scores + PQ values (decode_attn_pq_lut_kv)
 // mode 1: LUT scores + dense bf16 values (decode_attn_pq_lut)
 // mode 2: scores from q and the key codebook + dense bf16 values (decode_attn_dequant)
-// mode 3: mode 0 with the LUT built inside the kernel from q and the key
-//         codebook, entries scale * (q . codeword) exactly as bytes_pq_build_lut
-//         writes them (the softmax then takes the scores unscaled)
+// mode 3: mode 0 with no LUT in HBM.  G <= 8 without outliers (the grouped
+//         kernel): scores scale * (q . k_hat) on MFMA straight from the key
+//         codebook rows the codes select (exact products, fp32 sums), within
+//         the attention tolerance of bytes_pq_build_lut + mode 0.  G > 8: each
+//         workgroup builds the LUT in LDS, entries scale * (q . codeword)
+//         exactly as bytes_pq_build_lut writes them (bit-identical to the two
+//         calls).  The softmax takes the scores unscaled.
 int bytes_pq_decode_attn(int mode, const void* lut, const void* q, const void* kcb, const void* kidx,
                          const void* vidx, const void* vcb, const void* v, void* out, int out_dtype, int B, int Hq,
                          int Hk, int S, int D, int K, int64_t l_sb, int64_t l_sh, int64_t q_sb, int64_t q_sh,

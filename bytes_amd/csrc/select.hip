@@ -8,7 +8,12 @@
 //    an entry that is past the row's query position, negative, or at/after S
 //    becomes S, and slots past the input width are filled with S;
 //  * select_pages_kernel: page ids -> the token ids of their rows, clamped to
-//    S - 1 (:358-363).
+//    S - 1 (:358-363);
+//  * select_merge_kernel: one step of the streaming top-k over key chunks
+//    (:286-309): the top-k positions of a row's [running list | chunk]
+//    candidates become the next running list of (score, key index) pairs;
+//  * select_recent_kernel: the "recent" selector (:261-265), idx =
+//    max(pos - j, 0).
 // Row r of a [.., Qc, n] tensor belongs to query row r % Qc, whose position is
 // pos[r % Qc] (int64 on the device, the reference's q_pos).
 #include "common.h"
@@ -17,24 +22,62 @@ namespace bytes_amd {
 
 constexpr int kSelThreads = 256;
 
-// Candidate t stands for position t * unit (unit 1: tokens; page size: pages).
+// Candidate t stands for position (key0 + t) * unit (unit 1: tokens; page
+// size: pages; key0: the first candidate's index, for a chunk of keys).
 // Causally valid iff t * unit <= pos; forced (+inf) iff local_w > 0 and
 // t lies in [max(pos - local_w + 1, 0) / unit, pos / unit].
 __global__ __launch_bounds__(kSelThreads) void select_mask_kernel(float* s, int64_t rows, int n, int64_t rs,
-                                                                  const int64_t* pos, int Qc, int unit,
-                                                                  int local_w, int64_t blocks_per_row) {
+                                                                  int64_t key0, const int64_t* pos, int Qc,
+                                                                  int unit, int local_w, int64_t blocks_per_row) {
   const int64_t r = blockIdx.x / blocks_per_row;
-  const int64_t t = (blockIdx.x - r * blocks_per_row) * kSelThreads + threadIdx.x;
-  if (r >= rows || t >= n) return;
+  const int64_t j = (blockIdx.x - r * blocks_per_row) * kSelThreads + threadIdx.x;
+  if (r >= rows || j >= n) return;
+  const int64_t t = key0 + j;
   const int64_t p = pos[r % Qc];
   float* row = s + r * rs;
-  float v = row[t];
+  float v = row[j];
   if (t * unit > p) v = kNegInf;
   if (local_w > 0) {
     const int64_t lo = (p - local_w + 1 > 0 ? p - local_w + 1 : 0) / unit, hi = p / unit;
     if (t >= lo && t <= hi) v = __builtin_inff();
   }
-  row[t] = v;
+  row[j] = v;
+}
+
+// Row r's candidates are cand[r][off .. off + nrun + n): its running list of
+// nrun (score, key index) pairs (indices in ridx[r]) followed by the scores
+// of keys kc0, kc0 + 1, ...  sel[r] holds the top-ksel candidate positions;
+// entry i < ksel of the next running list is the candidate at sel[r][i],
+// entries ksel <= i < kout are fillers (-inf, S).
+__global__ __launch_bounds__(kSelThreads) void select_merge_kernel(const float* cand, int64_t cand_rs, int off,
+                                                                   int nrun, const int32_t* ridx, int64_t ridx_rs,
+                                                                   const int32_t* sel, int64_t sel_rs, int ksel,
+                                                                   int kc0, int S, int64_t rows, float* out_v,
+                                                                   int64_t out_v_rs, int out_off, int32_t* out_i,
+                                                                   int64_t out_i_rs, int kout,
+                                                                   int64_t blocks_per_row) {
+  const int64_t r = blockIdx.x / blocks_per_row;
+  const int i = (int)((blockIdx.x - r * blocks_per_row) * kSelThreads + threadIdx.x);
+  if (r >= rows || i >= kout) return;
+  float v = kNegInf;
+  int idx = S;
+  if (i < ksel) {
+    const int p = sel[r * sel_rs + i];
+    v = cand[r * cand_rs + off + p];
+    idx = p < nrun ? ridx[r * ridx_rs + p] : kc0 + (p - nrun);
+  }
+  if (out_v) out_v[r * out_v_rs + out_off + i] = v;
+  out_i[r * out_i_rs + i] = idx;
+}
+
+// "recent": the kb most recent causal positions of row r, pos - j clamped at 0.
+__global__ __launch_bounds__(kSelThreads) void select_recent_kernel(const int64_t* pos, int Qc, int64_t rows, int kb,
+                                                                    int64_t* out, int64_t blocks_per_row) {
+  const int64_t r = blockIdx.x / blocks_per_row;
+  const int j = (int)((blockIdx.x - r * blocks_per_row) * kSelThreads + threadIdx.x);
+  if (r >= rows || j >= kb) return;
+  const int64_t v = pos[r % Qc] - j;
+  out[r * kb + j] = v > 0 ? v : 0;
 }
 
 template <typename TI, typename TO>
@@ -76,15 +119,47 @@ using namespace bytes_amd;
 
 extern "C" {
 
-int bytes_select_mask(void* scores, int64_t rows, int n, int64_t row_stride, const void* pos, int Qc, int unit,
-                      int local_w, void* stream) {
-  if (!scores || !pos || rows <= 0 || n <= 0 || Qc <= 0 || unit <= 0 || local_w < 0 || row_stride < n)
+int bytes_select_mask_at(void* scores, int64_t rows, int n, int64_t row_stride, int64_t key0, const void* pos,
+                         int Qc, int unit, int local_w, void* stream) {
+  if (!scores || !pos || rows <= 0 || n <= 0 || Qc <= 0 || unit <= 0 || local_w < 0 || row_stride < n || key0 < 0)
     return (int)hipErrorInvalidValue;
   int64_t bpr, blocks;
   if (!grid_of(rows, n, &bpr, &blocks)) return (int)hipErrorInvalidConfiguration;
   hipLaunchKernelGGL(select_mask_kernel, dim3((unsigned)blocks), dim3(kSelThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<float*>(scores), rows, n, row_stride,
+                     static_cast<hipStream_t>(stream), static_cast<float*>(scores), rows, n, row_stride, key0,
                      static_cast<const int64_t*>(pos), Qc, unit, local_w, bpr);
+  return (int)hipGetLastError();
+}
+
+int bytes_select_mask(void* scores, int64_t rows, int n, int64_t row_stride, const void* pos, int Qc, int unit,
+                      int local_w, void* stream) {
+  return bytes_select_mask_at(scores, rows, n, row_stride, 0, pos, Qc, unit, local_w, stream);
+}
+
+int bytes_select_merge(const void* cand, int64_t cand_rs, int off, int nrun, const void* ridx, int64_t ridx_rs,
+                       const void* sel, int64_t sel_rs, int ksel, int kc0, int S, int64_t rows, void* out_vals,
+                       int64_t out_vals_rs, int out_off, void* out_idx, int64_t out_idx_rs, int kout,
+                       void* stream) {
+  if (!cand || !sel || !out_idx || rows <= 0 || ksel <= 0 || kout < ksel || nrun < 0 || off < 0 || kc0 < 0 ||
+      S <= 0 || out_off < 0 || (nrun > 0 && !ridx))
+    return (int)hipErrorInvalidValue;
+  int64_t bpr, blocks;
+  if (!grid_of(rows, kout, &bpr, &blocks)) return (int)hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(select_merge_kernel, dim3((unsigned)blocks), dim3(kSelThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const float*>(cand), cand_rs, off, nrun,
+                     static_cast<const int32_t*>(ridx), ridx_rs, static_cast<const int32_t*>(sel), sel_rs, ksel,
+                     kc0, S, rows, static_cast<float*>(out_vals), out_vals_rs, out_off,
+                     static_cast<int32_t*>(out_idx), out_idx_rs, kout, bpr);
+  return (int)hipGetLastError();
+}
+
+int bytes_select_recent(const void* pos, int Qc, int64_t rows, int kb, void* out, void* stream) {
+  if (!pos || !out || Qc <= 0 || rows <= 0 || kb <= 0) return (int)hipErrorInvalidValue;
+  int64_t bpr, blocks;
+  if (!grid_of(rows, kb, &bpr, &blocks)) return (int)hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(select_recent_kernel, dim3((unsigned)blocks), dim3(kSelThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const int64_t*>(pos), Qc, rows, kb,
+                     static_cast<int64_t*>(out), bpr);
   return (int)hipGetLastError();
 }
 

@@ -21,8 +21,11 @@
 //     the workgroup instead runs an exact radix select over the whole row
 //     (11/11/10-bit digits), collects in index order and sorts the k results.
 // Step 3 also clears the histogram and list counters, which are zero between
-// calls.  Short rows, and unsorted selections larger than the lists hold
-// (k > 8192), run step 3's exact path alone.
+// calls.  Short rows, and selections larger than the lists hold (k > 8192),
+// run step 3's exact path alone; for k > 8192 it lists the selection by
+// ascending index, and a sorted output then takes two more launches: blocks
+// of 8192 selected entries sorted in LDS, then each entry's final slot from
+// its rank in its own block plus binary searches in the others.
 #include "wave_select.h"
 
 namespace bytes_amd {
@@ -156,6 +159,7 @@ struct TopkWs {
   uint32_t* cnt;     // [kRowBatch][kCntStride]: above-list length, candidate count
   uint64_t* above;   // [kRowBatch][k]
   uint64_t* cand;    // [kRowBatch][kCandCap]
+  uint64_t* sorted;  // k > kTopkMaxK: [rows][kpad] sort values of the selection, sorted per 8192-entry block
 };
 
 // A row's two list counters have a 128-byte line of their own: the filter
@@ -165,21 +169,26 @@ constexpr int kCntStride = 32;
 constexpr size_t kTopkZeroBytes = (size_t)kRowBatch * kBins * 4 + (size_t)kRowBatch * kCntStride * 4;
 
 // Lists for the rows of one launch group (min(rows, kRowBatch)) follow the
-// fixed zero region.  k above kTopkMaxK (unsorted output only) runs the
-// one-workgroup-per-row exact path, which needs the zeroed region alone.
+// fixed zero region.  k above kTopkMaxK runs the one-workgroup-per-row exact
+// path, which needs the zeroed region, plus (sorted output) rows * kpad
+// 8-byte sort values, kpad = k rounded up to whole 8192-entry sort blocks.
+constexpr int kSortBlock = 8192;
+__host__ __device__ inline size_t topk_large_pad(int k) { return ((size_t)k + kSortBlock - 1) / kSortBlock * kSortBlock; }
+
 inline size_t topk_ws_bytes(int64_t rows, int k) {
-  if (k > kTopkMaxK) return kTopkZeroBytes;
+  if (k > kTopkMaxK) return kTopkZeroBytes + (size_t)(rows > 0 ? rows : 1) * topk_large_pad(k) * 8;
   const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
   return kTopkZeroBytes + r * k * 8 + r * kCandCap * 8;
 }
 
 inline TopkWs topk_ws_carve(void* ws, int64_t rows, int k) {
-  if (k > kTopkMaxK) k = 0;                      // exact path: no lists
-  const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
   char* p = static_cast<char*>(ws);
   TopkWs t;
   t.hist = reinterpret_cast<uint32_t*>(p);
   t.cnt = reinterpret_cast<uint32_t*>(p + (size_t)kRowBatch * kBins * 4);
+  t.sorted = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes);
+  if (k > kTopkMaxK) k = 0;                      // exact path: no lists
+  const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
   t.above = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes);
   t.cand = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes + r * k * 8);
   return t;
@@ -729,6 +738,81 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
   for (int i = tid; i < k; i += NT) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sb[i]);
 }
 
+// ---- sorted output for k > kTopkMaxK ----
+// Block j of a row's selection (entries j*8192 .. +8192 of `out`, listed by
+// ascending index): sort values (order key, index) sorted descending in LDS
+// and written to the row's part of `sorted`.
+__global__ __launch_bounds__(kTopkThreads) void topk_sort_block_kernel(const float* scores, int64_t row_stride,
+                                                                      int k, const int32_t* out,
+                                                                      int64_t out_stride, uint64_t* sorted,
+                                                                      int nblk) {
+  extern __shared__ uint64_t sortbuf[];          // [kSortBlock]
+  const int64_t row = blockIdx.x / nblk;
+  const int blk = (int)(blockIdx.x - row * nblk);
+  const int j0 = blk * kSortBlock, cnt = min(kSortBlock, k - j0);
+  const float* x = scores + row * row_stride;
+  const int32_t* o = out + row * out_stride + j0;
+  for (int i = threadIdx.x; i < kSortBlock; i += kTopkThreads) {
+    uint64_t v = 0ull;                           // padding sorts last (every real value is > 0)
+    if (i < cnt) {
+      const int idx = o[i];
+      v = sort_val(order_key(x[idx]), idx);
+    }
+    sortbuf[i] = v;
+  }
+  __syncthreads();
+  bitonic_desc<kTopkThreads>(sortbuf, kSortBlock);
+  uint64_t* dst = sorted + row * (int64_t)topk_large_pad(k) + j0;
+  for (int i = threadIdx.x; i < cnt; i += kTopkThreads) dst[i] = sortbuf[i];
+}
+
+// Final slot of each selected entry: its rank in its own sorted block plus,
+// for every other block, the number of that block's values above it (binary
+// search; values are distinct, since the index is part of each).
+constexpr int kRankThreads = 256;
+__global__ __launch_bounds__(kRankThreads) void topk_rank_merge_kernel(const uint64_t* sorted, int k, int32_t* out,
+                                                                      int64_t out_stride, int64_t per_row) {
+  const int64_t row = blockIdx.x / per_row;
+  const int j = (int)((blockIdx.x - row * per_row) * kRankThreads + threadIdx.x);
+  if (j >= k) return;
+  const uint64_t* srow = sorted + row * (int64_t)topk_large_pad(k);
+  const uint64_t v = srow[j];
+  const int own = j / kSortBlock;
+  int rank = j - own * kSortBlock;
+  const int nblk = (k + kSortBlock - 1) / kSortBlock;
+  for (int b = 0; b < nblk; ++b) {
+    if (b == own) continue;
+    const uint64_t* blk = srow + b * kSortBlock;
+    int lo = 0, hi = min(kSortBlock, k - b * kSortBlock);
+    while (lo < hi) {                            // count of values > v (blocks are descending)
+      const int mid = (lo + hi) >> 1;
+      if (blk[mid] > v) lo = mid + 1;
+      else hi = mid;
+    }
+    rank += lo;
+  }
+  out[row * out_stride + rank] = (int32_t)(0xFFFFFFFFu - (uint32_t)v);
+}
+
+static int topk_sort_large(const float* scores, int64_t rows, int64_t row_stride, int k, int32_t* out,
+                           int64_t out_stride, const TopkWs& ws, hipStream_t st) {
+  static bool lds_set = false;   // 64 KB of dynamic LDS: at the default limit, set once to be explicit
+  if (!lds_set) {
+    int rc = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_sort_block_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kSortBlock * 8);
+    if (rc) return rc;
+    lds_set = true;
+  }
+  const int nblk = (k + kSortBlock - 1) / kSortBlock;
+  const int64_t per_row = (k + kRankThreads - 1) / kRankThreads;
+  if (rows * nblk > 0x7FFFFFFFL || rows * per_row > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(topk_sort_block_kernel, dim3((unsigned)(rows * nblk)), dim3(kTopkThreads), kSortBlock * 8, st,
+                     scores, row_stride, k, out, out_stride, ws.sorted, nblk);
+  hipLaunchKernelGGL(topk_rank_merge_kernel, dim3((unsigned)(rows * per_row)), dim3(kRankThreads), 0, st, ws.sorted,
+                     k, out, out_stride, per_row);
+  return (int)hipGetLastError();
+}
+
 template <bool VEC>
 static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_stride, int k, int32_t* out,
                        int64_t out_stride, int sorted, int hist_ready, const TopkWs& ws, hipStream_t st) {
@@ -814,7 +898,6 @@ int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes) {
 int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int k, int sorted, int hist_ready,
                void* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
   if (!scores || !out || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
-  if (k > kTopkMaxK && sorted) return (int)hipErrorNotSupported;
   if (rows == 0) return 0;
   const long parts = (n + kSlice - 1) / kSlice;
   if (kRowBatch * parts > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
@@ -825,10 +908,13 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float* s = static_cast<const float*>(scores);
   int32_t* o = static_cast<int32_t*>(out);
-  const int so = sorted ? 1 : 0, hr = hist_ready ? 1 : 0;
+  // k > kTopkMaxK sorted: the selection by ascending index, then sorted
+  const bool large_sorted = sorted && k > kTopkMaxK;
+  const int so = (sorted && !large_sorted) ? 1 : 0, hr = hist_ready ? 1 : 0;
   prof_begin(kProfTopk, st);
-  const int rc = vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st)
-                     : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st);
+  int rc = vec ? topk_launch<true>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st)
+               : topk_launch<false>(s, rows, n, row_stride, k, o, out_stride, so, hr, ws, st);
+  if (rc == 0 && large_sorted) rc = topk_sort_large(s, rows, row_stride, k, o, out_stride, ws, st);
   prof_end(kProfTopk, st);
   return rc;
 }

@@ -13,7 +13,6 @@ import torch
 from . import _checks as C
 from ._lib import HIP_ERROR_NOT_SUPPORTED, call, lib, ptr, size_query, stream_of, workspace
 
-TOPK_MAX = 8192               # largest k of the score-ordered (sorted=True) output
 TOPK_HIST_ROWS = 1024         # rows whose digit histogram fits the top-k workspace's fixed region
 
 
@@ -38,9 +37,11 @@ def _qk_shapes(q: torch.Tensor, k: torch.Tensor, k_dim: int = None):
     return B, Hq, Hk, S, D
 
 
-def _score(q, k_score, scaling, group_sum: bool, hist=None, packed=None) -> torch.Tensor:
+def _score(q, k_score, scaling, group_sum: bool, hist=None, packed=None, out=None) -> torch.Tensor:
     """Launch the score kernel. packed = (scale, zero, bits) marks k_score as
-    uint8 4/2-bit codes along head_dim with bf16 per-32-dim scale/min."""
+    uint8 4/2-bit codes along head_dim with bf16 per-32-dim scale/min.  out:
+    an fp32 [B, H, S] destination (unit stride along S, any other strides),
+    else a new tensor."""
     if packed is None:
         B, Hq, Hk, S, D = _qk_shapes(q, k_score)
         if k_score.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
@@ -73,7 +74,10 @@ def _score(q, k_score, scaling, group_sum: bool, hist=None, packed=None) -> torc
     qs = C.rows16(q.squeeze(2))
     k = C.rows16(k_score)
     H = Hk if group_sum else Hq
-    out = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    if out is None:
+        out = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (B, H, S) or out.stride(-1) != 1:
+        raise ValueError(f"out: expected fp32 {(B, H, S)} with unit stride along S")
     call("bytes_sparse_score", ptr(qs), ptr(k), mode, ptr(sc) if sc is not None else None,
          ptr(zr) if zr is not None else None, ptr(out), B, Hq, Hk, S, D, int(group_sum),
          qs.stride(0), qs.stride(1), k.stride(0), k.stride(1), k.stride(2), *m_strides,
@@ -155,8 +159,9 @@ def topk_indices(scores: torch.Tensor, k: int, *, sorted: bool = True) -> torch.
     order: score descending, lowest index first among equal scores (+0 == -0;
     NaN ranks above +inf).  sorted=True orders the result by that order, like
     `scores.topk(k).indices` (src/attention_kernels.py:1262) with a
-    deterministic tie rule; sorted=False returns the same set by ascending
-    index (cheaper: no sort).  Returns int32 [..., k]."""
+    deterministic tie rule, for any k (above 8192 the selection is sorted in
+    blocks of 8192 and merged by rank); sorted=False returns the same set by
+    ascending index (cheaper: no sort).  Returns int32 [..., k]."""
     return _topk(scores, k, sorted=sorted)
 
 
@@ -170,9 +175,6 @@ def _topk(scores: torch.Tensor, k: int, *, sorted: bool, ws=None, hist_ready: bo
     n = scores.shape[-1]
     if not 1 <= k <= n:
         raise ValueError(f"k={k} outside [1, {n}]")
-    if k > TOPK_MAX and sorted:
-        raise ValueError(f"sorted output supports k <= {TOPK_MAX} (k={k}); sorted=False returns the same set "
-                         "by ascending index for any k")
     s = scores.reshape(-1, n)
     if s.stride(-1) != 1:
         s = s.contiguous()

@@ -196,8 +196,8 @@ int bytes_score_keys_pack(const void* x, int x_dtype, int64_t rows, int D, int64
  *   scores [rows, n] fp32 (row stride row_stride, unit stride along n)
  *   out    [rows, k] int32 (row stride out_stride): ordered by that order when
  *          sorted != 0, else the same set by ascending index.
- * 1 <= k <= n; sorted output needs k <= 8192 (else hipErrorNotSupported),
- * unsorted output takes any k.
+ * 1 <= k <= n, sorted or not.  k > 8192 takes a larger workspace (the
+ * selection's sort values, rows * k * 8 bytes rounded up to 8192 entries).
  * hist_ready = 1: the workspace's histogram region already holds the rows'
  *   digit histograms (bytes_sparse_score with hist); rows <= 1024.
  * ------------------------------------------------------------------------- */
@@ -282,9 +282,29 @@ int bytes_quest_gather_attn(const void* q, const void* k, const void* v, int kv_
  *   of :376).  in_dtype / out_dtype: 0 int32, 1 int64.
  * bytes_select_pages: out[r, j] = min(page_ids[r, j / page] * page + j % page,
  *   S - 1) int64 [rows, npick*page] from int32 page ids [rows, npick] (:358-363).
+ * bytes_select_mask_at: bytes_select_mask over a chunk of candidates whose
+ *   first one is candidate key0 (candidate j stands for position
+ *   (key0 + j) * unit): the per-tile mask of the streaming loop (:294-300).
+ * bytes_select_merge: one merge of the streaming top-k (:301-309).  Row r's
+ *   candidates are cand[r][off .. off + nrun + n) fp32 (row stride cand_rs):
+ *   its running list of nrun entries, whose key indices are ridx[r][0 .. nrun)
+ *   int32, then the scores of keys kc0, kc0 + 1, ...; sel[r][0 .. ksel) int32
+ *   are the positions the top-k picked there.  Writes the next running list:
+ *   out_vals[r][out_off + i] (if out_vals is not NULL) and out_idx[r][i] =
+ *   (score, key index) of candidate sel[r][i] for i < ksel, (-inf, S) for
+ *   ksel <= i < kout.
+ * bytes_select_recent: the "recent" selector (:261-265): out[r, j] =
+ *   max(pos[r % Qc] - j, 0) int64 [rows, kb].
  * ------------------------------------------------------------------------- */
 int bytes_select_mask(void* scores, int64_t rows, int n, int64_t row_stride, const void* pos, int Qc, int unit,
                       int local_w, void* stream);
+int bytes_select_mask_at(void* scores, int64_t rows, int n, int64_t row_stride, int64_t key0, const void* pos,
+                         int Qc, int unit, int local_w, void* stream);
+int bytes_select_merge(const void* cand, int64_t cand_rs, int off, int nrun, const void* ridx, int64_t ridx_rs,
+                       const void* sel, int64_t sel_rs, int ksel, int kc0, int S, int64_t rows, void* out_vals,
+                       int64_t out_vals_rs, int out_off, void* out_idx, int64_t out_idx_rs, int kout,
+                       void* stream);
+int bytes_select_recent(const void* pos, int Qc, int64_t rows, int kb, void* out, void* stream);
 int bytes_select_fill(const void* in, int in_dtype, int64_t in_rs, int k_in, void* out, int out_dtype,
                       int64_t out_rs, int k_out, int64_t rows, const void* pos, int Qc, int64_t S, void* stream);
 int bytes_select_pages(const void* page_ids, int64_t rows, int npick, int page, int64_t S, void* out,

@@ -773,6 +773,19 @@ def select_topk_from_scores(scores: torch.Tensor, q_pos: torch.Tensor, S: int, k
     return torch.where(run_i > S, torch.full_like(run_i, S), run_i)
 
 
+def select_recent(B: int, Hq: int, q_pos: torch.Tensor, kb: int) -> torch.Tensor:
+    """select_topk(selector="recent") of benchmarks/sparse_attention.py:261-265:
+    the kb most recent causal positions of each query row, pos, pos-1, ...,
+    clamped at 0 (so a row at position p < kb - 1 repeats key 0), for every
+    (b, h).  Returns int64 [B,Hq,Qc,kb].
+    Pinned by: the set of the first min(kb, p+1) entries equals the last
+    min(kb, p+1) positions of range(p+1), in descending order, and every
+    later entry is 0 (tests/test_oracle.py)."""
+    pos = q_pos.reshape(-1).long()
+    idx = (pos[:, None] - torch.arange(kb)[None, :]).clamp(min=0)
+    return idx[None, None].expand(B, Hq, pos.numel(), kb).contiguous()
+
+
 def select_topk_exact(q_blk, sel_keys, q_pos, S: int, kb: int, k_chunk: int, scaling: float,
                       local_w: int = 0) -> torch.Tensor:
     """select_topk(selector="exact"/"approx") of benchmarks/sparse_attention.py:226-325:

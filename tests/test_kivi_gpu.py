@@ -188,17 +188,19 @@ def test_decode_many_splits_use_the_merge_kernel(dev):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize("Sq,chunk,amp", [(16256, 512, 1800.0), (16288, 4096, 900.0)])
-def test_decode_rising_scores_large_values(dev, bits, Sq, chunk, amp):
+@pytest.mark.parametrize("Sq,chunk,amp,vamp", [(16256, 512, 1800.0, 1000.0), (16288, 4096, 900.0, 1000.0),
+                                               (16256, 512, 1800.0, 12000.0), (16288, 4096, 900.0, 12000.0)])
+def test_decode_rising_scores_large_values(dev, bits, Sq, chunk, amp, vamp):
     """Scores that climb by many octaves along the cache up to its middle (a
-    bump along head 0's query in every key) and values of magnitude ~1000
-    (value scales up to a few thousand), on splits long enough that each wave
-    runs several tiles: the two-half kernel (Sq = 16256, 512-token splits: a
-    wave's two tiles 256 tokens, ~7.7 octaves, apart) and the streaming kernel
-    (Sq = 16288, 4096-token splits: eight phases per wave, 512 tokens and
-    ~7.7 octaves apart).  The running maximum moves on many tiles, and
-    probabilities times value scales must stay finite in fp16.  Error bound
-    relative to the output's magnitude."""
+    bump along head 0's query in every key) and values of magnitude ~vamp
+    (2-bit value scales up to a few thousand at 1000, about 8K to 20K at
+    12000), on splits long enough that each wave runs several tiles: the
+    two-half kernel (Sq = 16256, 512-token splits: a wave's two tiles 256
+    tokens, ~7.7 octaves, apart) and the streaming kernel (Sq = 16288,
+    4096-token splits: eight phases per wave, 512 tokens and ~7.7 octaves
+    apart).  The running maximum moves on many tiles, and probabilities
+    times value scales must stay finite in fp16 for any finite fp16 scale.
+    Error bound relative to the output's magnitude."""
     B, Hq, Hk, D, Rw = 1, 7, 1, 128, 64
     raw = W.kivi_raw(B, Hq, Hk, D, Sq + Rw, Rw, seed=Sq + bits)
     q = raw["q"].float()
@@ -207,8 +209,12 @@ def test_decode_rising_scores_large_values(dev, bits, Sq, chunk, amp):
     qdir = q[0, 0, 0] / q[0, 0, 0].pow(2).sum()
     k = raw["k"].float() + (bump[:, None] * amp) * qdir
     raw["k"] = k.to(torch.bfloat16)
-    raw["v"] = (raw["v"].float() * 1000.0).to(torch.bfloat16)
+    raw["v"] = (raw["v"].float() * vamp).to(torch.bfloat16)
     cpu = W.kivi_pack_inputs(raw, R.kivi_quantize_and_pack_last_dim, bits)
+    vs_max = cpu["V_scale"].float().max().item()
+    print(f"kivi{bits} value scales up to {vs_max:.0f}", flush=True)
+    if vamp > 1000.0 and bits == 2:
+        assert vs_max > 8000.0
     gpu = _to(cpu, dev)
     names = ("Q", "Kq", "K_scale", "K_mn", "K_residual", "Vq", "V_scale", "V_mn", "V_residual")
     out = K.kivi_decode_attn(*[gpu[n] for n in names], bits, 32, chunk=chunk)
@@ -216,5 +222,5 @@ def test_decode_rising_scores_large_values(dev, bits, Sq, chunk, amp):
     assert torch.isfinite(out.float()).all()
     d = (out.float().cpu() - ref.float()).abs()
     mag = ref.float().abs().max()
-    print(f"kivi{bits} Sq{Sq} chunk{chunk} rising: max-abs {d.max():.3e} of |ref| max {mag:.3e}", flush=True)
+    print(f"kivi{bits} Sq{Sq} chunk{chunk} vamp{vamp:.0f} rising: max-abs {d.max():.3e} of |ref| max {mag:.3e}", flush=True)
     assert d.max() <= 2e-2 * mag and d.mean() <= 2e-3 * mag

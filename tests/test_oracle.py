@@ -534,6 +534,19 @@ def test_select_topk_exact_integer_keys():
     assert torch.equal(R.select_topk_exact(q, kr, pos, S, 9, 7, 0.5), got)
 
 
+def test_select_recent_is_the_most_recent_causal_window():
+    pos = torch.tensor([0, 3, 9, 40])
+    for kb in (1, 4, 10, 16):
+        got = R.select_recent(2, 3, pos, kb)
+        assert got.shape == (2, 3, 4, kb) and got.dtype == torch.int64
+        for r, p in enumerate(pos.tolist()):
+            m = min(kb, p + 1)
+            row = got[1, 2, r].tolist()
+            assert row[:m] == sorted(range(p + 1))[::-1][:m]          # the newest m positions, newest first
+            assert set(row[:m]) == set(range(p + 1 - m, p + 1))
+            assert all(x == 0 for x in row[m:])                        # clamp at 0 past the first key
+
+
 @pytest.mark.parametrize("local_w", [0, 20])
 def test_quest_select_rows_bruteforce(local_w):
     g = torch.Generator().manual_seed(13)

@@ -67,74 +67,125 @@ def test_select_topk_exact_integer_scores_end_to_end(dev):
         assert torch.equal(got.cpu(), want), (kb, lw)
 
 
-def test_select_topk_large_budget_unsorted(dev):
-    """k above 8192 comes back by ascending index; the set equals the oracle's."""
+def test_select_topk_large_budget(dev):
+    """kb above 8192 over several key chunks: the running list is longer than a
+    chunk, the last merge sorts more than 8192 entries; score order as the
+    oracle's."""
     B, Hq, Hk, Qc, S, D = 1, 2, 1, 2, 20000, 64
     q, k, _ = _inputs(B, Hq, Hk, Qc, S, D, seed=9)
     pos = torch.tensor([12000, 19999])
     got = SA.select_topk("exact", q.to(dev), k.to(dev), pos, S, 10000, 4096, 0.125)
     s = SP.sparse_score_scalar(q.reshape(B, Hq * Qc, 1, D).to(dev), k.to(dev), 0.125).cpu()
     want = R.select_topk_from_scores(s.reshape(B, Hq, Qc, S), pos, S, 10000, 4096)
-    assert torch.equal(got.cpu(), torch.sort(want, dim=-1).values)
+    assert torch.equal(got.cpu(), want)
 
 
-@pytest.mark.parametrize("B,Hq,Hk,Qc,S,D,kb,page,local_w,expanded", [
-    (1, 4, 2, 3, 1000, 128, 128, 16, 0, False),
-    (1, 28, 4, 4, 4100, 128, 512, 16, 64, True),    # G = 7, expanded keys, ragged last page
-    (2, 40, 2, 2, 700, 64, 100, 16, 0, False),      # G = 20: Qc * G = 40 heads per KV head
-    (1, 8, 8, 3, 333, 64, 64, 8, 20, False),
+def _soft_keys(selector, k, g):
+    """The selection keys the reference's make_selection_keys builds for a
+    selector (benchmarks/sparse_attention.py:127-150, without the RoPE, which
+    is the caller's): per-token asymmetric fake-quantization over head_dim
+    with 16 / 4 levels (int4 / int2), an fp8 e4m3fn round trip (fp8, also
+    passed as the fp8 tensor itself), a perturbed copy (approx)."""
+    if selector in ("int4", "int2"):
+        codes, scale, xmin = R.asym_quant_codes(k.float(), 16 if selector == "int4" else 4, -1)
+        return (codes.float() * scale + xmin).to(k.dtype)
+    if selector == "fp8":
+        return k.to(torch.float8_e4m3fn).to(k.dtype)
+    if selector == "fp8_native":
+        return k.to(torch.float8_e4m3fn)
+    return (k.float() + 0.05 * torch.randn(k.shape, generator=g)).to(k.dtype)
+
+
+@pytest.mark.parametrize("selector", ["approx", "int4", "int2", "fp8", "fp8_native"])
+@pytest.mark.parametrize("Qc,S,kb,k_chunk,local_w", [
+    (4, 600, 48, 100, 0),        # six chunks, the last partial
+    (5, 700, 200, 64, 8),        # running list longer than a chunk; early rows with sentinels; recent window
+    (3, 1000, 1, 333, 0),        # kb = 1
 ])
-def test_quest_select_rows_match_oracle(dev, B, Hq, Hk, Qc, S, D, kb, page, local_w, expanded):
-    q, k, _ = _inputs(B, Hq, Hk, Qc, S, D, seed=S + 7)
-    pos = torch.linspace(S // 3, S - 1, Qc).long()
-    keys = R.repeat_kv(k, Hq // Hk) if expanded else k
-    got = SA._quest_select(q.to(dev), keys.to(dev), pos, S, kb, page, 0.09, local_w)
-    want = R.quest_select_rows(q, keys, pos, S, kb, page, 0.09, local_w)
-    assert got.dtype == torch.int64 and torch.equal(got.cpu(), want)
-    # the selector surface routes "quest" here
-    via = SA.select_topk("quest", q.to(dev), keys.to(dev), pos, S, kb, 4096, 0.09, page=page, local_w=local_w)
-    assert torch.equal(via.cpu(), want)
+def test_select_topk_soft_selectors_stream(dev, selector, Qc, S, kb, k_chunk, local_w):
+    """Every SOFT_SELECTOR the reference routes through the same streaming
+    top-k (:35, :287-309) over the keys the caller passes: bit-exact against
+    the oracle's streaming selection on the GPU's own fp32 scores, with a
+    partial last chunk, sentinels and the recent window."""
+    B, Hq, Hk, D = 1, 14, 2, 128
+    q, k, _ = _inputs(B, Hq, Hk, Qc, S, D, seed=S + kb)
+    g = torch.Generator().manual_seed(kb)
+    sk = _soft_keys(selector, k, g)
+    pos = torch.linspace(S // 8, S - 1, Qc).long()
+    name = "fp8" if selector == "fp8_native" else selector
+    got = SA.select_topk(name, q.to(dev), sk.to(dev), pos, S, kb, k_chunk, 0.088, local_w=local_w)
+    assert got.dtype == torch.int64 and got.shape == (B, Hq, Qc, kb)
+    max_key = int(pos.max()) + 1
+    bits = 8 if sk.dtype == torch.float8_e4m3fn else 16
+    s = SP.sparse_score_scalar(q.reshape(B, Hq * Qc, 1, D).to(dev), sk[:, :, :max_key].to(dev), 0.088,
+                               score_bits=bits).cpu()
+    want = R.select_topk_from_scores(s.reshape(B, Hq, Qc, max_key), pos, S, kb, k_chunk, local_w)
+    assert torch.equal(got.cpu(), want)
 
 
-@pytest.mark.parametrize("B,Hq,Hk,Qc,S,D,ksel", [
-    (1, 4, 2, 3, 500, 64, 40),
-    (2, 28, 4, 2, 2048, 128, 256),
-    (1, 8, 8, 4, 129, 128, 64),
-])
-def test_attend_topk_matches_oracle(dev, B, Hq, Hk, Qc, S, D, ksel):
-    q, k, v = _inputs(B, Hq, Hk, Qc, S, D, seed=ksel)
-    pos = torch.linspace(S // 4, S - 1, Qc).long()
-    g = torch.Generator().manual_seed(3)
-    idx = torch.randint(-3, S + 5, (B, Hq, Qc, ksel), generator=g)       # negatives, sentinels, future rows
-    idx[..., 0] = 0
-    idx[..., 1] = idx[..., 2]                                            # duplicates count twice
-    out = SA.attend_topk(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), pos, 0.125)
-    assert out.shape == (B, Hq, Qc, D) and out.dtype == torch.bfloat16
-    _check(out, R.attend_topk(q, k, v, idx, pos, 0.125), f"attend_topk B{B} Hq{Hq} Hk{Hk} Qc{Qc} S{S}")
+def test_select_topk_recent(dev):
+    B, Hq, Hk, Qc, S, D = 2, 6, 2, 4, 500, 64
+    q, k, _ = _inputs(B, Hq, Hk, Qc, S, D, seed=21)
+    pos = torch.tensor([0, 5, 130, 499])
+    for kb in (1, 16, 200):
+        got = SA.select_topk("recent", q.to(dev), k.to(dev), pos, S, kb, 128, 0.1)
+        assert got.dtype == torch.int64
+        assert torch.equal(got.cpu(), R.select_recent(B, Hq, pos, kb)), kb
 
 
-def test_chunked_select_then_attend(dev):
-    """One query chunk of the chunked driver (benchmarks/sparse_attention.py:480-495):
-    exact selection with a recent window, then attention over the selection;
-    also Quest.  Compared with the oracle's select + attend on the same scores."""
-    B, Hq, Hk, Qc, S, D = 1, 28, 4, 8, 3000, 128
-    q, k, v = _inputs(B, Hq, Hk, Qc, S, D, seed=77)
-    pos = torch.arange(S - Qc, S)
-    kr, vr = R.repeat_kv(k, 7), R.repeat_kv(v, 7)
-    qd, krd, vrd = q.to(dev), kr.to(dev), vr.to(dev)
-    idx = SA.select_topk("exact", qd, krd, pos, S, 300, 1024, 0.088, local_w=32)
-    out = SA.attend_topk(qd, krd, vrd, idx, pos, 0.088)
-    _check(out, R.attend_topk(q, kr, vr, idx.cpu(), pos, 0.088), "chunk exact")
-    s = SP.sparse_score_scalar(qd.reshape(B, Hq * Qc, 1, D), krd, 0.088).cpu()
-    want = R.select_topk_from_scores(s.reshape(B, Hq, Qc, S), pos, S, 300, 1024, 32)
-    assert torch.equal(idx.cpu(), want)
-    qi = SA.select_topk("quest", qd, krd, pos, S, 512, 1024, 0.088, page=16, local_w=32)
-    assert torch.equal(qi.cpu(), R.quest_select_rows(q, kr, pos, S, 512, 16, 0.088, 32))
-    _check(SA.attend_topk(qd, krd, vrd, qi, pos, 0.088), R.attend_topk(q, kr, vr, qi.cpu(), pos, 0.088),
-           "chunk quest")
+def test_select_topk_memory_is_bounded_by_the_chunk(dev):
+    """benchmarks/test_sparse_eval.py:60-83 at its shape (Hq 8, Hk 1, D 64,
+    q_chunk 256, k_chunk 2048, frac 0.1): every query chunk of a prefill
+    window selected and attended; peak memory grows by less than 3x when S
+    doubles.  Then the selection alone at a fixed budget: its scratch does
+    not grow with the context (O(Qc * (k_chunk + kb)), :477), where a
+    one-shot selection would hold Hq * Qc * S fp32 scores."""
+    Hq, Hk, D, qc, kc = 8, 1, 64, 256, 2048
+    peaks = {}
+    for S in (4096, 8192, 16384):
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        g = torch.Generator().manual_seed(S)
+        q = torch.randn(1, Hq, S, D, generator=g).to(torch.bfloat16).to(dev)
+        k = torch.randn(1, Hk, S, D, generator=g).to(torch.bfloat16).to(dev)
+        v = torch.randn(1, Hk, S, D, generator=g).to(torch.bfloat16).to(dev)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        kb = max(1, round(0.1 * S))
+        for q0 in range(0, S, qc):
+            blk = q[:, :, q0:q0 + qc]
+            p = torch.arange(q0, q0 + blk.shape[2])
+            idx = SA.select_topk("exact", blk, k, p, S, kb, kc, D ** -0.5)
+            SA.attend_topk(blk, k, v, idx, p, D ** -0.5)
+        torch.cuda.synchronize()
+        peaks[S] = torch.cuda.max_memory_allocated()
+        del q, k, v
+    print(f"peak MB {({S: round(p / 1e6, 1) for S, p in peaks.items()})}", flush=True)
+    assert peaks[8192] / peaks[4096] < 3.0 and peaks[16384] / peaks[8192] < 3.0
+
+    extra = {}
+    kb = 512
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(1, Hq, qc, D, generator=g).to(torch.bfloat16).to(dev)
+    for S in (8192, 32768, 131072):
+        k = torch.randn(1, Hk, S, D, generator=g).to(torch.bfloat16).to(dev)
+        p = torch.arange(S - qc, S)
+        SA.select_topk("exact", q, k, p, S, kb, kc, D ** -0.5)        # workspaces at their size
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        idx = SA.select_topk("exact", q, k, p, S, kb, kc, D ** -0.5)
+        torch.cuda.synchronize()
+        extra[S] = torch.cuda.max_memory_allocated() - base
+        del k, idx
+    one_shot = Hq * qc * 131072 * 4
+    print(f"selection scratch MB {({S: round(e / 1e6, 1) for S, e in extra.items()})}; one-shot scores at "
+          f"S=131072: {one_shot / 1e6:.0f} MB", flush=True)
+    assert extra[131072] <= 1.1 * extra[8192] and extra[131072] < one_shot / 4
 
 
 def test_selectors_outside_the_hot_path_raise(dev):
     q, k, _ = _inputs(1, 2, 1, 1, 64, 64, seed=1)
-    with pytest.raises(ValueError):
-        SA.select_topk("h2o", q.to(dev), k.to(dev), torch.tensor([63]), 64, 8, 64, 0.1)
+    for sel in ("h2o", "snapkv", "signvq", "sparq", "random"):
+        with pytest.raises(ValueError):
+            SA.select_topk(sel, q.to(dev), k.to(dev), torch.tensor([63]), 64, 8, 64, 0.1)

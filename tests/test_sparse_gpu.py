@@ -84,14 +84,17 @@ def test_topk_bit_exact_with_ties(dev, rows, n, k, sorted_out):
     assert torch.equal(got.long(), ref)
 
 
-@pytest.mark.parametrize("rows,n,k", [(3, 40000, 10000), (2, 65536, 16384), (2, 9000, 9000), (130, 20000, 12000)])
-def test_topk_large_k_unsorted(dev, rows, n, k):
-    """k above the sorted-output limit: the same set, by ascending index."""
+@pytest.mark.parametrize("rows,n,k", [(3, 40000, 10000), (2, 65536, 16384), (2, 9000, 9000), (130, 20000, 12000),
+                                      (2, 131072, 32768), (3, 20000, 8193)])
+def test_topk_large_k(dev, rows, n, k):
+    """k above 8192: the same set by ascending index (sorted=False), and in the
+    total order (sorted=True: blocks of 8192 sorted in LDS, merged by rank),
+    both bit-exact against the oracle on tie-heavy rows."""
     s = _tie_heavy(rows, n, seed=n + k)
     got = SP.topk_indices(s.to(dev), k, sorted=False).cpu()
     assert torch.equal(got.long(), R.topk_indices(s, k, sorted_by_score=False))
-    with pytest.raises(ValueError):
-        SP.topk_indices(s.to(dev), k, sorted=True)
+    got_s = SP.topk_indices(s.to(dev), k, sorted=True).cpu()
+    assert torch.equal(got_s.long(), R.topk_indices(s, k, sorted_by_score=True))
 
 
 @pytest.mark.parametrize("sorted_out", [True, False])
