@@ -22,10 +22,10 @@
 // Quest selection in the prologue (bytes_quest_gather_attn): instead of a
 // page list, each workgroup receives its query head's row of page bounds and
 // selects the top npick pages itself (exact: bound descending, lowest
-// page first among equal bounds, the order of bytes_topk; a radix select by
-// the whole workgroup), listing them in ascending page order as the unfused
-// top-k does; the page top-k launch of benchmarks/sparse_attention.py:356-358
-// then disappears from the step.
+// page first among equal bounds, the order of bytes_topk; the workgroup radix
+// select of wave_select.h over bounds held in registers), listing them in
+// ascending page order as the unfused top-k does; the page top-k launch of
+// benchmarks/sparse_attention.py:356-358 then disappears from the step.
 #include "dense_tile.h"
 #include "wave_select.h"
 
@@ -60,8 +60,8 @@ constexpr int kGatherSelMax = 4096;     // pages per bound row selected in the p
 template <int D>
 struct GatherCfg {
   static constexpr int kRows = kGatherChunkMax * 4;
-  static constexpr int kSel = kBins * 4 + kGatherSelMax * 4 + block_select_words<kGatherWaves * 64>() * 4;
-  // histogram, bound row / page list, scan words
+  static constexpr int kSelWs = block_select_words<kGatherWaves * 64>();
+  static constexpr int kSel = kSelWs * 4 + kGatherSelMax * 4;   // selection words, page list
   static_assert(kSel <= DenseCfg<D>::kSmem, "the selection fits in the tile buffers");
   static constexpr int kSmem = DenseCfg<D>::kSmem + kRows;
 };
@@ -134,42 +134,35 @@ __global__ __launch_bounds__(kGatherWaves * 64, 2) void gather_decode_kernel(Gat
   bf16x8 qb[C::KK];
   load_q_bf16<D>(a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh, a.q_sh, nh, lane, qb);
 
-  // Quest selection: the head's bound row is staged in LDS (coalesced), then
-  // the workgroup selects the top kb / page pages (thread t ranking bounds
-  // SEL*t .. +SEL) and lists them, ascending, over the staged row
-  int32_t* pids = reinterpret_cast<int32_t*>(smem_raw + kBins * 4);
+  // Quest selection: thread t loads bounds SEL*t .. +SEL of the head's row
+  // straight into registers, the workgroup selects the top kb / page pages
+  // (block_select) and lists them, ascending, in LDS
+  int32_t* pids = reinterpret_cast<int32_t*>(smem_raw + GatherCfg<D>::kSelWs * 4);
   if constexpr (SEL > 0) {
     constexpr int NT = kGatherWaves * 64;
-    float* brow = reinterpret_cast<float*>(pids);
-    uint32_t* red = reinterpret_cast<uint32_t*>(smem_raw + kBins * 4 + kGatherSelMax * 4);
     const float* bsrc = a.bound + (int64_t)b * a.b_sb + (int64_t)hq0 * a.b_sh;
-    // all of a thread's loads in flight together (indices clamped to the row):
-    // 16-byte chunks where the row allows, else single floats
+    uint32_t key[SEL];
+    // all of a thread's loads in flight together (indices clamped to the
+    // row; elements past np are not selected): 16-byte chunks where the row
+    // allows, else single floats
     if (a.b_vec) {
       u32x4 bv[SEL / 4];
 #pragma unroll
-      for (int u = 0; u < SEL / 4; ++u) bv[u] = ld16(bsrc + 4 * min((int)threadIdx.x + NT * u, a.np / 4 - 1));
+      for (int u = 0; u < SEL / 4; ++u) bv[u] = ld16(bsrc + 4 * min((SEL / 4) * (int)threadIdx.x + u, a.np / 4 - 1));
 #pragma unroll
-      for (int u = 0; u < SEL / 4; ++u) *reinterpret_cast<u32x4*>(brow + 4 * (threadIdx.x + NT * u)) = bv[u];
+      for (int u = 0; u < SEL / 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) key[4 * u + e] = score_order_key(__uint_as_float(bv[u][e]));
     } else {
       float bv[SEL];
 #pragma unroll
-      for (int u = 0; u < SEL; ++u) bv[u] = bsrc[min((int)threadIdx.x + NT * u, a.np - 1)];
+      for (int u = 0; u < SEL; ++u) bv[u] = bsrc[min(SEL * (int)threadIdx.x + u, a.np - 1)];
 #pragma unroll
-      for (int u = 0; u < SEL; ++u) brow[threadIdx.x + NT * u] = bv[u];
+      for (int u = 0; u < SEL; ++u) key[u] = score_order_key(bv[u]);
     }
-    __syncthreads();
-    uint32_t key[SEL];
-#pragma unroll
-    for (int q4 = 0; q4 < SEL / 4; ++q4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(brow + SEL * threadIdx.x + 4 * q4);   // past np: unused
-#pragma unroll
-      for (int e = 0; e < 4; ++e) key[4 * q4 + e] = score_order_key(v[e]);
-    }
-    uint32_t T, need;
-    block_select_threshold<NT, SEL>(key, a.np, a.kb / a.page, reinterpret_cast<uint32_t*>(smem_raw), red, T, need);
-    // every thread's reads of the staged row precede the first list write
-    block_select_compact<NT, SEL>(key, a.np, T, need, red, [&](uint32_t pos, int idx, uint32_t) { pids[pos] = idx; });
+    uint32_t* ws = reinterpret_cast<uint32_t*>(smem_raw);
+    const BlockSel sel = block_select<NT, SEL>(key, a.np, a.kb / a.page, ws);
+    block_select_emit<NT, SEL>(key, a.np, sel, ws, [&](uint32_t pos, int idx, uint32_t) { pids[pos] = idx; });
     __syncthreads();
   }
 

@@ -679,14 +679,11 @@ __global__ __launch_bounds__(64 * kWaveRowsPerWG) void topk_wave_kernel(const fl
 
 // Rows of at most kSmallRow elements that the wave kernel does not take (few
 // rows, or larger k): one 256-thread workgroup per row, the row's order keys
-// in registers (thread t holds elements PER*t .. +PER, read from memory once).
-// The digit passes start at the highest bit in which the row's keys differ
-// (the bits above are common to every key), so rows of scores in a narrow
-// range take fewer passes and spread over the first histogram.  Each pass
-// histograms the keys that match the prefix so far, picks the digit from
-// wave suffix sums and the four wave totals (one barrier), and one scan of
-// packed (equal, greater) counts places the selection in index order, or into
-// an LDS list sorted by (score desc, index asc).
+// in registers (thread t holds elements PER*t .. +PER, read from memory once),
+// selected by block_select (8-bit digit passes from the highest bit in which
+// the row's keys differ, one barrier per pass); one scan of the per-thread
+// counts places the selection in index order, or into an LDS list sorted by
+// (score desc, index asc).
 constexpr int kSmallThreads = 256;
 constexpr int kSmallRow = 4096;
 constexpr int kSmallSortK = 1024;
@@ -695,13 +692,12 @@ template <bool VEC, int PER>
 __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* scores, int64_t row_stride, int n,
                                                                    int k, int32_t* out, int64_t out_stride,
                                                                    int sorted, uint32_t* ghist) {
-  constexpr int NT = kSmallThreads, NW = NT / 64;
-  constexpr int BPT = kBins / NT;                // histogram bins per thread
+  constexpr int NT = kSmallThreads;
+  constexpr int BPT = kBins / NT;                // caller histogram words cleared per thread
   static_assert(PER % 4 == 0 && NT * PER <= kSmallRow && BPT % 4 == 0, "keys and bins per thread");
-  __shared__ __attribute__((aligned(16))) uint32_t hist[kBins];
+  __shared__ __attribute__((aligned(16))) uint32_t ws[block_select_words<NT>()];
   __shared__ uint64_t sb[kSmallSortK];
-  __shared__ uint32_t red[block_select_words<NT>()];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* x = scores + row * row_stride;
   const auto rs = row_rsrc(x, n);
@@ -717,15 +713,14 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[4 * j + e] = kq[e];
   }
-  uint32_t T, need;
-  block_select_threshold<NT, PER>(key, n, k, hist, red, T, need);
+  const BlockSel sel = block_select<NT, PER>(key, n, k, ws);
   if (ghist) {                                   // a histogram the caller built: leave it at zero
     u32x4* gh = reinterpret_cast<u32x4*>(ghist + row * kBins) + tid * (BPT / 4);
 #pragma unroll
     for (int q = 0; q < BPT / 4; ++q) gh[q] = u32x4{0u, 0u, 0u, 0u};
   }
   // placement in index order
-  block_select_compact<NT, PER>(key, n, T, need, red, [&](uint32_t pos, int idx, uint32_t kk) {
+  block_select_emit<NT, PER>(key, n, sel, ws, [&](uint32_t pos, int idx, uint32_t kk) {
     if (sorted) sb[pos] = sort_val(kk, idx);
     else o[pos] = idx;
   });
