@@ -64,11 +64,14 @@ constexpr int kQuestSlots = kQuestThreads / kQuestPages;   // head slots per rou
 // t % 32, head slot t / 32).  The pages' min/max rows are widened to fp32 in
 // LDS (rows padded by 16 bytes, so the 16 pages a 16-lane group reads at one d
 // sit in distinct banks) and q is split into q+ = q (q >= 0 or NaN, else 0)
-// and q- = q (q < 0, else 0).  Each term is then fma(q-_d, kmin_d, q+_d *
-// kmax_d): one of the two products is an exact zero, so the term is the
-// rounded product max(q_d*kmin_d, q_d*kmax_d) picks (kmax >= kmin), NaN
-// propagating as that max does when the min/max rows carry it at the same d
-// (as every page with a NaN key does).  Terms are summed in ascending d.
+// and q- = q (q < 0, else 0).  On a page whose min/max rows are finite each
+// term is fma(q-_d, kmin_d, q+_d * kmax_d): one of the two products is an
+// exact zero, so the term is the rounded product max(q_d*kmin_d,
+// q_d*kmax_d) picks (kmax >= kmin).  A page with an infinite or NaN min/max
+// entry (a key with one) takes the literal form max(q*kmin, q*kmax), NaN if
+// either product is (torch.maximum): there 0 * inf on the side q does not
+// pick would otherwise turn the term into NaN.  Terms are summed in
+// ascending d.
 template <int D>
 __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                                                     const uint16_t* kmin, const uint16_t* kmax,
@@ -80,6 +83,7 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
   __shared__ __attribute__((aligned(16))) float mx_s[kQuestPages * PITCH];
   __shared__ __attribute__((aligned(16))) float qp_s[16 * D];
   __shared__ __attribute__((aligned(16))) float qm_s[16 * D];
+  __shared__ uint32_t bad_s[kQuestPages];          // per page: a non-finite min/max entry
   const int parts = (np + kQuestPages - 1) / kQuestPages;
   const int bhb = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
   const int bh = bhb / HB, hb = bhb - (bhb / HB) * HB;
@@ -149,6 +153,16 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
     *reinterpret_cast<f32x4*>(mn_s + pp * PITCH + c * 8 + 4) = a1;
     *reinterpret_cast<f32x4*>(mx_s + pp * PITCH + c * 8) = z0;
     *reinterpret_cast<f32x4*>(mx_s + pp * PITCH + c * 8 + 4) = z1;
+    // a bf16 exponent field of all ones: infinity or NaN.  Per half word,
+    // (h & 0x7F80) + 0x80 reaches bit 15 only then (no carry crosses halves);
+    // a page's CH chunks sit on CH consecutive lanes
+    uint32_t ex = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      ex |= ((av[u][j] & 0x7F807F80u) + 0x00800080u) | ((zv[u][j] & 0x7F807F80u) + 0x00800080u);
+    const unsigned long long m = __ballot((ex & 0x80008000u) != 0u);
+    const int lane = threadIdx.x & 63;
+    if (c == 0) bad_s[pp] = ((m >> (lane & (64 - CH))) & ((1ull << CH) - 1ull)) ? 1u : 0u;
   }
   __syncthreads();
   const int pp = threadIdx.x % kQuestPages;
@@ -163,11 +177,12 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
   }
   const float* mnr = mn_s + pp * PITCH;
   const float* mxr = mx_s + pp * PITCH;
+  const uint32_t nonfinite = bad_s[pp];
   for (int g = threadIdx.x / kQuestPages; g < GB; g += kQuestSlots) {
     const float* qpr = qp_s + g * D;
     const float* qmr = qm_s + g * D;
     float acc = 0.f;
-    {
+    if (!nonfinite) {
 #pragma clang fp contract(off)
 #pragma unroll 4
       for (int d4 = 0; d4 < D / 4; ++d4) {
@@ -181,6 +196,14 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(const uint16
           const float t = __builtin_fmaf(qm[e], lo[e], hp);
           acc = (d4 == 0 && e == 0) ? t : acc + t;
         }
+      }
+    } else {
+#pragma clang fp contract(off)
+      for (int d = 0; d < D; ++d) {
+        const float qd = qpr[d] + qmr[d];          // one of the two is an exact zero
+        const float a = qd * mnr[d], z = qd * mxr[d];
+        const float t = (a != a || z != z) ? __builtin_nanf("") : (a > z ? a : z);
+        acc = d == 0 ? t : acc + t;
       }
     }
     float v = acc * scale;

@@ -38,6 +38,28 @@ def test_page_scores_bit_exact(dev, B, Hq, Hk, S, D, scale):
     assert torch.equal(got.cpu(), ref)
 
 
+def test_page_scores_nonfinite_keys_bit_exact(dev):
+    """Keys with +-inf / NaN entries: the bound follows torch.maximum(q*kmin,
+    q*kmax) (benchmarks/sparse_attention.py:344), e.g. q_d < 0 with kmax_d = +inf
+    gives the finite q_d*kmin_d, and q_d = 0 next to an infinity gives NaN."""
+    x = W.dense(1, 8, 2, 128, 1024, seed=11)
+    k = x["k"].clone()
+    k[0, 0, 5, 3] = float("inf")          # page 0
+    k[0, 0, 40, 7] = float("-inf")        # page 2
+    k[0, 1, 100, 9] = float("nan")        # page 6 of head 1
+    k[0, 1, 300, 0] = float("inf")
+    k[0, 1, 301, 0] = float("-inf")       # page 18: both infinities at one d
+    q = x["q"].clone()
+    q[0, 0, 0, 3] = 0.0                   # q_d = 0 against the infinity of page 0
+    q[0, 1, 0, 7] = -0.0
+    rmin, rmax = R.quest_page_minmax(k, 16)
+    got = Q.quest_page_scores(q.to(dev), rmin.to(dev), rmax.to(dev), 0.5).cpu()
+    ref = R.quest_page_scores(q, rmin, rmax, 0.5)
+    same = (got == ref) | (got.isnan() & ref.isnan())
+    assert bool(same.all()), (got[~same], ref[~same])
+    assert bool(ref.isnan().any()) and bool(torch.isfinite(ref[0, 2:4, 0]).all())
+
+
 def test_page_scores_causal_and_recent_window(dev):
     x = W.dense(1, 8, 2, 128, 1000, seed=2)
     rmin, rmax = R.quest_page_minmax(x["k"], 16)
