@@ -158,7 +158,10 @@ struct TopkWs {
   uint32_t* hist;    // [kRowBatch][kBins]
   uint32_t* cnt;     // [kRowBatch][kCntStride]: above-list length, candidate count
   uint64_t* above;   // [kRowBatch][k]
-  uint64_t* cand;    // [kRowBatch][kCandCap]
+  uint64_t* cand;    // [kRowBatch][kCandCap]; k > kTopkMaxK: [kRowBatch][kLargeCand]
+  uint32_t* sabove;  // k > kTopkMaxK: [kRowBatch][parts] keys above the threshold digit per slice
+  uint32_t* soff;    // k > kTopkMaxK: [kRowBatch][parts] output offset of each slice
+  uint32_t* par;     // k > kTopkMaxK: [kRowBatch][kLargePar] the row's selection predicate
   uint64_t* sorted;  // k > kTopkMaxK: [rows][kpad] sort values of the selection, sorted per 8192-entry block
 };
 
@@ -168,29 +171,55 @@ struct TopkWs {
 constexpr int kCntStride = 32;
 constexpr size_t kTopkZeroBytes = (size_t)kRowBatch * kBins * 4 + (size_t)kRowBatch * kCntStride * 4;
 
+// k above kTopkMaxK on long rows: the keys of the threshold digit (up to
+// kLargeCand per row) are listed and selected among by one workgroup per row,
+// which leaves the row's selection predicate and each slice's output offset;
+// every slice then writes its selected indices in index order.
+constexpr int kLargeCand = 16384;   // 16 per thread of the select workgroup (more spills registers)
+constexpr int kLargeMaxParts = 2048;   // slices per row (rows up to 16 Mi elements)
+constexpr int kLargePar = 8;
+
 // Lists for the rows of one launch group (min(rows, kRowBatch)) follow the
-// fixed zero region.  k above kTopkMaxK runs the one-workgroup-per-row exact
-// path, which needs the zeroed region, plus (sorted output) rows * kpad
-// 8-byte sort values, kpad = k rounded up to whole 8192-entry sort blocks.
+// fixed zero region.  k above kTopkMaxK: the candidate lists, slice counts
+// and predicates of the launch group, then (sorted output) rows * kpad 8-byte
+// sort values, kpad = k rounded up to whole 8192-entry sort blocks.
 constexpr int kSortBlock = 8192;
 __host__ __device__ inline size_t topk_large_pad(int k) { return ((size_t)k + kSortBlock - 1) / kSortBlock * kSortBlock; }
 
-inline size_t topk_ws_bytes(int64_t rows, int k) {
-  if (k > kTopkMaxK) return kTopkZeroBytes + (size_t)(rows > 0 ? rows : 1) * topk_large_pad(k) * 8;
+inline int topk_parts(int n) { return (n + kSlice - 1) / kSlice; }
+
+inline size_t topk_large_list_bytes(size_t r, int n) {
+  return r * ((size_t)kLargeCand * 8 + (size_t)topk_parts(n) * 8 + kLargePar * 4);
+}
+
+inline size_t topk_ws_bytes(int64_t rows, int n, int k) {
   const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
+  if (k > kTopkMaxK)
+    return kTopkZeroBytes + topk_large_list_bytes(r, n) + (size_t)(rows > 0 ? rows : 1) * topk_large_pad(k) * 8;
   return kTopkZeroBytes + r * k * 8 + r * kCandCap * 8;
 }
 
-inline TopkWs topk_ws_carve(void* ws, int64_t rows, int k) {
+inline TopkWs topk_ws_carve(void* ws, int64_t rows, int n, int k) {
   char* p = static_cast<char*>(ws);
   TopkWs t;
   t.hist = reinterpret_cast<uint32_t*>(p);
   t.cnt = reinterpret_cast<uint32_t*>(p + (size_t)kRowBatch * kBins * 4);
-  t.sorted = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes);
-  if (k > kTopkMaxK) k = 0;                      // exact path: no lists
   const size_t r = (size_t)(rows < kRowBatch ? (rows > 0 ? rows : 1) : kRowBatch);
-  t.above = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes);
-  t.cand = reinterpret_cast<uint64_t*>(p + kTopkZeroBytes + r * k * 8);
+  char* l = p + kTopkZeroBytes;
+  if (k > kTopkMaxK) {
+    const int parts = topk_parts(n);
+    t.above = nullptr;
+    t.cand = reinterpret_cast<uint64_t*>(l);
+    t.sabove = reinterpret_cast<uint32_t*>(l + r * kLargeCand * 8);
+    t.soff = t.sabove + r * parts;
+    t.par = t.soff + r * parts;
+    t.sorted = reinterpret_cast<uint64_t*>(l + topk_large_list_bytes(r, n));
+  } else {
+    t.above = reinterpret_cast<uint64_t*>(l);
+    t.cand = reinterpret_cast<uint64_t*>(l + r * k * 8);
+    t.sabove = t.soff = t.par = nullptr;
+    t.sorted = nullptr;
+  }
   return t;
 }
 
@@ -733,6 +762,224 @@ __global__ __launch_bounds__(kSmallThreads) void topk_small_kernel(const float* 
   for (int i = tid; i < k; i += NT) o[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)sb[i]);
 }
 
+// ---- k > kTopkMaxK on long rows: the selection in index order ----
+// 1. filter (many workgroups per row): the digit d0 holding the k-th largest
+//    key (from the row's histogram); each slice records how many of its keys
+//    lie in larger digits and appends the keys of digit d0 to the row's
+//    candidate list (any order);
+// 2. select (one workgroup per row): among the candidates, block_select finds
+//    the (k - above)-th largest; ties at the threshold are ranked by index in a
+//    second block_select over the tied keys' complemented indices.  The result
+//    is a predicate on (key, index) that holds for exactly k elements, plus
+//    every slice's output offset (its above count and selected candidates,
+//    summed over the slices before it).  Rows whose candidates overflow the
+//    list run the one-workgroup exact path instead and are marked done;
+// 3. write (many workgroups per row): each slice writes the indices that
+//    satisfy the predicate, in index order, from its offset.
+template <bool VEC>
+__global__ __launch_bounds__(kPassThreads) void topk_large_filter_kernel(const float* scores, int64_t row_stride,
+                                                                         int n, int k, int parts, TopkWs ws) {
+  __shared__ uint32_t wsum[kPassThreads / 64];
+  __shared__ uint32_t sel[4];
+  const int row = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const float* x = scores + (int64_t)row * row_stride;
+  const auto rs = row_rsrc(x, n);
+  constexpr int R = kSlice / (kPassThreads * 4);
+  uint32_t key[R][4];
+  bool ok[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = part * kSlice + (r * kPassThreads + threadIdx.x) * 4;
+    load4<VEC>(rs, i, n, key[r], ok[r]);
+  }
+  find_digit<kPassThreads>(ws.hist + (int64_t)row * kBins, (uint32_t)k, wsum, sel);
+  const uint32_t d0 = sel[0];
+  uint32_t na = 0, nc = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!ok[r][j]) continue;
+      const uint32_t d = key[r][j] >> 21;
+      na += d > d0 ? 1u : 0u;
+      nc += d == d0 ? 1u : 0u;
+    }
+  static_assert(kSlice < 65536, "packed counts");
+  uint32_t tp;
+  const uint32_t packed = (nc << 16) | na;
+  const uint32_t op = block_incl_scan<kPassThreads>(packed, wsum, tp) - packed;
+  uint32_t oc = op >> 16;
+  const uint32_t tc = tp >> 16;
+  if (threadIdx.x == 0) {
+    ws.sabove[row * parts + part] = tp & 0xFFFFu;
+    sel[3] = tc ? atomicAdd(ws.cnt + row * kCntStride + 1, tc) : 0u;
+  }
+  __syncthreads();
+  oc += sel[3];
+  uint64_t* cl = ws.cand + (int64_t)row * kLargeCand;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!ok[r][j] || (key[r][j] >> 21) != d0) continue;
+      if (oc < (uint32_t)kLargeCand) cl[oc] = sort_val(key[r][j], part * kSlice + (r * kPassThreads + threadIdx.x) * 4 + j);
+      ++oc;
+    }
+}
+
+// One row's selection among its Cn <= NT*PER candidates (see above); thread t
+// holds candidates PER*t .. +PER.
+template <int PER>
+__device__ void topk_large_choose(const uint64_t* cl, uint32_t Cn, uint32_t kc, int parts, const uint32_t* sabove,
+                                  uint32_t* soff, uint32_t* pr, uint32_t* lws, uint32_t* sc, uint32_t* wsum) {
+  constexpr int NT = kTopkThreads;
+  const int tid = threadIdx.x;
+  uint32_t key[PER], idx[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j += 2) {
+    const int e = PER * tid + j;                 // even: one 16-byte load holds entries e, e+1
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (e < (int)Cn) v = ld16(cl + e);
+    if (e + 1 >= (int)Cn) v[2] = v[3] = 0u;
+    key[j] = v[1];
+    idx[j] = 0xFFFFFFFFu - v[0];
+    key[j + 1] = v[3];
+    idx[j + 1] = 0xFFFFFFFFu - v[2];
+  }
+  const BlockSel bs = block_select<NT, PER>(key, (int)Cn, (int)kc, lws);
+  uint32_t P2 = 0u, M2 = 0u;
+  if (!bs.all) {
+    // keys equal to the threshold (bs.M is full here): the bs.need lowest
+    // indices are the largest complemented indices
+    uint32_t k2[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) k2[j] = (PER * tid + j < (int)Cn && key[j] == bs.P) ? ~idx[j] : 0u;
+    __syncthreads();                             // every thread is done with lws
+    const BlockSel b2 = block_select<NT, PER>(k2, (int)Cn, (int)bs.need, lws);
+    P2 = b2.P;
+    M2 = b2.M;
+  }
+  for (int i = tid; i < parts; i += NT) sc[i] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (PER * tid + j >= (int)Cn) continue;
+    const uint32_t m = key[j] & bs.M;
+    const bool take = m > bs.P || (m == bs.P && (bs.all || ((~idx[j] & M2) >= P2)));
+    if (take) atomicAdd(&sc[idx[j] / kSlice], 1u);
+  }
+  __syncthreads();
+  // slice offsets: thread t owns slices 2t, 2t+1 (parts <= 2 * NT)
+  static_assert(kLargeMaxParts <= 2 * NT, "slices per thread");
+  const int s0 = 2 * tid, s1 = 2 * tid + 1;
+  const uint32_t v0 = s0 < parts ? sabove[s0] + sc[s0] : 0u;
+  const uint32_t v1 = s1 < parts ? sabove[s1] + sc[s1] : 0u;
+  uint32_t total;
+  const uint32_t excl = block_incl_scan<NT>(v0 + v1, wsum, total) - v0 - v1;
+  if (s0 < parts) soff[s0] = excl;
+  if (s1 < parts) soff[s1] = excl + v0;
+  if (tid == 0) {
+    pr[0] = bs.P;
+    pr[1] = bs.M;
+    pr[2] = P2;
+    pr[3] = M2;
+    pr[4] = bs.all;
+    pr[5] = 1u;
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kTopkThreads) void topk_large_select_kernel(const float* scores, int64_t row_stride,
+                                                                         int n, int k, int parts, TopkWs ws,
+                                                                         int32_t* out, int64_t out_stride) {
+  constexpr int NT = kTopkThreads;
+  __shared__ __attribute__((aligned(16))) uint32_t lws[block_select_words<NT>()];
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t wsum[NT / 64];
+  __shared__ uint32_t sel[8];
+  __shared__ uint32_t sc[kLargeMaxParts];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  uint32_t* pr = ws.par + row * kLargePar;
+  find_digit<NT>(ws.hist + (int64_t)row * kBins, (uint32_t)k, wsum, sel);
+  const uint32_t kc = (uint32_t)k - sel[1];      // to take among the candidates (keys above the digit: sel[1])
+  const uint32_t Cn = ws.cnt[row * kCntStride + 1];
+  const uint64_t* cl = ws.cand + (int64_t)row * kLargeCand;
+  const uint32_t* sa = ws.sabove + row * parts;
+  uint32_t* so = ws.soff + row * parts;
+  // as few candidates per thread as the list needs: every slot costs a
+  // histogram add in each digit pass
+  if (Cn <= (uint32_t)(NT * 4)) topk_large_choose<4>(cl, Cn, kc, parts, sa, so, pr, lws, sc, wsum);
+  else if (Cn <= (uint32_t)(NT * 8)) topk_large_choose<8>(cl, Cn, kc, parts, sa, so, pr, lws, sc, wsum);
+  else if (Cn <= (uint32_t)kLargeCand) topk_large_choose<kLargeCand / NT>(cl, Cn, kc, parts, sa, so, pr, lws, sc, wsum);
+  else {
+    // the threshold digit holds more keys than the list: exact path over the row
+    __syncthreads();
+    topk_row_exact<VEC>(scores + (int64_t)row * row_stride, n, k, 0, nullptr, hist, wsum, sel,
+                        out + (int64_t)row * out_stride);
+    if (tid == 0) pr[5] = 0u;                    // written: the write pass skips the row
+  }
+  // leave the row's histogram and list counters at zero for the next call
+  uint32_t* hr = ws.hist + (int64_t)row * kBins;
+  for (int b = tid; b < kBins; b += NT) hr[b] = 0u;
+  if (tid == 0) ws.cnt[row * kCntStride + 1] = 0u;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kPassThreads) void topk_large_write_kernel(const float* scores, int64_t row_stride,
+                                                                        int n, int k, int parts, TopkWs ws,
+                                                                        int32_t* out, int64_t out_stride) {
+  __shared__ uint32_t wsum[kPassThreads / 64];
+  const int row = blockIdx.x / parts, part = blockIdx.x - (blockIdx.x / parts) * parts;
+  const uint32_t* pr = ws.par + row * kLargePar;
+  if (pr[5] == 0u) return;                       // the select kernel wrote this row itself
+  const float* x = scores + (int64_t)row * row_stride;
+  const auto rs = row_rsrc(x, n);
+  constexpr int R = kSlice / (kPassThreads * 4);
+  static_assert(R == 4, "two packed scans of four 16-bit counts");
+  uint32_t key[R][4];
+  bool ok[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = part * kSlice + (r * kPassThreads + threadIdx.x) * 4;
+    load4<VEC>(rs, i, n, key[r], ok[r]);
+  }
+  const uint32_t P = pr[0], M = pr[1], P2 = pr[2], M2 = pr[3], all = pr[4];
+  bool take[R][4];
+  uint32_t c[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    c[r] = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t idx = (uint32_t)(part * kSlice + (r * kPassThreads + threadIdx.x) * 4 + j);
+      const uint32_t m = key[r][j] & M;
+      take[r][j] = ok[r][j] && (m > P || (m == P && (all || ((~idx & M2) >= P2))));
+      c[r] += take[r][j] ? 1u : 0u;
+    }
+  }
+  // element order is (r, thread, j): scans of the per-r counts, two packed per
+  // scan (each total <= 2048 < 2^16)
+  uint32_t t01, t23;
+  const uint32_t p01 = c[0] | (c[1] << 16), p23 = c[2] | (c[3] << 16);
+  const uint32_t e01 = block_incl_scan<kPassThreads>(p01, wsum, t01) - p01;
+  const uint32_t e23 = block_incl_scan<kPassThreads>(p23, wsum, t23) - p23;
+  const uint32_t tot[R] = {t01 & 0xFFFFu, t01 >> 16, t23 & 0xFFFFu, t23 >> 16};
+  const uint32_t ex[R] = {e01 & 0xFFFFu, e01 >> 16, e23 & 0xFFFFu, e23 >> 16};
+  int32_t* o = out + (int64_t)row * out_stride;
+  uint32_t base = ws.soff[row * parts + part];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t pos = base + ex[r];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (take[r][j]) {
+        if (pos < (uint32_t)k) o[pos] = part * kSlice + (r * kPassThreads + threadIdx.x) * 4 + j;
+        ++pos;
+      }
+    base += tot[r];
+  }
+}
+
 // ---- sorted output for k > kTopkMaxK ----
 // Block j of a row's selection (entries j*8192 .. +8192 of `out`, listed by
 // ascending index): sort values (order key, index) sorted descending in LDS
@@ -851,6 +1098,27 @@ static int topk_launch(const float* scores, int64_t rows, int n, int64_t row_str
                          out_stride, sorted, gh);
     return (int)hipGetLastError();
   }
+  // k beyond the list capacity on long rows: filter, per-row select, ordered write
+  if (k > kTopkMaxK && n > kShortRow && parts <= kLargeMaxParts) {
+    for (int64_t r0 = 0; r0 < rows; r0 += kRowBatch) {
+      const int nr = (int)(rows - r0 < kRowBatch ? rows - r0 : kRowBatch);
+      const float* s = scores + r0 * row_stride;
+      int32_t* o = out + r0 * out_stride;
+      const unsigned grid = (unsigned)(nr * parts);
+      if (!hist_ready)
+        hipLaunchKernelGGL(topk_hist_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, parts,
+                           ws.hist);
+      hipLaunchKernelGGL(topk_large_filter_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, k,
+                         parts, ws);
+      hipLaunchKernelGGL(topk_large_select_kernel<VEC>, dim3((unsigned)nr), dim3(kTopkThreads), 0, st, s, row_stride,
+                         n, k, parts, ws, o, out_stride);
+      hipLaunchKernelGGL(topk_large_write_kernel<VEC>, dim3(grid), dim3(kPassThreads), 0, st, s, row_stride, n, k,
+                         parts, ws, o, out_stride);
+      const int rc = (int)hipGetLastError();
+      if (rc) return rc;
+    }
+    return 0;
+  }
   // short rows, and k beyond the list capacity (unsorted output: the exact
   // path writes the selection straight to `out` in index order)
   const int exact = (n <= kShortRow || k > kTopkMaxK) ? 1 : 0;
@@ -886,7 +1154,7 @@ extern "C" {
 
 int bytes_topk_workspace_size(int64_t rows, int n, int k, size_t* bytes) {
   if (!bytes || rows < 0 || n <= 0 || k <= 0 || k > n) return (int)hipErrorInvalidValue;
-  *bytes = topk_ws_bytes(rows, k);
+  *bytes = topk_ws_bytes(rows, n, k);
   return 0;
 }
 
@@ -896,9 +1164,9 @@ int bytes_topk(const void* scores, int64_t rows, int n, int64_t row_stride, int 
   if (rows == 0) return 0;
   const long parts = (n + kSlice - 1) / kSlice;
   if (kRowBatch * parts > 0x7FFFFFFFL) return (int)hipErrorInvalidConfiguration;
-  if (!workspace || workspace_bytes < topk_ws_bytes(rows, k)) return (int)hipErrorInvalidValue;
+  if (!workspace || workspace_bytes < topk_ws_bytes(rows, n, k)) return (int)hipErrorInvalidValue;
   if (hist_ready && rows > kRowBatch) return (int)hipErrorInvalidValue;
-  const TopkWs ws = topk_ws_carve(workspace, rows, k);
+  const TopkWs ws = topk_ws_carve(workspace, rows, n, k);
   const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0) && (row_stride % 4 == 0) && (n % 4 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float* s = static_cast<const float*>(scores);

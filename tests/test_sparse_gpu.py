@@ -97,6 +97,28 @@ def test_topk_large_k(dev, rows, n, k):
     assert torch.equal(got_s.long(), R.topk_indices(s, k, sorted_by_score=True))
 
 
+@pytest.mark.parametrize("k", [8193, 13107, 32768, 65536, 131071])
+def test_topk_large_k_c5_rows(dev, k):
+    """k above 8192 on the C5 row shape (64 x 131072): threshold-digit
+    candidates, per-row selection and per-slice ordered writes, with a tied
+    block at the threshold, a row of rounded (heavily tied) scores and a row
+    whose keys share one top digit (the whole-row exact fallback)."""
+    g = torch.Generator().manual_seed(k)
+    s = torch.randn(64, 131072, generator=g)
+    s[3, 1000:1100] = 5.0
+    s[5, :] = s[5, :].round()
+    s[7, :] = 1.0 + torch.rand(131072, generator=g) * 0.2    # one top digit for every key
+    got = SP.topk_indices(s.to(dev), k, sorted=False).cpu().long()
+    assert torch.equal(got, R.topk_indices(s, k, sorted_by_score=False))
+
+
+def test_topk_large_k_row_batches(dev):
+    """More rows than one launch group (1024) with k above 8192."""
+    s = _tie_heavy(1100, 20000, seed=1)
+    got = SP.topk_indices(s.to(dev), 9000, sorted=False).cpu().long()
+    assert torch.equal(got, R.topk_indices(s, 9000, sorted_by_score=False))
+
+
 @pytest.mark.parametrize("sorted_out", [True, False])
 @pytest.mark.parametrize("rows,n,k", [(600, 2048, 128), (600, 1000, 1), (300, 4096, 256), (700, 2051, 17),
                                       (260, 64, 64), (1000, 4095, 200)])
