@@ -1161,6 +1161,331 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
                                  nh, (BITS == 2 && quant && !rtile) ? kDmapKivi2 : kDmapDense);
 }
 
+// ============================================================================
+// Pipelined decode for long caches: 4-wave workgroups, three per CU, each
+// walking a long run of 256-token granules through a two-stage LDS ring
+// ============================================================================
+// A split is a run of granules of one unit.  Granule i's key codes and value
+// codes go HBM -> LDS untouched (buffer loads with the LDS bit, no VGPRs),
+// its key scales/zeros and value scales/zeros through VGPRs (their staged
+// layouts are transposes of the stored ones).  While the waves compute
+// granule i from one stage (wave w: tile w, the granule's tokens
+// [64w, 64w + 64)), granule i + 1 streams into the other; one barrier per
+// granule publishes a stage.  The two stages are separate LDS arrays and
+// every read of a stage follows an explicit wait for the loads into it, so
+// the loads into the other stage stay in flight across the reads (the
+// compiler cannot tell the LDS-DMA destinations apart within one array and
+// would wait for all of them).  LDS ~49 KB and at most 168 VGPRs let three
+// workgroups share a CU, so one workgroup's barrier or loads overlap the
+// tiles of the others.  The bf16 residual window runs on splits of its own
+// (waves 0 and 1, two dense 32-token tiles each, in the stages' space).
+constexpr int kPipeWaves = 4;
+constexpr int kPipeGran = kPipeWaves * kKiviTile;      // tokens per granule
+constexpr int kPipeWgPerCu = 3;
+
+template <int D, int BITS>
+struct PipeCfg {
+  static_assert(D == 128 && BITS == 2, "pipelined decode: D = 128, 2-bit caches");
+  static constexpr int KK = D / 32;
+  static constexpr int KPR = kPipeGran * BITS / 8;      // bytes of a key channel row per granule (64)
+  static constexpr int KC = D * KPR;                     // key codes of a granule
+  static constexpr int KROWS_DMA = 1024 / KPR;           // key rows per 1 KB LDS-DMA instruction
+  static constexpr int KDMA = KC / (kPipeWaves * 1024);  // key LDS-DMA instructions per wave per granule
+  static constexpr int NGG = kPipeGran / 32;             // key groups per granule
+  // halfwords per staged (scale|zero, group) row: the 8-halfword pad puts the
+  // staging stores of a wave's four group rows in distinct banks
+  static constexpr int KMP = D + 8;
+  static constexpr int KM = 2 * NGG * KMP * 2;
+  static constexpr int VROW = D * BITS / 8;              // bytes of one token's value codes
+  static constexpr int VB = kKiviTile * VROW;            // one wave's value codes
+  static constexpr int VDMA = VB / 1024;
+  static constexpr int NGV = D / 32;
+  static constexpr int VMB = 2 * kKiviTile * NGV * 2 + kKiviOnes;   // one wave's value scales + zeros, then fp16 ones
+  static constexpr int OFF_KM = KC;
+  static constexpr int OFF_V = OFF_KM + KM;
+  static constexpr int OFF_VM = OFF_V + kPipeWaves * VB;
+  static constexpr int STAGE = OFF_VM + kPipeWaves * VMB;
+  static_assert(KPR == 64 && KROWS_DMA == 16, "four 16-byte key pieces per row and granule");
+  static_assert(KDMA * kPipeWaves * 1024 == KC && VDMA * 1024 == VB, "whole LDS-DMA instructions");
+  static_assert(kPipeWaves * 64 * 4 == 2 * D * NGG / 2, "four 4-byte key scale/zero words per thread and granule");
+  // residual tiles (waves 0 and 1, one dense tile buffer in each stage) and
+  // the split-K epilogue (waves 0-1 rows in stage 0, waves 2-3 in stage 1)
+  static_assert(DenseCfg<D>::WAVE <= STAGE, "a dense tile's K and V fit a stage");
+  static_assert((kPipeWaves * 16 * 2 + kPipeWaves / 2 * 16 * acc_pitch<D>()) * 4 <= STAGE, "epilogue rows fit");
+  static_assert(2 * STAGE <= 160 * 1024 / kPipeWgPerCu, "three workgroups per CU");
+};
+
+// One 64-token tile of the pipelined kernel: wave w's tile of the granule in
+// `stage`.  The arithmetic is kivi_tile's; only the addressing of the staged
+// granule differs: key channel row r holds the granule's four 16-byte pieces
+// (piece p = tokens [64p, 64p + 64)) in slots p ^ ((r >> 2) & 3), so the 16
+// rows a transposed read touches sit in distinct banks.  Every read stays in
+// `stage` (the value zero term's rows >= NGV read the ones after the wave's
+// value zeros), so the compiler sees that it cannot alias the loads in flight
+// into the other stage.
+template <int D, int BITS>
+__device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh)[D / 32], const char* stage,
+                                               float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
+  using C = PipeCfg<D, BITS>;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const char* kms = stage + C::OFF_KM;
+  const char* kbase = stage + l16 * C::KPR + ((w ^ (l16 >> 2)) << 4);
+  const char* vst = stage + C::OFF_V + w * C::VB;
+  const char* vml = stage + C::OFF_VM + w * C::VMB;
+
+  // sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
+  f32x4 sc[4];
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    const int grp = 2 * w + sg;
+    f16x8 qs[C::KK];
+    f32x4 z = negm;
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) {
+      const int off = (grp * C::KMP + lg * (D / 4) + kk * 8) * 2;
+      const u32x4 ks = *reinterpret_cast<const u32x4*>(kms + off);
+      const u32x4 kz = *reinterpret_cast<const u32x4*>(kms + C::NGG * C::KMP * 2 + off);
+      qs[kk] = scale8(qh[kk], ks);
+      z = mfma_f16(__builtin_bit_cast(f16x8, kz), qh[kk], z);
+    }
+    sc[sg * 2 + 0] = z;
+    sc[sg * 2 + 1] = z;
+#pragma unroll
+    for (int rd = 0; rd < C::KK / 2; ++rd) {
+      const u32x2 x = tr4(kbase + (lg * (D / 4) + rd * 16) * C::KPR + sg * 8);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int kk = rd * 2 + half;
+        const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
+        sc[sg * 2 + 0] = mfma_f16(codes_fp4(e), qs[kk], sc[sg * 2 + 0]);
+        sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
+      }
+    }
+  }
+
+  float p[16];
+  kivi_softmax<D>(sc, m_run, negm, acc, zv, p);
+  f16x8 pb[2];
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg)
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) pb[sg][jj] = (_Float16)p[(sg * 2 + (jj & 1)) * 4 + (jj >> 1)];
+
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    f16x8 pg[C::NGV];
+#pragma unroll
+    for (int g = 0; g < C::NGV; ++g)
+      pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
+    {
+      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, C::NGV), sg * 32) * 2 + lg * 16);
+      zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
+    }
+#pragma unroll
+    for (int rd = 0; rd < D / 64; ++rd) {
+      const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+      const int tok = 32 * sg + 8 * lg + r;
+      const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
+      const int ca = 2 * rd, cbb = 2 * rd + 1;
+      const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
+      const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
+      acc[ca * 2 + 0] = mfma_f16(codes_fp4(e0), pg[ca], acc[ca * 2 + 0]);
+      acc[cbb * 2 + 0] = mfma_f16(codes_fp4(e1), pg[cbb], acc[cbb * 2 + 0]);
+      acc[ca * 2 + 1] = mfma_f16(codes_fp4(o0), pg[ca], acc[ca * 2 + 1]);
+      acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
+    }
+  }
+}
+
+// One 16-byte-per-lane LDS-DMA request: lane l's 16 bytes at byte voff of the
+// buffer land at lds + 16 l (NT: with the non-temporal hint, for bytes read
+// once in whole cache lines).  Issued from inline assembly so
+// that the compiler does not track it: the compiler cannot tell LDS-DMA
+// destinations apart where a read's offset varies per lane, and would make
+// every read of one stage wait for the loads in flight into the other.  The
+// kernel waits for these requests itself (vmcnt) before a barrier publishes
+// the stage.  M0 holds the LDS base; one wait state before the load uses it.
+template <bool NT>
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const char* lds, uint32_t voff) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+  if (NT)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(r)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
+// A granule's loads: key codes and the wave's value codes into `stage` by
+// LDS-DMA, key and value scales/zeros into registers.  A granule reads 64 of
+// the 128 bytes of each key-row line and 16 of each key scale/zero line, the
+// rest of the lines belonging to the split's next granules: those loads keep
+// their lines in L2 (no non-temporal hint); value codes and value
+// scales/zeros are whole lines read once.
+template <int D, int BITS>
+struct PipeMeta {
+  uint32_t km[4];        // word t % 4 (groups 2(t%4), +1 of the granule) of (scale|zero, channel) row 64i + t / 4
+  u32x4 vm;              // value scales (lanes 0-31) / zeros (32-63) of tokens 2(l % 32), +1 of the wave's tile
+};
+
+template <int D, int BITS>
+__global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kernel(KiviArgs a) {
+  using C = PipeCfg<D, BITS>;
+  PREFETCH_ARGS(a);
+  __shared__ __attribute__((aligned(16))) char st0[C::STAGE];
+  __shared__ __attribute__((aligned(16))) char st1[C::STAGE];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const UnitLoc loc = splitk_locate(a.o);
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk, hb = loc.hb;
+  const int hq0 = hk * a.G + hb * 16;
+  const int nh = min(16, a.G - hb * 16);
+  const uint16_t* qrow0 = a.q + (int64_t)b * a.q_sb + (int64_t)hq0 * a.q_sh;
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool resid_only = split >= a.nsq;
+  if (resid_only) {
+    // residual tokens [r_begin, r_end): waves 0 and 1 take 32-token tiles
+    // w and w + 2; wave 0 stages in st0, wave 1 in st1
+    const int r_begin = (split - a.nsq) * kResidPerSplit;
+    const int r_end = min(r_begin + kResidPerSplit, a.R);
+    if (w < 2) {
+      bf16x8 qb[D / 32];
+      load_q_bf16<D>(qrow0, a.q_sh, nh, lane, qb);
+      const uint16_t* kb = a.kr + (int64_t)b * a.kr_sb + (int64_t)hk * a.kr_sh;
+      const uint16_t* vb = a.vr + (int64_t)b * a.vr_sb + (int64_t)hk * a.vr_sh;
+      char* kst = w == 0 ? st0 : st1;
+      char* vst = kst + DenseCfg<D>::VT;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int rt = r_begin + (w + 2 * j) * kTile;
+        if (rt < r_end) {
+          DenseRegs<D> rr;
+          dense_issue<D>(kb, vb, a.kr_ss, a.vr_ss, a.R, rt, r_end, lane, rr);
+          wave_lds_sync();
+          dense_stage<D>(lane, rr, kst, vst);
+          wave_lds_sync();
+          dense_compute<D>(range_mask(rt, r_end), a.scale_log2, lane, qb, kst, vst, m_run, l_run, acc);
+        }
+      }
+    }
+    splitk_epilogue<D, kPipeWaves>(m_run, l_run, acc, reinterpret_cast<float*>(st0), a.o, unit, split, b, hq0, nh,
+                                   kDmapDense, reinterpret_cast<float*>(st1));
+    return;
+  }
+
+  // ---- quantized split: granules [g_begin, g_end) of the unit ----
+  const int Sq = a.Sq;
+  const int t_begin = split * a.chunk;
+  const int t_end = min(t_begin + a.chunk, Sq);
+  const int ngr = (t_end - t_begin + kPipeGran - 1) / kPipeGran;
+  const uint32_t bh = (uint32_t)(b * a.Hk + hk);
+  const int ngk = Sq >> 5;
+  const uint32_t wkb = (uint32_t)Sq * BITS / 8;      // bytes per key channel row
+  const uint32_t kq_u = D * wkb, vq_u = (uint32_t)Sq * C::VROW;
+  const __amdgpu_buffer_rsrc_t rkq = buf_rsrc(reinterpret_cast<const char*>(a.kq) + (uint64_t)bh * kq_u, kq_u);
+  const __amdgpu_buffer_rsrc_t rvq = buf_rsrc(reinterpret_cast<const char*>(a.vq) + (uint64_t)bh * vq_u, vq_u);
+  // key LDS-DMA: wave w's instruction j covers key rows (w*KDMA + j)*16 + lane/4,
+  // slot lane % 4 <- piece (lane % 4) ^ ((lane >> 4) & 3)
+  const uint32_t kvoff = (uint32_t)(lane >> 2) * wkb + (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+  // key scales/zeros: rows 0..D-1 scales, D..2D-1 zeros of channels 0..D-1;
+  // thread t reads word t % 4 of the granule's 16 bytes of rows 64i + t / 4,
+  // four threads to a row (a request touches 16 lines per wave)
+  const int mwd = threadIdx.x & 3, mr0 = threadIdx.x >> 2;
+  static_assert(kPipeWaves * 64 / 4 == D / 2, "64 rows per step: steps 0-1 scales, 2-3 zeros");
+  const _Float16* mrow = a.ks + ((size_t)bh * D + mr0) * ngk + 2 * mwd;
+  const _Float16* zrow = a.km + ((size_t)bh * D + mr0) * ngk + 2 * mwd;
+  // value scales/zeros of two tokens per lane
+  const _Float16* vmb = (lane < 32 ? a.vs : a.vm) + (size_t)bh * Sq * C::NGV + 2 * (lane & 31) * C::NGV;
+
+  // Every offset is in the VGPR offset, which the buffer range check covers:
+  // pieces of a last, partial granule past the unit's cache read zeros.
+  auto issue = [&](int gi, char* stage, PipeMeta<D, BITS>& m) {
+    const int tg = t_begin + gi * kPipeGran;
+#pragma unroll
+    for (int j = 0; j < C::KDMA; ++j) {
+      const int blk = w * C::KDMA + j;
+      lds_dma16<false>(rkq, stage + blk * 1024, kvoff + (uint32_t)blk * C::KROWS_DMA * wkb + (uint32_t)tg * BITS / 8);
+    }
+    const int tt = tg + w * kKiviTile;
+#pragma unroll
+    for (int j = 0; j < C::VDMA; ++j)
+      lds_dma16<true>(rvq, stage + C::OFF_V + w * C::VB + j * 1024, (uint32_t)tt * C::VROW + j * 1024 + lane * 16);
+    // scales/zeros of groups and tokens past the cache end: clamped copies no tile reads
+    const int g0 = tg >> 5;
+    const int go = min(g0 + 2 * mwd, ngk - 2) - 2 * mwd;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      m.km[i] = *reinterpret_cast<const uint32_t*>((i < 2 ? mrow : zrow) + (size_t)((i & 1) * 64) * ngk + go);
+    m.vm = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vmb + (size_t)min(tt, Sq - kKiviTile) * C::NGV));
+  };
+  auto stage_meta = [&](char* stage, const PipeMeta<D, BITS>& m) {
+    _Float16* kd = reinterpret_cast<_Float16*>(stage + C::OFF_KM) + 2 * mwd * C::KMP + mr0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int o = (i >> 1) * C::NGG * C::KMP + (i & 1) * 64;
+      kd[o] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[i] & 0xFFFFu));
+      kd[o + C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[i] >> 16));
+    }
+    _Float16* vd = reinterpret_cast<_Float16*>(stage + C::OFF_VM + w * C::VMB);
+    const _Float16* hv = reinterpret_cast<const _Float16*>(&m.vm);
+    const int sm = lane >> 5, tau0 = 2 * (lane & 31);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int g = 0; g < C::NGV; ++g) vd[vmeta_slot<D, BITS>(sm, g, tau0 + u)] = hv[u * C::NGV + g];
+  };
+
+  PipeMeta<D, BITS> meta;
+  issue(0, st0, meta);
+  if (lane < 32) {
+    const int o = C::OFF_VM + w * C::VMB + 2 * kKiviTile * C::NGV * 2 + lane * 4;
+    *reinterpret_cast<uint32_t*>(st0 + o) = 0x3C003C00u;
+    *reinterpret_cast<uint32_t*>(st1 + o) = 0x3C003C00u;
+  }
+
+  // Q as the fp16 B operand scaled by scale*log2(e): lane holds
+  // Q[h = l16][ch = lg*(D/4) + kk*8 + jj] (head columns past nh take head hq0)
+  f16x8 qh[D / 32];
+  {
+    const uint16_t* qp = qrow0 + (int64_t)(l16 < nh ? l16 : 0) * a.q_sh + lg * (D / 4);
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, ld16(qp + kk * 8));
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[jj] * a.scale_log2);
+    }
+  }
+
+  f32x4 zv = {0.f, 0.f, 0.f, 0.f}, negm = {0.f, 0.f, 0.f, 0.f};
+  // One granule: wait for its loads (the only ones in flight), stage its
+  // meta, publish the stage, request the next granule into the other stage,
+  // compute this wave's tile.
+  auto step = [&](int gi, char* cur, char* nxt) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0)
+    stage_meta(cur, meta);
+    lds_barrier();
+    if (gi + 1 < ngr) issue(gi + 1, nxt, meta);
+    if (t_begin + gi * kPipeGran + w * kKiviTile < t_end)
+      kivi_pipe_tile<D, BITS>(w, lane, qh, cur, m_run, negm, acc, zv);
+  };
+  for (int gi = 0; gi < ngr; gi += 2) {
+    step(gi, st0, st1);
+    if (gi + 1 < ngr) step(gi + 1, st1, st0);
+  }
+  kivi_finish<D>(lane, zv, acc, l_run);
+  splitk_epilogue<D, kPipeWaves>(m_run, l_run, acc, reinterpret_cast<float*>(st0), a.o, unit, split, b, hq0, nh,
+                                 BITS == 2 ? kDmapKivi2 : kDmapDense, reinterpret_cast<float*>(st1));
+}
+
 // nw: 8-wave workgroups with 1024-token chunks (one per CU) when that grid
 // fills between half and all of the CUs in one go; else 4-wave workgroups with
 // chunks of up to 512 tokens (two per CU), whose pairs overlap one
@@ -1234,6 +1559,43 @@ static void kivi_stream_plan(int Sq, int R, long units, int chunk_req, int gran,
   *rchunk = 0;
 }
 
+// Granules per split of the pipelined kernel: 2048-token splits, whose 128
+// bytes of each key scale/zero row are one cache line's worth (measured best
+// at L = 64K against 4-16 granules).
+constexpr int kPipeGps = 8;
+
+// The pipelined kernel serves D = 128, 2-bit caches of whole 64-token tiles
+// and at least four granules: always when the caller asks for it (chunk_req
+// < 0), never when the caller sets a split length for the other kernels
+// (chunk_req > 0), and otherwise when 2048-token splits alone give every CU a
+// workgroup (long caches; shorter ones finish sooner on the two-half kernel).
+static bool kivi_use_pipe(int D, int bits, int Sq, long units, int chunk_req) {
+  if (D != 128 || bits != 2 || Sq % kKiviTile != 0 || Sq < 4 * kPipeGran) return false;
+  if (chunk_req != 0) return chunk_req < 0;
+  const long n = (Sq + kPipeGps * kPipeGran - 1) / (kPipeGps * kPipeGran);
+  return n * units >= device_cu_count();
+}
+
+// Plan of the pipelined kernel: the residual window on splits of its own
+// (128 tokens each), the quantized tokens of each unit cut into runs of
+// kPipeGps granules (-chunk_req when the caller sets it).
+static void kivi_pipe_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq, int* rsplit, int* rchunk) {
+  (void)units;
+  const int nr = (R + kResidPerSplit - 1) / kResidPerSplit;
+  const int ng = (Sq + kPipeGran - 1) / kPipeGran;
+  int gps = chunk_req < 0 ? -chunk_req : kPipeGps;
+  if (gps < 1) gps = 1;
+  int n = (ng + gps - 1) / gps;
+  if (n + nr > 1024) {                            // the merge takes up to 1024 splits
+    gps = (ng + 1023 - nr) / (1024 - nr);
+    n = (ng + gps - 1) / gps;
+  }
+  *chunk = gps * kPipeGran;
+  *nsq = n;
+  *rsplit = nr;
+  *rchunk = 0;
+}
+
 // Key piece width (bytes) and split granularity (tokens) of the streaming kernel.
 static void kivi_stream_shape(int bits, int* kpb, int* gran) {
   *kpb = bits == 2 ? 8 : 16;
@@ -1284,7 +1646,9 @@ int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D
   const int G = Hq / Hk, HB = (G + 15) / 16;
   const long units = (long)B * Hk * HB;
   int chunk, nsq, rsplit, rchunk;
-  if (Sq % kKiviTile == 0) {
+  if (kivi_use_pipe(D, bits, Sq, units, chunk_req)) {
+    kivi_pipe_plan(Sq, R, units, chunk_req, &chunk, &nsq, &rsplit, &rchunk);
+  } else if (Sq % kKiviTile == 0) {
     int nw;
     kivi_plan(Sq, R, units, chunk_req, &nw, &chunk, &nsq, &rsplit, &rchunk);
   } else {
@@ -1331,9 +1695,12 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   // Sq a multiple of 64: the two-half kernel; else (an odd number of 32-token
   // key groups) the streaming kernel, whose loads and tiles take 32-token
   // granularity
-  const bool halves = Sq % kKiviTile == 0;
+  const bool pipe = kivi_use_pipe(D, bits, Sq, units, chunk_req);
+  const bool halves = !pipe && Sq % kKiviTile == 0;
   int nw = 8, kpb = 16, gran = 32;
-  if (halves) {
+  if (pipe) {
+    kivi_pipe_plan(Sq, R, units, chunk_req, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
+  } else if (halves) {
     kivi_plan(Sq, R, units, chunk_req, &nw, &a.chunk, &a.nsq, &a.rsplit, &a.rchunk);
   } else {
     kivi_stream_shape(bits, &kpb, &gran);
@@ -1349,6 +1716,12 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   splitk_carve(workspace, units, ns, a.o);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(ns * units));
+  if (pipe) {
+    BYTES_LAUNCH(kProfKivi, (kivi_pipe_kernel<128, 2>), grid, dim3(kPipeWaves * 64), 0, st, a);
+    int rc = (int)hipGetLastError();
+    if (rc) return rc;
+    return splitk_combine(a.o, units, D, st);
+  }
   if (halves) {
     const dim3 block(nw * 64);
 #define KIVI_HALVES(DD, BB)                                                                         \

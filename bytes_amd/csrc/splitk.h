@@ -134,10 +134,14 @@ __device__ __forceinline__ int acc_d(int dmap, int db, int lg, int i) {
 // Every wave copies its state to LDS (acc as 16-byte runs of four consecutive
 // d), then each thread merges four consecutive d of one head over the waves,
 // computing that head's wave factors itself (no third barrier), in wave order.
+// smem holds the maxima, denominators and the accumulator rows of every wave,
+// splitk_smem_floats<D, NW>() floats; with smem_hi set, the rows of waves
+// NW/2.. go there instead (NW/2 * 16 * acc_pitch<D>() floats each side), for
+// kernels whose LDS is two separate arrays.
 template <int D, int NW>
 __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], float* smem,
                                 const SplitKOut& o, int unit, int split, int b, int hq0, int nh,
-                                int dmap = kDmapDense) {
+                                int dmap = kDmapDense, float* smem_hi = nullptr) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
   constexpr int NT = NW * 64;
   constexpr int P = acc_pitch<D>();
@@ -146,12 +150,14 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
   float* wm = smem;
   float* wl = wm + NW * 16;
   float* wacc = wl + NW * 16;
+  // accumulator rows of wave ww
+  auto wrow = [&](int ww) { return smem_hi && ww >= NW / 2 ? smem_hi + (ww - NW / 2) * 16 * P : wacc + ww * 16 * P; };
   __syncthreads();
   if (lg == 0) {
     wm[w * 16 + l16] = m_run;
     wl[w * 16 + l16] = l_run;
   }
-  f32x4* row = reinterpret_cast<f32x4*>(wacc + (w * 16 + l16) * P);
+  f32x4* row = reinterpret_cast<f32x4*>(wrow(w) + l16 * P);
   if (dmap == kDmapKivi2) {
     // acc[2k][i], acc[2k+1][i] hold d = 32k + 8lg + 2i + {0, 1}
 #pragma unroll
@@ -177,7 +183,7 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
     for (int ww = 0; ww < NW; ++ww) {
       const float f = fast_exp2(wm[ww * 16 + h] - Ms);
       L += f * wl[ww * 16 + h];
-      A += f * reinterpret_cast<const f32x4*>(wacc + (ww * 16 + h) * P)[d4];
+      A += f * reinterpret_cast<const f32x4*>(wrow(ww) + h * P)[d4];
     }
     if (o.nsplit <= 1) {
 #pragma unroll

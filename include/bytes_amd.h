@@ -131,10 +131,13 @@ int bytes_kivi_dequant(const void* code, const void* scale, const void* mn, int6
  *   v_scale, v_mn [B, Hk, Sq, D/32] f16
  *   v_res    [B, Hk, R, D] bf16 (strides vr_*)
  *   out      [B, Hq, D] bf16 (strides o_sb, o_sh)
- * Packed tensors and their metadata are contiguous.  Sq % 64 == 0 (0 allowed),
- * group size 32, D in {64, 128}; other Sq return hipErrorNotSupported (the
- * Python layer then dequantizes and calls bytes_decode_attn_bf16).
+ * Packed tensors and their metadata are contiguous.  Sq % 32 == 0 (0 allowed;
+ * other Sq return hipErrorInvalidValue), group size 32, D in {64, 128}.
  * scale: the reference uses 1/sqrt(D).
+ * chunk: 0 = automatic kernel and split plan; > 0 = split length (tokens) of
+ * the two-half / streaming kernels; < 0 = the pipelined kernel (D = 128,
+ * 2-bit, Sq % 64 == 0, Sq >= 1024; otherwise as 0) with splits of -chunk
+ * 256-token granules.  bytes_kivi_decode_workspace_size takes the same chunk.
  * ------------------------------------------------------------------------- */
 int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D, int bits, int chunk,
                                      size_t* bytes);
