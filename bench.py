@@ -157,8 +157,9 @@ class KiviCase(Case):
     kernel = "kivi_decode_kernel"
     family = 2
 
-    def __init__(self, name, bits, B=4, Hq=28, Hk=4, D=128, L=16384, R=128):
+    def __init__(self, name, bits, B=4, Hq=28, Hk=4, D=128, L=16384, R=128, kernel="kivi_decode_kernel"):
         self.name, self.bits, self.shape = name, bits, (B, Hq, Hk, D, L, R)
+        self.kernel = kernel   # the library's choice for this shape on MI355X (256 CUs)
         self.dtype = f"u{bits}+fp16 meta+bf16"
         self.workload = (f"KIVI-{bits} decode B{B} Hq{Hq} Hkv{Hk} D{D} L{L} "
                          f"(Sq={L - R} packed, residual {R} bf16, group 32)")
@@ -346,7 +347,7 @@ class PqCase(Case):
     (decode_attn_pq_kv_fused: q . k_hat on MFMA from the codebook rows, within
     the attention tolerance of pq_build_lut followed by decode_attn_pq_lut_kv);
     codebook fitting and encoding are setup."""
-    kernel = "pq_group_kernel"
+    kernel = "pq_wave_kernel"
     family = 3
 
     def __init__(self, name, B=1, Hq=28, Hk=4, D=128, L=32768, K=256):
@@ -432,7 +433,7 @@ def cases():
         "c1_dense": DenseCase("c1_dense", *W.SHAPES["c1_dense"]),
         "dense_16k": DenseCase("dense_16k", *W.SHAPES["dense_16k"]),
         "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
-        "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536),
+        "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536, kernel="kivi_pipe_kernel"),
         "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536),
         "c3_pq": PqCase("c3_pq"),
         "c4_quest": QuestCase("c4_quest"),

@@ -194,6 +194,28 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// One 16-byte-per-lane LDS-DMA request: lane l's 16 bytes at byte voff of the
+// buffer land at lds + 16 l (NT: with the non-temporal hint, for bytes read
+// once in whole cache lines).  Issued from inline assembly so
+// that the compiler does not track it: the compiler cannot tell LDS-DMA
+// destinations apart where a read's offset varies per lane, and would make
+// every LDS read wait for every such load in flight.  The caller waits for
+// these requests itself (vmcnt) before the LDS they fill is read.  M0 holds the LDS base; one wait state before the load uses it.
+template <bool NT>
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const char* lds, uint32_t voff) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+  if (NT)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(r)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 

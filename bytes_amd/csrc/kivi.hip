@@ -1297,29 +1297,6 @@ __device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh
   }
 }
 
-// One 16-byte-per-lane LDS-DMA request: lane l's 16 bytes at byte voff of the
-// buffer land at lds + 16 l (NT: with the non-temporal hint, for bytes read
-// once in whole cache lines).  Issued from inline assembly so
-// that the compiler does not track it: the compiler cannot tell LDS-DMA
-// destinations apart where a read's offset varies per lane, and would make
-// every read of one stage wait for the loads in flight into the other.  The
-// kernel waits for these requests itself (vmcnt) before a barrier publishes
-// the stage.  M0 holds the LDS base; one wait state before the load uses it.
-template <bool NT>
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const char* lds, uint32_t voff) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
-  if (NT)
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
-                 :
-                 : "s"(m0), "v"(voff), "s"(r)
-                 : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(m0), "v"(voff), "s"(r)
-                 : "memory", "m0");
-}
-
 // A granule's loads: key codes and the wave's value codes into `stage` by
 // LDS-DMA, key and value scales/zeros into registers.  A granule reads 64 of
 // the 128 bytes of each key-row line and 16 of each key scale/zero line, the

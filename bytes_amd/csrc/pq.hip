@@ -925,6 +925,211 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_group_kernel(PqArgs a) {
 }
 
 // ============================================================================
+// Per-wave grouped decode (mode 3 on contiguous caches, G <= 8; the C3 step):
+// a unit is (b, kv head) with all G query heads, a workgroup a chunk of
+// <= kPqgChunk tokens and wave w the chunk's tokens [64w, 64w + 64).  Both
+// codebooks (64 KB each at D = 128) go HBM/L2 -> LDS by LDS-DMA, the wave's
+// key and value codes into registers; once the key codebook is published
+// every wave runs on its own (a second barrier publishes the value codebook,
+// which streams in under the scores): scores q . k_hat on MFMA exactly as pq_group_kernel's
+// SRC 2 (the same scaled hi/lo q and MFMA order, so the same fp32 scores),
+// the softmax of its 64 tokens in registers (the probabilities never leave
+// them: the score MFMA's output layout is the P^T operand layout of the PV
+// MFMA), and PV over all D columns from transposed reads of the value
+// codebook.  The waves' states then merge in the split-K epilogue.  Against
+// pq_group_kernel this drops the LDS round trips of scores, probabilities
+// and per-head maxima and three of its five workgroup barriers.
+// ============================================================================
+template <int D>
+struct PqwCfg {
+  static constexpr int M = D / 8;
+  static constexpr int CB = M * kPqKMax * 16;                  // one fp16 codebook [M][256][8]
+  static constexpr int CPT = M * kPqKMax / kPqgThreads;        // codebook rows per thread
+  static constexpr int kEpi = splitk_smem_floats<D, kPqWaves>() * 4;
+  static constexpr int kSmem = 2 * CB > kEpi ? 2 * CB : kEpi;
+  static_assert(kPqgChunk == kPqWaves * 64, "64 tokens per wave");
+  static_assert(CPT * kPqgThreads == M * kPqKMax, "whole codebook rows per thread");
+};
+
+template <int D>
+__global__ __launch_bounds__(kPqgThreads, 1) void pq_wave_kernel(PqArgs a) {
+  using C = PqwCfg<D>;
+  constexpr int M = D / 8;
+  constexpr int KS = M / 4;                 // score MFMA k-steps (4 subspaces each)
+  constexpr int DB = D / 16;                // output column blocks
+  __shared__ __attribute__((aligned(16))) char smem[C::kSmem];
+  char* kcbl = smem;
+  char* vcbl = smem + C::CB;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const UnitLoc loc = splitk_locate(a.o);     // o.HB = 1: unit = b * Hk + hk
+  const int unit = loc.unit, split = loc.split, b = loc.b, hk = loc.hk;
+  const int G = a.G, hq0 = hk * G, K = a.K;
+  const int t_begin = split * a.chunk;
+  const int n = max(0, min(a.chunk, a.S - t_begin));
+  const int tw = 64 * w;
+
+  // Requests, oldest first: the key codebook (LDS-DMA), the q rows and codes,
+  // the value codebook (VGPRs, stored to LDS after the scores).  The scores
+  // need all but the value codebook, which arrives while they are computed;
+  // the compiler, which does not see the LDS-DMA requests, counts every
+  // later request exactly.  Codebook row s = (j, c) of 256 per subspace sits
+  // at s * 16 in LDS (codewords past K repeat codeword K - 1; no code reads
+  // them).
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.kcb + (int64_t)hk * a.kcb_sh, (uint32_t)(M * K * 16));
+  auto cb_off = [&](int i) {
+    const int sl = tid + kPqgThreads * i;
+    return (uint32_t)(((sl >> 8) * K + min(sl & 255, K - 1)) * 16);
+  };
+#pragma unroll
+  for (int i = 0; i < C::CPT; ++i) lds_dma16<false>(rk, kcbl + (kPqgThreads * i + 64 * w) * 16, cb_off(i));
+  // q of head l16 (columns past G take head 0 and are zeroed below), lane
+  // (l16, lg) holding channels 32 kk + 8 lg .. +7: the score B operand
+  u32x4 qraw[KS];
+  {
+    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hq0 + (l16 < G ? l16 : 0)) * a.q_sh + lg * 8;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qraw[kk] = ld16(qp + kk * 32);
+  }
+  // codes, clamped into the chunk: key codes of tokens tw + 16 bi + l16 (score
+  // A operands) and value codes of tokens tw + 32 k + 16 hf + 4 lg + l16 / 4
+  // (PV transposed reads)
+  const uint8_t* kb = a.kidx + (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh;
+  const uint8_t* vb = a.vidx + (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh;
+  auto crow = [&](int t) { return (int64_t)(t_begin + min(t, max(n - 1, 0))); };
+  u32x4 kc[4], vcw[2][2];
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi) kc[bi] = ld_codes<M>(kb + crow(tw + 16 * bi + l16) * a.ki_ss);
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+      vcw[k][hf] = ld_codes<M>(vb + crow(tw + 32 * k + 16 * hf + 4 * lg + (l16 >> 2)) * a.vi_ss);
+  u32x4 vraw[C::CPT];
+  {
+    const char* vcg = reinterpret_cast<const char*>(a.vcb + (int64_t)hk * a.vcb_sh);
+#pragma unroll
+    for (int i = 0; i < C::CPT; ++i) vraw[i] = ld16(vcg + cb_off(i));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // q scaled by 2^-k_h so the row fits fp16 (k_h from the row's largest |q|,
+  // the four lanes of head l16 holding the row), split into hi + lo fp16
+  // parts: the LUT contract's operands (lut_store_q, pq_group_kernel SRC 2)
+  const bool hlive = l16 < G;
+  float amax = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(bf16_bits_to_f32((uint16_t)(qraw[kk][i >> 1] >> (16 * (i & 1))))));
+  amax = col_max4(amax);
+  const int kh = lut_shift(amax);
+  const float mul = hlive ? ldexpf(a.lut_scale, kh) : 0.f;
+  f16x8 qhi[KS], qlo[KS];
+  bool nzl = false;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = hlive ? ldexpf(bf16_bits_to_f32((uint16_t)(qraw[kk][i >> 1] >> (16 * (i & 1)))), -kh) : 0.f;
+      const _Float16 hv = (_Float16)v;
+      qhi[kk][i] = hv;
+      qlo[kk][i] = (_Float16)(v - (float)hv);
+      nzl = nzl || (float)qlo[kk][i] != 0.f;
+    }
+  const bool nz = __ballot(nzl) != 0;
+
+  // every request but the value codebook's has returned (in order): the key
+  // codebook is in LDS, and the barrier publishes it
+  static_assert(C::CPT <= 15, "the value codebook's requests fit the wait count");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | C::CPT);      // vmcnt(CPT)
+  lds_barrier();
+
+  // ---- scores of the wave's 4 blocks of 16 tokens: head l16's scores of
+  // tokens tw + 16 bi + 4 lg + i in s[bi][i] ----
+  f16x8 cwd[4][KS];
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const uint32_t code = (kc[bi][kk] >> (8 * lg)) & 0xFFu;       // subspace 4 kk + lg
+      cwd[bi][kk] = *reinterpret_cast<const f16x8*>(kcbl + ((4 * kk + lg) * kPqKMax + (int)code) * 16);
+    }
+  f32x4 s[4];
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi) s[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (nz) {
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        s[bi] = mfma_f16(cwd[bi][kk], qhi[kk], s[bi]);
+        s[bi] = mfma_f16(cwd[bi][kk], qlo[kk], s[bi]);
+      }
+  } else {
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) s[bi] = mfma_f16(cwd[bi][kk], qhi[kk], s[bi]);
+  }
+
+  // ---- softmax of the wave's tokens (log2 domain; tokens past n: -inf) ----
+  float mx = kNegInf;
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = tw + 16 * bi + 4 * lg + i < n ? (mul * s[bi][i]) * a.scale_log2 : kNegInf;
+      s[bi][i] = x;
+      mx = fmaxf(mx, x);
+    }
+  const float m_run = col_max4(mx);
+  const float m_use = m_run == kNegInf ? 0.f : m_run;
+  float l_run = 0.f;
+  f16x8 ph[2];
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = hlive ? fast_exp2(s[bi][i] - m_use) : 0.f;
+      l_run += p;
+      ph[bi >> 1][(bi & 1) * 4 + i] = (_Float16)p;
+    }
+
+  // ---- the value codebook into LDS; publish it ----
+#pragma unroll
+  for (int i = 0; i < C::CPT; ++i) *reinterpret_cast<u32x4*>(vcbl + (tid + kPqgThreads * i) * 16) = vraw[i];
+  lds_barrier();
+
+  // ---- PV: O^T[d][h] += V^T[d][t] P^T[t][h] over the wave's two 32-token
+  // tiles; block db's rows come from codeword subspaces 2 db + sub ----
+  f32x4 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int sub = (l16 & 3) >> 1;
+  const char* vrow = vcbl + (sub * kPqKMax) * 16 + (l16 & 1) * 8;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    u32x2 hv[DB][2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int j = 2 * db + sub;                                  // subspace
+        const uint32_t code = (vcw[k][hf][j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        hv[db][hf] = tr16(vrow + (2 * db * kPqKMax + (int)code) * 16);
+      }
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const u32x4 raw = {hv[db][0][0], hv[db][0][1], hv[db][1][0], hv[db][1][1]};
+      acc[db] = mfma_f16(__builtin_bit_cast(f16x8, raw), ph[k], acc[db]);
+    }
+  }
+  splitk_epilogue<D, kPqWaves>(m_run, l_run, acc, reinterpret_cast<float*>(smem), a.o, unit, split, b, hq0, G,
+                               kDmapDense);
+}
+
+// ============================================================================
 // Per-key LUT scores: out[b, h, t] = sum_j lut[b, h, j, k_idx[t, j]] (j in
 // order) + sum_c q_out[b, h, c] * k_out[t, c] (C > 0), fp32.  A workgroup
 // stages the LUTs of one (b, kv head, group of <= 4 query heads) in LDS and
@@ -1236,6 +1441,13 @@ static int pq_launch(PqArgs& a, int mode, bool vf8, int B, int Hq, int Hk, int S
       a.o.Hk = Hk; a.o.HB = 1; a.o.G = a.G; a.o.hbs = a.G;
       splitk_carve(workspace, gunits, gns, a.o);
       const dim3 grid((unsigned)(gns * gunits)), block(kPqgThreads);
+      if (mode == 3 && !a.btab) {
+        if (D == 128) BYTES_LAUNCH(kProfPq, (pq_wave_kernel<128>), grid, block, 0, st, a);
+        else BYTES_LAUNCH(kProfPq, (pq_wave_kernel<64>), grid, block, 0, st, a);
+        const int rc = (int)hipGetLastError();
+        if (rc) return rc;
+        return splitk_combine(a.o, gunits, D, st);
+      }
 #define PQG_LAUNCH(DD, BL, HP)                                                                   \
   if (a.btab) BYTES_LAUNCH(kProfPq, (pq_group_kernel<DD, BL, HP, true>), grid, block, 0, st, a);  \
   else BYTES_LAUNCH(kProfPq, (pq_group_kernel<DD, BL, HP, false>), grid, block, 0, st, a);

@@ -157,17 +157,20 @@ __device__ void splitk_epilogue(float m_run, float l_run, f32x4 (&acc)[D / 16], 
     wm[w * 16 + l16] = m_run;
     wl[w * 16 + l16] = l_run;
   }
+  // rows of head columns past nh are never read: not written
   f32x4* row = reinterpret_cast<f32x4*>(wrow(w) + l16 * P);
-  if (dmap == kDmapKivi2) {
-    // acc[2k][i], acc[2k+1][i] hold d = 32k + 8lg + 2i + {0, 1}
+  if (l16 < nh) {
+    if (dmap == kDmapKivi2) {
+      // acc[2k][i], acc[2k+1][i] hold d = 32k + 8lg + 2i + {0, 1}
 #pragma unroll
-    for (int k = 0; k < D / 32; ++k) {
-      row[8 * k + 2 * lg] = f32x4{acc[2 * k][0], acc[2 * k + 1][0], acc[2 * k][1], acc[2 * k + 1][1]};
-      row[8 * k + 2 * lg + 1] = f32x4{acc[2 * k][2], acc[2 * k + 1][2], acc[2 * k][3], acc[2 * k + 1][3]};
+      for (int k = 0; k < D / 32; ++k) {
+        row[8 * k + 2 * lg] = f32x4{acc[2 * k][0], acc[2 * k + 1][0], acc[2 * k][1], acc[2 * k + 1][1]};
+        row[8 * k + 2 * lg + 1] = f32x4{acc[2 * k][2], acc[2 * k + 1][2], acc[2 * k][3], acc[2 * k + 1][3]};
+      }
+    } else {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) row[4 * db + lg] = acc[db];
     }
-  } else {
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) row[4 * db + lg] = acc[db];
   }
   __syncthreads();
 
