@@ -1215,44 +1215,40 @@ struct PipeCfg {
   static_assert(2 * STAGE <= 160 * 1024 / kPipeWgPerCu, "three workgroups per CU");
 };
 
-// One 64-token tile of the pipelined kernel: wave w's tile of the granule in
-// `stage`.  The arithmetic is kivi_tile's; only the addressing of the staged
-// granule differs: key channel row r holds the granule's four 16-byte pieces
-// (piece p = tokens [64p, 64p + 64)) in slots p ^ ((r >> 2) & 3), so the 16
-// rows a transposed read touches sit in distinct banks.  Every read stays in
-// `stage` (the value zero term's rows >= NGV read the ones after the wave's
-// value zeros), so the compiler sees that it cannot alias the loads in flight
-// into the other stage.
-template <int D, int BITS>
-__device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh)[D / 32], const char* stage,
-                                               float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
-  using C = PipeCfg<D, BITS>;
+// One 64-token 2-bit tile from staged operands, the arithmetic of kivi_tile:
+// kbase is this lane's byte of key channel row l16 of the tile's 16-byte
+// piece (rows KPR bytes apart, 8 bytes per 32-token key group), kms the
+// staged key scales ([group][KMP] fp16) with the zeros kzo bytes on and grp0
+// the tile's first group there, vst / vml the tile's value codes and value
+// scales/zeros (vmeta_slot layout, fp16 ones after the zeros).
+template <int D, int BITS, int KPR, int KMP>
+__device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32], const char* kbase, const char* kms,
+                                             int kzo, int grp0, const char* vst, const char* vml, float& m_run,
+                                             f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
+  static_assert(BITS == 2, "2-bit tiles");
+  constexpr int KK = D / 32, NGV = D / 32, VROW = D * BITS / 8;
   const int l16 = lane & 15, lg = lane >> 4;
-  const char* kms = stage + C::OFF_KM;
-  const char* kbase = stage + l16 * C::KPR + ((w ^ (l16 >> 2)) << 4);
-  const char* vst = stage + C::OFF_V + w * C::VB;
-  const char* vml = stage + C::OFF_VM + w * C::VMB;
 
   // sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
   f32x4 sc[4];
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    const int grp = 2 * w + sg;
-    f16x8 qs[C::KK];
+    const int grp = grp0 + sg;
+    f16x8 qs[KK];
     f32x4 z = negm;
 #pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk) {
-      const int off = (grp * C::KMP + lg * (D / 4) + kk * 8) * 2;
+    for (int kk = 0; kk < KK; ++kk) {
+      const int off = (grp * KMP + lg * (D / 4) + kk * 8) * 2;
       const u32x4 ks = *reinterpret_cast<const u32x4*>(kms + off);
-      const u32x4 kz = *reinterpret_cast<const u32x4*>(kms + C::NGG * C::KMP * 2 + off);
+      const u32x4 kz = *reinterpret_cast<const u32x4*>(kms + kzo + off);
       qs[kk] = scale8(qh[kk], ks);
       z = mfma_f16(__builtin_bit_cast(f16x8, kz), qh[kk], z);
     }
     sc[sg * 2 + 0] = z;
     sc[sg * 2 + 1] = z;
 #pragma unroll
-    for (int rd = 0; rd < C::KK / 2; ++rd) {
-      const u32x2 x = tr4(kbase + (lg * (D / 4) + rd * 16) * C::KPR + sg * 8);
+    for (int rd = 0; rd < KK / 2; ++rd) {
+      const u32x2 x = tr4(kbase + (lg * (D / 4) + rd * 16) * KPR + sg * 8);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int kk = rd * 2 + half;
@@ -1273,19 +1269,19 @@ __device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh
 
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    f16x8 pg[C::NGV];
+    f16x8 pg[NGV];
 #pragma unroll
-    for (int g = 0; g < C::NGV; ++g)
+    for (int g = 0; g < NGV; ++g)
       pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
     {
-      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, C::NGV), sg * 32) * 2 + lg * 16);
+      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, NGV), sg * 32) * 2 + lg * 16);
       zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
     }
 #pragma unroll
     for (int rd = 0; rd < D / 64; ++rd) {
       const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
       const int tok = 32 * sg + 8 * lg + r;
-      const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
+      const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
       const int ca = 2 * rd, cbb = 2 * rd + 1;
       const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
       const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
@@ -1295,6 +1291,20 @@ __device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh
       acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
     }
   }
+}
+
+// Wave w's tile of the granule staged in `stage` (pipelined kernel): key
+// channel row r holds the granule's four 16-byte pieces (piece p = tokens
+// [64p, 64p + 64)) in slots p ^ ((r >> 2) & 3), so the 16 rows a transposed
+// read touches sit in distinct banks.  Every read stays in `stage`.
+template <int D, int BITS>
+__device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh)[D / 32], const char* stage,
+                                               float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
+  using C = PipeCfg<D, BITS>;
+  const int l16 = lane & 15;
+  kivi_tile_at<D, BITS, C::KPR, C::KMP>(lane, qh, stage + l16 * C::KPR + ((w ^ (l16 >> 2)) << 4), stage + C::OFF_KM,
+                                        C::NGG * C::KMP * 2, 2 * w, stage + C::OFF_V + w * C::VB,
+                                        stage + C::OFF_VM + w * C::VMB, m_run, negm, acc, zv);
 }
 
 // A granule's loads: key codes and the wave's value codes into `stage` by
