@@ -434,7 +434,7 @@ def cases():
         "dense_16k": DenseCase("dense_16k", *W.SHAPES["dense_16k"]),
         "dense_32k": DenseCase("dense_32k", 4, 28, 4, 128, 32768),
         "c2_kivi2_64k": KiviCase("c2_kivi2_64k", 2, L=65536, kernel="kivi_pipe_kernel"),
-        "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536),
+        "c2_kivi4_64k": KiviCase("c2_kivi4_64k", 4, L=65536, kernel="kivi_pipe_kernel"),
         "c3_pq": PqCase("c3_pq"),
         "c4_quest": QuestCase("c4_quest"),
         "c5_topk256": TopkCase("c5_topk256", 256),

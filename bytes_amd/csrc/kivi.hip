@@ -1162,8 +1162,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
 }
 
 // ============================================================================
-// Pipelined decode for long caches: 4-wave workgroups, three per CU, each
-// walking a long run of 256-token granules through a two-stage LDS ring
+// Pipelined decode for long caches: 4-wave workgroups (three per CU for
+// 2-bit caches, two for 4-bit), each walking a long run of 256-token granules
+// through a two-stage LDS ring
 // ============================================================================
 // A split is a run of granules of one unit.  Granule i's key codes and value
 // codes go HBM -> LDS untouched (buffer loads with the LDS bit, no VGPRs),
@@ -1175,61 +1176,76 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
 // every read of a stage follows an explicit wait for the loads into it, so
 // the loads into the other stage stay in flight across the reads (the
 // compiler cannot tell the LDS-DMA destinations apart within one array and
-// would wait for all of them).  LDS ~49 KB and at most 168 VGPRs let three
-// workgroups share a CU, so one workgroup's barrier or loads overlap the
-// tiles of the others.  The bf16 residual window runs on splits of its own
-// (waves 0 and 1, two dense 32-token tiles each, in the stages' space).
+// would wait for all of them).  A 2-bit workgroup's ~50 KB of LDS and at
+// most 168 VGPRs let three share a CU, a 4-bit one's 80 KB two, so one
+// workgroup's barrier or loads overlap the tiles of the others.  The bf16
+// residual window runs on splits of its own (waves 0 and 1, two dense
+// 32-token tiles each, in the stages' space).
 constexpr int kPipeWaves = 4;
 constexpr int kPipeGran = kPipeWaves * kKiviTile;      // tokens per granule
-constexpr int kPipeWgPerCu = 3;
+template <int BITS>
+constexpr int pipe_wg_per_cu() { return BITS == 2 ? 3 : 2; }
 
 template <int D, int BITS>
 struct PipeCfg {
-  static_assert(D == 128 && BITS == 2, "pipelined decode: D = 128, 2-bit caches");
+  static_assert(D == 128 && (BITS == 2 || BITS == 4), "pipelined decode: D = 128, 2- or 4-bit caches");
   static constexpr int KK = D / 32;
-  static constexpr int KPR = kPipeGran * BITS / 8;      // bytes of a key channel row per granule (64)
+  static constexpr int KPR = kPipeGran * BITS / 8;      // bytes of a key channel row per granule (64 | 128)
+  static constexpr int NPC = KPR / 16;                   // 16-byte key pieces per row and granule
   static constexpr int KC = D * KPR;                     // key codes of a granule
   static constexpr int KROWS_DMA = 1024 / KPR;           // key rows per 1 KB LDS-DMA instruction
   static constexpr int KDMA = KC / (kPipeWaves * 1024);  // key LDS-DMA instructions per wave per granule
   static constexpr int NGG = kPipeGran / 32;             // key groups per granule
-  // halfwords per staged (scale|zero, group) row: the 8-halfword pad puts the
-  // staging stores of a wave's four group rows in distinct banks
-  static constexpr int KMP = D + 8;
+  // halfwords per staged (scale|zero, group) row: for 2-bit caches the
+  // 8-halfword pad puts the staging stores of a wave's four group rows in
+  // distinct banks; 4-bit stages go without it to fit two workgroups per CU
+  static constexpr int KMP = BITS == 2 ? D + 8 : D;
   static constexpr int KM = 2 * NGG * KMP * 2;
   static constexpr int VROW = D * BITS / 8;              // bytes of one token's value codes
   static constexpr int VB = kKiviTile * VROW;            // one wave's value codes
   static constexpr int VDMA = VB / 1024;
   static constexpr int NGV = D / 32;
-  static constexpr int VMB = 2 * kKiviTile * NGV * 2 + kKiviOnes;   // one wave's value scales + zeros, then fp16 ones
+  static constexpr int VMB = 2 * kKiviTile * NGV * 2;   // one wave's value scales + zeros
   static constexpr int OFF_KM = KC;
   static constexpr int OFF_V = OFF_KM + KM;
   static constexpr int OFF_VM = OFF_V + kPipeWaves * VB;
   static constexpr int STAGE = OFF_VM + kPipeWaves * VMB;
-  static_assert(KPR == 64 && KROWS_DMA == 16, "four 16-byte key pieces per row and granule");
+  static constexpr int WG_PER_CU = pipe_wg_per_cu<BITS>();
+  static_assert(NPC == 4 * BITS / 2 && KROWS_DMA * NPC == 64, "one key row per NPC lanes of an LDS-DMA instruction");
   static_assert(KDMA * kPipeWaves * 1024 == KC && VDMA * 1024 == VB, "whole LDS-DMA instructions");
   static_assert(kPipeWaves * 64 * 4 == 2 * D * NGG / 2, "four 4-byte key scale/zero words per thread and granule");
   // residual tiles (waves 0 and 1, one dense tile buffer in each stage) and
   // the split-K epilogue (waves 0-1 rows in stage 0, waves 2-3 in stage 1)
   static_assert(DenseCfg<D>::WAVE <= STAGE, "a dense tile's K and V fit a stage");
   static_assert((kPipeWaves * 16 * 2 + kPipeWaves / 2 * 16 * acc_pitch<D>()) * 4 <= STAGE, "epilogue rows fit");
-  static_assert(2 * STAGE <= 160 * 1024 / kPipeWgPerCu, "three workgroups per CU");
+  static_assert(2 * STAGE <= 160 * 1024 / WG_PER_CU, "WG_PER_CU workgroups per CU");
 };
 
-// One 64-token 2-bit tile from staged operands, the arithmetic of kivi_tile:
-// kbase is this lane's byte of key channel row l16 of the tile's 16-byte
-// piece (rows KPR bytes apart, 8 bytes per 32-token key group), kms the
-// staged key scales ([group][KMP] fp16) with the zeros kzo bytes on and grp0
-// the tile's first group there, vst / vml the tile's value codes and value
-// scales/zeros (vmeta_slot layout, fp16 ones after the zeros).
+// Slot of 16-byte key piece p in staged key channel row r: the 16 rows a
+// transposed read touches (r = 16k .. 16k + 15) then sit in distinct banks
+// (rows 64 bytes apart for 2-bit caches, 128 for 4-bit, 256-byte bank cycle).
+template <int BITS>
+__device__ __forceinline__ int pipe_kslot(int p, int r) {
+  return BITS == 2 ? p ^ ((r >> 2) & 3) : p ^ ((r >> 1) & 7);
+}
+
+// One 64-token tile from staged operands, the arithmetic of kivi_tile:
+// kb[sg] is this lane's byte of key channel row l16 for the tile's tokens
+// [32sg, 32sg + 32) (rows KPR bytes apart; 8 bytes for 2-bit caches, 16 - two
+// 16-token blocks of 8 - for 4-bit), kms the staged key scales ([group][KMP]
+// fp16, k-slot channel order) with the zeros kzo bytes on and grp0 the tile's
+// first group there, vst / vml the tile's value codes and value scales/zeros
+// (vmeta_slot layout).  The value zero-term MFMA's rows past the value groups
+// are ones (the softmax denominators).
 template <int D, int BITS, int KPR, int KMP>
-__device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32], const char* kbase, const char* kms,
-                                             int kzo, int grp0, const char* vst, const char* vml, float& m_run,
-                                             f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
-  static_assert(BITS == 2, "2-bit tiles");
+__device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32], const char* const (&kb)[2],
+                                             const char* kms, int kzo, int grp0, const char* vst, const char* vml,
+                                             float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
   constexpr int KK = D / 32, NGV = D / 32, VROW = D * BITS / 8;
   const int l16 = lane & 15, lg = lane >> 4;
 
-  // sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
+  // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
+  // 4-bit: sc[tb][i]       is tile token 16tb + 4lg + i
   f32x4 sc[4];
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
@@ -1247,26 +1263,36 @@ __device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32]
     sc[sg * 2 + 0] = z;
     sc[sg * 2 + 1] = z;
 #pragma unroll
-    for (int rd = 0; rd < KK / 2; ++rd) {
-      const u32x2 x = tr4(kbase + (lg * (D / 4) + rd * 16) * KPR + sg * 8);
+    for (int bb = 0; bb < (BITS == 2 ? 1 : 2); ++bb)
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int kk = rd * 2 + half;
-        const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
-        sc[sg * 2 + 0] = mfma_f16(codes_fp4(e), qs[kk], sc[sg * 2 + 0]);
-        sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
+      for (int rd = 0; rd < KK / 2; ++rd) {
+        const u32x2 x = tr4(kb[sg] + (lg * (D / 4) + rd * 16) * KPR + bb * 8);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int kk = rd * 2 + half;
+          if (BITS == 2) {
+            const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
+            sc[sg * 2 + 0] = mfma_f16(codes_fp4(e), qs[kk], sc[sg * 2 + 0]);
+            sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
+          } else {
+            const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
+            sc[sg * 2 + bb] = mfma_f16(codes_fp8(lo, hi), qs[kk], sc[sg * 2 + bb]);
+          }
+        }
       }
-    }
   }
 
   float p[16];
   kivi_softmax<D>(sc, m_run, negm, acc, zv, p);
+  // P^T as the B operand, k-slot jj of sub-tile sg (the orders of kivi_tile)
   f16x8 pb[2];
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg)
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) pb[sg][jj] = (_Float16)p[(sg * 2 + (jj & 1)) * 4 + (jj >> 1)];
+    for (int jj = 0; jj < 8; ++jj)
+      pb[sg][jj] = (_Float16)p[BITS == 2 ? (sg * 2 + (jj & 1)) * 4 + (jj >> 1) : (2 * sg + (jj >> 2)) * 4 + (jj & 3)];
 
+  constexpr uint32_t kOnes = 0x3C003C00u;
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
     f16x8 pg[NGV];
@@ -1274,45 +1300,65 @@ __device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32]
     for (int g = 0; g < NGV; ++g)
       pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
     {
-      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, NGV), sg * 32) * 2 + lg * 16);
+      u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, NGV - 1), sg * 32) * 2 + lg * 16);
+      if (l16 >= NGV) vz = u32x4{kOnes, kOnes, kOnes, kOnes};
       zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
     }
+    if (BITS == 2) {
 #pragma unroll
-    for (int rd = 0; rd < D / 64; ++rd) {
-      const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
-      const int tok = 32 * sg + 8 * lg + r;
-      const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
-      const int ca = 2 * rd, cbb = 2 * rd + 1;
-      const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
-      const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
-      acc[ca * 2 + 0] = mfma_f16(codes_fp4(e0), pg[ca], acc[ca * 2 + 0]);
-      acc[cbb * 2 + 0] = mfma_f16(codes_fp4(e1), pg[cbb], acc[cbb * 2 + 0]);
-      acc[ca * 2 + 1] = mfma_f16(codes_fp4(o0), pg[ca], acc[ca * 2 + 1]);
-      acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
+      for (int rd = 0; rd < D / 64; ++rd) {
+        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+        const int tok = 32 * sg + 8 * lg + r;
+        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
+        const int ca = 2 * rd, cbb = 2 * rd + 1;
+        const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
+        const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
+        acc[ca * 2 + 0] = mfma_f16(codes_fp4(e0), pg[ca], acc[ca * 2 + 0]);
+        acc[cbb * 2 + 0] = mfma_f16(codes_fp4(e1), pg[cbb], acc[cbb * 2 + 0]);
+        acc[ca * 2 + 1] = mfma_f16(codes_fp4(o0), pg[ca], acc[ca * 2 + 1]);
+        acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int rd = 0; rd < D / 32; ++rd) {
+        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
+        const int tok = (r & 1) ? 32 * sg + 16 + 4 * lg + (r >> 1) : 32 * sg + 4 * lg + (r >> 1);
+        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
+        const uint32_t lo0 = x[0] & 0x0F0F0F0Fu, hi0 = (x[0] >> 4) & 0x0F0F0F0Fu;
+        const uint32_t lo1 = x[1] & 0x0F0F0F0Fu, hi1 = (x[1] >> 4) & 0x0F0F0F0Fu;
+        acc[2 * rd] = mfma_f16(codes_fp8(lo0, hi0), pg[rd], acc[2 * rd]);
+        acc[2 * rd + 1] = mfma_f16(codes_fp8(lo1, hi1), pg[rd], acc[2 * rd + 1]);
+      }
     }
   }
 }
 
 // Wave w's tile of the granule staged in `stage` (pipelined kernel): key
-// channel row r holds the granule's four 16-byte pieces (piece p = tokens
-// [64p, 64p + 64)) in slots p ^ ((r >> 2) & 3), so the 16 rows a transposed
-// read touches sit in distinct banks.  Every read stays in `stage`.
+// channel row r holds the granule's NPC 16-byte pieces (piece p = tokens
+// [256p/NPC, 256(p+1)/NPC)) in slots pipe_kslot(p, r); the tile's tokens are
+// piece w (2-bit) or pieces 2w, 2w + 1 (4-bit), and for the rows a lane reads
+// (l16 + 16k) the slot depends on l16 only.  Every read stays in `stage`.
 template <int D, int BITS>
 __device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh)[D / 32], const char* stage,
                                                float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
   using C = PipeCfg<D, BITS>;
   const int l16 = lane & 15;
-  kivi_tile_at<D, BITS, C::KPR, C::KMP>(lane, qh, stage + l16 * C::KPR + ((w ^ (l16 >> 2)) << 4), stage + C::OFF_KM,
-                                        C::NGG * C::KMP * 2, 2 * w, stage + C::OFF_V + w * C::VB,
-                                        stage + C::OFF_VM + w * C::VMB, m_run, negm, acc, zv);
+  const char* row = stage + l16 * C::KPR;
+  const char* const kb[2] = {
+      BITS == 2 ? row + (pipe_kslot<BITS>(w, l16) << 4) : row + (pipe_kslot<BITS>(2 * w, l16) << 4),
+      BITS == 2 ? row + (pipe_kslot<BITS>(w, l16) << 4) + 8 : row + (pipe_kslot<BITS>(2 * w + 1, l16) << 4)};
+  kivi_tile_at<D, BITS, C::KPR, C::KMP>(lane, qh, kb, stage + C::OFF_KM, C::NGG * C::KMP * 2, 2 * w,
+                                        stage + C::OFF_V + w * C::VB, stage + C::OFF_VM + w * C::VMB, m_run, negm,
+                                        acc, zv);
 }
 
 // A granule's loads: key codes and the wave's value codes into `stage` by
-// LDS-DMA, key and value scales/zeros into registers.  A granule reads 64 of
-// the 128 bytes of each key-row line and 16 of each key scale/zero line, the
-// rest of the lines belonging to the split's next granules: those loads keep
-// their lines in L2 (no non-temporal hint); value codes and value
-// scales/zeros are whole lines read once.
+// LDS-DMA, key and value scales/zeros into registers.  A granule reads 64
+// (2-bit) or 128 (4-bit) bytes of each key row, not aligned to its lines, and
+// 16 of each 128-byte key scale/zero line, the rest of the lines belonging to
+// the split's neighbouring granules: those loads keep their lines in L2 (no
+// non-temporal hint); value codes and value scales/zeros are whole lines read
+// once.
 template <int D, int BITS>
 struct PipeMeta {
   uint32_t km[4];        // word t % 4 (groups 2(t%4), +1 of the granule) of (scale|zero, channel) row 64i + t / 4
@@ -1320,7 +1366,7 @@ struct PipeMeta {
 };
 
 template <int D, int BITS>
-__global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kernel(KiviArgs a) {
+__global__ __launch_bounds__(kPipeWaves * 64, pipe_wg_per_cu<BITS>()) void kivi_pipe_kernel(KiviArgs a) {
   using C = PipeCfg<D, BITS>;
   PREFETCH_ARGS(a);
   __shared__ __attribute__((aligned(16))) char st0[C::STAGE];
@@ -1380,9 +1426,15 @@ __global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kerne
   const uint32_t kq_u = D * wkb, vq_u = (uint32_t)Sq * C::VROW;
   const __amdgpu_buffer_rsrc_t rkq = buf_rsrc(reinterpret_cast<const char*>(a.kq) + (uint64_t)bh * kq_u, kq_u);
   const __amdgpu_buffer_rsrc_t rvq = buf_rsrc(reinterpret_cast<const char*>(a.vq) + (uint64_t)bh * vq_u, vq_u);
-  // key LDS-DMA: wave w's instruction j covers key rows (w*KDMA + j)*16 + lane/4,
-  // slot lane % 4 <- piece (lane % 4) ^ ((lane >> 4) & 3)
-  const uint32_t kvoff = (uint32_t)(lane >> 2) * wkb + (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+  // key LDS-DMA: instruction blk covers key rows blk*KROWS_DMA + lane/NPC,
+  // slot lane % NPC <- the piece pipe_kslot maps there (an involution), which
+  // depends on blk only through its parity (4-bit caches)
+  uint32_t kvoff[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int row = par * C::KROWS_DMA + lane / C::NPC;
+    kvoff[par] = (uint32_t)(lane / C::NPC) * wkb + (uint32_t)(pipe_kslot<BITS>(lane % C::NPC, row) << 4);
+  }
   // key scales/zeros: rows 0..D-1 scales, D..2D-1 zeros of channels 0..D-1;
   // thread t reads word t % 4 of the granule's 16 bytes of rows 64i + t / 4,
   // four threads to a row (a request touches 16 lines per wave)
@@ -1400,7 +1452,7 @@ __global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kerne
 #pragma unroll
     for (int j = 0; j < C::KDMA; ++j) {
       const int blk = w * C::KDMA + j;
-      lds_dma16<false>(rkq, stage + blk * 1024, kvoff + (uint32_t)blk * C::KROWS_DMA * wkb + (uint32_t)tg * BITS / 8);
+      lds_dma16<false>(rkq, stage + blk * 1024, kvoff[blk & 1] + (uint32_t)blk * C::KROWS_DMA * wkb + (uint32_t)tg * BITS / 8);
     }
     const int tt = tg + w * kKiviTile;
 #pragma unroll
@@ -1415,10 +1467,10 @@ __global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kerne
     m.vm = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vmb + (size_t)min(tt, Sq - kKiviTile) * C::NGV));
   };
   auto stage_meta = [&](char* stage, const PipeMeta<D, BITS>& m) {
-    _Float16* kd = reinterpret_cast<_Float16*>(stage + C::OFF_KM) + 2 * mwd * C::KMP + mr0;
+    _Float16* kd = reinterpret_cast<_Float16*>(stage + C::OFF_KM) + 2 * mwd * C::KMP;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int o = (i >> 1) * C::NGG * C::KMP + (i & 1) * 64;
+      const int o = (i >> 1) * C::NGG * C::KMP + kslot_pos<BITS>((i & 1) * 64 + mr0);
       kd[o] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[i] & 0xFFFFu));
       kd[o + C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[i] >> 16));
     }
@@ -1433,14 +1485,9 @@ __global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kerne
 
   PipeMeta<D, BITS> meta;
   issue(0, st0, meta);
-  if (lane < 32) {
-    const int o = C::OFF_VM + w * C::VMB + 2 * kKiviTile * C::NGV * 2 + lane * 4;
-    *reinterpret_cast<uint32_t*>(st0 + o) = 0x3C003C00u;
-    *reinterpret_cast<uint32_t*>(st1 + o) = 0x3C003C00u;
-  }
 
   // Q as the fp16 B operand scaled by scale*log2(e): lane holds
-  // Q[h = l16][ch = lg*(D/4) + kk*8 + jj] (head columns past nh take head hq0)
+  // Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)] (head columns past nh take head hq0)
   f16x8 qh[D / 32];
   {
     const uint16_t* qp = qrow0 + (int64_t)(l16 < nh ? l16 : 0) * a.q_sh + lg * (D / 4);
@@ -1448,7 +1495,7 @@ __global__ __launch_bounds__(kPipeWaves * 64, kPipeWgPerCu) void kivi_pipe_kerne
     for (int kk = 0; kk < D / 32; ++kk) {
       const bf16x8 qv = __builtin_bit_cast(bf16x8, ld16(qp + kk * 8));
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[jj] * a.scale_log2);
+      for (int jj = 0; jj < 8; ++jj) qh[kk][jj] = (_Float16)((float)qv[kslot_ch<BITS>(jj)] * a.scale_log2);
     }
   }
 
@@ -1546,31 +1593,36 @@ static void kivi_stream_plan(int Sq, int R, long units, int chunk_req, int gran,
   *rchunk = 0;
 }
 
-// Granules per split of the pipelined kernel: 2048-token splits, whose 128
-// bytes of each key scale/zero row are one cache line's worth (measured best
-// at L = 64K against 4-16 granules).
-constexpr int kPipeGps = 8;
+// Granules per split of the pipelined kernel chosen by the library: the
+// fewest that keep the grid within two workgroups per CU (one pass of the
+// grid, measured best at L = 24K-128K, B4 H_k4, for both bit widths: e.g. 2-bit
+// L32K 22.0 us at four granules against 27.0 at eight, L64K 31.0 at eight
+// against 33.2 at six and 32.5 at ten).
+static int kivi_pipe_gps(int Sq, long units) {
+  const long ng = (Sq + kPipeGran - 1) / kPipeGran;
+  const long slots = 2L * device_cu_count();
+  return (int)((ng * units + slots - 1) / slots);
+}
 
-// The pipelined kernel serves D = 128, 2-bit caches of whole 64-token tiles
-// and at least four granules: always when the caller asks for it (chunk_req
-// < 0), never when the caller sets a split length for the other kernels
-// (chunk_req > 0), and otherwise when 2048-token splits alone give every CU a
-// workgroup (long caches; shorter ones finish sooner on the two-half kernel).
+// The pipelined kernel serves D = 128 caches (2- or 4-bit) of whole 64-token
+// tiles and at least four granules: always when the caller asks for it
+// (chunk_req < 0), never when the caller sets a split length for the other
+// kernels (chunk_req > 0), and otherwise when its splits are at least three
+// granules long (B4 H_k4 from L = 24K; shorter caches finish sooner on the
+// two-half kernel, whose splits are shorter).
 static bool kivi_use_pipe(int D, int bits, int Sq, long units, int chunk_req) {
-  if (D != 128 || bits != 2 || Sq % kKiviTile != 0 || Sq < 4 * kPipeGran) return false;
+  if (D != 128 || Sq % kKiviTile != 0 || Sq < 4 * kPipeGran) return false;
   if (chunk_req != 0) return chunk_req < 0;
-  const long n = (Sq + kPipeGps * kPipeGran - 1) / (kPipeGps * kPipeGran);
-  return n * units >= device_cu_count();
+  return kivi_pipe_gps(Sq, units) >= 3;
 }
 
 // Plan of the pipelined kernel: the residual window on splits of its own
 // (128 tokens each), the quantized tokens of each unit cut into runs of
-// kPipeGps granules (-chunk_req when the caller sets it).
+// kivi_pipe_gps granules (-chunk_req when the caller sets it).
 static void kivi_pipe_plan(int Sq, int R, long units, int chunk_req, int* chunk, int* nsq, int* rsplit, int* rchunk) {
-  (void)units;
   const int nr = (R + kResidPerSplit - 1) / kResidPerSplit;
   const int ng = (Sq + kPipeGran - 1) / kPipeGran;
-  int gps = chunk_req < 0 ? -chunk_req : kPipeGps;
+  int gps = chunk_req < 0 ? -chunk_req : kivi_pipe_gps(Sq, units);
   if (gps < 1) gps = 1;
   int n = (ng + gps - 1) / gps;
   if (n + nr > 1024) {                            // the merge takes up to 1024 splits
@@ -1704,7 +1756,8 @@ int bytes_kivi_decode_attn(const void* q, const void* kq, const void* k_scale, c
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(ns * units));
   if (pipe) {
-    BYTES_LAUNCH(kProfKivi, (kivi_pipe_kernel<128, 2>), grid, dim3(kPipeWaves * 64), 0, st, a);
+    if (bits == 2) BYTES_LAUNCH(kProfKivi, (kivi_pipe_kernel<128, 2>), grid, dim3(kPipeWaves * 64), 0, st, a);
+    else BYTES_LAUNCH(kProfKivi, (kivi_pipe_kernel<128, 4>), grid, dim3(kPipeWaves * 64), 0, st, a);
     int rc = (int)hipGetLastError();
     if (rc) return rc;
     return splitk_combine(a.o, units, D, st);

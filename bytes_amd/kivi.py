@@ -93,9 +93,9 @@ def kivi_decode_attn(Q, Kq, K_scale, K_mn, K_residual, Vq, V_scale, V_mn, V_resi
     Vq [B,Hk,Sq,D*bits/32]; V_scale/V_mn [B,Hk,Sq,D/32]; V_residual [B,Hk,R,D].
     Returns [B,Hq,1,D] in Q's dtype.  `scale` defaults to 1/sqrt(D) (:76).
     `chunk` (a tuning hint, default 0 = automatic): > 0 sets the split length
-    in tokens of the two-half / streaming kernels; < 0 runs D = 128 2-bit
-    caches (Sq a multiple of 64, at least 1024) on the pipelined kernel with
-    splits of -chunk 256-token granules.
+    in tokens of the two-half / streaming kernels; < 0 runs D = 128 caches
+    (Sq a multiple of 64, at least 1024) on the pipelined kernel with splits
+    of -chunk 256-token granules.
     """
     C.cuda_tensors(Q, K_residual, V_residual)
     C.dtype_in(Q, "Q", torch.bfloat16)

@@ -136,7 +136,7 @@ int bytes_kivi_dequant(const void* code, const void* scale, const void* mn, int6
  * scale: the reference uses 1/sqrt(D).
  * chunk: 0 = automatic kernel and split plan; > 0 = split length (tokens) of
  * the two-half / streaming kernels; < 0 = the pipelined kernel (D = 128,
- * 2-bit, Sq % 64 == 0, Sq >= 1024; otherwise as 0) with splits of -chunk
+ * Sq % 64 == 0, Sq >= 1024; otherwise as 0) with splits of -chunk
  * 256-token granules.  bytes_kivi_decode_workspace_size takes the same chunk.
  * ------------------------------------------------------------------------- */
 int bytes_kivi_decode_workspace_size(int B, int Hq, int Hk, int Sq, int R, int D, int bits, int chunk,

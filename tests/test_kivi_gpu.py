@@ -187,6 +187,7 @@ def test_decode_many_splits_use_the_merge_kernel(dev):
     _decode_case(dev, 2, 1, 7, 1, 128, 69120 + 32, 32, seed=6, chunk=256)
 
 
+@pytest.mark.parametrize("bits", [2, 4])
 @pytest.mark.parametrize("B,Hq,Hk,L,Rw,gps", [
     (1, 7, 1, 4096 + 128, 128, 3),      # splits of 3 granules, the last one granule long
     (2, 8, 2, 4160 + 72, 72, 2),        # a last granule with one 64-token tile, ragged residual
@@ -194,17 +195,18 @@ def test_decode_many_splits_use_the_merge_kernel(dev):
     (2, 32, 2, 5184 + 100, 100, 5),     # G = 16 (a full head block), Sq = 64 (mod 128)
     (1, 7, 1, 2048 + 300, 300, 1),      # one granule per split, three residual splits
 ])
-def test_decode_pipelined(dev, B, Hq, Hk, L, Rw, gps):
-    """The pipelined kernel (D = 128, 2-bit) forced with splits of `gps`
-    256-token granules: partial last granules and splits, residual splits,
-    head blocks of 16 and fewer columns."""
-    _decode_case(dev, 2, B, Hq, Hk, 128, L, Rw, seed=L + gps, chunk=-gps)
+def test_decode_pipelined(dev, bits, B, Hq, Hk, L, Rw, gps):
+    """The pipelined kernel (D = 128, 2- and 4-bit) forced with splits of
+    `gps` 256-token granules: partial last granules and splits, residual
+    splits, head blocks of 16 and fewer columns."""
+    _decode_case(dev, bits, B, Hq, Hk, 128, L, Rw, seed=L + gps + bits, chunk=-gps)
 
 
-def test_decode_pipelined_long_cache_automatic(dev):
-    """A long cache (B=4, Hk=4, Sq=32768: 2048-token splits give every CU a
-    workgroup) takes the pipelined kernel by default."""
-    _decode_case(dev, 2, 4, 28, 4, 128, 32768 + 128, 128, seed=11)
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_pipelined_long_cache_automatic(dev, bits):
+    """A long cache (B=4, Hk=4, Sq=32768: four-granule splits fill two
+    workgroups per CU) takes the pipelined kernel by default."""
+    _decode_case(dev, bits, 4, 28, 4, 128, 32768 + 128, 128, seed=11 + bits)
 
 
 @pytest.mark.parametrize("bits", [2, 4])
@@ -219,7 +221,7 @@ def test_decode_rising_scores_large_values(dev, bits, Sq, chunk, amp, vamp):
     two-half kernel (Sq = 16256, 512-token splits: a wave's two tiles 256
     tokens, ~7.7 octaves, apart), the streaming kernel (Sq = 16288,
     4096-token splits: eight phases per wave, 512 tokens and ~7.7 octaves
-    apart) and, 2-bit, the pipelined kernel (chunk -8: 2048-token splits,
+    apart) and the pipelined kernel (chunk -8: 2048-token splits,
     eight tiles per wave 256 tokens apart).  The running maximum moves on many tiles, and probabilities
     times value scales must stay finite in fp16 for any finite fp16 scale.
     Error bound relative to the output's magnitude."""
