@@ -11,7 +11,9 @@ own copy of the inputs, rotating through enough copies to exceed 2x the
 is timed with HIP events on the capture's stream, between two device
 synchronisations.  The step's dominant kernel is then timed on its own: at
 least 60 more (eager) steps, each with a HIP event pair that the library
-records on the kernel's stream right around that launch, and the median pair.
+records on the kernel's stream right around that launch, and the median pair;
+the steps are queued behind a spin kernel in chunks, so they run back to
+back as the graph-replayed ones do.
 
 Before a config is timed, one step on its own inputs is checked against the
 CPU oracle (test infrastructure, oracle/, used only as the checker): outside
@@ -501,7 +503,10 @@ def time_kernel(case: Case, inps, steps: int) -> float:
     event pair on the kernel's own stream right before and after that launch
     (bytes_set_kernel_events), one pair per step, over at least 60 steps; the
     median of the pairs (a single pair is perturbed now and then by the host's
-    launch timing)."""
+    launch timing).  The steps are launched in chunks of 20 queued behind a
+    spin kernel, so they run back to back as the graph-replayed steps do: a
+    launch onto an idle GPU starts its XCDs up to ~2 us apart (measured with
+    per-wave timestamps), which would otherwise land in the pair."""
     from bytes_amd import _lib
     if case.family == 0:                  # not a library kernel: the step is the kernel
         return time_step(case, inps, steps)
@@ -514,11 +519,21 @@ def time_kernel(case: Case, inps, steps: int) -> float:
         e0.record(s)
         e1.record(s)
     torch.cuda.synchronize()
+    chunk, spin = 20, 4_000_000
     try:
-        for i, (e0, e1) in enumerate(evs):
-            _lib.check(lib.bytes_set_kernel_events(case.family, e0.cuda_event, e1.cuda_event),
-                       "bytes_set_kernel_events")
-            case.step(inps[i % copies])
+        for c0 in range(0, steps, chunk):
+            while True:
+                torch.cuda._sleep(spin)   # holds the queue while the chunk is launched
+                for i in range(c0, min(c0 + chunk, steps)):
+                    e0, e1 = evs[i]
+                    _lib.check(lib.bytes_set_kernel_events(case.family, e0.cuda_event, e1.cuda_event),
+                               "bytes_set_kernel_events")
+                    case.step(inps[i % copies])
+                caught_up = evs[c0][0].query()   # the GPU reached the chunk before it was all queued
+                torch.cuda.synchronize()
+                if not caught_up or spin >= 256_000_000:
+                    break
+                spin *= 2
     finally:
         lib.bytes_set_kernel_events(0, None, None)
     torch.cuda.synchronize()
