@@ -203,7 +203,7 @@ __device__ __forceinline__ void lds_barrier() {
 // these requests itself (vmcnt) before the LDS they fill is read.  M0 holds the LDS base; one wait state before the load uses it.
 template <bool NT>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const char* lds, uint32_t voff) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds);
   if (NT)
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
                  :

@@ -140,35 +140,50 @@ template <int D, int BITS, int NW = 4>
 struct KiviCfg {
   static constexpr int CHUNK = NW * 2 * kKiviTile;         // tokens per workgroup
   static constexpr int KK = D / 32;                        // MFMA k-steps over channels
-  static constexpr int KPIECES = CHUNK * BITS / 128;       // 16-byte key pieces per channel per chunk
   // Key codes are staged per half chunk ([half][channel][row]) so that the
   // first half's block, read by no wave once the second half is staged, can
-  // hold the dense residual tiles of the first waves (RES_EARLY of them).
-  static constexpr int KCROW = KPIECES / 2 * 16 + 16;      // LDS bytes per channel row of a half (+16: bank spread)
-  static constexpr int KHALF = D * KCROW;
+  // hold the dense residual tiles of the first waves (RES_EARLY of them).  A
+  // channel row of a half is NPC 16-byte pieces (piece p: the half's tokens
+  // [p * 128 / BITS, (p + 1) * 128 / BITS)) in the slots kslot_swz<NPC> maps
+  // them to, with no pad, so that a half arrives by LDS-DMA, 1 KB (KROWS_DMA
+  // rows) per request.
+  static constexpr int NPC = CHUNK * BITS / 256;           // key pieces per channel row of a half
+  static constexpr int KROW = NPC * 16;
+  static constexpr int KROWS_DMA = 1024 / KROW;
+  static constexpr int KHALF = D * KROW;
+  static constexpr int KDMA = KHALF / (NW * 1024);          // key LDS-DMA requests per wave per half
   static constexpr int KCBYTES = 2 * KHALF;                // staged key codes of one chunk
   static constexpr int RES_EARLY = KHALF / DenseCfg<D>::WAVE;
   static constexpr int KMG = CHUNK / 32;                   // key groups per chunk
   // staged key scales + zeros, one row of KMP fp16 per (scale|zero, group): the
-  // 8-halfword pad puts the staging stores of a wave's eight groups in distinct banks
-  static constexpr int KMP = D + 8;
+  // 8-halfword pad puts the staging stores of a wave's eight groups in
+  // distinct banks (4-bit caches go without it, to fit two 4-wave workgroups
+  // per CU)
+  static constexpr int KMP = BITS == 2 ? D + 8 : D;
   static constexpr int KMETA = 2 * KMG * KMP * 2;
   static constexpr int VROW = D * BITS / 8;                // LDS bytes of one token's value codes
   static constexpr int VBYTES = kKiviTile * VROW;
-  static constexpr int VDMA = VBYTES / 1024;               // 16-byte value chunks per lane per tile
+  static constexpr int VDMA = VBYTES / 1024;               // value LDS-DMA requests per wave per tile
   static constexpr int NGV = D / 32;                        // value groups per token
   static constexpr int VMBYTES = 2 * kKiviTile * NGV * 2;   // value scale + zero of one tile
-  static constexpr int WAVE_BYTES = VBYTES + VMBYTES + kKiviOnes;
+  // per wave: the value codes of its two tiles (each half's arrive while the
+  // other's tile may still be read), then one tile's value scales/zeros
+  static constexpr int WAVE_BYTES = 2 * VBYTES + VMBYTES;
   // Q of the unit's 16 head columns as the fp16 B operand (scaled, k-slot
   // order within each 8-channel chunk), staged once per workgroup: row pitch
-  // D*2 + 16 bytes so the 16 head rows a 16-lane group reads sit in distinct banks
-  static constexpr int QP = D * 2 + 16;
-  static constexpr int QOFF = KCBYTES + KMETA + NW * WAVE_BYTES;
+  // D*2 + 16 bytes so the 16 head rows a 16-lane group reads sit in distinct
+  // banks, where that still fits two 4-wave workgroups per CU
+  static constexpr int QBASE = KCBYTES + KMETA + NW * WAVE_BYTES;
+  static constexpr int QP = (NW == 4 && QBASE + 16 * (D * 2 + 16) > 80 * 1024) ? D * 2 : D * 2 + 16;
+  static constexpr int QOFF = QBASE;
   static constexpr int kQuant = QOFF + 16 * QP;
   static constexpr int kDense = DenseCfg<D>::kSmem;        // residual tiles of waves 0-3 (and their merge)
   static constexpr int kEpi = splitk_smem_floats<D, NW>() * 4;
   static constexpr int kSmem0 = kQuant > kDense ? kQuant : kDense;
   static constexpr int kSmem = kSmem0 > kEpi ? kSmem0 : kEpi;
+  static_assert(KROWS_DMA * KROW == 1024 && KDMA * NW * 1024 == KHALF && VDMA * 1024 == VBYTES,
+                "whole LDS-DMA requests");
+  static_assert(NW == 8 ? kSmem <= 160 * 1024 : kSmem <= 80 * 1024, "workgroups per CU of the launch bounds");
 };
 
 // Position of the k-slot order inside an 8-channel block (4-bit keys interleave
@@ -324,14 +339,6 @@ __device__ __forceinline__ void kivi_finish(int lane, const f32x4& zv, f32x4 (&a
   l_run = (lane >> 4) == kKiviOnesRow / 4 ? zv[0] : 0.f;
 }
 
-// One tile's prefetched value codes and value scales/zeros (written to the
-// wave's LDS buffers when the tile runs).
-template <int D, int BITS>
-struct KiviRegs {
-  u32x4 v[KiviCfg<D, BITS>::VDMA];
-  VMetaReg<D> vm;         // value scales (lanes 0-31) / zeros (32-63) of two tokens
-};
-
 // Buffer resources over one unit's quantized cache.  A split without
 // quantized tokens gets zero-sized resources: its requests are issued like
 // any other (every wait counts the same requests on every path) and read
@@ -344,38 +351,41 @@ struct KiviRsrc {
   const char* vz;          // the split has no quantized tokens)
 };
 
-// Issue the value loads of the tile at token o into registers.  Value codes
-// and value scales/zeros of a tile are contiguous in HBM; lanes 0-31 take the
-// scales and lanes 32-63 the zeros of tokens o + 2(l % 32), +1.
-template <int D, int BITS>
-__device__ __forceinline__ void kivi_issue(const KiviRsrc& rs, bool quant, int o, int lane, KiviRegs<D, BITS>& r) {
-  using C = KiviCfg<D, BITS>;
-  const int vo = o * C::VROW;
-#pragma unroll
-  for (int i = 0; i < C::VDMA; ++i)
-    r.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vq, lane * 16 + i * 1024, vo, kNonTemporal));
+// Value scales (lanes 0-31) / zeros (32-63) of tokens o + 2(l % 32), +1 of the
+// tile at token o: contiguous in HBM.
+template <int D>
+__device__ __forceinline__ VMetaReg<D> kivi_load_vmeta(const KiviRsrc& rs, bool quant, int o, int lane) {
   const char* mb = lane < 32 ? rs.vs : rs.vz;
-  r.vm = __builtin_nontemporal_load(reinterpret_cast<const VMetaReg<D>*>(mb + (quant ? (uint32_t)(o + 2 * (lane & 31)) * C::NGV * 2 : 0u)));
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const VMetaReg<D>*>(mb + (quant ? (uint32_t)(o + 2 * (lane & 31)) * (D / 32) * 2 : 0u)));
 }
 
-// Write one tile's prefetched value codes and scales/zeros to the wave's LDS buffers.
+// Write one tile's value scales/zeros to the wave's LDS buffer (vmeta_slot layout).
 template <int D, int BITS>
-__device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg, char* vst, char* vmeta_lds) {
-  using C = KiviCfg<D, BITS>;
-#pragma unroll
-  for (int i = 0; i < C::VDMA; ++i) *reinterpret_cast<u32x4*>(vst + (lane + 64 * i) * 16) = rg.v[i];
-  const _Float16* hv = reinterpret_cast<const _Float16*>(&rg.vm);
+__device__ __forceinline__ void kivi_stage_vmeta(int lane, const VMetaReg<D>& vm, char* vmeta_lds) {
+  constexpr int NGV = D / 32;
+  const _Float16* hv = reinterpret_cast<const _Float16*>(&vm);
   const int sm = lane >> 5, tau0 = 2 * (lane & 31);
   _Float16* dst = reinterpret_cast<_Float16*>(vmeta_lds);
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int g = 0; g < C::NGV; ++g) dst[vmeta_slot<D, BITS>(sm, g, tau0 + u)] = hv[u * C::NGV + g];
+    for (int g = 0; g < NGV; ++g) dst[vmeta_slot<D, BITS>(sm, g, tau0 + u)] = hv[u * NGV + g];
 }
 
-// One 64-token tile: scores from the workgroup's staged key chunk (kc points at
-// this tile's first byte of channel row 0), online softmax, value accumulation
-// from the wave's staged value tile.
+// Slot of 16-byte key piece p in a staged key channel row r of NPC pieces
+// (rows 16 * NPC bytes apart): the 16 rows a transposed read touches (r =
+// 16k .. 16k + 15) then sit in distinct banks of the 256-byte bank cycle, and
+// the slot depends on r % 16 only.  An involution in p, so it also maps a
+// slot to the piece it holds.
+template <int NPC>
+__device__ __forceinline__ int kslot_swz(int p, int r) {
+  static_assert(NPC == 4 || NPC == 8 || NPC == 16, "64-, 128- or 256-byte rows");
+  return NPC == 4 ? p ^ ((r >> 2) & 3) : NPC == 8 ? p ^ ((r >> 1) & 7) : p ^ (r & 15);
+}
+
+// One 64-token tile: scores from staged key codes, online softmax, value
+// accumulation from staged value codes.
 //
 // Scales are folded into the other MFMA operand, so codes enter the MFMAs as
 // exact fp16 integers:
@@ -388,48 +398,45 @@ __device__ __forceinline__ void kivi_stage(int lane, const KiviRegs<D, BITS>& rg
 //          (g = value group of channel c; the second sum accumulates in zv,
 //          rows = groups, and is added to acc once after the last tile; rows
 //          of ones in the same MFMA sum p, the softmax denominator).
-template <int D, int BITS, int NW>
-__device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[D / 32], const char* kc,
-                                          const char* vst, const char* vmeta_lds, const char* kmeta, float& m_run,
-                                          f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
-  using C = KiviCfg<D, BITS, NW>;
+//
+// Operands:
+// kb[sg] is this lane's byte of key channel row l16 for the tile's tokens
+// [32sg, 32sg + 32) (rows KPR bytes apart; 8 bytes for 2-bit caches, 16 - two
+// 16-token blocks of 8 - for 4-bit), kms the staged key scales ([group][KMP]
+// fp16, k-slot channel order) with the zeros kzo bytes on and grp0 the tile's
+// first group there, vst / vml the tile's value codes and value scales/zeros
+// (vmeta_slot layout).  The value zero-term MFMA's rows past the value groups
+// are ones (the softmax denominators).
+template <int D, int BITS, int KPR, int KMP>
+__device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32], const char* const (&kb)[2],
+                                             const char* kms, int kzo, int grp0, const char* vst, const char* vml,
+                                             float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
+  constexpr int KK = D / 32, NGV = D / 32, VROW = D * BITS / 8;
   const int l16 = lane & 15, lg = lane >> 4;
-  constexpr int KMG = C::KMG;
-  const _Float16* kms = reinterpret_cast<const _Float16*>(kmeta);
-  const _Float16* kmz = kms + KMG * C::KMP;
 
-  // ---------------- scores ----------------
   // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
   // 4-bit: sc[tb][i]       is tile token 16tb + 4lg + i
   f32x4 sc[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) sc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    // key group sg of the tile (tokens 32sg .. 32sg+31): Q scaled by the
-    // group's channel scales, and the zero term as the initial scores
     const int grp = grp0 + sg;
-    f16x8 qs[C::KK];
+    f16x8 qs[KK];
     f32x4 z = negm;
 #pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk) {
-      const int off = (grp * C::KMP + lg * (D / 4) + kk * 8) * 2;
-      const u32x4 ks = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kms) + off);
-      const u32x4 kz = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kmz) + off);
+    for (int kk = 0; kk < KK; ++kk) {
+      const int off = (grp * KMP + lg * (D / 4) + kk * 8) * 2;
+      const u32x4 ks = *reinterpret_cast<const u32x4*>(kms + off);
+      const u32x4 kz = *reinterpret_cast<const u32x4*>(kms + kzo + off);
       qs[kk] = scale8(qh[kk], ks);
       z = mfma_f16(__builtin_bit_cast(f16x8, kz), qh[kk], z);
     }
-    // 2-bit: one 32-token block per group, even/odd tokens in sc[2sg], sc[2sg+1]
-    // 4-bit: two 16-token blocks per group, sc[2sg], sc[2sg+1]
     sc[sg * 2 + 0] = z;
     sc[sg * 2 + 1] = z;
 #pragma unroll
-    for (int bb = 0; bb < (BITS == 2 ? 1 : 2); ++bb) {
-      const int blk = BITS == 2 ? sg : sg * 2 + bb;
+    for (int bb = 0; bb < (BITS == 2 ? 1 : 2); ++bb)
 #pragma unroll
-      for (int rd = 0; rd < C::KK / 2; ++rd) {
-        const int ch = lg * (D / 4) + rd * 16 + l16;
-        const u32x2 x = tr4(kc + ch * C::KCROW + blk * 8);
+      for (int rd = 0; rd < KK / 2; ++rd) {
+        const u32x2 x = tr4(kb[sg] + (lg * (D / 4) + rd * 16) * KPR + bb * 8);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int kk = rd * 2 + half;
@@ -439,51 +446,40 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
             sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
           } else {
             const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
-            sc[blk] = mfma_f16(codes_fp8(lo, hi), qs[kk], sc[blk]);
+            sc[sg * 2 + bb] = mfma_f16(codes_fp8(lo, hi), qs[kk], sc[sg * 2 + bb]);
           }
         }
       }
-    }
   }
 
-  // ---------------- online softmax (Q carries scale*log2(e); tiles are full) ----------------
   float p[16];
   kivi_softmax<D>(sc, m_run, negm, acc, zv, p);
-
-  // P^T as the B operand, k-slot jj of sub-tile sg:
-  //   2-bit: token 32sg + 8lg + jj  -> p[(sg*2 + jj%2)*4 + jj/2]
-  //   4-bit: tokens [tb=2sg: i0..3, tb=2sg+1: i0..3] -> p[(2sg + jj/4)*4 + jj%4]
+  // P^T as the B operand, k-slot jj of sub-tile sg (the orders of kivi_tile)
   f16x8 pb[2];
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg)
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const int idx = BITS == 2 ? (sg * 2 + (jj & 1)) * 4 + (jj >> 1) : (2 * sg + (jj >> 2)) * 4 + (jj & 3);
-      pb[sg][jj] = (_Float16)p[idx];
-    }
+    for (int jj = 0; jj < 8; ++jj)
+      pb[sg][jj] = (_Float16)p[BITS == 2 ? (sg * 2 + (jj & 1)) * 4 + (jj >> 1) : (2 * sg + (jj >> 2)) * 4 + (jj & 3)];
 
-  // ---------------- values ----------------
-  const char* vml = vmeta_lds;
+  constexpr uint32_t kOnes = 0x3C003C00u;
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    // P^T scaled by each value group's token scales; the zero term on MFMA
-    // rows = groups (lane row l16 reads group l16), rows >= NGV read the
-    // wave's ones rows and sum P^T (the denominator)
-    f16x8 pg[C::NGV];
+    f16x8 pg[NGV];
 #pragma unroll
-    for (int g = 0; g < C::NGV; ++g)
+    for (int g = 0; g < NGV; ++g)
       pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
     {
-      const u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, C::NGV), sg * 32) * 2 + lg * 16);
+      u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, NGV - 1), sg * 32) * 2 + lg * 16);
+      if (l16 >= NGV) vz = u32x4{kOnes, kOnes, kOnes, kOnes};
       zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
     }
     if (BITS == 2) {
-      // cb = 32-channel block; one tr read covers cb pair (2rd, 2rd+1)
 #pragma unroll
       for (int rd = 0; rd < D / 64; ++rd) {
         const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
         const int tok = 32 * sg + 8 * lg + r;
-        const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
+        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
         const int ca = 2 * rd, cbb = 2 * rd + 1;
         const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
         const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
@@ -493,12 +489,11 @@ __device__ __forceinline__ void kivi_tile(int grp0, int lane, const f16x8 (&qh)[
         acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
       }
     } else {
-      // cb = 16-channel block; one tr read covers cb pair (2rd, 2rd+1), both in group rd
 #pragma unroll
       for (int rd = 0; rd < D / 32; ++rd) {
         const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
         const int tok = (r & 1) ? 32 * sg + 16 + 4 * lg + (r >> 1) : 32 * sg + 4 * lg + (r >> 1);
-        const u32x2 x = tr4(vst + tok * C::VROW + cbr * 8);
+        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
         const uint32_t lo0 = x[0] & 0x0F0F0F0Fu, hi0 = (x[0] >> 4) & 0x0F0F0F0Fu;
         const uint32_t lo1 = x[1] & 0x0F0F0F0Fu, hi1 = (x[1] >> 4) & 0x0F0F0F0Fu;
         acc[2 * rd] = mfma_f16(codes_fp8(lo0, hi0), pg[rd], acc[2 * rd]);
@@ -956,14 +951,16 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
 
   char* kchunk = smem_raw;
   char* kmeta = smem_raw + C::KCBYTES;
-  char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;
-  char* vml = vst + C::VBYTES;
+  char* vst = kmeta + C::KMETA + w * C::WAVE_BYTES;   // value codes of the wave's tile in half ph: + ph * VBYTES
+  char* vml = vst + 2 * C::VBYTES;
 
-  // The first half is requested on every path, so that each wait counts the
-  // same requests whatever the path (the counts of a wait after paths that
-  // issued different requests are those of the shortest).  A split without
-  // quantized tokens (a residual-only split, or Sq == 0 with no quantized
-  // cache at all) requests through zero-sized resources and reads zeros.
+  // The first half's scale/zero requests are issued on every path, so that
+  // each wait the compiler counts sees the same requests whatever the path
+  // (the counts of a wait after paths that issued different requests are
+  // those of the shortest).  A split without quantized tokens (a residual-only
+  // split, or Sq == 0 with no quantized cache at all) requests them through
+  // zero-sized resources and reads zeros, and requests no codes (their LDS-DMA
+  // would land in the residual tiles' buffers).
   const uint32_t wkb = (uint32_t)Sq * BITS / 8;    // bytes per key channel row
   const uint32_t mrb = (uint32_t)ngk * 2;          // bytes per key scale/zero row
   // a unit's part of each tensor: unit bytes (32-bit) times the unit index
@@ -978,6 +975,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   rs.vq = buf_rsrc(at(a.vq, vq_u), quant ? vq_u : 0u);
   rs.vs = quant ? at(a.vs, vm_u) : reinterpret_cast<const char*>(qrow0);
   rs.vz = quant ? at(a.vm, vm_u) : reinterpret_cast<const char*>(qrow0);
+  // the code resources again, in scalar registers for the LDS-DMA requests
+  const __amdgpu_buffer_rsrc_t rkq = buf_rsrc_uniform(at(a.kq, kq_u), quant ? kq_u : 0u);
+  const __amdgpu_buffer_rsrc_t rvq = buf_rsrc_uniform(at(a.vq, vq_u), quant ? vq_u : 0u);
 
   // Q as the fp16 B operand (scaled by scale*log2e):
   //   lane holds Q[h = l16][ch = lg*(D/4) + kk*8 + kslot_ch(jj)],
@@ -990,47 +990,55 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
   u32x4 qraw1;
 
   // The chunk is staged in two halves of C::CHUNK/2 tokens, each the
-  // first (ph = 0) or second (ph = 1) tile of every wave.
-  //   keys: channel rows of 16-byte pieces, consecutive threads covering
-  //   consecutive pieces of a row; key scales/zeros two groups per 4-byte word.
+  // first (ph = 0) or second (ph = 1) tile of every wave.  Key codes and
+  // value codes go HBM -> LDS by LDS-DMA (no VGPRs: loads returning into
+  // VGPRs while the waves compute the first half measured ~1.5x slower
+  // tiles); key scales/zeros, two groups per 4-byte word, and value
+  // scales/zeros go through VGPRs into their transposed layouts.
   constexpr int STEP = NW * kKiviTile;
   constexpr int NTW = C::CHUNK / STEP;
   static_assert(NTW == 2, "two halves, one tile per wave each");
   constexpr int NT = NW * 64;
-  constexpr int HP = C::KPIECES / 2;               // key pieces per channel per half
-  constexpr int PERH = D * HP / NT;                // key pieces per thread per half
+  constexpr int NPC = C::NPC;
   constexpr int WRH = C::KMG / 4;                  // meta words per (scale|zero, channel) per half
   constexpr int PERMH = 2 * D * WRH / NT;
-  static_assert(NT % HP == 0 && NT / WRH == 64 && D % 64 == 0, "row blocks of the staging loops");
-  const int pieces = quant ? (t_end - t_begin) * BITS / 128 : 1;
+  static_assert(NT / WRH == 64 && D % 64 == 0, "row blocks of the staging loops");
   const int nwr = quant ? ngs >> 1 : 1;
-  // per-thread parts of the offsets: thread t takes piece t % HP of key
-  // channel row t / HP (+ NT / HP rows per step i) and word t % WRH of meta
+  // per-thread parts of the offsets: key LDS-DMA request j of wave w covers
+  // rows blk * KROWS_DMA + lane / NPC (blk = w * KDMA + j), slot lane % NPC
+  // <- the piece kslot_swz maps there; thread t takes word t % WRH of meta
   // row t / WRH (+ 64 rows per step, scales then zeros)
   const int tid = threadIdx.x;
-  const uint32_t krow = (uint32_t)(tid / HP) * wkb, kpc = tid % HP;
   const uint32_t mrow = (uint32_t)(tid / WRH) * mrb, mwd = tid % WRH;
-  const uint32_t ksplit = (uint32_t)t_begin * BITS / 8, msplit = (uint32_t)g_lo * 2;
+  const uint32_t msplit = (uint32_t)g_lo * 2;
   const int tw = t_begin + w * kKiviTile;
-  u32x4 kv[NTW][PERH];
   uint32_t mv[NTW][PERMH];
-  KiviRegs<D, BITS> rg[NTW];
-  // A half's requests: this wave's value tile first, then the workgroup's key
-  // codes and scales/zeros, so that the value tile has arrived by the time
-  // the barrier after the key staging lets the wave go on to its tile.
+  VMetaReg<D> vm[NTW];
+  // A half's requests: the wave's value codes and its share of the key codes
+  // (LDS-DMA), then the key and value scales/zeros (VGPRs).  Every offset of
+  // a code request is in the VGPR offset, which the range check covers.
   auto issue = [&](auto phc) {
     constexpr int ph = decltype(phc)::value;
     const int t = tw + ph * STEP;
-    kivi_issue<D, BITS>(rs, quant, t < t_end ? t : t_begin, lane, rg[ph]);
-    __builtin_amdgcn_sched_barrier(0);
-    const int ko = krow + min(ph * HP + (int)kpc, pieces - 1) * 16;
-    // non-temporal when a half's pieces of a channel row fill whole 128-byte
-    // lines (else the other half of each line is fetched again later)
-    constexpr int KPOL = HP * 16 >= 128 ? kNonTemporal : 0;
+    const int tv = t < t_end ? t : t_begin;
+    if (quant) {
 #pragma unroll
-    for (int i = 0; i < PERH; ++i)
-      kv[ph][i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kq, ko, (int)(ksplit + i * (NT / HP) * wkb), KPOL));
+      for (int i = 0; i < C::VDMA; ++i)
+        lds_dma16<true>(rvq, vst + ph * C::VBYTES + i * 1024, (uint32_t)(tv * C::VROW + i * 1024 + lane * 16));
+      // non-temporal when a half's pieces of a channel row fill whole 128-byte
+      // lines (else the other half of each line is fetched again later)
+      constexpr bool KNT = C::KROW >= 128;
+      const uint32_t kh = (uint32_t)(t_begin + ph * STEP) * BITS / 8;
+#pragma unroll
+      for (int j = 0; j < C::KDMA; ++j) {
+        const int blk = w * C::KDMA + j;
+        const int row = blk * C::KROWS_DMA + lane / NPC;
+        const uint32_t off = (uint32_t)row * wkb + (uint32_t)(kslot_swz<NPC>(lane % NPC, row) << 4) + kh;
+        lds_dma16<KNT>(rkq, kchunk + ph * C::KHALF + blk * 1024, off);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    vm[ph] = kivi_load_vmeta<D>(rs, quant, tv, lane);
     const int mo = mrow + min(ph * WRH + (int)mwd, nwr - 1) * 4;
 #pragma unroll
     for (int i = 0; i < PERMH; ++i) {
@@ -1063,21 +1071,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
 
     _Float16* km_lds = reinterpret_cast<_Float16*>(kmeta);
     // value zero term: row g = value group, column = head; rows >= NGV: the
-    // denominators (from this wave's ones rows, published by the first barrier)
+    // denominators
     f32x4 zv = {0.f, 0.f, 0.f, 0.f}, negm = {0.f, 0.f, 0.f, 0.f};
-    reinterpret_cast<uint16_t*>(vml + C::VMBYTES)[lane] = 0x3C00u;
 #pragma unroll
     for (int ph = 0; ph < NTW; ++ph) {
-      // this half's key codes and scales/zeros into LDS, stored unconditionally
-      // (pieces and groups past the chunk end hold clamped copies no tile
-      // reads): a store under a lane mask lets the compiler sink the load
-      // feeding it down to the store, behind waits for every earlier load
-#pragma unroll
-      for (int i = 0; i < PERH; ++i) {
-        const int pc = threadIdx.x + NT * i;
-        const int ch = pc / HP, q = pc - (pc / HP) * HP;
-        *reinterpret_cast<u32x4*>(kchunk + ph * C::KHALF + ch * C::KCROW + q * 16) = kv[ph][i];
-      }
+      // every request of this half (and, at ph 0, Q) done: the LDS-DMA data
+      // is in LDS once its request has counted down
+      __builtin_amdgcn_s_waitcnt(0x0F70);         // vmcnt(0)
+      // this half's key scales/zeros into LDS, stored unconditionally (groups
+      // past the chunk end hold clamped copies no tile reads): a store under
+      // a lane mask lets the compiler sink the load feeding it down to the
+      // store, behind waits for every earlier load
 #pragma unroll
       for (int i = 0; i < PERMH; ++i) {
         const int pc = threadIdx.x + NT * i;
@@ -1092,9 +1096,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
       // halves, and the second half streams in while the first tiles run.
       // One workgroup per CU (NW = 8): once the whole workgroup's first half
       // has arrived (measured faster there); several rounds of 4-wave
-      // workgroups: by each wave once its own share has arrived (the stores
-      // above waited for it; the barrier then orders LDS only, so those
-      // requests stay in flight), which keeps more bytes in flight.
+      // workgroups: by each wave once its own share has arrived (the wait
+      // above; the barrier then orders LDS only, so those requests stay in
+      // flight), which keeps more bytes in flight.
       constexpr bool kWaveIssue = NW == 4;
       if (kWaveIssue && ph == 0) issue(std::integral_constant<int, 1>());
       if (kWaveIssue) lds_barrier();
@@ -1107,13 +1111,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void kivi_decode_kernel(KiviArgs a
       if (!kWaveIssue && ph == 0) issue(std::integral_constant<int, 1>());
       const int t = tw + ph * STEP;
       wave_lds_sync();
-      kivi_stage<D, BITS>(lane, rg[ph], vst, vml);
+      kivi_stage_vmeta<D, BITS>(lane, vm[ph], vml);
       if (ph == 1 && rtile) issue_resid();        // arrives during the last tiles
       wave_lds_sync();
       if (t < t_end) {
-        const int off = t - t_begin;
-        kivi_tile<D, BITS, NW>((t >> 5) - g_lo, lane, qh, kchunk + ph * C::KHALF + (off - ph * STEP) * BITS / 8, vst, vml,
-                               kmeta, m_run, negm, acc, zv);
+        // the wave's tile is piece w (2-bit) or pieces 2w, 2w + 1 (4-bit) of
+        // each key channel row of the half
+        const char* krow0 = kchunk + ph * C::KHALF + l16 * C::KROW;
+        const char* const kb[2] = {
+            BITS == 2 ? krow0 + (kslot_swz<NPC>(w, l16) << 4) : krow0 + (kslot_swz<NPC>(2 * w, l16) << 4),
+            BITS == 2 ? krow0 + (kslot_swz<NPC>(w, l16) << 4) + 8 : krow0 + (kslot_swz<NPC>(2 * w + 1, l16) << 4)};
+        kivi_tile_at<D, BITS, C::KROW, C::KMP>(lane, qh, kb, kmeta, C::KMG * C::KMP * 2, (t >> 5) - g_lo,
+                                               vst + ph * C::VBYTES, vml, m_run, negm, acc, zv);
       }
     }
     kivi_finish<D>(lane, zv, acc, l_run);
@@ -1221,121 +1230,9 @@ struct PipeCfg {
   static_assert(2 * STAGE <= 160 * 1024 / WG_PER_CU, "WG_PER_CU workgroups per CU");
 };
 
-// Slot of 16-byte key piece p in staged key channel row r: the 16 rows a
-// transposed read touches (r = 16k .. 16k + 15) then sit in distinct banks
-// (rows 64 bytes apart for 2-bit caches, 128 for 4-bit, 256-byte bank cycle).
-template <int BITS>
-__device__ __forceinline__ int pipe_kslot(int p, int r) {
-  return BITS == 2 ? p ^ ((r >> 2) & 3) : p ^ ((r >> 1) & 7);
-}
-
-// One 64-token tile from staged operands, the arithmetic of kivi_tile:
-// kb[sg] is this lane's byte of key channel row l16 for the tile's tokens
-// [32sg, 32sg + 32) (rows KPR bytes apart; 8 bytes for 2-bit caches, 16 - two
-// 16-token blocks of 8 - for 4-bit), kms the staged key scales ([group][KMP]
-// fp16, k-slot channel order) with the zeros kzo bytes on and grp0 the tile's
-// first group there, vst / vml the tile's value codes and value scales/zeros
-// (vmeta_slot layout).  The value zero-term MFMA's rows past the value groups
-// are ones (the softmax denominators).
-template <int D, int BITS, int KPR, int KMP>
-__device__ __forceinline__ void kivi_tile_at(int lane, const f16x8 (&qh)[D / 32], const char* const (&kb)[2],
-                                             const char* kms, int kzo, int grp0, const char* vst, const char* vml,
-                                             float& m_run, f32x4& negm, f32x4 (&acc)[D / 16], f32x4& zv) {
-  constexpr int KK = D / 32, NGV = D / 32, VROW = D * BITS / 8;
-  const int l16 = lane & 15, lg = lane >> 4;
-
-  // 2-bit: sc[sg*2 + p][i] is tile token 32sg + 8lg + 2i + p
-  // 4-bit: sc[tb][i]       is tile token 16tb + 4lg + i
-  f32x4 sc[4];
-#pragma unroll
-  for (int sg = 0; sg < 2; ++sg) {
-    const int grp = grp0 + sg;
-    f16x8 qs[KK];
-    f32x4 z = negm;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const int off = (grp * KMP + lg * (D / 4) + kk * 8) * 2;
-      const u32x4 ks = *reinterpret_cast<const u32x4*>(kms + off);
-      const u32x4 kz = *reinterpret_cast<const u32x4*>(kms + kzo + off);
-      qs[kk] = scale8(qh[kk], ks);
-      z = mfma_f16(__builtin_bit_cast(f16x8, kz), qh[kk], z);
-    }
-    sc[sg * 2 + 0] = z;
-    sc[sg * 2 + 1] = z;
-#pragma unroll
-    for (int bb = 0; bb < (BITS == 2 ? 1 : 2); ++bb)
-#pragma unroll
-      for (int rd = 0; rd < KK / 2; ++rd) {
-        const u32x2 x = tr4(kb[sg] + (lg * (D / 4) + rd * 16) * KPR + bb * 8);
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int kk = rd * 2 + half;
-          if (BITS == 2) {
-            const uint32_t e = x[half] & 0x33333333u, od = (x[half] >> 2) & 0x33333333u;
-            sc[sg * 2 + 0] = mfma_f16(codes_fp4(e), qs[kk], sc[sg * 2 + 0]);
-            sc[sg * 2 + 1] = mfma_f16(codes_fp4(od), qs[kk], sc[sg * 2 + 1]);
-          } else {
-            const uint32_t lo = x[half] & 0x0F0F0F0Fu, hi = (x[half] >> 4) & 0x0F0F0F0Fu;
-            sc[sg * 2 + bb] = mfma_f16(codes_fp8(lo, hi), qs[kk], sc[sg * 2 + bb]);
-          }
-        }
-      }
-  }
-
-  float p[16];
-  kivi_softmax<D>(sc, m_run, negm, acc, zv, p);
-  // P^T as the B operand, k-slot jj of sub-tile sg (the orders of kivi_tile)
-  f16x8 pb[2];
-#pragma unroll
-  for (int sg = 0; sg < 2; ++sg)
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      pb[sg][jj] = (_Float16)p[BITS == 2 ? (sg * 2 + (jj & 1)) * 4 + (jj >> 1) : (2 * sg + (jj >> 2)) * 4 + (jj & 3)];
-
-  constexpr uint32_t kOnes = 0x3C003C00u;
-#pragma unroll
-  for (int sg = 0; sg < 2; ++sg) {
-    f16x8 pg[NGV];
-#pragma unroll
-    for (int g = 0; g < NGV; ++g)
-      pg[g] = scale8(pb[sg], *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(0, g, sg * 32) * 2 + lg * 16));
-    {
-      u32x4 vz = *reinterpret_cast<const u32x4*>(vml + vmeta_slot<D, BITS>(1, min(l16, NGV - 1), sg * 32) * 2 + lg * 16);
-      if (l16 >= NGV) vz = u32x4{kOnes, kOnes, kOnes, kOnes};
-      zv = mfma_f16(__builtin_bit_cast(f16x8, vz), pb[sg], zv);
-    }
-    if (BITS == 2) {
-#pragma unroll
-      for (int rd = 0; rd < D / 64; ++rd) {
-        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
-        const int tok = 32 * sg + 8 * lg + r;
-        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
-        const int ca = 2 * rd, cbb = 2 * rd + 1;
-        const uint32_t e0 = x[0] & 0x33333333u, e1 = x[1] & 0x33333333u;
-        const uint32_t o0 = (x[0] >> 2) & 0x33333333u, o1 = (x[1] >> 2) & 0x33333333u;
-        acc[ca * 2 + 0] = mfma_f16(codes_fp4(e0), pg[ca], acc[ca * 2 + 0]);
-        acc[cbb * 2 + 0] = mfma_f16(codes_fp4(e1), pg[cbb], acc[cbb * 2 + 0]);
-        acc[ca * 2 + 1] = mfma_f16(codes_fp4(o0), pg[ca], acc[ca * 2 + 1]);
-        acc[cbb * 2 + 1] = mfma_f16(codes_fp4(o1), pg[cbb], acc[cbb * 2 + 1]);
-      }
-    } else {
-#pragma unroll
-      for (int rd = 0; rd < D / 32; ++rd) {
-        const int r = l16 & 7, cbr = 2 * rd + (l16 >> 3);
-        const int tok = (r & 1) ? 32 * sg + 16 + 4 * lg + (r >> 1) : 32 * sg + 4 * lg + (r >> 1);
-        const u32x2 x = tr4(vst + tok * VROW + cbr * 8);
-        const uint32_t lo0 = x[0] & 0x0F0F0F0Fu, hi0 = (x[0] >> 4) & 0x0F0F0F0Fu;
-        const uint32_t lo1 = x[1] & 0x0F0F0F0Fu, hi1 = (x[1] >> 4) & 0x0F0F0F0Fu;
-        acc[2 * rd] = mfma_f16(codes_fp8(lo0, hi0), pg[rd], acc[2 * rd]);
-        acc[2 * rd + 1] = mfma_f16(codes_fp8(lo1, hi1), pg[rd], acc[2 * rd + 1]);
-      }
-    }
-  }
-}
-
 // Wave w's tile of the granule staged in `stage` (pipelined kernel): key
 // channel row r holds the granule's NPC 16-byte pieces (piece p = tokens
-// [256p/NPC, 256(p+1)/NPC)) in slots pipe_kslot(p, r); the tile's tokens are
+// [256p/NPC, 256(p+1)/NPC)) in slots kslot_swz<NPC>(p, r); the tile's tokens are
 // piece w (2-bit) or pieces 2w, 2w + 1 (4-bit), and for the rows a lane reads
 // (l16 + 16k) the slot depends on l16 only.  Every read stays in `stage`.
 template <int D, int BITS>
@@ -1345,8 +1242,8 @@ __device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh
   const int l16 = lane & 15;
   const char* row = stage + l16 * C::KPR;
   const char* const kb[2] = {
-      BITS == 2 ? row + (pipe_kslot<BITS>(w, l16) << 4) : row + (pipe_kslot<BITS>(2 * w, l16) << 4),
-      BITS == 2 ? row + (pipe_kslot<BITS>(w, l16) << 4) + 8 : row + (pipe_kslot<BITS>(2 * w + 1, l16) << 4)};
+      BITS == 2 ? row + (kslot_swz<C::NPC>(w, l16) << 4) : row + (kslot_swz<C::NPC>(2 * w, l16) << 4),
+      BITS == 2 ? row + (kslot_swz<C::NPC>(w, l16) << 4) + 8 : row + (kslot_swz<C::NPC>(2 * w + 1, l16) << 4)};
   kivi_tile_at<D, BITS, C::KPR, C::KMP>(lane, qh, kb, stage + C::OFF_KM, C::NGG * C::KMP * 2, 2 * w,
                                         stage + C::OFF_V + w * C::VB, stage + C::OFF_VM + w * C::VMB, m_run, negm,
                                         acc, zv);
@@ -1427,13 +1324,13 @@ __global__ __launch_bounds__(kPipeWaves * 64, pipe_wg_per_cu<BITS>()) void kivi_
   const __amdgpu_buffer_rsrc_t rkq = buf_rsrc(reinterpret_cast<const char*>(a.kq) + (uint64_t)bh * kq_u, kq_u);
   const __amdgpu_buffer_rsrc_t rvq = buf_rsrc(reinterpret_cast<const char*>(a.vq) + (uint64_t)bh * vq_u, vq_u);
   // key LDS-DMA: instruction blk covers key rows blk*KROWS_DMA + lane/NPC,
-  // slot lane % NPC <- the piece pipe_kslot maps there (an involution), which
+  // slot lane % NPC <- the piece kslot_swz maps there (an involution), which
   // depends on blk only through its parity (4-bit caches)
   uint32_t kvoff[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
     const int row = par * C::KROWS_DMA + lane / C::NPC;
-    kvoff[par] = (uint32_t)(lane / C::NPC) * wkb + (uint32_t)(pipe_kslot<BITS>(lane % C::NPC, row) << 4);
+    kvoff[par] = (uint32_t)(lane / C::NPC) * wkb + (uint32_t)(kslot_swz<C::NPC>(lane % C::NPC, row) << 4);
   }
   // key scales/zeros: rows 0..D-1 scales, D..2D-1 zeros of channels 0..D-1;
   // thread t reads word t % 4 of the granule's 16 bytes of rows 64i + t / 4,

@@ -94,6 +94,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// The same over a base and size the caller knows to be wave-uniform, built
+// from their first lane's values so that the resource sits in scalar
+// registers (an LDS-DMA request in inline assembly takes it there).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_uniform(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p), hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return buf_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
+
 __device__ __forceinline__ void store_out(const SplitKOut& o, int b, int hq, int d, float v) {
   int64_t off = (int64_t)b * o.o_sb + (int64_t)hq * o.o_sh + d;
   if (o.out_dtype == kOutBF16) {
