@@ -969,13 +969,14 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_wave_kernel(PqArgs a) {
   const int n = max(0, min(a.chunk, a.S - t_begin));
   const int tw = 64 * w;
 
-  // Requests, oldest first: the key codebook (LDS-DMA), the q rows and codes,
-  // the value codebook (VGPRs, stored to LDS after the scores).  The scores
-  // need all but the value codebook, which arrives while they are computed;
-  // the compiler, which does not see the LDS-DMA requests, counts every
-  // later request exactly.  Codebook row s = (j, c) of 256 per subspace sits
-  // at s * 16 in LDS (codewords past K repeat codeword K - 1; no code reads
-  // them).
+  // Requests, oldest first: the key codebook (LDS-DMA), the q rows and codes
+  // (VGPRs), the value codebook (LDS-DMA into its own region).  The scores
+  // need all but the value codebook, which arrives while they are computed
+  // (into LDS: returns into VGPRs measured to slow the tiles they overlap);
+  // the compiler, which does not see the LDS-DMA requests, counts the later
+  // requests short and so waits at most longer than needed.  Codebook row
+  // s = (j, c) of 256 per subspace sits at s * 16 in LDS (codewords past K
+  // repeat codeword K - 1; no code reads them).
   const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.kcb + (int64_t)hk * a.kcb_sh, (uint32_t)(M * K * 16));
   auto cb_off = [&](int i) {
     const int sl = tid + kPqgThreads * i;
@@ -1005,11 +1006,11 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_wave_kernel(PqArgs a) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
       vcw[k][hf] = ld_codes<M>(vb + crow(tw + 32 * k + 16 * hf + 4 * lg + (l16 >> 2)) * a.vi_ss);
-  u32x4 vraw[C::CPT];
+  __builtin_amdgcn_sched_barrier(0);
   {
-    const char* vcg = reinterpret_cast<const char*>(a.vcb + (int64_t)hk * a.vcb_sh);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc_uniform(a.vcb + (int64_t)hk * a.vcb_sh, (uint32_t)(M * K * 16));
 #pragma unroll
-    for (int i = 0; i < C::CPT; ++i) vraw[i] = ld16(vcg + cb_off(i));
+    for (int i = 0; i < C::CPT; ++i) lds_dma16<false>(rv, vcbl + (kPqgThreads * i + 64 * w) * 16, cb_off(i));
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -1096,9 +1097,8 @@ __global__ __launch_bounds__(kPqgThreads, 1) void pq_wave_kernel(PqArgs a) {
       ph[bi >> 1][(bi & 1) * 4 + i] = (_Float16)p;
     }
 
-  // ---- the value codebook into LDS; publish it ----
-#pragma unroll
-  for (int i = 0; i < C::CPT; ++i) *reinterpret_cast<u32x4*>(vcbl + (tid + kPqgThreads * i) * 16) = vraw[i];
+  // ---- the value codebook in LDS (its requests done); publish it ----
+  __builtin_amdgcn_s_waitcnt(0x0F70);               // vmcnt(0)
   lds_barrier();
 
   // ---- PV: O^T[d][h] += V^T[d][t] P^T[t][h] over the wave's two 32-token
