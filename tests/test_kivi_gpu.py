@@ -75,6 +75,8 @@ def _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=0, chunk=0):
     (2, 8, 2, 128, 256 + 384, 384),     # more residual than four 128-token pieces hold: own splits
     (1, 7, 1, 128, 2080 + 128, 128),    # Sq = 2080, an odd number of key groups: the streaming kernel
     (2, 4, 4, 64, 1056 + 32, 32),       # the same at D = 64, G = 1
+    (8, 8, 8, 64, 2048 + 32, 32),       # 64 units x two 1024-token chunks: eight-wave workgroups at D = 64
+    (4, 28, 4, 128, 2048 + 96, 96),     # 16 units, four-wave workgroups over a short cache, ragged residual
 ])
 def test_decode_small(dev, bits, B, Hq, Hk, D, L, Rw):
     _decode_case(dev, bits, B, Hq, Hk, D, L, Rw, seed=L + bits)
