@@ -157,9 +157,9 @@ struct KiviCfg {
   static constexpr int KMG = CHUNK / 32;                   // key groups per chunk
   // staged key scales + zeros, one row of KMP fp16 per (scale|zero, group): the
   // 8-halfword pad puts the staging stores of a wave's eight groups in
-  // distinct banks (4-bit caches go without it, to fit two 4-wave workgroups
-  // per CU)
-  static constexpr int KMP = BITS == 2 ? D + 8 : D;
+  // distinct banks (4-bit caches on 4-wave workgroups go without it, to fit
+  // two workgroups per CU)
+  static constexpr int KMP = (BITS == 4 && NW == 4) ? D : D + 8;
   static constexpr int KMETA = 2 * KMG * KMP * 2;
   static constexpr int VROW = D * BITS / 8;                // LDS bytes of one token's value codes
   static constexpr int VBYTES = kKiviTile * VROW;
