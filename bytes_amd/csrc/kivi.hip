@@ -15,19 +15,27 @@
 //          groups of 32 channels)
 //   residual K_res/V_res bf16 [B,Hk,R,D]
 //
-// Decode data path, per wave and 64-token tile (waves take interleaved tiles):
-//  * packed key and value words go HBM -> LDS untouched (global_load_lds_dwordx4);
-//  * ds_read_b64_tr_b4 transposes them at 4-bit granularity, which turns
-//    "16 tokens of one channel" (keys) / "16 channels of one token" (values)
-//    into the per-lane K-contiguous layout MFMA operands need;
+// Decode data path, per wave and 64-token tile:
+//  * packed key and value words go HBM -> LDS untouched (buffer loads with the
+//    LDS bit, issued from inline assembly with explicit vmcnt waits); key and
+//    value scales/zeros go through VGPRs into transposed LDS layouts;
+//  * ds_read_b64_tr_b4 transposes the packed words at 4-bit granularity, which
+//    turns "16 tokens of one channel" (keys) / "16 channels of one token"
+//    (values) into the per-lane K-contiguous layout MFMA operands need;
 //  * two masks split each nibble into fp4 (2-bit codes, value c/2) or fp8
 //    (4-bit codes, value c*2^-9) operands that v_cvt_scalef32_pk_f16_{fp4,fp8}
-//    turn into exact fp16 codes; one v_pk_fma_f16 applies scale and zero;
+//    turn into exact fp16 codes, which enter the MFMAs unscaled: key scales
+//    multiply Q per 32-token group, value scales multiply P per 32-channel
+//    group, and both zero terms are MFMA chains of their own;
 //  * S^T = K_dq Q^T and O^T += V_dq^T P^T run on v_mfma_f32_16x16x32_f16 with
-//    fp32 accumulation and an fp32 online softmax.
-// The bf16 residual window runs with the dense tile loop, as one extra split
-// per unit when the grid stays resident (its 2*R*D*2 bytes then do not
-// lengthen a quantized split), else ahead of the last split's chunk.
+//    fp32 accumulation and an fp32 online softmax (kivi_tile_at).
+// Three kernels share that tile: the two-half kernel (a workgroup stages its
+// chunk in two halves, one tile per wave each), the pipelined kernel for long
+// caches (runs of 256-token granules through a two-stage LDS ring) and the
+// streaming kernel for caches with an odd number of 32-token key groups
+// (which has a tile of its own, 32-token granular).  The bf16 residual window
+// runs with the dense tile loop, on splits of its own or in pieces on the last
+// splits after their quantized tiles.
 #include "dense_tile.h"
 
 namespace bytes_amd {
