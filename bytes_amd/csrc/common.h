@@ -200,7 +200,9 @@ __device__ __forceinline__ void lds_barrier() {
 // that the compiler does not track it: the compiler cannot tell LDS-DMA
 // destinations apart where a read's offset varies per lane, and would make
 // every LDS read wait for every such load in flight.  The caller waits for
-// these requests itself (vmcnt) before the LDS they fill is read.  M0 holds the LDS base; one wait state before the load uses it.
+// these requests itself (vmcnt) before the LDS they fill is read.  lds is
+// wave-uniform (its first lane's value is used) and goes to M0; one wait state
+// before the load uses it.  r must be wave-uniform too (scalar registers).
 template <bool NT>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const char* lds, uint32_t voff) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds);
