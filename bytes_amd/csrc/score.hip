@@ -57,7 +57,7 @@ struct ScoreArgs {
 };
 
 constexpr int kScoreWaves = 4;
-constexpr int kStoreBatch = 4;   // wave iterations whose group sums are stored together
+constexpr int kStoreBatch = 4;   // wave iterations whose group sums are emitted together
 constexpr int kWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): every vector memory request done
 
 // Score stores go through a buffer resource over the unit's output rows
@@ -84,13 +84,46 @@ __device__ __forceinline__ void score_emit_sum(const ScoreArgs& a, float tot, in
 }
 
 // Group-summed scores of 64 consecutive tokens, one per lane (lane l holds
-// token tok = t + l): one store instruction of whole lines.  (Stores of 16
-// lanes per column tile cost ~15% of the score pass's time at C5.)
-__device__ __forceinline__ void score_emit_sum64(const ScoreArgs& a, float tot, int tok, int b, int hk,
+// token tok = t + l), into the workgroup's LDS score buffer (which starts at
+// token tb) and its histogram.
+__device__ __forceinline__ void score_emit_sum64(const ScoreArgs& a, float tot, int tok, int tb, float* sbuf,
                                                  uint32_t* hlds) {
-  const bool ok = tok < a.S;
-  score_store(a, b, hk, 1, 0, tok, ok, tot);
-  if (hlds && ok) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
+  if (tok < a.S) {
+    sbuf[tok - tb] = tot;
+    if (hlds) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
+  }
+}
+
+// Tokens of group sums one workgroup's LDS score buffer holds: what is left of
+// a CU's 160 KB beside the key-row reservation and the 2048-bin histogram, in
+// whole 256-token steps, at most 8192 (the host's largest workgroup range).
+constexpr int score_sum_buf_tokens(int reserve) {
+  const int t = (160 * 1024 - reserve - 2048 * 4) / 4 / 256 * 256;
+  return t < 8192 ? t : 8192;
+}
+
+// The buffer's first n group sums (tokens tb .. tb+n-1 of the unit's output
+// row) leave in one burst of non-temporal stores, 16 bytes per lane where the
+// row is 16-byte aligned.  Sums go to LDS during the loop and to memory only
+// here because a store issued between two batches of key loads holds up
+// every later wait for key rows until it is acknowledged (the memory counter
+// completes in order): stored from the loop, even four iterations' sums
+// together, they cost 3.4% of the C5 score pass (339 against 327 us).
+__device__ __forceinline__ void score_flush_sums(const ScoreArgs& a, int b, int hk, int tb, int n, const float* sbuf,
+                                                 int nthreads) {
+  float* row = a.out + (int64_t)b * a.o_sb + (int64_t)hk * a.o_sh;
+  const auto rs = buf_rsrc(row, (uint32_t)a.S * 4u);
+  const bool vec = (reinterpret_cast<uintptr_t>(row + tb) & 15) == 0;
+  for (int i = threadIdx.x * 4; i < n; i += nthreads * 4) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(sbuf + i);
+    if (vec && i + 4 <= n) {
+      __builtin_amdgcn_raw_buffer_store_b128(v, rs, (tb + i) * 4, 0, kNonTemporal);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + e < n) __builtin_amdgcn_raw_buffer_store_b32(v[e], rs, (tb + i + e) * 4, 0, kNonTemporal);
+    }
+  }
 }
 
 // ---- bf16 / fp8 keys ------------------------------------------------------
@@ -115,6 +148,9 @@ struct DenseKeys {
   // leaves room for only one.  Narrower rows keep two (128 KB in flight).
   static constexpr int kLdsReserve = D * ES >= 256 ? 2 * kLds : kLds;
   static_assert(kLdsReserve + 2048 * 4 <= 160 * 1024, "the reservation and the histogram fit a CU's LDS");
+  // group sums: tokens of the LDS score buffer (the host keeps a workgroup's range within it)
+  static constexpr int kSumBuf = GS ? score_sum_buf_tokens(kLdsReserve) : 4;
+  static_assert(!GS || kSumBuf >= 1024, "room for a useful workgroup range");
   struct Regs {
     u32x4 k[CPR];            // chunk lane + 64 i: row (lane + 64 i) / CPR, chunk (lane + 64 i) % CPR
   };
@@ -241,6 +277,7 @@ struct PackedKeys {
   static constexpr int kLds = 16;              // operands come straight from registers
   static constexpr int kLdsReserve = kLds;
   static constexpr bool kDeferStore = false;   // scores are stored by tile()
+  static constexpr int kSumBuf = 4;            // (unused)
   char* kst;
   // Buffer resources over one KV head's codes and scale/min rows: every load
   // is a 32-bit lane offset plus a uniform row offset, and rows at or past S
@@ -497,6 +534,7 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   const int t_end = min(t_begin + a.tok_per_wg, a.S);
   constexpr int STEP = kScoreWaves * 16 * P::CT;
   __shared__ uint32_t hlds_mem[2048];
+  __shared__ __attribute__((aligned(16))) float sbuf[P::kSumBuf];
   uint32_t* hlds = nullptr;
   if (a.hist) {
     for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64) hlds_mem[i] = 0u;
@@ -516,10 +554,8 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     typename P::Regs r0, r1;
     pol.issue(a, t, t_end, lane, r0);
     if constexpr (P::kDeferStore) {
-      // Group sums of kStoreBatch iterations are stored together: each store
-      // sits in the in-order memory counter between two batches of key
-      // loads, so one store per iteration would hold up every wait for the
-      // next rows until the write is acknowledged.
+      // Group sums go to the LDS score buffer, kStoreBatch iterations' worth
+      // together, and to memory after the loop (score_flush_sums).
       static_assert(kStoreBatch % 2 == 0, "the register sets alternate within a batch");
       // one iteration: the next rows are requested (past the range the
       // resource has zero length, so the last step's requests read nothing
@@ -536,10 +572,9 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
         t += STEP;
         return more;
       };
-      // Each exit waits for its last (empty) requests in a block of its own:
-      // the compiler's wait placement does not tell paths apart, so requests
-      // still in flight where an exit joins the full-batch stores would make
-      // those stores wait for the next batch's rows.
+      // Each exit waits for its last (empty) requests in a block of its own,
+      // so no path reaches the emits with requests of the next batch still
+      // counted.
       while (true) {
         float sc[kStoreBatch];
         const int t0 = t;
@@ -559,12 +594,12 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
         }
         if (n == 0) {
 #pragma unroll
-          for (int j = 0; j < kStoreBatch; ++j) score_emit_sum64(a, sc[j], t0 + j * STEP + lane, b, hk, hlds);
+          for (int j = 0; j < kStoreBatch; ++j) score_emit_sum64(a, sc[j], t0 + j * STEP + lane, t_begin, sbuf, hlds);
           continue;
         }
 #pragma unroll
         for (int j = 0; j < kStoreBatch; ++j)
-          if (j < n) score_emit_sum64(a, sc[j], t0 + j * STEP + lane, b, hk, hlds);
+          if (j < n) score_emit_sum64(a, sc[j], t0 + j * STEP + lane, t_begin, sbuf, hlds);
         break;
       }
     } else while (true) {
@@ -581,6 +616,10 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
       t += STEP;
       if (!more0) break;
     }
+  }
+  if constexpr (P::kDeferStore) {
+    __syncthreads();
+    score_flush_sums(a, b, hk, t_begin, t_end - t_begin, sbuf, kScoreWaves * 64);
   }
   if (a.hist) {
     __syncthreads();
@@ -683,7 +722,15 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   long per = ((long)S * units + target - 1) / target;
   per = (per + step - 1) / step * step;
   if (per < step) per = step;
-  if (per > 8192) per = 8192;
+  // group sums of dense keys: a workgroup's range fits its LDS score buffer
+  long cap = 8192;
+  if (a.group_sum && !packed) {
+    if (D == 128)
+      cap = k_mode == kKeyBf16 ? DenseKeys<128, false, true>::kSumBuf : DenseKeys<128, true, true>::kSumBuf;
+    else
+      cap = k_mode == kKeyBf16 ? DenseKeys<64, false, true>::kSumBuf : DenseKeys<64, true, true>::kSumBuf;
+  }
+  if (per > cap) per = cap;
   a.tok_per_wg = (int)per;
   a.parts = (int)((S + per - 1) / per);
   const long grid = units * a.parts;
