@@ -76,13 +76,6 @@ __device__ __forceinline__ void score_store(const ScoreArgs& a, int b, int row0,
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), buf_rsrc(base, span), (int)off, 0, kNonTemporal);
 }
 
-__device__ __forceinline__ void score_emit_sum(const ScoreArgs& a, float tot, int tok, int b, int hk, int lg,
-                                               uint32_t* hlds) {
-  const bool ok = lg == 0 && tok < a.S;
-  score_store(a, b, hk, 1, 0, tok, ok, tot);
-  if (hlds && ok) atomicAdd(&hlds[score_order_key(tot) >> 21], 1u);
-}
-
 // Group-summed scores of 64 consecutive tokens, one per lane (lane l holds
 // token tok = t + l), into the workgroup's LDS score buffer (which starts at
 // token tb) and its histogram.
@@ -276,13 +269,18 @@ struct PackedKeys {
   };
   static constexpr int kLds = 16;              // operands come straight from registers
   static constexpr int kLdsReserve = kLds;
-  static constexpr bool kDeferStore = false;   // scores are stored by tile()
-  static constexpr int kSumBuf = 4;            // (unused)
+  // group sums are returned by tile() (token t + lane per lane) and collected
+  // by the driver; per-head scores are stored by tile()
+  static constexpr bool kDeferStore = GS;
+  static constexpr int kSumBuf = GS ? score_sum_buf_tokens(kLdsReserve + kScoreWaves * 64 * NG * 4) : 4;
   char* kst;
-  // Buffer resources over one KV head's codes and scale/min rows: every load
-  // is a 32-bit lane offset plus a uniform row offset, and rows at or past S
-  // read as zero (their scores are not stored).
-  __amdgpu_buffer_rsrc_t rk, rsc, rmn;
+  // One KV head's codes and scale/min rows, addressed through buffer
+  // resources: every load is a 32-bit lane offset plus a uniform row offset,
+  // and rows at or past S read as zero (their scores are not stored); an
+  // issue at or past its range limit reads nothing.
+  const uint8_t* kb;
+  const uint16_t *scb, *mnb;
+  uint32_t kspan, mspan;
   uint32_t koff;                               // lane part of the code offsets (bytes)
   uint32_t k_row, m_row;                       // row strides (bytes)
   bf16x8 qa[NB][NG];                           // [row block][k-step]
@@ -303,11 +301,11 @@ struct PackedKeys {
     const int grp = lg * NG / 4;
     k_row = (uint32_t)a.k_ss;
     m_row = (uint32_t)a.m_ss * 2;
-    const uint32_t kspan = (uint32_t)((a.S - 1) * a.k_ss + LB * 4);
-    const uint32_t mspan = (uint32_t)(((a.S - 1) * a.m_ss + NG) * 2);
-    rk = buf_rsrc(static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh, kspan);
-    rsc = buf_rsrc(a.ksc + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh, mspan);
-    rmn = buf_rsrc(a.kmn + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh, mspan);
+    kspan = (uint32_t)((a.S - 1) * a.k_ss + LB * 4);
+    mspan = (uint32_t)(((a.S - 1) * a.m_ss + NG) * 2);
+    kb = static_cast<const uint8_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    scb = a.ksc + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh;
+    mnb = a.kmn + (int64_t)b * a.m_sb + (int64_t)hk * a.m_sh;
     koff = (uint32_t)l16 * k_row + lg * LB;
     const bool in_group = (l16 / R) == grp;
     const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + lg * (D / 4);
@@ -365,8 +363,12 @@ struct PackedKeys {
     }
   }
 
-  // (lim is not used: the resources end at S)
+  // rows t .. t+63; t and lim are wave-uniform, and t >= lim reads nothing
   __device__ __forceinline__ void issue(const ScoreArgs& a, int t, int lim, int lane, Regs& r) const {
+    const bool live = t < lim;
+    const auto rk = buf_rsrc(kb, live ? kspan : 0u);
+    const auto rsc = buf_rsrc(scb, live ? mspan : 0u);
+    const auto rmn = buf_rsrc(mnb, live ? mspan : 0u);
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
       const uint32_t row = (uint32_t)(t + c * 16);                  // wave-uniform
@@ -424,9 +426,10 @@ struct PackedKeys {
     }
   }
 
-  __device__ __forceinline__ void tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
-                                       int nh, uint32_t* hlds) const {
+  __device__ __forceinline__ float tile(const ScoreArgs& a, const Regs& r, int t, int lane, int b, int hk, int hq0,
+                                        int nh, uint32_t* hlds) const {
     const int l16 = lane & 15, lg = lane >> 4;
+    float keep = 0.f;                          // group sum: lane group lg keeps column tile lg's
     // per wave: [token][group] words (bf16 scale low, bf16 min high)
     __shared__ uint32_t sm_lds[kScoreWaves][64 * NG];
     uint32_t* my = sm_lds[threadIdx.x >> 6];
@@ -469,7 +472,7 @@ struct PackedKeys {
         float v = fmaf(sc, g[0] + g[1], mn128 * (qsum[0][0] + qsum[0][1]));
         v += __shfl_xor(v, 16, 64);
         v += __shfl_xor(v, 32, 64);
-        score_emit_sum(a, v * a.scaling, tok, b, hk, lg, hlds);
+        keep = lg == c ? v * a.scaling : keep;
       } else {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -505,6 +508,7 @@ struct PackedKeys {
         }
       }
     }
+    return keep;
   }
 };
 
