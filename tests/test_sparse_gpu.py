@@ -59,6 +59,34 @@ def test_group_scores_long_ragged(dev):
     assert torch.equal(idx.cpu().long(), R.topk_indices(s.cpu(), 1024, sorted_by_score=False))
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_group_scores_full_lds_buffer(dev, fp8):
+    """Rows long enough that, on 256 CUs, each score workgroup's token range
+    is the largest its LDS score buffer holds (6144 tokens with bf16 keys,
+    8192 with fp8), with a ragged end: group sums at the start, across
+    workgroup boundaries and at the end of every row against the oracle on
+    those key slices (fp8 keys widened to bf16, which is exact)."""
+    B, Hq, Hk, D = 1, 24, 8, 128
+    cap = 8192 if fp8 else 6144
+    S = 2048 * cap // Hk + 1001
+    g = torch.Generator(device=dev).manual_seed(11)
+    q = torch.randn(B, Hq, 1, D, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(B, Hk, S, D, device=dev, generator=g, dtype=torch.bfloat16)
+    if fp8:
+        k = k.to(torch.float8_e4m3fn)
+    s = SP.group_scores(q, k, 0.088)
+    assert s.shape == (B, Hk, S)
+    qc = q.cpu()
+    for a, b in ((0, 3000), (cap - 700, cap + 700), (5 * cap - 300, 5 * cap + 300), (S - 4000, S)):
+        ks = k[:, :, a:b].cpu()
+        ref = R.group_scores(qc, ks.to(torch.bfloat16) if fp8 else ks, 0.088)
+        d = (s[:, :, a:b].cpu() - ref).abs().max().item()
+        print(f"tokens {a}..{b}: max-abs {d:.3e}", flush=True)
+        assert d <= SCORE_TOL, (a, b)
+    del k, s
+    torch.cuda.empty_cache()
+
+
 def _tie_heavy(rows, n, seed):
     g = torch.Generator().manual_seed(seed)
     s = torch.randint(-8, 8, (rows, n), generator=g).float() * 0.25      # many exact ties
