@@ -570,7 +570,7 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
         __builtin_amdgcn_sched_barrier(0);
         sc = pol.tile(a, cur, t, lane, b, hk, hq0, nh, hlds);
         // finished here: left alone, the compiler sinks each tile's group sums
-        // down to the stores, past the next batch's loads, and then needs
+        // down to the emits, past the next batch's loads, and then needs
         // registers that those loads are still filling
         asm volatile("" : "+v"(sc));
         t += STEP;
