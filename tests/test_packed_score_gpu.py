@@ -149,3 +149,30 @@ def test_token_topk_packed_score_keys(dev, bits, B, Hq, Hk, S, kb, D):
     gi = ridx.unsqueeze(-1).expand(B, Hk, kb, D)
     _check(out, R.decode_attn(x["q"], torch.gather(x["k"], 2, gi), torch.gather(x["v"], 2, gi), scale=x["scale"]),
            f"token top-k {bits}-bit score keys B{B} S{S} kb{kb} D{D}")
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_packed_group_scores_full_lds_buffer(dev, bits):
+    """Packed selection keys on rows long enough that, on 256 CUs, each score
+    workgroup's token range is the largest the host plans (8192 tokens, the
+    LDS score buffer's capacity), with a ragged end: group sums at the start,
+    across workgroup boundaries and at the end against the oracle on those
+    slices of the dequantized keys."""
+    B, Hq, Hk, D = 1, 24, 8, 128
+    S = 2048 * 8192 // Hk + 777
+    g = torch.Generator(device=dev).manual_seed(13)
+    q = torch.randn(B, Hq, 1, D, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(B, Hk, S, D, device=dev, generator=g, dtype=torch.bfloat16)
+    p, s, z = AK.quantize_and_pack_score_keys(k, bits, 32)
+    del k
+    out = SP._score(q, p, 0.088, group_sum=True, packed=(s, z, bits))
+    assert out.shape == (B, Hk, S)
+    qc = q.cpu()
+    for a, b in ((0, 3000), (8192 - 700, 8192 + 700), (5 * 8192 - 300, 5 * 8192 + 300), (S - 4000, S)):
+        kd = R.score_keys_dequant(p[:, :, a:b].cpu(), s[:, :, a:b].cpu(), z[:, :, a:b].cpu(), bits, 32)
+        d = (out[:, :, a:b].cpu() - R.group_scores(qc, kd, 0.088)).abs().max().item()
+        print(f"{bits}-bit tokens {a}..{b}: max-abs {d:.3e}", flush=True)
+        assert d <= SCORE_TOL, (a, b)
+    del p, s, z, out
+    torch.cuda.empty_cache()
+
