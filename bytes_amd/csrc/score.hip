@@ -60,14 +60,12 @@ constexpr int kScoreWaves = 4;
 constexpr int kStoreBatch = 4;   // wave iterations whose group sums are emitted together
 constexpr int kWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): every vector memory request done
 
-// Score stores go through a buffer resource over the unit's output rows
-// [row0, row0 + rows), and a lane that must not store gets an offset past the
-// resource (the store is dropped).  The store instruction is then issued on
-// every path, with no branch around it, so the waits for the next rows'
-// loads count the same requests in every iteration.  (The host keeps each
-// unit's output span below 2^31 bytes.)  The stores carry the non-temporal
-// hint: the scores are read back only by the next pass, and plain stores
-// interleaved with the streaming key reads cost ~4% of the pass at C5.
+// Per-head scores stored straight from the tile (packed keys, and dense keys
+// with 256-byte rows) go through a buffer resource over the unit's output
+// rows [row0, row0 + rows); a lane that must not store gets an offset past
+// the resource (the store is dropped), so the store instruction is issued on
+// every path.  (An LDS score buffer for packed keys took their workgroups
+// from six to three per CU: int2 keys 75 -> 84 us at B32 H_q64 S16K.)
 __device__ __forceinline__ void score_store(const ScoreArgs& a, int b, int row0, int rows, int r, int tok, bool ok,
                                             float v) {
   float* base = a.out + (int64_t)b * a.o_sb + (int64_t)row0 * a.o_sh;
@@ -95,26 +93,34 @@ constexpr int score_sum_buf_tokens(int reserve) {
   return t < 8192 ? t : 8192;
 }
 
-// The buffer's first n group sums (tokens tb .. tb+n-1 of the unit's output
-// row) leave in one burst of non-temporal stores, 16 bytes per lane where the
-// row is 16-byte aligned.  Sums go to LDS during the loop and to memory only
+// LDS floats of the score buffer of a per-head policy: what is left of the
+// workgroup's LDS budget beside its other LDS (the host keeps nh rows of a
+// workgroup's token range within it).
+constexpr int score_head_buf_floats(int budget, int other) { return (budget - other) / 4; }
+
+// The workgroup's scores leave the LDS score buffer in one burst of
+// non-temporal stores, 16 bytes per lane where a row is 16-byte aligned: rows
+// row0 .. row0+rows-1 of the unit's output (the KV head's group-sum row, or
+// the query heads' rows), buffer row r holding tokens tb .. tb+n-1 at
+// sbuf[r * pitch ..].  Scores go to LDS during the loop and to memory only
 // here because a store issued between two batches of key loads holds up
 // every later wait for key rows until it is acknowledged (the memory counter
-// completes in order): stored from the loop, even four iterations' sums
-// together, they cost 3.4% of the C5 score pass (339 against 327 us).
-__device__ __forceinline__ void score_flush_sums(const ScoreArgs& a, int b, int hk, int tb, int n, const float* sbuf,
-                                                 int nthreads) {
-  float* row = a.out + (int64_t)b * a.o_sb + (int64_t)hk * a.o_sh;
-  const auto rs = buf_rsrc(row, (uint32_t)a.S * 4u);
-  const bool vec = (reinterpret_cast<uintptr_t>(row + tb) & 15) == 0;
-  for (int i = threadIdx.x * 4; i < n; i += nthreads * 4) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(sbuf + i);
-    if (vec && i + 4 <= n) {
-      __builtin_amdgcn_raw_buffer_store_b128(v, rs, (tb + i) * 4, 0, kNonTemporal);
+// completes in order): stored from the loop, even four iterations' group
+// sums together, they cost 3.4% of the C5 score pass (339 against 327 us).
+__device__ __forceinline__ void score_flush(const ScoreArgs& a, int b, int row0, int rows, int tb, int n, int pitch,
+                                            const float* sbuf, int nthreads) {
+  const int per_row = (n + 3) / 4;                 // 4-token pieces per row
+  for (int e = threadIdx.x; e < rows * per_row; e += nthreads) {
+    const int r = e / per_row, i = (e - r * per_row) * 4;
+    float* row = a.out + (int64_t)b * a.o_sb + (int64_t)(row0 + r) * a.o_sh;
+    const auto rs = buf_rsrc(row, (uint32_t)a.S * 4u);
+    const float* src = sbuf + r * pitch + i;
+    if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(row + tb) | reinterpret_cast<uintptr_t>(src)) & 15) == 0) {
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(src), rs, (tb + i) * 4, 0, kNonTemporal);
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i + e < n) __builtin_amdgcn_raw_buffer_store_b32(v[e], rs, (tb + i + e) * 4, 0, kNonTemporal);
+      for (int q = 0; q < 4; ++q)
+        if (i + q < n) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(src[q]), rs, (tb + i + q) * 4, 0, kNonTemporal);
     }
   }
 }
@@ -139,11 +145,24 @@ struct DenseKeys {
   // would keep 256 KB of key rows in flight per CU; one (128 KB) streams
   // faster (C5: 336 against 347 us per score pass), so the reservation
   // leaves room for only one.  Narrower rows keep two (128 KB in flight).
-  static constexpr int kLdsReserve = D * ES >= 256 ? 2 * kLds : kLds;
+  static constexpr bool kOneWg = D * ES >= 256;
+  static constexpr int kLdsReserve = kOneWg ? 2 * kLds : kLds;
   static_assert(kLdsReserve + 2048 * 4 <= 160 * 1024, "the reservation and the histogram fit a CU's LDS");
-  // group sums: tokens of the LDS score buffer (the host keeps a workgroup's range within it)
-  static constexpr int kSumBuf = GS ? score_sum_buf_tokens(kLdsReserve) : 4;
+  // Per-head scores of narrower rows (fp8, or D = 64) go through an LDS score
+  // buffer too, a row per head, filling the two workgroups' share of LDS:
+  // B32 H_q64 fp8 keys 138 -> 133 us at S16K, 42 -> 36 us at S4K.  With
+  // 256-byte rows (one workgroup per CU) the end-of-range flush cost more than
+  // it saved at S4K (bf16 67 -> 71 us), so those store from the tile.
+  static constexpr bool kHeadBuf = !GS && !kOneWg;
+  // LDS score buffer, in floats: group sums, one row of the workgroup's
+  // tokens; per-head scores, a row per head (the host keeps a workgroup's
+  // range within it)
+  static constexpr int kSumBuf = GS ? score_sum_buf_tokens(kLdsReserve)
+                                    : (kHeadBuf ? score_head_buf_floats(80 * 1024, kLdsReserve) : 4);
   static_assert(!GS || kSumBuf >= 1024, "room for a useful workgroup range");
+  static_assert(!kHeadBuf || kSumBuf >= 8 * 1024, "room for sixteen heads of a 512-token range");
+  float* hbuf;                 // per-head scores: the LDS score buffer, rows of hpitch tokens from htb
+  int hpitch, htb;
   struct Regs {
     u32x4 k[CPR];            // chunk lane + 64 i: row (lane + 64 i) / CPR, chunk (lane + 64 i) % CPR
   };
@@ -234,7 +253,11 @@ struct DenseKeys {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int h = lg * 4 + i;
-          score_store(a, b, hq0, nh, h, tok, h < nh && tok < a.S, s[i] * a.scaling);
+          if constexpr (kHeadBuf) {
+            if (h < nh && tok < a.S) hbuf[h * hpitch + (tok - htb)] = s[i] * a.scaling;
+          } else {
+            score_store(a, b, hq0, nh, h, tok, h < nh && tok < a.S, s[i] * a.scaling);
+          }
         }
       }
     }
@@ -272,7 +295,10 @@ struct PackedKeys {
   // group sums are returned by tile() (token t + lane per lane) and collected
   // by the driver; per-head scores are stored by tile()
   static constexpr bool kDeferStore = GS;
+  // LDS score buffer of group sums (as for dense keys); per-head scores are
+  // stored by tile()
   static constexpr int kSumBuf = GS ? score_sum_buf_tokens(kLdsReserve + kScoreWaves * 64 * NG * 4) : 4;
+  static constexpr bool kHeadBuf = false;
   char* kst;
   // One KV head's codes and scale/min rows, addressed through buffer
   // resources: every load is a 32-bit lane offset plus a uniform row offset,
@@ -537,13 +563,20 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   const int t_begin = part * a.tok_per_wg;
   const int t_end = min(t_begin + a.tok_per_wg, a.S);
   constexpr int STEP = kScoreWaves * 16 * P::CT;
-  __shared__ uint32_t hlds_mem[2048];
+  __shared__ uint32_t hlds_mem[P::kDeferStore ? 2048 : 1];   // histogram: group sums only
   __shared__ __attribute__((aligned(16))) float sbuf[P::kSumBuf];
+  if constexpr (P::kHeadBuf) {
+    pol.hbuf = sbuf;
+    pol.hpitch = a.tok_per_wg;
+    pol.htb = t_begin;
+  }
   uint32_t* hlds = nullptr;
-  if (a.hist) {
-    for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64) hlds_mem[i] = 0u;
-    __syncthreads();
-    hlds = hlds_mem;
+  if constexpr (P::kDeferStore) {
+    if (a.hist) {
+      for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64) hlds_mem[i] = 0u;
+      __syncthreads();
+      hlds = hlds_mem;
+    }
   }
   constexpr int ITER = 16 * P::CT;
   // wave-uniform (the compiler cannot see it from threadIdx), so the loop runs
@@ -559,7 +592,7 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
     pol.issue(a, t, t_end, lane, r0);
     if constexpr (P::kDeferStore) {
       // Group sums go to the LDS score buffer, kStoreBatch iterations' worth
-      // together, and to memory after the loop (score_flush_sums).
+      // together, and to memory after the loop (score_flush).
       static_assert(kStoreBatch % 2 == 0, "the register sets alternate within a batch");
       // one iteration: the next rows are requested (past the range the
       // resource has zero length, so the last step's requests read nothing
@@ -623,13 +656,18 @@ __global__ __launch_bounds__(kScoreWaves * 64, 2) void score_kernel(ScoreArgs a)
   }
   if constexpr (P::kDeferStore) {
     __syncthreads();
-    score_flush_sums(a, b, hk, t_begin, t_end - t_begin, sbuf, kScoreWaves * 64);
-  }
-  if (a.hist) {
+    score_flush(a, b, hk, 1, t_begin, t_end - t_begin, 0, sbuf, kScoreWaves * 64);
+  } else if constexpr (P::kHeadBuf) {
     __syncthreads();
-    uint32_t* hr = a.hist + ((int64_t)b * a.Hk + hk) * 2048;
-    for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64)
-      if (hlds_mem[i]) atomicAdd(hr + i, hlds_mem[i]);
+    score_flush(a, b, hq0, nh, t_begin, t_end - t_begin, a.tok_per_wg, sbuf, kScoreWaves * 64);
+  }
+  if constexpr (P::kDeferStore) {
+    if (a.hist) {
+      __syncthreads();
+      uint32_t* hr = a.hist + ((int64_t)b * a.Hk + hk) * 2048;
+      for (int i = threadIdx.x; i < 2048; i += kScoreWaves * 64)
+        if (hlds_mem[i]) atomicAdd(hr + i, hlds_mem[i]);
+    }
   }
 }
 
@@ -726,14 +764,26 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   long per = ((long)S * units + target - 1) / target;
   per = (per + step - 1) / step * step;
   if (per < step) per = step;
-  // group sums of dense keys: a workgroup's range fits its LDS score buffer
-  long cap = 8192;
-  if (a.group_sum && !packed) {
-    if (D == 128)
-      cap = k_mode == kKeyBf16 ? DenseKeys<128, false, true>::kSumBuf : DenseKeys<128, true, true>::kSumBuf;
-    else
-      cap = k_mode == kKeyBf16 ? DenseKeys<64, false, true>::kSumBuf : DenseKeys<64, true, true>::kSumBuf;
-  }
+  // a workgroup's range fits its LDS score buffer: one row of group sums, or
+  // a row per query head of the unit
+  static_assert(!DenseKeys<128, false, false>::kHeadBuf && DenseKeys<128, true, false>::kHeadBuf &&
+                    DenseKeys<64, false, false>::kHeadBuf && DenseKeys<64, true, false>::kHeadBuf,
+                "which per-head policies buffer their scores");
+  long buf;
+  const bool bf = k_mode == kKeyBf16;
+  if (packed)
+    buf = 8192;                              // group sums; per-head scores are stored directly
+  else if (a.group_sum)
+    buf = D == 128 ? (bf ? DenseKeys<128, false, true>::kSumBuf : DenseKeys<128, true, true>::kSumBuf)
+                   : (bf ? DenseKeys<64, false, true>::kSumBuf : DenseKeys<64, true, true>::kSumBuf);
+  else if (D == 128 && bf)
+    buf = 8192;                              // per-head scores are stored directly
+  else
+    buf = (D == 128 ? DenseKeys<128, true, false>::kSumBuf
+                    : (bf ? DenseKeys<64, false, false>::kSumBuf : DenseKeys<64, true, false>::kSumBuf)) /
+          (a.HPU < a.G ? a.HPU : a.G);       // a row per head of the unit
+  long cap = buf / step * step;
+  if (cap > 8192) cap = 8192;
   if (per > cap) per = cap;
   a.tok_per_wg = (int)per;
   a.parts = (int)((S + per - 1) / per);
