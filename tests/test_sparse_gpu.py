@@ -59,6 +59,34 @@ def test_group_scores_long_ragged(dev):
     assert torch.equal(idx.cpu().long(), R.topk_indices(s.cpu(), 1024, sorted_by_score=False))
 
 
+@pytest.mark.parametrize("fp8,D", [(True, 128), (False, 64)])
+def test_score_per_head_full_lds_buffer(dev, fp8, D):
+    """Per-head scores (16 query heads on one KV head) on a row long enough
+    that, on 256 CUs, each score workgroup's token range is the largest its
+    LDS score buffer holds for 16 head rows (768 tokens for fp8 keys and for
+    D = 64), with a ragged end: slices at the start, across workgroup
+    boundaries and at the end against the oracle (fp8 keys widened to bf16,
+    which is exact)."""
+    B, Hq, Hk = 1, 16, 1
+    S = 2048 * 768 + 555
+    g = torch.Generator(device=dev).manual_seed(17)
+    q = torch.randn(B, Hq, 1, D, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(B, Hk, S, D, device=dev, generator=g, dtype=torch.bfloat16)
+    if fp8:
+        k = k.to(torch.float8_e4m3fn)
+    s = SP.sparse_score_scalar(q, k, 0.088, score_bits=8 if fp8 else 16)
+    assert s.shape == (B, Hq, S)
+    qc = q.cpu()
+    for a, b in ((0, 2000), (768 - 300, 768 + 300), (7 * 768 - 200, 7 * 768 + 200), (S - 3000, S)):
+        ks = k[:, :, a:b].cpu()
+        ref = R.sparse_score_scalar(qc, ks.to(torch.bfloat16) if fp8 else ks, 0.088)
+        d = (s[:, :, a:b].cpu() - ref).abs().max().item()
+        print(f"tokens {a}..{b}: max-abs {d:.3e}", flush=True)
+        assert d <= SCORE_TOL, (a, b)
+    del k, s
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 def test_group_scores_full_lds_buffer(dev, fp8):
     """Rows long enough that, on 256 CUs, each score workgroup's token range
