@@ -296,8 +296,11 @@ struct PackedKeys {
   // by the driver; per-head scores are stored by tile()
   static constexpr bool kDeferStore = GS;
   // LDS score buffer of group sums (as for dense keys); per-head scores are
-  // stored by tile()
-  static constexpr int kSumBuf = GS ? score_sum_buf_tokens(kLdsReserve + kScoreWaves * 64 * NG * 4) : 4;
+  // stored by tile().  2-bit keys keep it at 4096 tokens, so more
+  // workgroups fit a CU (C5 int2 score pass 95 -> 88 us; 4-bit keys ran
+  // 1% slower with it, and both slower at 2048).
+  static constexpr int kSumBuf =
+      GS ? (BITS == 2 ? 4096 : score_sum_buf_tokens(kLdsReserve + kScoreWaves * 64 * NG * 4)) : 4;
   static constexpr bool kHeadBuf = false;
   char* kst;
   // One KV head's codes and scale/min rows, addressed through buffer
@@ -766,13 +769,17 @@ int bytes_sparse_score(const void* q, const void* k, int k_mode, const void* k_s
   if (per < step) per = step;
   // a workgroup's range fits its LDS score buffer: one row of group sums, or
   // a row per query head of the unit
+  static_assert(PackedKeys<64, 2, 1, true>::kSumBuf == PackedKeys<128, 2, 1, true>::kSumBuf &&
+                    PackedKeys<64, 4, 1, true>::kSumBuf >= PackedKeys<128, 4, 1, true>::kSumBuf,
+                "packed group-sum buffers of D = 64 hold at least the D = 128 ones");
   static_assert(!DenseKeys<128, false, false>::kHeadBuf && DenseKeys<128, true, false>::kHeadBuf &&
                     DenseKeys<64, false, false>::kHeadBuf && DenseKeys<64, true, false>::kHeadBuf,
                 "which per-head policies buffer their scores");
   long buf;
   const bool bf = k_mode == kKeyBf16;
   if (packed)
-    buf = 8192;                              // group sums; per-head scores are stored directly
+    buf = k_mode == kKeyP2 ? PackedKeys<128, 2, 1, true>::kSumBuf    // group sums (per-head
+                           : PackedKeys<128, 4, 1, true>::kSumBuf;   // scores are stored directly)
   else if (a.group_sum)
     buf = D == 128 ? (bf ? DenseKeys<128, false, true>::kSumBuf : DenseKeys<128, true, true>::kSumBuf)
                    : (bf ? DenseKeys<64, false, true>::kSumBuf : DenseKeys<64, true, true>::kSumBuf);

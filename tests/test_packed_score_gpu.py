@@ -154,8 +154,9 @@ def test_token_topk_packed_score_keys(dev, bits, B, Hq, Hk, S, kb, D):
 @pytest.mark.parametrize("bits", [4, 2])
 def test_packed_group_scores_full_lds_buffer(dev, bits):
     """Packed selection keys on rows long enough that, on 256 CUs, each score
-    workgroup's token range is the largest the host plans (8192 tokens, the
-    LDS score buffer's capacity), with a ragged end: group sums at the start,
+    workgroup's token range is the largest the host plans (the LDS score
+    buffer's capacity: 8192 tokens with 4-bit keys, 4096 with 2-bit), with
+    a ragged end: group sums at the start,
     across workgroup boundaries and at the end against the oracle on those
     slices of the dequantized keys."""
     B, Hq, Hk, D = 1, 24, 8, 128
