@@ -16,6 +16,13 @@
 // read.  The output tile lands with head (l/16)*4 + i and token l%16 in lane
 // l, so the group sum of up to four heads is a sum inside one lane.
 //
+// Group sums (and the per-head scores of fp8 keys and of D = 64 rows) are
+// collected in an LDS score buffer over the workgroup's whole token range
+// and leave in one burst of 16-byte stores after its last key load: a store
+// issued between two batches of key loads would hold up every later wait
+// for key rows until it is acknowledged.  The host sizes each workgroup's
+// range to fit the buffer.
+//
 // fp8 (OCP e4m3fn) keys (`score_bits=8`, :1113) load 8 bytes per operand and
 // are widened to bf16 exactly in registers.
 //
