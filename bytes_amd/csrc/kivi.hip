@@ -1266,8 +1266,7 @@ __device__ __forceinline__ void kivi_pipe_tile(int w, int lane, const f16x8 (&qh
 // once.
 template <int D, int BITS>
 struct PipeMeta {
-  uint32_t km[8];        // word t % 8 (groups 2(t%8), +1 of the two-granule block) of row k: scales (k < 4) or
-                         // zeros of channel 32(k % 4) + t / 8
+  uint32_t km[4];        // word t % 4 (groups 2(t%4), +1 of the granule) of (scale|zero, channel) row 64i + t / 4
   u32x4 vm;              // value scales (lanes 0-31) / zeros (32-63) of tokens 2(l % 32), +1 of the wave's tile
 };
 
@@ -1341,15 +1340,13 @@ __global__ __launch_bounds__(kPipeWaves * 64, pipe_wg_per_cu<BITS>()) void kivi_
     const int row = par * C::KROWS_DMA + lane / C::NPC;
     kvoff[par] = (uint32_t)(lane / C::NPC) * wkb + (uint32_t)(kslot_swz<C::NPC>(lane % C::NPC, row) << 4);
   }
-  // key scales/zeros, read for two granules at a time: thread t reads word
-  // t % 8 of the block's 32 bytes of the scale and zero rows of channels
-  // 32k + t / 8, eight threads to a row (a request touches 8 lines per wave;
-  // one granule at a time, four threads to a row, it touched 16 for half the
-  // bytes)
-  const int mw8 = threadIdx.x & 7, mr8 = threadIdx.x >> 3;
-  static_assert(kPipeWaves * 64 / 8 * 4 == D, "32 channels per load: loads 0-3 scales, 4-7 zeros");
-  const _Float16* mrow = a.ks + ((size_t)bh * D + mr8) * ngk + 2 * mw8;
-  const _Float16* zrow = a.km + ((size_t)bh * D + mr8) * ngk + 2 * mw8;
+  // key scales/zeros: rows 0..D-1 scales, D..2D-1 zeros of channels 0..D-1;
+  // thread t reads word t % 4 of the granule's 16 bytes of rows 64i + t / 4,
+  // four threads to a row (a request touches 16 lines per wave)
+  const int mwd = threadIdx.x & 3, mr0 = threadIdx.x >> 2;
+  static_assert(kPipeWaves * 64 / 4 == D / 2, "64 rows per step: steps 0-1 scales, 2-3 zeros");
+  const _Float16* mrow = a.ks + ((size_t)bh * D + mr0) * ngk + 2 * mwd;
+  const _Float16* zrow = a.km + ((size_t)bh * D + mr0) * ngk + 2 * mwd;
   // value scales/zeros of two tokens per lane
   const _Float16* vmb = (lane < 32 ? a.vs : a.vm) + (size_t)bh * Sq * C::NGV + 2 * (lane & 31) * C::NGV;
 
@@ -1366,29 +1363,21 @@ __global__ __launch_bounds__(kPipeWaves * 64, pipe_wg_per_cu<BITS>()) void kivi_
 #pragma unroll
     for (int j = 0; j < C::VDMA; ++j)
       lds_dma16<true>(rvq, stage + C::OFF_V + w * C::VB + j * 1024, (uint32_t)tt * C::VROW + j * 1024 + lane * 16);
-    // scales/zeros of groups and tokens past the cache end: clamped copies no
-    // tile reads (the pipelined kernel runs only for Sq >= 1024, so the
-    // clamped word stays inside its row)
-    if ((gi & 1) == 0) {
-      const int g0 = tg >> 5;
-      const int go = min(g0 + 2 * mw8, ngk - 2) - 2 * mw8;
+    // scales/zeros of groups and tokens past the cache end: clamped copies no tile reads
+    const int g0 = tg >> 5;
+    const int go = min(g0 + 2 * mwd, ngk - 2) - 2 * mwd;
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        m.km[k] = *reinterpret_cast<const uint32_t*>((k < 4 ? mrow : zrow) + (size_t)((k & 3) * 32) * ngk + go);
-    }
+    for (int i = 0; i < 4; ++i)
+      m.km[i] = *reinterpret_cast<const uint32_t*>((i < 2 ? mrow : zrow) + (size_t)((i & 1) * 64) * ngk + go);
     m.vm = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vmb + (size_t)min(tt, Sq - kKiviTile) * C::NGV));
   };
-  // half: which granule of the two-granule block (the threads holding its
-  // words, t % 8 / 4 == half, stage them)
-  auto stage_meta = [&](char* stage, const PipeMeta<D, BITS>& m, int half) {
-    if ((mw8 >> 2) == half) {
-      _Float16* kd = reinterpret_cast<_Float16*>(stage + C::OFF_KM) + 2 * (mw8 & 3) * C::KMP;
+  auto stage_meta = [&](char* stage, const PipeMeta<D, BITS>& m) {
+    _Float16* kd = reinterpret_cast<_Float16*>(stage + C::OFF_KM) + 2 * mwd * C::KMP;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int o = (k >> 2) * C::NGG * C::KMP + kslot_pos<BITS>((k & 3) * 32 + mr8);
-        kd[o] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[k] & 0xFFFFu));
-        kd[o + C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[k] >> 16));
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int o = (i >> 1) * C::NGG * C::KMP + kslot_pos<BITS>((i & 1) * 64 + mr0);
+      kd[o] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[i] & 0xFFFFu));
+      kd[o + C::KMP] = __builtin_bit_cast(_Float16, (uint16_t)(m.km[i] >> 16));
     }
     _Float16* vd = reinterpret_cast<_Float16*>(stage + C::OFF_VM + w * C::VMB);
     const _Float16* hv = reinterpret_cast<const _Float16*>(&m.vm);
@@ -1421,7 +1410,7 @@ __global__ __launch_bounds__(kPipeWaves * 64, pipe_wg_per_cu<BITS>()) void kivi_
   // compute this wave's tile.
   auto step = [&](int gi, char* cur, char* nxt) {
     __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0)
-    stage_meta(cur, meta, gi & 1);
+    stage_meta(cur, meta);
     lds_barrier();
     if (gi + 1 < ngr) issue(gi + 1, nxt, meta);
     if (t_begin + gi * kPipeGran + w * kKiviTile < t_end)
